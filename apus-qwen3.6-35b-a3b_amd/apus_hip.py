@@ -1,0 +1,255 @@
+"""Python binding of libapus_hip.so (the C ABI in include/apus_hip.h).
+
+Tier-1 wrappers take and return numpy arrays (bf16 as uint16 codes, fp32
+as float32) and keep the reference's argument meaning (c/gdn.h:107-192,
+c/attn.h:87-158). Tier-2 wrappers take torch tensors that live on the GPU
+and pass their device pointers; torch is only the allocator here.
+
+Every call raises ApusHipError when the library returns nonzero, so a
+missing or failing GPU path is never silently replaced by anything else.
+"""
+import ctypes as C
+import os
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libapus_hip.so")
+
+_u16p = C.POINTER(C.c_uint16)
+_f32p = C.POINTER(C.c_float)
+_i32p = C.POINTER(C.c_int32)
+_sz = C.c_size_t
+_vp = C.c_void_p
+
+# Every symbol include/apus_hip.h declares (checked by the CPU tests).
+EXPORTS = [
+    "apus_hip_init", "apus_hip_is_enabled", "apus_hip_last_error",
+    "apus_hip_set_stream", "apus_hip_synchronize", "apus_hip_malloc",
+    "apus_hip_free", "apus_hip_memcpy_h2d", "apus_hip_memcpy_d2h",
+    "apus_hip_memset",
+    "apus_hip_gdn_conv1d", "apus_hip_gdn_conv1d_step", "apus_hip_gdn_decay",
+    "apus_hip_gdn_beta", "apus_hip_gdn_l2norm", "apus_hip_gdn_step",
+    "apus_hip_gdn_step_mt", "apus_hip_gdn_recurrent", "apus_hip_gdn_onorm",
+    "apus_hip_attn_rmsnorm", "apus_hip_attn_rope", "apus_hip_attn_gqa",
+    "apus_hip_attn_gqa_decode", "apus_hip_attn_gqa_mt",
+    "apus_hip_attn_gqa_decode_mt", "apus_hip_attn_outgate",
+    "apus_hip_gdn_decode",
+]
+
+
+class ApusHipError(RuntimeError):
+    def __init__(self, code, msg):
+        super().__init__(f"apus_hip error {code}: {msg}")
+        self.code = code
+
+
+class GdnLayer(C.Structure):
+    """ApusHipGdnLayer (include/apus_hip.h)."""
+    _fields_ = [("hk", _sz), ("hv", _sz), ("dk", _sz), ("dv", _sz),
+                ("conv_w", _vp), ("A_log", _vp), ("dt_bias", _vp),
+                ("onorm_w", _vp)]
+
+
+_lib = None
+
+
+def load(path=LIB_PATH):
+    """Load the library (once). Raises if it was not built."""
+    global _lib
+    if _lib is None:
+        # torch ships its own libamdhip64.so.7. Importing it first makes the
+        # dynamic loader bind this library to that same HIP runtime (by
+        # SONAME), so tensors allocated by torch and our kernels share one
+        # runtime; loading ours first would map a second runtime that then
+        # hides the GPU from torch.
+        try:
+            import torch  # noqa: F401
+        except ImportError:
+            pass
+        if not os.path.exists(path):
+            raise FileNotFoundError(
+                f"{path} is missing: build it with "
+                "`python -c 'import __graft_entry__ as g; g.build()'`")
+        _lib = C.CDLL(path)
+        for name in EXPORTS:
+            getattr(_lib, name).restype = C.c_int
+        _lib.apus_hip_last_error.restype = _sz
+    return _lib
+
+
+def last_error():
+    buf = C.create_string_buffer(512)
+    load().apus_hip_last_error(buf, 512)
+    return buf.value.decode(errors="replace")
+
+
+def _chk(rc):
+    if rc != 0:
+        raise ApusHipError(rc, last_error())
+
+
+def _u16(a):
+    assert a.dtype == np.uint16 and a.flags["C_CONTIGUOUS"]
+    return a.ctypes.data_as(_u16p)
+
+
+def _f32(a):
+    assert a.dtype == np.float32 and a.flags["C_CONTIGUOUS"]
+    return a.ctypes.data_as(_f32p)
+
+
+def _dp(t):
+    """Device pointer of a torch tensor (or None)."""
+    if t is None:
+        return None
+    assert t.is_cuda and t.is_contiguous(), "tier-2 tensors must be contiguous GPU tensors"
+    return _vp(t.data_ptr())
+
+
+def init(device=0):
+    err = C.create_string_buffer(512)
+    rc = load().apus_hip_init(C.c_int(device), err, 512)
+    if rc != 0:
+        raise ApusHipError(rc, err.value.decode(errors="replace"))
+
+
+def set_stream(stream_handle):
+    _chk(load().apus_hip_set_stream(_vp(stream_handle)))
+
+
+def synchronize():
+    _chk(load().apus_hip_synchronize())
+
+
+# ---------------------------------------------------------------- tier 1
+def gdn_conv1d(x, w, state):
+    T, Cc = x.shape
+    out = np.empty_like(x)
+    _chk(load().apus_hip_gdn_conv1d(_u16(x), _u16(w), _u16(out), _sz(Cc),
+                                    _sz(T), _u16(state)))
+    return out
+
+
+def gdn_conv1d_step(x, w, state):
+    out = np.empty_like(x)
+    _chk(load().apus_hip_gdn_conv1d_step(_u16(x), _u16(w), _u16(out),
+                                         _sz(x.size), _u16(state)))
+    return out
+
+
+def gdn_decay(a, A_log, dt_bias):
+    g = np.empty(a.size, np.float32)
+    _chk(load().apus_hip_gdn_decay(_u16(a), _f32(A_log), _f32(dt_bias),
+                                   _f32(g), _sz(a.size)))
+    return g
+
+
+def gdn_beta(b):
+    beta = np.empty_like(b)
+    _chk(load().apus_hip_gdn_beta(_u16(b), _u16(beta), _sz(b.size)))
+    return beta
+
+
+def gdn_l2norm(x, H, D, scale):
+    y = np.empty(H * D, np.float32)
+    _chk(load().apus_hip_gdn_l2norm(_u16(x), _f32(y), _sz(H), _sz(D),
+                                    C.c_float(scale)))
+    return y
+
+
+def gdn_step(S, q, k, v, g, beta, H, Dk, Dv):
+    o = np.empty(H * Dv, np.float32)
+    _chk(load().apus_hip_gdn_step(_f32(S), _f32(q), _f32(k), _u16(v), _f32(g),
+                                  _u16(beta), _f32(o), _sz(H), _sz(Dk),
+                                  _sz(Dv)))
+    return o
+
+
+def gdn_step_mt(S, q, k, v, g, beta, H, Dk, Dv):
+    o = np.empty(H * Dv, np.float32)
+    _chk(load().apus_hip_gdn_step_mt(_f32(S), _f32(q), _f32(k), _u16(v),
+                                     _f32(g), _u16(beta), _f32(o), _sz(H),
+                                     _sz(Dk), _sz(Dv)))
+    return o
+
+
+def gdn_recurrent(S, q, k, v, g, beta, T, H, Dk, Dv):
+    o = np.empty(T * H * Dv, np.float32)
+    _chk(load().apus_hip_gdn_recurrent(_f32(S), _f32(q), _f32(k), _u16(v),
+                                       _f32(g), _u16(beta), _f32(o), _sz(T),
+                                       _sz(H), _sz(Dk), _sz(Dv)))
+    return o
+
+
+def gdn_onorm(o, z, w, H, D):
+    y = np.empty(H * D, np.uint16)
+    _chk(load().apus_hip_gdn_onorm(_u16(o), _u16(z), _u16(w), _u16(y),
+                                   _sz(H), _sz(D)))
+    return y
+
+
+def attn_rmsnorm(x, w):
+    y = np.empty_like(x)
+    _chk(load().apus_hip_attn_rmsnorm(_u16(x), _u16(w), _u16(y), _sz(x.size)))
+    return y
+
+
+def attn_rope(x, rot, pos, theta=1e7):
+    y = np.empty_like(x)
+    _chk(load().apus_hip_attn_rope(_u16(x), _u16(y), _sz(x.size), _sz(rot),
+                                   C.c_float(pos), C.c_double(theta)))
+    return y
+
+
+def attn_gqa(q, kc, vc, Tq, Tk, H, Hkv, D, scale):
+    o = np.empty(Tq * H * D, np.uint16)
+    _chk(load().apus_hip_attn_gqa(_u16(q), _u16(kc), _u16(vc), _u16(o),
+                                  _sz(Tq), _sz(Tk), _sz(H), _sz(Hkv), _sz(D),
+                                  C.c_float(scale), None, None))
+    return o
+
+
+def attn_gqa_decode(q, kc, vc, Tk, H, Hkv, D, scale):
+    o = np.empty(H * D, np.uint16)
+    _chk(load().apus_hip_attn_gqa_decode(_u16(q), _u16(kc), _u16(vc), _u16(o),
+                                         _sz(Tk), _sz(H), _sz(Hkv), _sz(D),
+                                         C.c_float(scale), None, None))
+    return o
+
+
+def attn_gqa_mt(q, kc, vc, Tq, Tk, H, Hkv, D, scale):
+    o = np.empty(Tq * H * D, np.uint16)
+    _chk(load().apus_hip_attn_gqa_mt(_u16(q), _u16(kc), _u16(vc), _u16(o),
+                                     _sz(Tq), _sz(Tk), _sz(H), _sz(Hkv),
+                                     _sz(D), C.c_float(scale)))
+    return o
+
+
+def attn_outgate(o, gate):
+    y = np.empty_like(o)
+    _chk(load().apus_hip_attn_outgate(_u16(o), _u16(gate), _u16(y),
+                                      _sz(o.size)))
+    return y
+
+
+# ---------------------------------------------------------------- tier 2
+def _cu_arr(cu):
+    cu = np.ascontiguousarray(np.asarray(cu, dtype=np.int32))
+    return cu, cu.ctypes.data_as(_i32p), len(cu) - 1
+
+
+def gdn_layer(dims, w):
+    """Build an ApusHipGdnLayer from dims (hk, hv, dk, dv) and a dict of
+    device tensors conv_w, A_log, dt_bias, onorm_w. Keep `w` alive."""
+    hk, hv, dk, dv = dims
+    return GdnLayer(hk, hv, dk, dv, w["conv_w"].data_ptr(),
+                    w["A_log"].data_ptr(), w["dt_bias"].data_ptr(),
+                    w["onorm_w"].data_ptr())
+
+
+def gdn_decode(layer, cu, qkv, z, a, b, conv_state, S, y):
+    cu, cup, B = _cu_arr(cu)
+    _chk(load().apus_hip_gdn_decode(C.byref(layer), _sz(B), cup, _dp(qkv),
+                                    _dp(z), _dp(a), _dp(b), _dp(conv_state),
+                                    _dp(S), _dp(y)))

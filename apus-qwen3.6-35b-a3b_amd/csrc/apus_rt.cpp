@@ -1,0 +1,251 @@
+// apus_rt.cpp -- host runtime of libapus_hip (see apus_rt.h).
+#include "apus_rt.h"
+
+#include <math.h>
+#include <stdarg.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+#include <vector>
+
+#include "../../include/apus_hip.h"
+
+namespace apus {
+namespace {
+
+char g_err[512];
+int g_ready = 0;
+int g_device = 0;
+hipStream_t g_stream = nullptr;
+
+struct Buf {
+    void *p = nullptr;
+    size_t n = 0;
+};
+Buf g_scratch[kScratchSlots];
+Buf g_small[kScratchSlots];
+
+struct RopeTab {
+    size_t rot = 0;
+    double theta = 0.0;
+    size_t npos = 0;
+    uint16_t *dev = nullptr;
+};
+RopeTab g_rope;
+
+// RNE narrow on the host, c/bf16.h:268-274 rule.
+uint16_t host_bf16(float x) {
+    uint32_t u;
+    memcpy(&u, &x, 4);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)(u >> 16);
+    return (uint16_t)((u + 0x7fffu + ((u >> 16) & 1u)) >> 16);
+}
+
+bool disabled_by_env() {
+    const char *e = getenv("APUS_HIP_DISABLE");
+    return e && *e && strcmp(e, "0") != 0;
+}
+
+}  // namespace
+
+int set_error(int code, const char *fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_err, sizeof g_err, fmt, ap);
+    va_end(ap);
+    return code;
+}
+
+int hip_fail(hipError_t e, const char *what, const char *file, int line) {
+    return set_error(kErrHip, "%s failed: %s (%s:%d)", what,
+                     hipGetErrorString(e), file, line);
+}
+
+int ensure_ready() {
+    if (disabled_by_env())
+        return set_error(kErrDisabled, "disabled by APUS_HIP_DISABLE");
+    if (g_ready) return kOk;
+    int n = 0;
+    hipError_t e = hipGetDeviceCount(&n);
+    if (e != hipSuccess || n <= 0)
+        return set_error(kErrDisabled, "no HIP device visible (%s)",
+                         hipGetErrorString(e));
+    if (g_device >= n)
+        return set_error(kErrArgument, "device %d out of range (%d)",
+                         g_device, n);
+    APUS_HIP_TRY(hipSetDevice(g_device));
+    hipDeviceProp_t prop;
+    APUS_HIP_TRY(hipGetDeviceProperties(&prop, g_device));
+    if (strncmp(prop.gcnArchName, "gfx950", 6) != 0)
+        return set_error(kErrUnsupported,
+                         "device %d is %s; this build targets gfx950",
+                         g_device, prop.gcnArchName);
+    g_ready = 1;
+    return kOk;
+}
+
+hipStream_t stream() { return g_stream; }
+void set_stream(hipStream_t s) { g_stream = s; }
+
+void *scratch(int slot, size_t bytes) {
+    Buf &b = g_scratch[slot];
+    if (bytes == 0) bytes = 1;
+    if (b.n >= bytes) return b.p;
+    if (b.p) {
+        // pending work may still use the old buffer
+        if (hipStreamSynchronize(g_stream) != hipSuccess) return nullptr;
+        (void)hipFree(b.p);
+        b.p = nullptr;
+        b.n = 0;
+    }
+    size_t want = bytes + bytes / 4;
+    if (hipMalloc(&b.p, want) != hipSuccess) {
+        b.p = nullptr;
+        set_error(kErrHip, "hipMalloc of %zu bytes failed", want);
+        return nullptr;
+    }
+    b.n = want;
+    return b.p;
+}
+
+void *upload_small(int slot, const void *host, size_t bytes) {
+    Buf &b = g_small[slot];
+    if (b.n < bytes) {
+        if (b.p) {
+            if (hipStreamSynchronize(g_stream) != hipSuccess) return nullptr;
+            (void)hipFree(b.p);
+        }
+        size_t want = bytes < 4096 ? 4096 : bytes * 2;
+        if (hipMalloc(&b.p, want) != hipSuccess) {
+            b.p = nullptr;
+            b.n = 0;
+            set_error(kErrHip, "hipMalloc of %zu bytes failed", want);
+            return nullptr;
+        }
+        b.n = want;
+    }
+    // Synchronous with respect to the host buffer: the caller may reuse
+    // its array as soon as we return.
+    if (hipMemcpyAsync(b.p, host, bytes, hipMemcpyHostToDevice, g_stream) !=
+            hipSuccess ||
+        hipStreamSynchronize(g_stream) != hipSuccess) {
+        set_error(kErrHip, "upload of %zu bytes failed", bytes);
+        return nullptr;
+    }
+    return b.p;
+}
+
+const uint16_t *rope_table(size_t rot, double theta, size_t max_pos) {
+    if (g_rope.dev && g_rope.rot == rot && g_rope.theta == theta &&
+        g_rope.npos >= max_pos)
+        return g_rope.dev;
+    size_t npos = max_pos < 4096 ? 4096 : max_pos;
+    if (g_rope.dev && g_rope.rot == rot && g_rope.theta == theta &&
+        npos < g_rope.npos * 2)
+        npos = g_rope.npos * 2;
+    size_t R = rot / 2;
+    std::vector<float> invf(R);
+    for (size_t i = 0; i < R; i++)
+        invf[i] = (float)(1.0 / pow(theta, 2.0 * (double)i / (double)rot));
+    std::vector<uint16_t> tab(npos * rot);
+    for (size_t p = 0; p < npos; p++) {
+        float pos = (float)p;
+        uint16_t *row = tab.data() + p * rot;
+        for (size_t i = 0; i < R; i++) {
+            float ang = pos * invf[i];
+            row[i] = host_bf16(cosf(ang));
+            row[R + i] = host_bf16(sinf(ang));
+        }
+    }
+    if (g_rope.dev) {
+        if (hipStreamSynchronize(g_stream) != hipSuccess) return nullptr;
+        (void)hipFree(g_rope.dev);
+        g_rope.dev = nullptr;
+    }
+    if (hipMalloc(&g_rope.dev, tab.size() * 2) != hipSuccess) {
+        g_rope.dev = nullptr;
+        set_error(kErrHip, "hipMalloc of the rope table failed");
+        return nullptr;
+    }
+    if (hipMemcpy(g_rope.dev, tab.data(), tab.size() * 2,
+                  hipMemcpyHostToDevice) != hipSuccess) {
+        set_error(kErrHip, "rope table upload failed");
+        return nullptr;
+    }
+    g_rope.rot = rot;
+    g_rope.theta = theta;
+    g_rope.npos = npos;
+    return g_rope.dev;
+}
+
+}  // namespace apus
+
+using namespace apus;
+
+extern "C" {
+
+int apus_hip_init(int device, char *err, size_t errcap) {
+    g_device = device;
+    g_ready = 0;
+    int r = ensure_ready();
+    if (r != kOk && err && errcap) snprintf(err, errcap, "%s", g_err);
+    return r;
+}
+
+int apus_hip_is_enabled(void) { return ensure_ready() == kOk; }
+
+size_t apus_hip_last_error(char *buf, size_t cap) {
+    size_t n = strlen(g_err);
+    if (buf && cap) snprintf(buf, cap, "%s", g_err);
+    return n;
+}
+
+int apus_hip_set_stream(void *s) {
+    APUS_READY();
+    set_stream((hipStream_t)s);
+    return kOk;
+}
+
+int apus_hip_synchronize(void) {
+    APUS_READY();
+    APUS_HIP_TRY(hipStreamSynchronize(g_stream));
+    return kOk;
+}
+
+int apus_hip_malloc(void **dptr, size_t bytes) {
+    APUS_READY();
+    if (!dptr) return set_error(kErrArgument, "dptr is NULL");
+    APUS_HIP_TRY(hipMalloc(dptr, bytes ? bytes : 1));
+    return kOk;
+}
+
+int apus_hip_free(void *dptr) {
+    APUS_READY();
+    APUS_HIP_TRY(hipFree(dptr));
+    return kOk;
+}
+
+int apus_hip_memcpy_h2d(void *dst, const void *src, size_t bytes) {
+    APUS_READY();
+    APUS_HIP_TRY(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice,
+                                g_stream));
+    APUS_HIP_TRY(hipStreamSynchronize(g_stream));
+    return kOk;
+}
+
+int apus_hip_memcpy_d2h(void *dst, const void *src, size_t bytes) {
+    APUS_READY();
+    APUS_HIP_TRY(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost,
+                                g_stream));
+    APUS_HIP_TRY(hipStreamSynchronize(g_stream));
+    return kOk;
+}
+
+int apus_hip_memset(void *dst, int value, size_t bytes) {
+    APUS_READY();
+    APUS_HIP_TRY(hipMemsetAsync(dst, value, bytes, g_stream));
+    return kOk;
+}
+
+}  // extern "C"

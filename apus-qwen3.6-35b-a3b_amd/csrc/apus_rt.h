@@ -1,0 +1,64 @@
+// apus_rt.h -- host runtime of libapus_hip: error reporting, the current
+// stream, grow-only device scratch, pinned staging and the RoPE table.
+//
+// Conventions follow the reference's backend hooks (c/backend_metal.h:
+// 16-20, 79-88; c/bf16.h:199-205, 250-259): every entry point returns
+// int, 0 when it handled the op and nonzero otherwise, with a message
+// retrievable through apus_hip_last_error. One compute thread drives the
+// library (c/pool.h:7-16 model); it is not safe for concurrent callers.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace apus {
+
+enum Status : int {
+    kOk = 0,
+    kErrUnsupported = 1,   // shape/config not handled: caller uses its CPU op
+    kErrDisabled = 2,      // APUS_HIP_DISABLE set or library not initialised
+    kErrArgument = 3,      // invalid argument
+    kErrHip = 4,           // HIP runtime error
+};
+
+int set_error(int code, const char *fmt, ...);
+int hip_fail(hipError_t e, const char *what, const char *file, int line);
+
+// Lazily initialises the device on first use (device 0 unless
+// apus_hip_init chose another). Returns kOk or an error code.
+int ensure_ready();
+hipStream_t stream();
+void set_stream(hipStream_t s);
+
+// Grow-only device scratch, one buffer per slot. Valid until the next
+// call with the same slot and a larger size.
+enum ScratchSlot { kScratchIn = 0, kScratchIn2, kScratchIn3, kScratchIn4,
+                   kScratchIn5, kScratchIn6, kScratchOut, kScratchOut2,
+                   kScratchWork, kScratchWork2, kScratchWork3, kScratchMeta,
+                   kScratchSlots };
+void *scratch(int slot, size_t bytes);
+
+// Device RoPE table for (rot, theta): [npos][rot] bf16 codes, per
+// position cos for pairs 0..rot/2-1 then sin. Computed on the host with
+// the platform libm exactly as c/attn.h:251-255 and uploaded; grows to
+// cover positions 0..max_pos-1.
+const uint16_t *rope_table(size_t rot, double theta, size_t max_pos);
+
+// Upload a small host array (e.g. token offsets) to device memory owned
+// by the library; stream-ordered, valid until the next call with `slot`.
+void *upload_small(int slot, const void *host, size_t bytes);
+
+}  // namespace apus
+
+#define APUS_HIP_TRY(expr)                                                   \
+    do {                                                                     \
+        hipError_t e_ = (expr);                                              \
+        if (e_ != hipSuccess)                                                \
+            return ::apus::hip_fail(e_, #expr, __FILE__, __LINE__);          \
+    } while (0)
+
+#define APUS_READY()                                                         \
+    do {                                                                     \
+        int r_ = ::apus::ensure_ready();                                     \
+        if (r_ != ::apus::kOk) return r_;                                    \
+    } while (0)

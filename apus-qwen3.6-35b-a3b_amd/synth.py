@@ -1,0 +1,87 @@
+"""Seeded synthetic inputs for the BASELINE configurations.
+
+bf16 values are drawn in fp32 and narrowed with round-to-nearest-even (the
+reference's c/bf16.h:268-274 rule), so host (numpy) and device (torch)
+generation give the same codes for the same fp32 draws. Shapes are the
+model's (reference/config.json via c/layer.h:113-131):
+GDN hk=16, hv=32, dk=dv=128 (conv_dim 8192); GQA nh=16, nkv=2, d=256,
+rot=64, theta=1e7.
+
+Distributions (choices the config leaves open are
+recorded here and in the design notes): pre-conv qkv ~ N(0,1); conv_w ~
+N(0,0.1); A_log ~ U(0,2.7); dt_bias = 1.0 (the HF init, ones); a,b,z ~
+N(0,1); onorm_w = 1 + N(0,0.1); S0 ~ N(0,0.02) fp32; conv_state ~ N(0,1);
+attention qg/k/v ~ N(0,1); q/k norm weights ~ N(0,0.1) (stored gain-1).
+"""
+import numpy as np
+
+GDN_DIMS = (16, 32, 128, 128)           # hk, hv, dk, dv
+ATTN_DIMS = (16, 2, 256, 64, 1e7)       # nh, nkv, d, rot, theta
+
+
+def bf16_bits(x):
+    """fp32 -> bf16 codes, RNE, NaN passed through (c/bf16.h:268-274)."""
+    u = np.ascontiguousarray(x, dtype=np.float32).view(np.uint32)
+    nan = (u & 0x7FFFFFFF) > 0x7F800000
+    r = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+    return np.where(nan, (u >> 16).astype(np.uint16), r)
+
+
+def bf16_f32(b):
+    """bf16 codes -> fp32 (exact)."""
+    return (np.asarray(b, dtype=np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
+def normal_bf16(rng, shape, std=1.0, mean=0.0):
+    x = rng.standard_normal(shape, dtype=np.float32) * np.float32(std)
+    if mean:
+        x = x + np.float32(mean)
+    return bf16_bits(x)
+
+
+def gdn_weights(rng, dims=GDN_DIMS):
+    hk, hv, dk, dv = dims
+    cd = 2 * hk * dk + hv * dv
+    return dict(
+        conv_w=normal_bf16(rng, (cd, 4), 0.1),
+        A_log=rng.uniform(0.0, 2.7, hv).astype(np.float32),
+        dt_bias=np.ones(hv, np.float32),
+        onorm_w=normal_bf16(rng, (dv,), 0.1, mean=1.0),
+    )
+
+
+def gdn_tokens(rng, T, dims=GDN_DIMS):
+    """Projection outputs for T tokens: qkv, z, a, b (bf16 codes)."""
+    hk, hv, dk, dv = dims
+    cd = 2 * hk * dk + hv * dv
+    return dict(qkv=normal_bf16(rng, (T, cd)), z=normal_bf16(rng, (T, hv * dv)),
+                a=normal_bf16(rng, (T, hv)), b=normal_bf16(rng, (T, hv)))
+
+
+def gdn_state(rng, B, dims=GDN_DIMS, zero=False):
+    hk, hv, dk, dv = dims
+    cd = 2 * hk * dk + hv * dv
+    if zero:
+        return (np.zeros((B, cd * 3), np.uint16),
+                np.zeros((B, hv, dk, dv), np.float32))
+    conv = normal_bf16(rng, (B, cd * 3))
+    S = (rng.standard_normal((B, hv, dk, dv), dtype=np.float32)
+         * np.float32(0.02))
+    return conv, S
+
+
+def attn_weights(rng, dims=ATTN_DIMS):
+    nh, nkv, d, rot, theta = dims
+    return dict(qn_w=normal_bf16(rng, (d,), 0.1), kn_w=normal_bf16(rng, (d,), 0.1))
+
+
+def attn_tokens(rng, T, dims=ATTN_DIMS):
+    nh, nkv, d, rot, theta = dims
+    return dict(qg=normal_bf16(rng, (T, nh, 2 * d)), k=normal_bf16(rng, (T, nkv, d)),
+                v=normal_bf16(rng, (T, nkv, d)))
+
+
+def lognormal_contexts(rng, B, mu=np.log(4096.0), sigma=1.0, lo=256, hi=65536):
+    """Config 4 context lengths: LogNormal(mu, sigma) clipped to [lo, hi]."""
+    c = np.exp(rng.normal(mu, sigma, B))
+    return np.clip(np.round(c), lo, hi).astype(np.int64)

@@ -1,0 +1,159 @@
+/*
+ * include/apus_hip.h -- C ABI of libapus_hip.so, the MI355X (gfx950)
+ * implementation of the apus-qwen attention hot path: the Gated DeltaNet
+ * ops (reference c/gdn.h) and the gated-GQA ops (reference c/attn.h).
+ *
+ * Plain C: no HIP or torch types. bf16 travels as uint16_t codes, fp32 as
+ * float, dims as size_t, exactly as in the reference headers. Every entry
+ * point returns int: 0 when it handled the op, nonzero otherwise (the
+ * reference hook convention, c/backend_metal.h:16-20 and c/bf16.h:199-205:
+ * a nonzero return means "run your CPU kernel"); apus_hip_last_error()
+ * gives the message. Setting APUS_HIP_DISABLE=1 in the environment makes
+ * every entry point return APUS_HIP_ERR_DISABLED, which forces a host
+ * engine onto its CPU path (the forced-fallback switch of
+ * c/backend_metal.mm:490-495).
+ *
+ * The library is driven by one compute thread, like the reference engine
+ * (c/pool.h:7-16); it is not safe for concurrent callers.
+ *
+ * Tier 1 (drop-in): name-for-name replacements of the reference ops with
+ *   the same argument lists, HOST pointers, synchronous. Results equal
+ *   the reference scalar anchors up to libm ulps (expf/log1pf in the
+ *   gates); see each declaration for the reference signature replaced.
+ * Tier 2 (batched, device-resident): DEVICE pointers, stream-ordered on
+ *   the library's current stream (apus_hip_set_stream), state and caches
+ *   kept in HBM across calls.
+ */
+#ifndef APUS_HIP_H
+#define APUS_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define APUS_HIP_OK 0
+#define APUS_HIP_ERR_UNSUPPORTED 1
+#define APUS_HIP_ERR_DISABLED 2
+#define APUS_HIP_ERR_ARGUMENT 3
+#define APUS_HIP_ERR_HIP 4
+
+/* ---- library control ------------------------------------------------
+ * apus_hip_init mirrors `int apus_metal_enable(char *err, size_t errcap)`
+ * (c/bf16.h:250-254): 0 on success, else nonzero with a message in err.
+ * Calling it is optional; the first op initialises device 0. */
+int    apus_hip_init(int device, char *err, size_t errcap);
+/* mirrors apus_metal_is_enabled (c/bf16.h:256) */
+int    apus_hip_is_enabled(void);
+size_t apus_hip_last_error(char *buf, size_t cap);
+/* stream is a hipStream_t passed as void* (NULL = the null stream) */
+int    apus_hip_set_stream(void *stream);
+int    apus_hip_synchronize(void);
+/* Device memory for hosts that do not link HIP themselves (state, KV). */
+int    apus_hip_malloc(void **dptr, size_t bytes);
+int    apus_hip_free(void *dptr);
+int    apus_hip_memcpy_h2d(void *dst, const void *src, size_t bytes);
+int    apus_hip_memcpy_d2h(void *dst, const void *src, size_t bytes);
+int    apus_hip_memset(void *dst, int value, size_t bytes);
+
+/* ---- Tier 1: GDN ops (c/gdn.h) -------------------------------------- */
+/* replaces apus_gdn_conv1d      (c/gdn.h:107-108, impl 314-318) */
+int apus_hip_gdn_conv1d(const uint16_t *x, const uint16_t *w, uint16_t *out,
+                        size_t C, size_t T, uint16_t *state);
+/* replaces apus_gdn_conv1d_step (c/gdn.h:111-112, impl 305-312) */
+int apus_hip_gdn_conv1d_step(const uint16_t *x, const uint16_t *w,
+                             uint16_t *out, size_t C, uint16_t *state);
+/* replaces apus_gdn_decay       (c/gdn.h:123-124, impl 322-363) */
+int apus_hip_gdn_decay(const uint16_t *a, const float *A_log,
+                       const float *dt_bias, float *g, size_t H);
+/* replaces apus_gdn_beta        (c/gdn.h:133, impl 366-399) */
+int apus_hip_gdn_beta(const uint16_t *b, uint16_t *beta, size_t H);
+/* replaces apus_gdn_l2norm      (c/gdn.h:141-142, impl 402-465) */
+int apus_hip_gdn_l2norm(const uint16_t *x, float *y, size_t H, size_t D,
+                        float scale);
+/* replaces apus_gdn_step        (c/gdn.h:153-156, impl 587-595) */
+int apus_hip_gdn_step(float *S, const float *q, const float *k,
+                      const uint16_t *v, const float *g, const uint16_t *beta,
+                      float *o, size_t H, size_t Dk, size_t Dv);
+/* replaces apus_gdn_step_mt     (c/gdn.h:159-162, impl 619-625) */
+int apus_hip_gdn_step_mt(float *S, const float *q, const float *k,
+                         const uint16_t *v, const float *g,
+                         const uint16_t *beta, float *o, size_t H, size_t Dk,
+                         size_t Dv);
+/* replaces apus_gdn_recurrent   (c/gdn.h:166-169, impl 627-635) */
+int apus_hip_gdn_recurrent(float *S, const float *q, const float *k,
+                           const uint16_t *v, const float *g,
+                           const uint16_t *beta, float *o, size_t T,
+                           size_t H, size_t Dk, size_t Dv);
+/* replaces apus_gdn_onorm       (c/gdn.h:183-184, impl 639-661) */
+int apus_hip_gdn_onorm(const uint16_t *o, const uint16_t *z,
+                       const uint16_t *w, uint16_t *y, size_t H, size_t D);
+
+/* ---- Tier 1: attention ops (c/attn.h) ------------------------------- */
+/* replaces apus_attn_rmsnorm    (c/attn.h:87-88, impl 175-186) */
+int apus_hip_attn_rmsnorm(const uint16_t *x, const uint16_t *w, uint16_t *y,
+                          size_t N);
+/* replaces apus_attn_rope       (c/attn.h:99-100, impl 244-266) */
+int apus_hip_attn_rope(const uint16_t *x, uint16_t *y, size_t D, size_t rot,
+                       float pos, double theta);
+/* replaces apus_attn_gqa        (c/attn.h:112-115, impl 450-464);
+ * abuf/ebuf are accepted and unused (device scratch is used instead) */
+int apus_hip_attn_gqa(const uint16_t *q, const uint16_t *kc,
+                      const uint16_t *vc, uint16_t *o, size_t Tq, size_t Tk,
+                      size_t H, size_t Hkv, size_t D, float scale,
+                      uint16_t *abuf, float *ebuf);
+/* replaces apus_attn_gqa_decode (c/attn.h:119-122, impl 466-471) */
+int apus_hip_attn_gqa_decode(const uint16_t *q, const uint16_t *kc,
+                             const uint16_t *vc, uint16_t *o, size_t Tk,
+                             size_t H, size_t Hkv, size_t D, float scale,
+                             uint16_t *abuf, float *ebuf);
+/* replaces apus_attn_gqa_mt     (c/attn.h:128-131, impl 507-513) */
+int apus_hip_attn_gqa_mt(const uint16_t *q, const uint16_t *kc,
+                         const uint16_t *vc, uint16_t *o, size_t Tq,
+                         size_t Tk, size_t H, size_t Hkv, size_t D,
+                         float scale);
+/* replaces apus_attn_gqa_decode_mt (c/attn.h:132-135, impl 515-520) */
+int apus_hip_attn_gqa_decode_mt(const uint16_t *q, const uint16_t *kc,
+                                const uint16_t *vc, uint16_t *o, size_t Tk,
+                                size_t H, size_t Hkv, size_t D, float scale);
+/* replaces apus_attn_outgate    (c/attn.h:151-152, impl 524-531) */
+int apus_hip_attn_outgate(const uint16_t *o, const uint16_t *gate,
+                          uint16_t *y, size_t N);
+
+/* ---- Tier 2: batched device-resident mixers ---------------------------
+ * A "mixer" is the hot path between a layer's input projections and its
+ * output projection, i.e. the op sequence of c/layer.h:250-273 (GDN) and
+ * c/layer.h:300-322 (full attention), for B independent sequences.
+ * Tokens are packed: sequence s owns rows cu[s] .. cu[s+1]-1 (cu is a
+ * HOST array of B+1 ascending offsets, cu[0] = 0). Weight, activation,
+ * state and cache pointers are DEVICE pointers. */
+
+/* GDN layer weights + dims (the hot fields of ApusLayerCfg/ApusLayerW,
+ * c/layer.h:113-157). Device pointers. */
+typedef struct {
+    size_t hk, hv, dk, dv;          /* 16, 32, 128, 128 */
+    const uint16_t *conv_w;         /* [conv_dim, 4] bf16 */
+    const float *A_log, *dt_bias;   /* [hv] f32 */
+    const uint16_t *onorm_w;        /* [dv] bf16, direct weight */
+} ApusHipGdnLayer;
+
+/* Fused GDN decode / verify: for each sequence, its tokens in order run
+ * conv1d+SiLU, beta, decay, l2norm, the delta-rule step and the gated
+ * RMSNorm (c/layer.h:250-273 per token; 1..k tokens per sequence, the MTP
+ * verify shape of c/mtp.h:36-75).
+ *   qkv [Ttot, 2*hk*dk + hv*dv], z [Ttot, hv*dv], a,b [Ttot, hv] bf16;
+ *   conv_state [B, conv_dim*3] bf16 (in/out); S [B, hv, dk, dv] f32
+ *   (in/out); y [Ttot, hv*dv] bf16 (feeds w_out).
+ * Supports dk = dv = 128 and hv = 2*hk (the model's shape). */
+int apus_hip_gdn_decode(const ApusHipGdnLayer *L, size_t B,
+                        const int32_t *cu, const uint16_t *qkv,
+                        const uint16_t *z, const uint16_t *a,
+                        const uint16_t *b, uint16_t *conv_state, float *S,
+                        uint16_t *y);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* APUS_HIP_H */

@@ -1,0 +1,72 @@
+"""Tolerance checks shared by the parity tests.
+
+Tolerances (made precise here):
+  * bf16 outputs: relative error ||c - r||_2 / ||r||_2 <= 2e-3 over the
+    tensor, and no element further than `max_ulp` bf16 ulps from the
+    oracle (1 for ops that keep the reference's summation order, where a
+    difference can only come from a libm ulp or a summation-order ulp
+    crossing a bf16 rounding boundary) unless its absolute difference is
+    below 1e-3 of the tensor's rms (values that are tiny through
+    cancellation, where an upstream fp32 ulp moves several bf16 ulps).
+  * fp32 recurrent state: max |c - r| / max |r| <= 1e-4.
+  * integer-like data (codes of exact copies, cache rows): bit-exact.
+"""
+import numpy as np
+
+BF16_REL = 2e-3
+STATE_REL = 1e-4
+
+
+def _ordered(codes):
+    """Map bf16 codes to integers whose difference is the ulp distance."""
+    c = np.asarray(codes, dtype=np.uint16).astype(np.int32)
+    return np.where(c & 0x8000, 0x8000 - c, c)
+
+
+def ulp_diff(a, b):
+    return np.abs(_ordered(a) - _ordered(b))
+
+
+def f32_of(codes):
+    return (np.asarray(codes, dtype=np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
+def bf16_stats(c, r):
+    c = np.asarray(c).ravel()
+    r = np.asarray(r).ravel()
+    cf = f32_of(c).astype(np.float64)
+    rf = f32_of(r).astype(np.float64)
+    nr = np.linalg.norm(rf)
+    rel = np.linalg.norm(cf - rf) / nr if nr > 0 else np.linalg.norm(cf)
+    ud = ulp_diff(c, r)
+    rms = np.sqrt(np.mean(rf * rf)) if rf.size else 0.0
+    far = np.abs(cf - rf) > 1e-3 * rms
+    return dict(rel=float(rel), max_ulp=int(ud[far].max()) if far.any() else int(min(1, ud.max(initial=0))),
+                exact=float(np.mean(ud == 0)) if ud.size else 1.0, n=int(ud.size),
+                raw_max_ulp=int(ud.max(initial=0)))
+
+
+def assert_bf16_close(c, r, max_ulp=1, rel=BF16_REL, what=""):
+    st = bf16_stats(c, r)
+    assert st["rel"] <= rel and st["max_ulp"] <= max_ulp, f"{what}: {st}"
+    return st
+
+
+def state_rel(c, r):
+    c = np.asarray(c, dtype=np.float64)
+    r = np.asarray(r, dtype=np.float64)
+    den = np.max(np.abs(r))
+    return float(np.max(np.abs(c - r)) / den) if den > 0 else float(np.max(np.abs(c)))
+
+
+def assert_state_close(c, r, rel=STATE_REL, what=""):
+    e = state_rel(c, r)
+    assert e <= rel, f"{what}: state rel err {e:.3g} > {rel}"
+    return e
+
+
+def f32_stats(c, r):
+    c = np.asarray(c, np.float32).ravel()
+    r = np.asarray(r, np.float32).ravel()
+    same = np.mean(c.view(np.uint32) == r.view(np.uint32)) if c.size else 1.0
+    return dict(exact=float(same), rel=state_rel(c, r))

@@ -1,0 +1,155 @@
+"""GPU parity: Gated DeltaNet ops through the C ABI against the oracle.
+
+Drop-in ops keep the reference's summation order, so outputs must be
+bit-identical to the oracle except where a libm ulp (expf/log1pf in the
+gates, which the GPU evaluates correctly rounded) crosses a rounding
+boundary: bf16 outputs within 1 ulp and 2e-3 relative (tests/numerics.py),
+fp32 outputs within 1e-4 relative, with the exact-match fraction reported.
+The fused decode is held to the same bar at BASELINE config 0 (B=1), at
+B=64, and on ragged multi-token verify batches (config 4's shape).
+"""
+import numpy as np
+import pytest
+
+import synth
+from numerics import assert_bf16_close, assert_state_close, f32_stats
+
+pytestmark = pytest.mark.gpu
+
+
+def _f32(rng, n, s=1.0):
+    return rng.standard_normal(n, dtype=np.float32) * np.float32(s)
+
+
+@pytest.mark.parametrize("C,T", [(37, 9), (8192, 1), (8192, 64)])
+def test_conv1d(hip, orc, rng, C, T):
+    x = synth.normal_bf16(rng, (T, C), 1.5)
+    w = synth.normal_bf16(rng, (C, 4), 0.7)
+    st = synth.normal_bf16(rng, (C * 3,))
+    s1, s2 = st.copy(), st.copy()
+    assert_bf16_close(hip.gdn_conv1d(x, w, s1), orc.gdn_conv1d(x, w, s2), what="conv")
+    assert np.array_equal(s1, s2)          # state = exact input codes
+
+
+def test_decay_beta(hip, orc, rng):
+    H = 4099
+    a = synth.normal_bf16(rng, (H,), 3.0)
+    b = synth.normal_bf16(rng, (H,), 6.0)
+    A = rng.uniform(-1, 2.7, H).astype(np.float32)
+    dt = _f32(rng, H, 4.0)
+    g1, g2 = hip.gdn_decay(a, A, dt), orc.gdn_decay(a, A, dt)
+    st = f32_stats(g1, g2)
+    assert st["rel"] <= 1e-6, st
+    assert_bf16_close(hip.gdn_beta(b), orc.gdn_beta(b), what="beta")
+    corner = synth.bf16_bits(np.array([0.0, 20.0], np.float32))
+    assert list(hip.gdn_beta(corner)) == [0x3F00, 0x3F80]
+
+
+@pytest.mark.parametrize("H,D,scale", [(2, 65, 1.0), (16, 128, 128 ** -0.5)])
+def test_l2norm_bitwise(hip, orc, rng, H, D, scale):
+    x = synth.normal_bf16(rng, (H * D,))
+    y1, y2 = hip.gdn_l2norm(x, H, D, scale), orc.gdn_l2norm(x, H, D, scale)
+    assert np.array_equal(y1.view(np.uint32), y2.view(np.uint32))
+
+
+@pytest.mark.parametrize("H,Dk,Dv,T", [(2, 32, 32, 10), (32, 128, 128, 4), (1, 16, 48, 5)])
+def test_recurrent(hip, orc, rng, H, Dk, Dv, T):
+    q = _f32(rng, T * H * Dk, 0.25)
+    k = _f32(rng, T * H * Dk, 0.25)
+    v = synth.normal_bf16(rng, (T * H * Dv,), 1.5)
+    g = (-5.0 * rng.random(T * H)).astype(np.float32)
+    beta = synth.bf16_bits(rng.random(T * H).astype(np.float32))
+    S0 = _f32(rng, H * Dk * Dv, 0.02)
+    S1, S2 = S0.copy(), S0.copy()
+    o1 = hip.gdn_recurrent(S1, q, k, v, g, beta, T, H, Dk, Dv)
+    o2 = orc.gdn_recurrent(S2, q, k, v, g, beta, T, H, Dk, Dv)
+    assert f32_stats(o1, o2)["rel"] <= 1e-4
+    assert_state_close(S1, S2, what="recurrent S")
+    # step == recurrent token by token, on the GPU too
+    S3 = S0.copy()
+    o3 = np.concatenate([hip.gdn_step(S3, q[t * H * Dk:(t + 1) * H * Dk], k[t * H * Dk:(t + 1) * H * Dk],
+                                      v[t * H * Dv:(t + 1) * H * Dv], g[t * H:(t + 1) * H],
+                                      beta[t * H:(t + 1) * H], H, Dk, Dv) for t in range(T)])
+    assert np.array_equal(o3.view(np.uint32), o1.view(np.uint32))
+    assert np.array_equal(S3.view(np.uint32), S1.view(np.uint32))
+
+
+def test_recurrent_corners(hip, rng):
+    D = 32
+    S0 = ((np.arange(D * D) % 7) * 0.25 - 0.75).astype(np.float32)
+    S1 = S0.copy()
+    q1 = _f32(rng, D)
+    k1 = _f32(rng, D)
+    v1 = synth.normal_bf16(rng, (D,))
+    hip.gdn_step(S1, q1, k1, v1, np.zeros(1, np.float32), np.zeros(1, np.uint16), 1, D, D)
+    assert np.array_equal(S1.view(np.uint32), S0.view(np.uint32))
+    S2 = S0.copy()
+    hip.gdn_step(S2, q1, np.zeros(D, np.float32), np.zeros(D, np.uint16),
+                 np.array([-5.0], np.float32), synth.bf16_bits(np.array([0.5], np.float32)), 1, D, D)
+    assert np.array_equal(S2, S0 * np.float32(np.exp(-5.0)))
+
+
+@pytest.mark.parametrize("H,D", [(3, 96), (32, 128)])
+def test_onorm(hip, orc, rng, H, D):
+    o = synth.normal_bf16(rng, (H * D,), 1.5)
+    z = synth.normal_bf16(rng, (H * D,), 2.0)
+    w = synth.normal_bf16(rng, (D,), 0.8)
+    assert_bf16_close(hip.gdn_onorm(o, z, w, H, D), orc.gdn_onorm(o, z, w, H, D), what="onorm")
+
+
+# ---------------------------------------------------------------- fused decode
+def _run_decode(hip, orc, rng, cu, zero_state=False):
+    import torch
+    dims = synth.GDN_DIMS
+    B = len(cu) - 1
+    T = int(cu[-1])
+    w = synth.gdn_weights(rng)
+    tok = synth.gdn_tokens(rng, T)
+    conv, S = synth.gdn_state(rng, B, zero=zero_state)
+    # oracle
+    c_o, S_o = conv.copy(), S.copy()
+    y_o, tr = orc.gdn_mixer(dims, w, np.asarray(cu, np.int32), tok["qkv"], tok["z"], tok["a"],
+                            tok["b"], c_o, S_o, trace=True)
+    # GPU (tier 2, device resident)
+    dev = torch.device("cuda")
+    tw = {k: torch.from_numpy(v.view(np.int16) if v.dtype == np.uint16 else v).to(dev)
+          for k, v in w.items()}
+    layer = hip.gdn_layer(dims, tw)
+    t = {k: torch.from_numpy(v.view(np.int16)).to(dev) for k, v in tok.items()}
+    dconv = torch.from_numpy(conv.view(np.int16)).to(dev)
+    dS = torch.from_numpy(S).to(dev)
+    y = torch.empty((T, dims[1] * dims[3]), dtype=torch.int16, device=dev)
+    hip.gdn_decode(layer, cu, t["qkv"], t["z"], t["a"], t["b"], dconv, dS, y)
+    torch.cuda.synchronize()
+    y_h = y.cpu().numpy().view(np.uint16)
+    st = assert_bf16_close(y_h, y_o, what="gdn_decode y")
+    assert np.array_equal(dconv.cpu().numpy().view(np.uint16), c_o)
+    e = assert_state_close(dS.cpu().numpy(), S_o, what="gdn_decode S")
+    return st, e
+
+
+def test_gdn_decode_config0(hip, orc):
+    """one layer, one decode step, batch 1, prior state."""
+    st, e = _run_decode(hip, orc, np.random.default_rng(20260829), [0, 1])
+    print(f"config0 y: {st} state rel {e:.3g}")
+
+
+def test_gdn_decode_batch64(hip, orc):
+    """Config 0 at batch 64 (the HBM-bound decode shape)."""
+    cu = np.arange(65, dtype=np.int32)
+    st, e = _run_decode(hip, orc, np.random.default_rng(64), cu)
+    print(f"B=64 y: {st} state rel {e:.3g}")
+
+
+def test_gdn_decode_ragged_verify(hip, orc):
+    """Config 4's GDN shape: each sequence verifies 1..4 tokens."""
+    rng = np.random.default_rng(4)
+    k = rng.integers(1, 5, 9)
+    cu = np.concatenate([[0], np.cumsum(k)]).astype(np.int32)
+    _run_decode(hip, orc, rng, cu)
+
+
+def test_gdn_decode_zero_state_long(hip, orc):
+    """A 32-token single sequence from zero state: decode stepping through
+    a prefill-length span keeps matching the sequential recurrence."""
+    _run_decode(hip, orc, np.random.default_rng(7), [0, 32], zero_state=True)
