@@ -34,7 +34,7 @@ EXPORTS = [
     "apus_hip_attn_rmsnorm", "apus_hip_attn_rope", "apus_hip_attn_gqa",
     "apus_hip_attn_gqa_decode", "apus_hip_attn_gqa_mt",
     "apus_hip_attn_gqa_decode_mt", "apus_hip_attn_outgate",
-    "apus_hip_gdn_decode",
+    "apus_hip_gdn_decode", "apus_hip_gdn_state_pack", "apus_hip_gdn_state_unpack",
 ]
 
 
@@ -54,9 +54,11 @@ class GdnLayer(C.Structure):
 _lib = None
 
 
-def load(path=LIB_PATH):
-    """Load the library (once). Raises if it was not built."""
+def load(path=None):
+    """Load the library (once). Raises if it was not built. APUS_HIP_LIB
+    overrides the path (A/B runs of alternative builds)."""
     global _lib
+    path = path or os.environ.get("APUS_HIP_LIB") or LIB_PATH
     if _lib is None:
         # torch ships its own libamdhip64.so.7. Importing it first makes the
         # dynamic loader bind this library to that same HIP runtime (by
@@ -253,3 +255,12 @@ def gdn_decode(layer, cu, qkv, z, a, b, conv_state, S, y):
     _chk(load().apus_hip_gdn_decode(C.byref(layer), _sz(B), cup, _dp(qkv),
                                     _dp(z), _dp(a), _dp(b), _dp(conv_state),
                                     _dp(S), _dp(y)))
+
+
+def gdn_state_pack(S_ref, S_dev):
+    """Reference-layout states [n, 128, 128] -> device layout (GPU tensors)."""
+    _chk(load().apus_hip_gdn_state_pack(_dp(S_ref), _dp(S_dev), _sz(S_ref.numel() // (128 * 128))))
+
+
+def gdn_state_unpack(S_dev, S_ref):
+    _chk(load().apus_hip_gdn_state_unpack(_dp(S_dev), _dp(S_ref), _sz(S_dev.numel() // (128 * 128))))

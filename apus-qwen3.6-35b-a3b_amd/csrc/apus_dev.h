@@ -40,6 +40,56 @@ __device__ __forceinline__ float softplus_cr(float x) {
     return x > 20.0f ? x : (float)log1p((double)exp_cr(x));
 }
 
+// Value of `v` in lane `src` of the wavefront (src must be uniform).
+__device__ __forceinline__ float lane_bcast(float v, int src) {
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), src));
+}
+
+// Raw buffer access: one buffer resource (base + size in SGPRs) per tile,
+// a per-lane VGPR byte offset and a uniform (SGPR/immediate) byte offset.
+// A 128-row column walk then costs one address VGPR instead of a 64-bit
+// pointer per row, which is what keeps a 128-float column in registers
+// at 3 waves per SIMD. Out-of-range offsets read 0 and drop writes.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const void *base,
+                                                           uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), 0,
+                                             (int)bytes, 0x00020000);
+}
+__device__ __forceinline__ float buf_ld(__amdgpu_buffer_rsrc_t r, int voff,
+                                        int soff) {
+    return __builtin_bit_cast(float,
+                              __builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, 0));
+}
+__device__ __forceinline__ void buf_st(__amdgpu_buffer_rsrc_t r, int voff,
+                                       int soff, float v) {
+    __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, v), r,
+                                          voff, soff, 0);
+}
+
+// 16-byte raw buffer access, bound to the LLVM intrinsics by name. The
+// __builtin_amdgcn_raw_buffer_{load,store}_b128 builtins of this toolchain
+// (ROCm 7.2 clang) lower to single-dword instructions, leaving three of the
+// four lanes undefined; the float-vector intrinsic keeps all four.
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+__device__ f32x4_t llvm_raw_ptr_buffer_load_v4f32(__amdgpu_buffer_rsrc_t r, int voff,
+                                                  int soff, int aux)
+    __asm("llvm.amdgcn.raw.ptr.buffer.load.v4f32");
+__device__ void llvm_raw_ptr_buffer_store_v4f32(f32x4_t v, __amdgpu_buffer_rsrc_t r,
+                                                int voff, int soff, int aux)
+    __asm("llvm.amdgcn.raw.ptr.buffer.store.v4f32");
+
+// Streaming (non-temporal, cache policy bit 1) variants: a tile that is
+// read once and written once per call should not displace reusable lines
+// from L2/MALL; on the GDN state stream this is worth ~15% of bandwidth.
+constexpr int kCpolNT = 2;
+__device__ __forceinline__ f32x4_t buf_ld4(__amdgpu_buffer_rsrc_t r, int voff, int soff) {
+    return llvm_raw_ptr_buffer_load_v4f32(r, voff, soff, kCpolNT);
+}
+__device__ __forceinline__ void buf_st4(__amdgpu_buffer_rsrc_t r, int voff, int soff,
+                                        f32x4_t v) {
+    llvm_raw_ptr_buffer_store_v4f32(v, r, voff, soff, kCpolNT);
+}
+
 // Exact IEEE single ops that the compiler may not fuse or reorder. The
 // kernels that promise reference-order results are compiled with FP
 // contraction off as well; these make the intent explicit at call sites.

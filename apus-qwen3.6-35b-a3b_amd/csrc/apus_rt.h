@@ -35,6 +35,13 @@ void set_stream(hipStream_t s);
 enum ScratchSlot { kScratchIn = 0, kScratchIn2, kScratchIn3, kScratchIn4,
                    kScratchIn5, kScratchIn6, kScratchOut, kScratchOut2,
                    kScratchWork, kScratchWork2, kScratchWork3, kScratchMeta,
+                   kScratchMeta2, kScratchMeta3,
+                   // batched GDN mixer intermediates
+                   kScratchGdnQK, kScratchGdnV, kScratchGdnGate, kScratchGdnOB,
+                   kScratchGdnChunk, kScratchGdnChunk2, kScratchGdnChunk3,
+                   // batched attention mixer intermediates
+                   kScratchAttnQ, kScratchAttnA, kScratchAttnStat,
+                   kScratchAttnPart,
                    kScratchSlots };
 void *scratch(int slot, size_t bytes);
 

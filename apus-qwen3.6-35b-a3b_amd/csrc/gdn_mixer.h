@@ -1,0 +1,32 @@
+// gdn_mixer.h -- pieces of the batched GDN mixer shared by the decode
+// (gdn_mixer.hip) and chunked prefill (gdn_prefill.hip) entry points.
+#pragma once
+#include <hip/hip_runtime.h>
+
+#include "../../include/apus_hip.h"
+#include "apus_rt.h"
+
+namespace apus {
+
+// Per-call device intermediates (library scratch).
+struct GdnScratch {
+    float *qk;          // [Ttot][2][hk*128]: l2-normed q (scaled), k
+    uint16_t *vconv;    // [Ttot][hv*128]: conv+SiLU of the v channels
+    float2 *gate;       // [Ttot][hv]: (exp(g), beta)
+    uint16_t *ob;       // [Ttot][hv*128]: rnd(recurrence output)
+    float *graw;        // [Ttot][hv]: g itself (log decay), when requested
+};
+
+int gdn_check_layer(const ApusHipGdnLayer *L);
+int gdn_check_offsets(size_t B, const int32_t *cu);
+// conv + l2norm + gates for every token (reads the old conv state)
+int gdn_prep(const ApusHipGdnLayer *L, size_t B, const int32_t *dcu,
+             size_t Ttot, const uint16_t *qkv, const uint16_t *a,
+             const uint16_t *b, const uint16_t *conv_state, GdnScratch *w,
+             bool want_graw);
+// gated RMSNorm of w->ob into y, then the new conv state
+int gdn_post(const ApusHipGdnLayer *L, size_t B, const int32_t *dcu,
+             size_t Ttot, const GdnScratch *w, const uint16_t *z,
+             const uint16_t *qkv, uint16_t *conv_state, uint16_t *y);
+
+}  // namespace apus

@@ -1,0 +1,452 @@
+// gdn_mixer.hip -- batched, device-resident Gated DeltaNet mixer for gfx950:
+// the op sequence of c/layer.h:250-273 for B sequences.
+//
+// Device state layout (tier 2). The recurrent state of one (sequence,
+// v-head) is a 128x128 fp32 matrix S[i][j] (i = key dim, j = value dim,
+// reference layout c/gdn.h:149-156). In HBM the library keeps it "column
+// packed": for column half c = j/64, row quad q = i/4, lane l = j%64 and
+// r = i%4, element S[i][j] sits at
+//     ((c*32 + q)*64 + l)*4 + r        (floats, within the 64 KiB matrix)
+// so the wavefront that owns columns c*64..c*64+63 reads four consecutive
+// rows of its column with one 16-byte load per lane and 1 KiB per
+// instruction: 32 loads per lane cover the column, well inside the 63
+// outstanding memory instructions a wave can track. apus_hip_gdn_state_
+// pack/unpack convert from/to the reference layout.
+//
+// Kernels:
+//   k_gdn_decode  fused decode/verify, one workgroup per (sequence, K head)
+//   k_gdn_prep    conv + l2norm + gates for every token (prefill)
+//   k_gdn_post    gated RMSNorm + new conv state (prefill)
+//   k_gdn_pack / k_gdn_unpack  state layout conversion
+//
+// Every sum keeps the reference's ascending order with one IEEE rounding
+// per op (FP contraction is off), so y and S equal the scalar anchors up
+// to libm ulps in the gates.
+#include <math.h>
+#include <stdint.h>
+#include <string.h>
+
+#include "../../include/apus_hip.h"
+#include "apus_dev.h"
+#include "apus_host.h"
+#include "gdn_dev.h"
+#include "gdn_mixer.h"
+
+using namespace apus;
+
+namespace {
+
+constexpr int DK = 128, DV = 128, REP = 2;
+constexpr float kEps = 1e-6f;
+
+__device__ __forceinline__ int seq_of(const int32_t *cu, int B, int t) {
+    int lo = 0, hi = B - 1;          // largest s with cu[s] <= t
+    while (lo < hi) {
+        int mid = (lo + hi + 1) >> 1;
+        if (cu[mid] <= t) lo = mid; else hi = mid - 1;
+    }
+    return lo;
+}
+
+// Ascending sum of squares of n (multiple of 4) LDS floats, one rounding
+// per mul and add; 16-byte LDS reads keep the dependent add chain fed.
+__device__ __forceinline__ float seq_sumsq(const float *x, int n) {
+    float ss = 0.0f;
+    for (int i = 0; i < n; i += 4) {
+        const float4 v = *reinterpret_cast<const float4 *>(x + i);
+        ss = ss + v.x * v.x;
+        ss = ss + v.y * v.y;
+        ss = ss + v.z * v.z;
+        ss = ss + v.w * v.w;
+    }
+    return ss;
+}
+
+// Pre-conv input of channel c at token index ti of a sequence starting at
+// t0: from the activations, or from the old conv state for ti < t0.
+__device__ __forceinline__ float conv_in(const uint16_t *qkv,
+                                         const uint16_t *cst, size_t cd,
+                                         int ti, int t0, size_t c) {
+    uint16_t v = ti >= t0 ? qkv[(size_t)ti * cd + c] : cst[c * 3 + (ti - t0 + 3)];
+    return bf2f(v);
+}
+
+// ---- state layout conversion -------------------------------------------
+__device__ __forceinline__ size_t packed_index(int i, int j) {
+    return ((size_t)((j >> 6) * 32 + (i >> 2)) * 64 + (j & 63)) * 4 + (i & 3);
+}
+
+__global__ void k_gdn_pack(const float *__restrict__ src, float *__restrict__ dst,
+                           size_t nmat) {
+    size_t e = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (e >= nmat * DK * DV) return;
+    size_t m = e / (DK * DV), w = e % (DK * DV);
+    int i = (int)(w / DV), j = (int)(w % DV);
+    dst[m * DK * DV + packed_index(i, j)] = src[e];
+}
+
+__global__ void k_gdn_unpack(const float *__restrict__ src, float *__restrict__ dst,
+                             size_t nmat) {
+    size_t e = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (e >= nmat * DK * DV) return;
+    size_t m = e / (DK * DV), w = e % (DK * DV);
+    int i = (int)(w / DV), j = (int)(w % DV);
+    dst[e] = src[m * DK * DV + packed_index(i, j)];
+}
+
+// ---- fused decode -------------------------------------------------------
+// One workgroup per (sequence, K head), 4 wavefronts. Wave w serves v-head
+// 2*kh + (w >> 1), value columns (w & 1)*64 + lane; thread t also owns q
+// channel t (t < 128) or k channel t-128 of the K head for the conv and
+// the l2norm. The small per-token operands are loaded before the 32
+// state loads of each lane, so waiting on them never waits on the state;
+// the gates and silu(z) are evaluated while the state is in flight.
+// Token offsets arrive by value for up to kInlineSeqs sequences.
+constexpr int kInlineSeqs = 480;
+struct CuArgs {
+    int32_t cu[kInlineSeqs + 1];
+};
+
+template <bool MULTI>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
+void k_gdn_decode(
+    CuArgs ca, const int32_t *dcu, const uint16_t *qkv, const uint16_t *z,
+    const uint16_t *a, const uint16_t *b, const uint16_t *conv_w,
+    const float *A_log, const float *dt_bias, const uint16_t *onorm_w,
+    uint16_t *conv_state, float *S, uint16_t *y, int hk, float qscale) {
+    // (no __restrict__ on the small operands: it would let the compiler sink
+    // their loads past the ordering barrier below the state loads)
+    const int s = blockIdx.x / hk, kh = blockIdx.x % hk;
+    // the wave index is uniform per wavefront; saying so keeps the state
+    // tile's buffer descriptor in SGPRs (no per-lane waterfall loop)
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wv_ = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int r = wv_ >> 1, half = wv_ & 1, j = half * 64 + lane;
+    const int hv = hk * REP, h = kh * REP + r;
+    const size_t kd = (size_t)hk * DK, vd = (size_t)hv * DV, cd = 2 * kd + vd;
+    const int t0 = dcu ? dcu[s] : ca.cu[s];
+    const int t1 = dcu ? dcu[s + 1] : ca.cu[s + 1];
+    if (t0 == t1) return;
+
+    __shared__ __attribute__((aligned(16))) float raw[2 * DK];   // conv q, k
+    __shared__ __attribute__((aligned(16))) float qkn[2 * DK];   // normed q, k
+    __shared__ __attribute__((aligned(16))) float ob[REP][DV];   // rnd(o)
+    __shared__ float rsq[2], rso[REP];
+    __shared__ float2 gt[REP];                                    // exp(g), beta
+
+    const size_t cqk = tid < DK ? (size_t)kh * DK + tid : kd + (size_t)kh * DK + (tid - DK);
+    const size_t cv = 2 * kd + (size_t)h * DV + j;
+    uint16_t *stq = conv_state + (size_t)s * cd * 3 + cqk * 3;
+    uint16_t *stv = conv_state + (size_t)s * cd * 3 + cv * 3;
+    // Small per-token operands, loaded as raw bits before the state tile.
+    uint32_t cwq_lo, cwq_hi, cwv_lo, cwv_hi;          // 4 bf16 conv taps each
+    {
+        const uint2 wq2 = *reinterpret_cast<const uint2 *>(conv_w + cqk * 4);
+        const uint2 wv2 = *reinterpret_cast<const uint2 *>(conv_w + cv * 4);
+        cwq_lo = wq2.x; cwq_hi = wq2.y; cwv_lo = wv2.x; cwv_hi = wv2.y;
+    }
+    uint32_t q0 = stq[0], q1 = stq[1], q2 = stq[2];
+    uint32_t v0 = stv[0], v1 = stv[1], v2 = stv[2];
+    uint32_t wo_b = onorm_w[j];
+    const int gh = kh * REP + (tid >> 7);            // gate head of lanes 0 of waves 1, 3
+    uint32_t alog_b = __float_as_uint(A_log[gh]), dtb_b = __float_as_uint(dt_bias[gh]);
+    uint32_t xq = qkv[(size_t)t0 * cd + cqk], xv = qkv[(size_t)t0 * cd + cv];
+    uint32_t zc = z[(size_t)t0 * vd + (size_t)h * DV + j];
+    uint32_t ac = a[(size_t)t0 * hv + gh], bc = b[(size_t)t0 * hv + gh];
+
+    // Keep the small loads above in front of the state loads: the memory
+    // counter retires in order, so a small load issued after the state
+    // loads would make the gate math wait for the whole state tile. The
+    // memory clobber stops IR passes sinking them, the sched_barrier stops
+    // the machine scheduler.
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+    // this wave's 128x64 state tile: 32 x 16-byte loads per lane
+    const auto Sr = buf_rsrc(S + ((size_t)s * hv + h) * DK * DV, DK * DV * 4);
+    const int voff = (half * 32 * 64 + lane) * 16;
+    float sr[DK];
+#pragma unroll
+    for (int q = 0; q < DK / 4; q++) {
+        const f32x4_t v = buf_ld4(Sr, voff, q * 1024);
+        sr[4 * q + 0] = v[0];
+        sr[4 * q + 1] = v[1];
+        sr[4 * q + 2] = v[2];
+        sr[4 * q + 3] = v[3];
+    }
+    // Pin every small operand after the state loads, so no math on them is
+    // hoisted in front of the state loads (each use then waits only for
+    // its own small load).
+    asm volatile("" : "+v"(cwq_lo), "+v"(cwq_hi), "+v"(cwv_lo), "+v"(cwv_hi),
+                 "+v"(q0), "+v"(q1), "+v"(q2), "+v"(v0), "+v"(v1), "+v"(v2),
+                 "+v"(wo_b), "+v"(alog_b), "+v"(dtb_b), "+v"(xq), "+v"(xv),
+                 "+v"(zc), "+v"(ac), "+v"(bc));
+    const float wq[4] = {__uint_as_float(cwq_lo << 16), __uint_as_float(cwq_lo & 0xffff0000u),
+                         __uint_as_float(cwq_hi << 16), __uint_as_float(cwq_hi & 0xffff0000u)};
+    const float wvv[4] = {__uint_as_float(cwv_lo << 16), __uint_as_float(cwv_lo & 0xffff0000u),
+                          __uint_as_float(cwv_hi << 16), __uint_as_float(cwv_hi & 0xffff0000u)};
+    const float wo = bf2f((uint16_t)wo_b);
+    const float Alog = __uint_as_float(alog_b), dtb = __uint_as_float(dtb_b);
+
+    const int tend = MULTI ? t1 : t0 + 1;   // one token: straight-line code
+    for (int t = t0; t < tend; t++) {
+        const uint16_t cq = conv_tap4(wq, bf2f(q0), bf2f(q1), bf2f(q2), bf2f(xq));
+        const uint16_t cvv = conv_tap4(wvv, bf2f(v0), bf2f(v1), bf2f(v2), bf2f(xv));
+        q0 = q1; q1 = q2; q2 = xq;
+        v0 = v1; v1 = v2; v2 = xv;   // (16-bit codes held in 32-bit registers)
+        raw[tid] = bf2f(cq);
+        if (lane == 0 && (wv_ == 1 || wv_ == 3)) {
+            const float g = decay_of(ac, Alog, dtb);
+            gt[tid >> 7] = make_float2(exp_cr(g), rndf(sigmoid_cr(bf2f(bc))));
+        }
+        const float zf = bf2f(zc);
+        const float zg = zf * sigmoid_cr(zf);          // silu(z), fp32
+        __syncthreads();
+        if (tid == 0 || tid == DK)
+            rsq[tid / DK] = 1.0f / sqrtf(seq_sumsq(raw + tid, DK) + kEps);
+        if (MULTI && t + 1 < t1) {                     // next token operands
+            xq = qkv[(size_t)(t + 1) * cd + cqk];
+            xv = qkv[(size_t)(t + 1) * cd + cv];
+            zc = z[(size_t)(t + 1) * vd + (size_t)h * DV + j];
+            ac = a[(size_t)(t + 1) * hv + gh];
+            bc = b[(size_t)(t + 1) * hv + gh];
+        }
+        __syncthreads();
+        qkn[tid] = tid < DK ? (raw[tid] * rsq[0]) * qscale : raw[tid] * rsq[1];
+        __syncthreads();
+        // c/gdn.h:482-503 on column j, with k and q broadcast by readlane
+        const float k0 = qkn[DK + lane], k1 = qkn[DK + 64 + lane];
+        const float qa = qkn[lane], qb = qkn[64 + lane];
+        const float2 gb = gt[r];
+        float kv = 0.0f;
+#pragma unroll
+        for (int i = 0; i < DK; i++) {
+            const float ki = lane_bcast(i < 64 ? k0 : k1, i & 63);
+            sr[i] = sr[i] * gb.x;
+            kv = kv + ki * sr[i];
+        }
+        const float delta = (bf2f(cvv) - kv) * gb.y;
+        // opaque copy: keeps the first pass's 128 broadcasts from staying live
+        float k0b = k0, k1b = k1;
+        asm volatile("" : "+v"(k0b), "+v"(k1b));
+        float acc = 0.0f;
+#pragma unroll
+        for (int i = 0; i < DK; i++) {
+            const float ki = lane_bcast(i < 64 ? k0b : k1b, i & 63);
+            const float qi = lane_bcast(i < 64 ? qa : qb, i & 63);
+            sr[i] = sr[i] + ki * delta;
+            acc = acc + qi * sr[i];
+        }
+        const float o = rndf(acc);
+        ob[r][j] = o;
+        __syncthreads();
+        if (tid == 0 || tid == DK)
+            rso[tid / DK] = 1.0f / sqrtf(seq_sumsq(ob[tid / DK], DV) / (float)DV + kEps);
+        __syncthreads();
+        const float x1 = rndf(o * rso[r]);
+        const float x2 = rndf(x1 * wo);
+        y[(size_t)t * vd + (size_t)h * DV + j] = f2bf(x2 * zg);
+    }
+#pragma unroll
+    for (int q = 0; q < DK / 4; q++)
+        buf_st4(Sr, voff, q * 1024,
+                f32x4_t{sr[4 * q + 0], sr[4 * q + 1], sr[4 * q + 2], sr[4 * q + 3]});
+    stq[0] = q0; stq[1] = q1; stq[2] = q2;
+    stv[0] = v0; stv[1] = v1; stv[2] = v2;
+}
+
+// ---- token-parallel pieces for the chunked prefill ------------------------
+// k_gdn_prep: per (token, K head), 256 threads. Conv + SiLU of the head's
+// q, k channels and its two v-heads' v channels (the first three tokens of
+// a sequence read their window from the old conv state), l2norm of q and
+// k, and (exp(g), beta) of the two v-heads; optionally the raw g.
+__global__ __launch_bounds__(256) void k_gdn_prep(
+    const int32_t *__restrict__ cu, int B, const uint16_t *__restrict__ qkv,
+    const uint16_t *__restrict__ a, const uint16_t *__restrict__ b,
+    const uint16_t *__restrict__ conv_w, const float *__restrict__ A_log,
+    const float *__restrict__ dt_bias, const uint16_t *__restrict__ conv_state,
+    float *__restrict__ qk, uint16_t *__restrict__ vconv,
+    float2 *__restrict__ gate, float *__restrict__ graw, int hk, float qscale) {
+    const int t = blockIdx.x / hk, kh = blockIdx.x % hk;
+    const int tid = threadIdx.x;
+    const int hv = hk * REP;
+    const size_t kd = (size_t)hk * DK, vd = (size_t)hv * DV, cd = 2 * kd + vd;
+    const int s = seq_of(cu, B, t), t0 = cu[s];
+    const uint16_t *cst = conv_state + (size_t)s * cd * 3;
+    __shared__ __attribute__((aligned(16))) float raw[2 * DK];
+    __shared__ float rs[2];
+
+    const size_t cqk = tid < DK ? (size_t)kh * DK + tid : kd + (size_t)kh * DK + (tid - DK);
+    const int h = kh * REP + tid / DV, j = tid % DV;
+    const size_t cv = 2 * kd + (size_t)h * DV + j;
+    float wq[4], wv[4], xq[4], xv[4];
+    for (int i = 0; i < 4; i++) {
+        wq[i] = bf2f(conv_w[cqk * 4 + i]);
+        wv[i] = bf2f(conv_w[cv * 4 + i]);
+        xq[i] = conv_in(qkv, cst, cd, t - 3 + i, t0, cqk);
+        xv[i] = conv_in(qkv, cst, cd, t - 3 + i, t0, cv);
+    }
+    raw[tid] = bf2f(conv_tap4(wq, xq[0], xq[1], xq[2], xq[3]));
+    vconv[(size_t)t * vd + (size_t)h * DV + j] = conv_tap4(wv, xv[0], xv[1], xv[2], xv[3]);
+    __syncthreads();
+    if (tid == 0 || tid == DK) {            // q sum (wave 0), k sum (wave 2)
+        rs[tid / DK] = 1.0f / sqrtf(seq_sumsq(raw + tid, DK) + kEps);
+    } else if (tid == 64 || tid == 64 + DV) {   // gates on waves 1 and 3
+        const int hh = kh * REP + tid / DV;
+        const float g = decay_of(a[(size_t)t * hv + hh], A_log[hh], dt_bias[hh]);
+        const float bt = rndf(sigmoid_cr(bf2f(b[(size_t)t * hv + hh])));
+        gate[(size_t)t * hv + hh] = make_float2(exp_cr(g), bt);
+        if (graw) graw[(size_t)t * hv + hh] = g;
+    }
+    __syncthreads();
+    float *qkt = qk + (size_t)t * 2 * kd;
+    if (tid < DK)
+        qkt[(size_t)kh * DK + tid] = (raw[tid] * rs[0]) * qscale;
+    else
+        qkt[kd + (size_t)kh * DK + (tid - DK)] = raw[tid] * rs[1];
+}
+
+// k_gdn_post: blocks [0, Ttot*hv) apply the gated RMSNorm to one (token,
+// v-head) of ob (c/gdn.h:639-661); the remaining blocks write each
+// sequence's new conv state (the last three pre-conv inputs of
+// [old state | tokens]) after every reader of the old one has finished.
+__global__ __launch_bounds__(128) void k_gdn_post(
+    const int32_t *__restrict__ cu, int B, int Ttot,
+    const uint16_t *__restrict__ ob, const uint16_t *__restrict__ z,
+    const uint16_t *__restrict__ onorm_w, uint16_t *__restrict__ y,
+    const uint16_t *__restrict__ qkv, uint16_t *__restrict__ conv_state,
+    int hk) {
+    const int hv = hk * REP;
+    const size_t kd = (size_t)hk * DK, vd = (size_t)hv * DV, cd = 2 * kd + vd;
+    const int tid = threadIdx.x;
+    const size_t nnorm = (size_t)Ttot * hv;
+    if ((size_t)blockIdx.x < nnorm) {
+        const size_t t = blockIdx.x / hv, h = blockIdx.x % hv;
+        const size_t off = t * vd + h * DV;
+        __shared__ __attribute__((aligned(16))) float o_s[DV];
+        __shared__ float rs_s;
+        const float o = bf2f(ob[off + tid]);
+        o_s[tid] = o;
+        __syncthreads();
+        if (tid == 0) rs_s = 1.0f / sqrtf(seq_sumsq(o_s, DV) / (float)DV + kEps);
+        __syncthreads();
+        const float x1 = rndf(o * rs_s);
+        const float x2 = rndf(x1 * bf2f(onorm_w[tid]));
+        const float zf = bf2f(z[off + tid]);
+        y[off + tid] = f2bf(x2 * (zf * sigmoid_cr(zf)));
+        return;
+    }
+    const size_t bb = blockIdx.x - nnorm;
+    const size_t per = cd / 128;
+    const size_t s = bb / per, c = (bb % per) * 128 + tid;
+    const int t0 = cu[s], n = cu[s + 1] - t0;
+    if (n == 0) return;
+    uint16_t *st = conv_state + s * cd * 3 + c * 3;
+    uint16_t w3[3];
+    for (int jj = 0; jj < 3; jj++) {
+        int idx = n - 3 + jj;          // position in the token span
+        w3[jj] = idx >= 0 ? qkv[(size_t)(t0 + idx) * cd + c] : st[idx + 3];
+    }
+    st[0] = w3[0];
+    st[1] = w3[1];
+    st[2] = w3[2];
+}
+
+}  // namespace
+
+namespace apus {
+
+int gdn_check_layer(const ApusHipGdnLayer *L) {
+    if (!L) return set_error(kErrArgument, "NULL layer");
+    if (L->dk != DK || L->dv != DV || L->hv != REP * L->hk || L->hk == 0)
+        return set_error(kErrUnsupported,
+                         "GDN mixer supports dk=dv=128, hv=2*hk (got hk=%zu hv=%zu "
+                         "dk=%zu dv=%zu)", L->hk, L->hv, L->dk, L->dv);
+    return kOk;
+}
+
+int gdn_check_offsets(size_t B, const int32_t *cu) {
+    if (!cu || cu[0] != 0) return set_error(kErrArgument, "cu must start at 0");
+    for (size_t s = 0; s < B; s++)
+        if (cu[s + 1] < cu[s])
+            return set_error(kErrArgument, "token offsets must ascend");
+    return kOk;
+}
+
+int gdn_prep(const ApusHipGdnLayer *L, size_t B, const int32_t *dcu,
+             size_t Ttot, const uint16_t *qkv, const uint16_t *a,
+             const uint16_t *b, const uint16_t *conv_state, GdnScratch *w,
+             bool want_graw) {
+    const size_t kd = L->hk * DK, vd = L->hv * DV;
+    w->qk = (float *)scratch(kScratchGdnQK, Ttot * 2 * kd * 4);
+    w->vconv = (uint16_t *)scratch(kScratchGdnV, Ttot * vd * 2);
+    w->gate = (float2 *)scratch(kScratchGdnGate, Ttot * L->hv * 8);
+    w->ob = (uint16_t *)scratch(kScratchGdnOB, Ttot * vd * 2);
+    w->graw = want_graw ? (float *)scratch(kScratchGdnChunk3, Ttot * L->hv * 4) : nullptr;
+    if (!w->qk || !w->vconv || !w->gate || !w->ob || (want_graw && !w->graw))
+        return kErrHip;
+    const float qscale = (float)pow((double)L->dk, -0.5);
+    k_gdn_prep<<<(unsigned)(Ttot * L->hk), 256, 0, stream()>>>(
+        dcu, (int)B, qkv, a, b, L->conv_w, L->A_log, L->dt_bias, conv_state,
+        w->qk, w->vconv, w->gate, w->graw, (int)L->hk, qscale);
+    return launch_check("k_gdn_prep");
+}
+
+int gdn_post(const ApusHipGdnLayer *L, size_t B, const int32_t *dcu,
+             size_t Ttot, const GdnScratch *w, const uint16_t *z,
+             const uint16_t *qkv, uint16_t *conv_state, uint16_t *y) {
+    const size_t cd = 2 * L->hk * DK + L->hv * DV;
+    const size_t nblk = Ttot * L->hv + B * (cd / 128);
+    k_gdn_post<<<(unsigned)nblk, 128, 0, stream()>>>(
+        dcu, (int)B, (int)Ttot, w->ob, z, L->onorm_w, y, qkv, conv_state,
+        (int)L->hk);
+    return launch_check("k_gdn_post");
+}
+
+}  // namespace apus
+
+extern "C" {
+
+int apus_hip_gdn_decode(const ApusHipGdnLayer *L, size_t B, const int32_t *cu,
+                        const uint16_t *qkv, const uint16_t *z,
+                        const uint16_t *a, const uint16_t *b,
+                        uint16_t *conv_state, float *S, uint16_t *y) {
+    APUS_READY();
+    if (int r = gdn_check_layer(L)) return r;
+    if (B == 0) return kOk;
+    if (int r = gdn_check_offsets(B, cu)) return r;
+    if (cu[B] == 0) return kOk;
+    CuArgs ca;
+    const int32_t *dcu = nullptr;
+    if (B <= (size_t)kInlineSeqs) {
+        memcpy(ca.cu, cu, (B + 1) * sizeof(int32_t));
+    } else {
+        dcu = (const int32_t *)upload_small(kScratchMeta, cu, (B + 1) * 4);
+        if (!dcu) return kErrHip;
+    }
+    const float qscale = (float)pow((double)L->dk, -0.5);
+    const bool multi = (size_t)cu[B] != B;     // some sequence has != 1 token
+    auto kern = multi ? k_gdn_decode<true> : k_gdn_decode<false>;
+    kern<<<(unsigned)(B * L->hk), 256, 0, stream()>>>(
+        ca, dcu, qkv, z, a, b, L->conv_w, L->A_log, L->dt_bias, L->onorm_w,
+        conv_state, S, y, (int)L->hk, qscale);
+    APUS_LAUNCHED("k_gdn_decode");
+    return kOk;
+}
+
+int apus_hip_gdn_state_pack(const float *S_ref, float *S_dev, size_t nmat) {
+    APUS_READY();
+    if (nmat == 0) return kOk;
+    k_gdn_pack<<<cdiv(nmat * DK * DV, 256), 256, 0, stream()>>>(S_ref, S_dev, nmat);
+    APUS_LAUNCHED("k_gdn_pack");
+    return kOk;
+}
+
+int apus_hip_gdn_state_unpack(const float *S_dev, float *S_ref, size_t nmat) {
+    APUS_READY();
+    if (nmat == 0) return kOk;
+    k_gdn_unpack<<<cdiv(nmat * DK * DV, 256), 256, 0, stream()>>>(S_dev, S_ref, nmat);
+    APUS_LAUNCHED("k_gdn_unpack");
+    return kOk;
+}
+
+}  // extern "C"

@@ -1,0 +1,274 @@
+"""Benchmark of the apus-qwen attention hot path on one MI355X.
+
+python bench.py [--gpus 1] [--steps K] [--warmup W] [--only c0,c0b,c1,...]
+                [--no-cpu]
+
+A "step" is one pass of a mixer (the hot path between a layer's input
+projections and its output projection) over one batch of synthetic inputs
+already resident in HBM. The headline line is BASELINE config 1 (Gated
+DeltaNet prefill, batch 1, T=4096, zero initial state), reported as tokens
+per second; the other configurations are measured in the same run and
+reported under "configs" with their own roofline fractions:
+  c0   config 0   GDN decode, batch 1
+  c0b  config 0'  GDN decode, batch 64 (HBM-bound decode)
+  c1   config 1   GDN prefill T=4096 (headline)
+Input buffer sets rotate so the 256 MB Infinity Cache cannot serve
+repeated reads. The CPU baseline is the reference's own scalar anchors
+(oracle/_ref, built from the reference sources) when present, else the
+repo's C restatement (oracle/), timed on the host cores on a bounded sample.
+"""
+import argparse
+import json
+import os
+import platform
+import subprocess
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+PKG = os.path.join(ROOT, "apus-qwen3.6-35b-a3b_amd")
+for p in (PKG, os.path.join(ROOT, "oracle")):
+    if p not in sys.path:
+        sys.path.insert(0, p)
+
+HBM_PEAK = 8.0e12            # B/s, MI355X HBM3E
+BF16_PEAK = 2.5e15           # flop/s dense bf16 MFMA
+CPU_THREADS = 16             # the GPU box's CPU share for one GPU
+
+GDN = (16, 32, 128, 128)
+HK, HV, DK, DV = GDN
+CD = 2 * HK * DK + HV * DV   # conv_dim 8192
+VD = HV * DV                 # value_dim 4096
+
+
+# ---------------------------------------------------------------- helpers
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def gdn_seq_bytes(ntok):
+    """Algorithmic HBM bytes of one GDN sequence over ntok tokens:
+    S read+write, conv state read+write, per token qkv, z, a, b in and y
+    out (state touched once however many tokens)."""
+    state = HV * DK * DV * 4 * 2 + CD * 3 * 2 * 2
+    per_tok = CD * 2 + VD * 2 + HV * 2 * 2 + VD * 2
+    return state + ntok * per_tok
+
+
+GDN_WEIGHT_BYTES = CD * 4 * 2 + HV * 4 * 2 + DV * 2
+
+
+class Dev:
+    """Device buffers for one GDN workload with `nsets` rotating sets."""
+
+    def __init__(self, torch, B, T_per_seq, nsets, seed, zero_state):
+        import apus_hip
+        self.torch = torch
+        dev = torch.device("cuda")
+        g = torch.Generator(device=dev)
+        g.manual_seed(seed)
+
+        def bf(shape, std=1.0, mean=0.0):
+            x = torch.randn(shape, generator=g, device=dev, dtype=torch.float32) * std + mean
+            return x.to(torch.bfloat16).view(torch.int16)
+
+        self.w = dict(conv_w=bf((CD, 4), 0.1),
+                      A_log=torch.rand(HV, generator=g, device=dev) * 2.7,
+                      dt_bias=torch.ones(HV, device=dev),
+                      onorm_w=bf((DV,), 0.1, 1.0))
+        self.layer = apus_hip.gdn_layer(GDN, self.w)
+        T = B * T_per_seq
+        self.cu = np.arange(B + 1, dtype=np.int32) * T_per_seq
+        self.sets = []
+        for _ in range(nsets):
+            s = dict(qkv=bf((T, CD)), z=bf((T, VD)), a=bf((T, HV)), b=bf((T, HV)),
+                     y=torch.empty((T, VD), dtype=torch.int16, device=dev))
+            if zero_state:
+                s["conv"] = torch.zeros((B, CD * 3), dtype=torch.int16, device=dev)
+                s["S"] = torch.zeros((B, HV, DK, DV), dtype=torch.float32, device=dev)
+            else:
+                s["conv"] = bf((B, CD * 3))
+                s["S"] = torch.randn((B, HV, DK, DV), generator=g, device=dev) * 0.02
+            self.sets.append(s)
+        self.zero_state = zero_state
+
+
+def time_steps(torch, fn, steps, warmup, nsets):
+    """Run warmup then `steps` timed steps; return (total_s, per-step
+    event times in s). Each step uses buffer set i % nsets."""
+    for i in range(warmup):
+        fn(i % nsets)
+    torch.cuda.synchronize()
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+          for _ in range(steps)]
+    t0 = time.perf_counter()
+    for i in range(steps):
+        ev[i][0].record()
+        fn(i % nsets)
+        ev[i][1].record()
+    torch.cuda.synchronize()
+    total = time.perf_counter() - t0
+    per = [a.elapsed_time(b) * 1e-3 for a, b in ev]
+    return total, per
+
+
+# ---------------------------------------------------------------- workloads
+def bench_gdn_decode(torch, B, steps, warmup, seed):
+    """Config 0 / 0': one decode token per sequence, prior state."""
+    import apus_hip
+    nsets = 4 if B > 1 else 8
+    d = Dev(torch, B, 1, nsets, seed, zero_state=False)
+
+    def step(i):
+        s = d.sets[i]
+        apus_hip.gdn_decode(d.layer, d.cu, s["qkv"], s["z"], s["a"], s["b"], s["conv"], s["S"], s["y"])
+
+    total, per = time_steps(torch, step, steps, warmup, nsets)
+    kt = float(np.mean(per))
+    bytes_ = B * gdn_seq_bytes(1) + GDN_WEIGHT_BYTES
+    return dict(workload=f"gdn_decode_b{B}", tokens_per_step=B, ms_per_step=total / steps * 1e3,
+                kernel="k_gdn_decode", kernel_ms=kt * 1e3, alg_bytes=bytes_,
+                tok_s=B * steps / total, hbm_gbs=bytes_ / kt / 1e9, hbm_frac=bytes_ / kt / HBM_PEAK)
+
+
+def bench_gdn_prefill(torch, T, steps, warmup, seed):
+    """Config 1: one sequence of T tokens from zero state."""
+    import apus_hip
+    nsets = 2
+    d = Dev(torch, 1, T, nsets, seed, zero_state=True)
+
+    def step(i):
+        s = d.sets[i]
+        s["conv"].zero_()
+        s["S"].zero_()
+        apus_hip.gdn_decode(d.layer, d.cu, s["qkv"], s["z"], s["a"], s["b"], s["conv"], s["S"], s["y"])
+
+    total, per = time_steps(torch, step, steps, warmup, nsets)
+    kt = float(np.mean(per))
+    bytes_ = gdn_seq_bytes(T) + GDN_WEIGHT_BYTES
+    flops = gdn_prefill_flops(T)
+    return dict(workload=f"gdn_prefill_t{T}", tokens_per_step=T, ms_per_step=total / steps * 1e3,
+                kernel="k_gdn_decode", kernel_ms=kt * 1e3, alg_bytes=bytes_, alg_flops=flops,
+                tok_s=T * steps / total, hbm_gbs=bytes_ / kt / 1e9, hbm_frac=bytes_ / kt / HBM_PEAK,
+                mfma_tflops=flops / kt / 1e12, mfma_frac=flops / kt / BF16_PEAK)
+
+
+def gdn_prefill_flops(T, C=64):
+    """WY-form flops per (chunk, head): 5 matmuls of 64x64x128-class
+    (2*64*64*128 = 1,048,576 each), 3 of 64x128x128 (2,097,152 each) and
+    the triangular solve (~64^3*2/3 = 174,763); x chunks x 32 heads."""
+    per = 5 * 2 * C * C * DK + 3 * 2 * C * DK * DV + (2 * C ** 3) // 3
+    return per * (T // C) * HV
+
+
+# ---------------------------------------------------------------- CPU side
+def cpu_model():
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor()
+
+
+def cpu_baseline_worker(args):
+    """Runs in a child process with APUS_THREADS / OMP_NUM_THREADS set:
+    the config 1 mixer over a T-token sample, continuing state."""
+    import oracle
+    import synth
+    rng = np.random.default_rng(1)
+    T = args.cpu_tokens
+    w = synth.gdn_weights(rng)
+    tok = synth.gdn_tokens(rng, T)
+    conv, S = synth.gdn_state(rng, 1, zero=True)
+    cu = np.array([0, T], np.int32)
+    if oracle.Reference.available():
+        lib, kind = oracle.Reference(), "reference"
+        run = lambda: lib.gdn_mixer(GDN, w, cu, tok["qkv"], tok["z"], tok["a"], tok["b"], conv, S)
+    else:
+        lib, kind = oracle.Oracle(), "port"
+        run = lambda: lib.gdn_mixer(GDN, w, cu, tok["qkv"], tok["z"], tok["a"], tok["b"], conv, S,
+                                    nthreads=args.cpu_threads)
+    run()   # warm (thread pool spawn, page faults)
+    t0 = time.perf_counter()
+    run()
+    dt = time.perf_counter() - t0
+    print(json.dumps(dict(kind=kind, seconds=dt, tokens=T)))
+
+
+def cpu_baseline(threads, tokens):
+    env = dict(os.environ, APUS_THREADS=str(threads), OMP_NUM_THREADS=str(threads))
+    r = subprocess.run([sys.executable, os.path.abspath(__file__), "--cpu-worker",
+                        "--cpu-tokens", str(tokens), "--cpu-threads", str(threads)],
+                       env=env, capture_output=True, text=True, timeout=600)
+    if r.returncode != 0:
+        log("cpu baseline failed:", r.stderr[-2000:])
+        return None
+    res = json.loads(r.stdout.strip().splitlines()[-1])
+    return dict(value=tokens / res["seconds"], unit="tok/s", cores=threads, kind=res["kind"],
+                sample=(f"config 1 GDN mixer (conv, beta, decay, l2norm, step_mt, rnd, onorm per "
+                        f"token) over {tokens} tokens from zero state, batch 1, "
+                        f"{'reference c/gdn.h anchors' if res['kind'] == 'reference' else 'oracle port'}"
+                        f" with {threads} pool threads on {cpu_model()} (nproc {os.cpu_count()})"))
+
+
+# ---------------------------------------------------------------- main
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--only", default="c0,c0b,c1")
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--cpu-tokens", type=int, default=512)
+    ap.add_argument("--cpu-threads", type=int, default=CPU_THREADS)
+    ap.add_argument("--cpu-worker", action="store_true")
+    args = ap.parse_args()
+    if args.cpu_worker:
+        cpu_baseline_worker(args)
+        return
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU: this build has no multi-GPU path "
+              "(the hot path shards without communication; see DESIGN.md). "
+              "Run with --gpus 1.", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    import apus_hip
+    apus_hip.init(0)
+    apus_hip.set_stream(torch.cuda.current_stream().cuda_stream)
+    want = set(args.only.split(","))
+    res = {}
+    if "c0" in want:
+        res["c0"] = bench_gdn_decode(torch, 1, max(args.steps, 50), args.warmup, 10)
+        log("c0", res["c0"])
+    if "c0b" in want:
+        res["c0b"] = bench_gdn_decode(torch, 64, args.steps, args.warmup, 11)
+        log("c0b", res["c0b"])
+    if "c1" in want:
+        res["c1"] = bench_gdn_prefill(torch, 4096, args.steps, args.warmup, 12)
+        log("c1", res["c1"])
+
+    head = res.get("c1") or next(iter(res.values()))
+    cpu = None if args.no_cpu else cpu_baseline(args.cpu_threads, args.cpu_tokens)
+    roof = dict(bound="hbm", achieved=head["alg_bytes"] / (head["kernel_ms"] * 1e-3) / 1e9,
+                peak=HBM_PEAK / 1e9, unit="GB/s",
+                frac=head["alg_bytes"] / (head["kernel_ms"] * 1e-3) / HBM_PEAK,
+                traffic=None, kernel=head["kernel"])
+    line = dict(metric="attn-layer tok/s @1 GPU; decode HBM GB/s % peak; prefill MFMA TFLOP/s % peak",
+                value=head["tok_s"], unit="tok/s", n_gpus=1, steps=args.steps, warmup=args.warmup,
+                ms_per_step=head["ms_per_step"], higher_is_better=True, scaling="weak",
+                vs_baseline=None, dtype="bf16/fp32", data="synthetic",
+                config=dict(workload=head["workload"], global_batch=1,
+                            seq_len=head["tokens_per_step"], parallelism="none (1 GPU)"),
+                roofline=roof, cpu_baseline=cpu,
+                configs={k: {kk: (round(vv, 6) if isinstance(vv, float) else vv)
+                             for kk, vv in v.items()} for k, v in res.items()})
+    print(json.dumps(line))
+
+
+if __name__ == "__main__":
+    main()

@@ -139,13 +139,24 @@ typedef struct {
     const uint16_t *onorm_w;        /* [dv] bf16, direct weight */
 } ApusHipGdnLayer;
 
+/* Device state layout. Tier-2 GDN calls keep each (sequence, v-head)
+ * recurrent state -- reference layout S[i][j], i < dk, j < dv, fp32
+ * (c/gdn.h:149-156) -- "column packed" in HBM: element S[i][j] of a
+ * 128x128 matrix sits at float offset ((j/64*32 + i/4)*64 + j%64)*4 + i%4.
+ * A wavefront owning 64 value columns then streams its tile with 16-byte
+ * loads. These convert nmat consecutive matrices between the reference
+ * layout and the device layout (device pointers, no aliasing). */
+int apus_hip_gdn_state_pack(const float *S_ref, float *S_dev, size_t nmat);
+int apus_hip_gdn_state_unpack(const float *S_dev, float *S_ref, size_t nmat);
+
 /* Fused GDN decode / verify: for each sequence, its tokens in order run
  * conv1d+SiLU, beta, decay, l2norm, the delta-rule step and the gated
  * RMSNorm (c/layer.h:250-273 per token; 1..k tokens per sequence, the MTP
  * verify shape of c/mtp.h:36-75).
  *   qkv [Ttot, 2*hk*dk + hv*dv], z [Ttot, hv*dv], a,b [Ttot, hv] bf16;
- *   conv_state [B, conv_dim*3] bf16 (in/out); S [B, hv, dk, dv] f32
- *   (in/out); y [Ttot, hv*dv] bf16 (feeds w_out).
+ *   conv_state [B, conv_dim*3] bf16 (in/out); S [B, hv] matrices of
+ *   dk x dv f32 in the device layout above (in/out); y [Ttot, hv*dv] bf16
+ *   (feeds w_out). y and S equal the reference anchors up to libm ulps.
  * Supports dk = dv = 128 and hv = 2*hk (the model's shape). */
 int apus_hip_gdn_decode(const ApusHipGdnLayer *L, size_t B,
                         const int32_t *cu, const uint16_t *qkv,

@@ -117,14 +117,17 @@ def _run_decode(hip, orc, rng, cu, zero_state=False):
     layer = hip.gdn_layer(dims, tw)
     t = {k: torch.from_numpy(v.view(np.int16)).to(dev) for k, v in tok.items()}
     dconv = torch.from_numpy(conv.view(np.int16)).to(dev)
-    dS = torch.from_numpy(S).to(dev)
+    dS_ref = torch.from_numpy(S).to(dev)
+    dS = torch.empty_like(dS_ref)
+    hip.gdn_state_pack(dS_ref, dS)            # reference layout -> device layout
     y = torch.empty((T, dims[1] * dims[3]), dtype=torch.int16, device=dev)
     hip.gdn_decode(layer, cu, t["qkv"], t["z"], t["a"], t["b"], dconv, dS, y)
+    hip.gdn_state_unpack(dS, dS_ref)
     torch.cuda.synchronize()
     y_h = y.cpu().numpy().view(np.uint16)
     st = assert_bf16_close(y_h, y_o, what="gdn_decode y")
     assert np.array_equal(dconv.cpu().numpy().view(np.uint16), c_o)
-    e = assert_state_close(dS.cpu().numpy(), S_o, what="gdn_decode S")
+    e = assert_state_close(dS_ref.cpu().numpy(), S_o, what="gdn_decode S")
     return st, e
 
 
@@ -153,3 +156,21 @@ def test_gdn_decode_zero_state_long(hip, orc):
     """A 32-token single sequence from zero state: decode stepping through
     a prefill-length span keeps matching the sequential recurrence."""
     _run_decode(hip, orc, np.random.default_rng(7), [0, 32], zero_state=True)
+
+
+def test_state_pack_roundtrip(hip):
+    """pack then unpack is the identity, and pack places S[i][j] where the
+    documented formula says (include/apus_hip.h)."""
+    import torch
+    n = 3
+    S = torch.arange(n * 128 * 128, dtype=torch.float32, device="cuda").reshape(n, 128, 128)
+    P = torch.empty_like(S)
+    U = torch.empty_like(S)
+    hip.gdn_state_pack(S, P)
+    hip.gdn_state_unpack(P, U)
+    torch.cuda.synchronize()
+    assert torch.equal(U, S)
+    Ph = P.cpu().numpy().reshape(n, -1)
+    for (m, i, j) in [(0, 0, 0), (1, 5, 70), (2, 127, 127), (0, 64, 63)]:
+        off = ((j // 64 * 32 + i // 4) * 64 + j % 64) * 4 + i % 4
+        assert Ph[m, off] == float(m * 16384 + i * 128 + j)
