@@ -35,6 +35,7 @@ EXPORTS = [
     "apus_hip_attn_gqa_decode", "apus_hip_attn_gqa_mt",
     "apus_hip_attn_gqa_decode_mt", "apus_hip_attn_outgate",
     "apus_hip_gdn_decode", "apus_hip_gdn_state_pack", "apus_hip_gdn_state_unpack",
+    "apus_hip_attn_cache_pack", "apus_hip_attn_cache_unpack", "apus_hip_attn_decode",
 ]
 
 
@@ -49,6 +50,12 @@ class GdnLayer(C.Structure):
     _fields_ = [("hk", _sz), ("hv", _sz), ("dk", _sz), ("dv", _sz),
                 ("conv_w", _vp), ("A_log", _vp), ("dt_bias", _vp),
                 ("onorm_w", _vp)]
+
+
+class AttnLayer(C.Structure):
+    """ApusHipAttnLayer (include/apus_hip.h)."""
+    _fields_ = [("nh", _sz), ("nkv", _sz), ("d", _sz), ("rot", _sz), ("theta", C.c_double),
+                ("qn_w", _vp), ("kn_w", _vp)]
 
 
 _lib = None
@@ -264,3 +271,29 @@ def gdn_state_pack(S_ref, S_dev):
 
 def gdn_state_unpack(S_dev, S_ref):
     _chk(load().apus_hip_gdn_state_unpack(_dp(S_dev), _dp(S_ref), _sz(S_dev.numel() // (128 * 128))))
+
+
+def attn_layer(dims, w):
+    """ApusHipAttnLayer from dims (nh, nkv, d, rot, theta) and device tensors
+    qn_w, kn_w. Keep `w` alive while the layer is used."""
+    nh, nkv, d, rot, theta = dims
+    return AttnLayer(nh, nkv, d, rot, theta, w["qn_w"].data_ptr(), w["kn_w"].data_ptr())
+
+
+def attn_cache_pack(kc_ref, vc_ref, ntok, nkv, d, kcache, vcache, max_seq):
+    """One sequence: reference-layout caches [ntok, nkv, d] -> device layout."""
+    _chk(load().apus_hip_attn_cache_pack(_dp(kc_ref), _dp(vc_ref), _sz(ntok), _sz(nkv), _sz(d),
+                                         _dp(kcache), _dp(vcache), _sz(max_seq)))
+
+
+def attn_cache_unpack(kcache, vcache, ntok, nkv, d, max_seq, kc_ref, vc_ref):
+    _chk(load().apus_hip_attn_cache_unpack(_dp(kcache), _dp(vcache), _sz(ntok), _sz(nkv), _sz(d),
+                                           _sz(max_seq), _dp(kc_ref), _dp(vc_ref)))
+
+
+def attn_decode(layer, cu, pos0, qg, k, v, kcache, vcache, max_seq, y):
+    cu, cup, B = _cu_arr(cu)
+    pos0 = np.ascontiguousarray(np.asarray(pos0, dtype=np.int32))
+    _chk(load().apus_hip_attn_decode(C.byref(layer), _sz(B), cup, pos0.ctypes.data_as(_i32p),
+                                     _dp(qg), _dp(k), _dp(v), _dp(kcache), _dp(vcache),
+                                     _sz(max_seq), _dp(y)))

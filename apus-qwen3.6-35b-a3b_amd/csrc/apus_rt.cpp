@@ -17,6 +17,7 @@ namespace {
 char g_err[512];
 int g_ready = 0;
 int g_device = 0;
+int g_cus = 256;
 hipStream_t g_stream = nullptr;
 
 struct Buf {
@@ -81,9 +82,12 @@ int ensure_ready() {
         return set_error(kErrUnsupported,
                          "device %d is %s; this build targets gfx950",
                          g_device, prop.gcnArchName);
+    g_cus = prop.multiProcessorCount > 0 ? prop.multiProcessorCount : 256;
     g_ready = 1;
     return kOk;
 }
+
+int cu_count() { return g_cus; }
 
 hipStream_t stream() { return g_stream; }
 void set_stream(hipStream_t s) { g_stream = s; }

@@ -28,6 +28,7 @@ int hip_fail(hipError_t e, const char *what, const char *file, int line);
 // apus_hip_init chose another). Returns kOk or an error code.
 int ensure_ready();
 hipStream_t stream();
+int cu_count();     // compute units of the current device
 void set_stream(hipStream_t s);
 
 // Grow-only device scratch, one buffer per slot. Valid until the next

@@ -1,0 +1,609 @@
+// attn_mixer.hip -- batched, device-resident gated-GQA mixer for gfx950:
+// the op sequence of c/layer.h:300-322 (decode) for B sequences of 1..n
+// new tokens each (n > 1 is the MTP verify shape, c/mtp.h:36-75).
+//
+// Device KV-cache layout (tier 2). Sequence s of a batch owns
+//   K  kcache + s*nkv*max_seq*d   as [nkv][max_seq][d]
+//   V  vcache + s*nkv*d*max_seq   as [nkv][max_seq/32][d][32]
+// K rows keep d contiguous (the QK^T MFMA operand reads 8 consecutive d of
+// a key). V is stored transposed in 32-key blocks: the P.V MFMA operand
+// reads 8 consecutive keys of one d with one 16-byte load, and the 32 keys
+// x 256 d of a step are one contiguous 16 KiB block (long DRAM bursts; a
+// plain [d][max_seq] transpose made every 64-byte piece a separate DRAM
+// page). The reference's cache is [pos][nkv][d] for both
+// (c/layer.h:164-165); apus_hip_attn_cache_pack/unpack convert.
+//
+// Decode kernels (split-K over the context, one wavefront per (split, kv
+// head); the 8 q heads of a kv head and up to 4 new tokens form the MFMA
+// rows, so K and V are read once per group). The split sizes are chosen
+// per call so each kernel's grid is one full round of resident waves:
+//   k_attn_prep     q/k (1+w) RMSNorm, RoPE, cache append
+//   k_attn_scores   A = rnd(rnd(q.k)*scale) on MFMA 32x32x16 bf16 into a
+//                   bf16 score buffer, per-split (max, sum exp)
+//   k_attn_pv       P = rnd(exp(A-m)/s) with the global (m, s) -- the
+//                   reference's normalised bf16 probabilities
+//                   (c/attn.h:354-360) -- times V on MFMA, fp32 partials
+//   k_attn_combine  sum of the partials, rnd, sigmoid output gate
+// Scores and the P.V sum accumulate in a different order than the
+// reference's sequential loops (a tolerance class); everything else
+// follows the reference op for op.
+#include <math.h>
+#include <stdint.h>
+#include <string.h>
+
+#include <vector>
+
+#include "../../include/apus_hip.h"
+#include "apus_dev.h"
+#include "apus_host.h"
+#include "attn_mixer.h"
+
+using namespace apus;
+
+namespace {
+
+constexpr int D = 256, ROT = 64, GRP = 8;     // head dim, rotary dims, q heads per kv head
+constexpr int kRows = 32;                     // rows: GRP heads x up to 4 tokens
+constexpr float kEps = 1e-6f;
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned short u16x8 __attribute__((ext_vector_type(8)));
+
+__device__ __forceinline__ bf16x8 ld_bf16x8(const uint16_t *p) {
+    return __builtin_bit_cast(bf16x8, *reinterpret_cast<const u16x8 *>(p));
+}
+
+__device__ __forceinline__ int seq_of(const int32_t *off, int n, int x) {
+    int lo = 0, hi = n - 1;          // largest s with off[s] <= x
+    while (lo < hi) {
+        int mid = (lo + hi + 1) >> 1;
+        if (off[mid] <= x) lo = mid; else hi = mid - 1;
+    }
+    return lo;
+}
+
+// exp(x) for x <= 0 in fp32 via the hardware exp2 with the rounding error
+// of x*log2(e) folded back in (a few ulp; the score path is a tolerance
+// class, see the file comment).
+__device__ __forceinline__ float exp_fast(float x) {
+    if (x == -INFINITY) return 0.0f;
+    const float L2E = 1.44269504088896341f;
+    const float t = x * L2E;
+    const float r = fmaf(x, L2E, -t) + x * 1.925963001e-8f;
+    const float e = __builtin_amdgcn_exp2f(t);
+    return fmaf(e, r * 0.693147180559945f, e);
+}
+
+// Metadata views: by value (AttnSeqs) or, for large batches, a device
+// array cu[B+1] | pos0[B] | soff[B+1] | soff2[B+1].
+struct Meta {
+    const int32_t *cu, *pos0, *soff, *soff2;
+};
+__device__ __forceinline__ Meta meta_of(const AttnSeqs &sq, const int32_t *dmeta) {
+    if (!dmeta) return Meta{sq.cu, sq.pos0, sq.soff, sq.soff2};
+    const int n = sq.n;
+    return Meta{dmeta, dmeta + n + 1, dmeta + 2 * n + 1, dmeta + 3 * n + 2};
+}
+
+// ---- k_attn_prep: one block per (token, head slot), 256 threads -------
+// slots 0..nh-1: q heads; nh..nh+nkv-1: kv heads (k normed+roped into the
+// K cache, v copied into the transposed V cache).
+__global__ __launch_bounds__(D) void k_attn_prep(
+    AttnSeqs sq, const int32_t *__restrict__ dmeta, const uint16_t *__restrict__ qg,
+    const uint16_t *__restrict__ kin, const uint16_t *__restrict__ vin,
+    const uint16_t *__restrict__ qn_w, const uint16_t *__restrict__ kn_w,
+    const uint16_t *__restrict__ rope, uint16_t *__restrict__ kcache,
+    uint16_t *__restrict__ vcache, size_t max_seq, uint16_t *__restrict__ qn,
+    int nh, int nkv) {
+    const Meta mt = meta_of(sq, dmeta);
+    const int32_t *cu = mt.cu, *pos0 = mt.pos0;
+    const int nslot = nh + nkv;
+    const int tt = blockIdx.x / nslot, slot = blockIdx.x % nslot;
+    const int s = seq_of(cu, sq.n, tt);
+    const int pos = pos0[s] + (tt - cu[s]);
+    const int i = threadIdx.x;
+    const bool isq = slot < nh;
+    const int kvh = slot - nh;
+    const uint16_t *x = isq ? qg + ((size_t)tt * nh + slot) * 2 * D
+                            : kin + ((size_t)tt * nkv + kvh) * D;
+    const uint16_t *w = isq ? qn_w : kn_w;
+    __shared__ __attribute__((aligned(16))) float xs[D];
+    __shared__ float rs_s;
+    __shared__ float ns[D];
+    const float xf = bf2f(x[i]);
+    xs[i] = xf;
+    __syncthreads();
+    if (i == 0) {                       // ascending sum of squares (c/attn.h:177-182)
+        float ss = 0.0f;
+        for (int j = 0; j < D; j += 4) {
+            const float4 v4 = *reinterpret_cast<const float4 *>(xs + j);
+            ss = ss + v4.x * v4.x;
+            ss = ss + v4.y * v4.y;
+            ss = ss + v4.z * v4.z;
+            ss = ss + v4.w * v4.w;
+        }
+        rs_s = 1.0f / sqrtf(ss / (float)D + kEps);
+    }
+    __syncthreads();
+    const float nv = rndf((xf * rs_s) * (1.0f + bf2f(w[i])));
+    ns[i] = nv;
+    __syncthreads();
+    // partial NeoX RoPE with the host-made cos/sin codes (c/attn.h:244-266)
+    const uint16_t *cs = rope + (size_t)pos * ROT;
+    constexpr int R = ROT / 2;
+    float out = nv;
+    if (i < R) {
+        const float c = bf2f(cs[i]), sn = bf2f(cs[R + i]);
+        out = rndf(rndf(nv * c) + rndf(-ns[i + R] * sn));
+    } else if (i < ROT) {
+        const float c = bf2f(cs[i - R]), sn = bf2f(cs[i]);
+        out = rndf(rndf(nv * c) + rndf(ns[i - R] * sn));
+    }
+    if (isq) {
+        qn[((size_t)tt * nh + slot) * D + i] = f2bf(out);
+    } else {
+        uint16_t *kc = kcache + ((size_t)s * nkv + kvh) * max_seq * D;
+        kc[(size_t)pos * D + i] = f2bf(out);
+        uint16_t *vc = vcache + ((size_t)s * nkv + kvh) * D * max_seq;
+        vc[((size_t)(pos / 32) * D + i) * 32 + pos % 32] = vin[((size_t)tt * nkv + kvh) * D + i];
+    }
+}
+
+// Row n of the 32 MFMA rows is (token n / GRP, q head n % GRP of the kv
+// head); rows past the sequence's tokens are padding.
+struct SplitCtx {
+    int s, kvh, sp, gsplit, tq, pos0, ctx, k0, k1;
+};
+
+__device__ __forceinline__ SplitCtx split_ctx(const int32_t *cu, const int32_t *pos0,
+                                              const int32_t *soff, int nseq, int nkv, int ks) {
+    SplitCtx c;
+    c.kvh = blockIdx.x % nkv;
+    c.gsplit = blockIdx.x / nkv;
+    c.s = seq_of(soff, nseq, c.gsplit);
+    c.sp = c.gsplit - soff[c.s];
+    c.tq = cu[c.s + 1] - cu[c.s];
+    c.pos0 = pos0[c.s];
+    c.ctx = c.pos0 + c.tq;
+    c.k0 = c.sp * ks;
+    c.k1 = min(c.ctx, c.k0 + ks);
+    return c;
+}
+
+// ---- k_attn_scores: one wavefront per (split, kv head) -----------------
+// MFMA 16x16x32 bf16 (A: lane l holds row l%16, k (l/16)*8..+8; B: col
+// l%16, same k; D: rows (l/16)*4+i, col l%16). S^T[key][row] = K Q^T: the
+// four lanes of a key row read 64 contiguous bytes of it per instruction.
+// NRB row blocks of 16 (NRB = 2 when a sequence has more than 2 tokens).
+template <int NRB>
+__global__ __launch_bounds__(64) void k_attn_scores(
+    AttnSeqs sq, const int32_t *__restrict__ dmeta, const uint16_t *__restrict__ qn,
+    const uint16_t *__restrict__ kcache, size_t max_seq, int nh, int nkv, float scale,
+    uint16_t *__restrict__ As, float2 *__restrict__ stats) {
+    const Meta mt = meta_of(sq, dmeta);
+    const int32_t *cu = mt.cu;
+    const SplitCtx c = split_ctx(cu, mt.pos0, mt.soff, sq.n, nkv, sq.ks1);
+    const int l = threadIdx.x, c16 = l & 15, q4 = l >> 4;
+
+    bf16x8 qf[NRB][D / 32];
+    int lim[NRB];
+    bool vrow[NRB];
+#pragma unroll
+    for (int rb = 0; rb < NRB; rb++) {
+        const int n = rb * 16 + c16, t = n / GRP, g = n % GRP;
+        vrow[rb] = t < c.tq;
+        lim[rb] = c.pos0 + t;
+        const uint16_t *qrow =
+            qn + ((size_t)(cu[c.s] + (vrow[rb] ? t : 0)) * nh + c.kvh * GRP + g) * D;
+#pragma unroll
+        for (int ds = 0; ds < D / 32; ds++) {
+            const bf16x8 v = ld_bf16x8(qrow + ds * 32 + q4 * 8);
+            qf[rb][ds] = vrow[rb] ? v : bf16x8{};
+        }
+    }
+    const uint16_t *Kb = kcache + ((size_t)c.s * nkv + c.kvh) * max_seq * D;
+    // score rows of this (sequence, kv head): [row][cap] with absolute keys
+    const size_t cap = (size_t)(mt.soff[c.s + 1] - mt.soff[c.s]) * sq.ks1;
+    uint16_t *Ab = As + (size_t)mt.soff[c.s] * sq.ks1 * nkv * kRows + (size_t)c.kvh * kRows * cap;
+    float mrun[NRB], lrun[NRB];
+#pragma unroll
+    for (int rb = 0; rb < NRB; rb++) { mrun[rb] = -INFINITY; lrun[rb] = 0.0f; }
+
+    // K fragments of the next 16-key block are loaded while the current
+    // block is multiplied (double buffering keeps 16 loads per lane in flight)
+    // Keys are processed in groups of 64 as four MFMA blocks j = 0..3. MFMA
+    // row m of block j is key g0 + (m/4)*16 + 4*j + m%4, so the lane whose
+    // output rows are m = 4*q4 .. 4*q4+3 ends a group holding the 16
+    // consecutive scores g0 + 16*q4 .. +15 of its row: one 32-byte store per
+    // lane and 128 contiguous bytes per row. K rows past the split end are
+    // clamped to a valid row, never zeroed (touching a loaded value on issue
+    // would wait for it); their scores are never stored or counted.
+    bf16x8 kf[D / 32];
+    auto load_k = [&](int g0, int j, bf16x8 *f) {
+        const int key = min(g0 + (c16 >> 2) * 16 + 4 * j + (c16 & 3), c.k1 - 1);
+        const uint16_t *kr = Kb + (size_t)key * D + q4 * 8;
+#pragma unroll
+        for (int ds = 0; ds < D / 32; ds++) f[ds] = ld_bf16x8(kr + ds * 32);
+    };
+    load_k(c.k0, 0, kf);
+    for (int g0 = c.k0; g0 < c.k1; g0 += 64) {
+        uint16_t sc[NRB][16];
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            bf16x8 kn[D / 32];
+            const bool more = j < 3 || g0 + 64 < c.k1;
+            if (more) load_k(j < 3 ? g0 : g0 + 64, (j + 1) & 3, kn);
+            f32x4 acc[NRB];
+#pragma unroll
+            for (int rb = 0; rb < NRB; rb++) acc[rb] = f32x4{};
+#pragma unroll
+            for (int ds = 0; ds < D / 32; ds++)
+#pragma unroll
+                for (int rb = 0; rb < NRB; rb++)
+                    acc[rb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf[ds], qf[rb][ds], acc[rb], 0, 0, 0);
+#pragma unroll
+            for (int rb = 0; rb < NRB; rb++)
+#pragma unroll
+                for (int e = 0; e < 4; e++) sc[rb][4 * j + e] = f2bf(rndf(acc[rb][e]) * scale);
+#pragma unroll
+            for (int ds = 0; ds < D / 32; ds++) kf[ds] = kn[ds];
+        }
+        const int kq = g0 + 16 * q4;           // this lane's 16 keys
+#pragma unroll
+        for (int rb = 0; rb < NRB; rb++) {
+            if (!vrow[rb]) continue;
+            if (kq < c.k1) {
+                u16x8 lo, hi;
+#pragma unroll
+                for (int e = 0; e < 8; e++) { lo[e] = sc[rb][e]; hi[e] = sc[rb][8 + e]; }
+                u16x8 *dst = reinterpret_cast<u16x8 *>(Ab + (size_t)(rb * 16 + c16) * cap + kq);
+                dst[0] = lo;
+                dst[1] = hi;
+            }
+            float bmax = -INFINITY;
+#pragma unroll
+            for (int e = 0; e < 16; e++) {
+                const int kk = kq + e;
+                if (kk <= lim[rb] && kk < c.k1) bmax = fmaxf(bmax, bf2f(sc[rb][e]));
+            }
+            if (bmax > -INFINITY) {
+                const float mn = fmaxf(mrun[rb], bmax);
+                float add = 0.0f;
+#pragma unroll
+                for (int e = 0; e < 16; e++) {
+                    const int kk = kq + e;
+                    if (kk <= lim[rb] && kk < c.k1) add += exp_fast(bf2f(sc[rb][e]) - mn);
+                }
+                lrun[rb] = lrun[rb] * exp_fast(mrun[rb] - mn) + add;
+                mrun[rb] = mn;
+            }
+        }
+    }
+    // the four lanes l%16 + {0,16,32,48} hold the key quarters of one row
+#pragma unroll
+    for (int rb = 0; rb < NRB; rb++) {
+        float m = mrun[rb], ls = lrun[rb];
+#pragma unroll
+        for (int off = 16; off < 64; off <<= 1) {
+            const float mo = __shfl_xor(m, off), lo = __shfl_xor(ls, off);
+            const float mm = fmaxf(m, mo);
+            ls = mm > -INFINITY ? ls * exp_fast(m - mm) + lo * exp_fast(mo - mm) : 0.0f;
+            m = mm;
+        }
+        if (q4 == 0 && vrow[rb])
+            stats[((size_t)c.gsplit * nkv + c.kvh) * kRows + rb * 16 + c16] = make_float2(m, ls);
+    }
+}
+
+// ---- k_attn_pv: one wavefront per (split, kv head) ---------------------
+// O^T[d][row] = sum_key V^T[d][key] P^T[key][row] on MFMA 16x16x32: the
+// transposed V cache is the A operand (4 lanes read 64 contiguous bytes of
+// one d row), the probabilities the B operand.
+template <int NRB>
+__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void k_attn_pv(
+    AttnSeqs sq, const int32_t *__restrict__ dmeta, const uint16_t *__restrict__ vcache,
+    size_t max_seq, int nkv, const uint16_t *__restrict__ As,
+    const float2 *__restrict__ stats, float *__restrict__ Op) {
+    const Meta mt = meta_of(sq, dmeta);
+    const int32_t *soff = mt.soff;
+    const SplitCtx c = split_ctx(mt.cu, mt.pos0, mt.soff2, sq.n, nkv, sq.ks2);
+    const int l = threadIdx.x, c16 = l & 15, q4 = l >> 4;
+
+    // global (max, sum) of each row over every split of this (seq, kv head)
+    float m[NRB], rsum[NRB];
+    bool vrow[NRB];
+    int lim[NRB];
+    const int ns = soff[c.s + 1] - soff[c.s];
+#pragma unroll
+    for (int rb = 0; rb < NRB; rb++) {
+        const int n = rb * 16 + c16, t = n / GRP;
+        vrow[rb] = t < c.tq;
+        lim[rb] = c.pos0 + t;
+        float mm = -INFINITY, ss = 0.0f;
+        if (vrow[rb]) {
+            for (int p = 0; p < ns; p++) {
+                const float2 st = stats[((size_t)(soff[c.s] + p) * nkv + c.kvh) * kRows + n];
+                if (st.x == -INFINITY) continue;
+                const float mn = fmaxf(mm, st.x);
+                ss = ss * exp_fast(mm - mn) + st.y * exp_fast(st.x - mn);
+                mm = mn;
+            }
+        }
+        m[rb] = mm;
+        rsum[rb] = ss;
+    }
+    const uint16_t *Vb = vcache + ((size_t)c.s * nkv + c.kvh) * D * max_seq;
+    const size_t cap = (size_t)(soff[c.s + 1] - soff[c.s]) * sq.ks1;
+    const uint16_t *Ab = As + (size_t)soff[c.s] * sq.ks1 * nkv * kRows + (size_t)c.kvh * kRows * cap;
+    f32x4 acc[NRB][D / 16];
+#pragma unroll
+    for (int rb = 0; rb < NRB; rb++)
+#pragma unroll
+        for (int b = 0; b < D / 16; b++) acc[rb][b] = f32x4{};
+
+    // V^T and score fragments of the next 32-key step are loaded while the
+    // current step is multiplied. Loads never touch their value on issue
+    // (that would wait for them): addresses are clamped into the cache's
+    // valid 8-key groups and the out-of-range keys are masked at use.
+    const int kclamp = ((c.k1 - 1) / 8) * 8;   // last aligned group holding a valid key
+    u16x8 vf[D / 16], af[NRB];
+    auto load_step = [&](int kb, u16x8 *fv, u16x8 *fa) {
+        const int kq = min(kb + q4 * 8, kclamp);
+#pragma unroll
+        for (int b = 0; b < D / 16; b++)
+            fv[b] = *reinterpret_cast<const u16x8 *>(
+                Vb + ((size_t)(kq / 32) * D + b * 16 + c16) * 32 + kq % 32);
+#pragma unroll
+        for (int rb = 0; rb < NRB; rb++)
+            fa[rb] = *reinterpret_cast<const u16x8 *>(Ab + (size_t)(rb * 16 + c16) * cap + kq);
+    };
+    load_step(c.k0, vf, af);
+    for (int kb = c.k0; kb < c.k1; kb += 32) {
+        u16x8 vn[D / 16], an[NRB];
+        if (kb + 32 < c.k1) load_step(kb + 32, vn, an);
+        const int kq = kb + q4 * 8;            // this lane's 8 keys
+        bf16x8 pf[NRB];
+#pragma unroll
+        for (int rb = 0; rb < NRB; rb++) {
+            u16x8 pv = {};
+            if (vrow[rb]) {
+#pragma unroll
+                for (int e = 0; e < 8; e++) {
+                    const int kk = kq + e;
+                    if (kk <= lim[rb] && kk < c.k1)
+                        pv[e] = f2bf(exp_fast(bf2f(af[rb][e]) - m[rb]) / rsum[rb]);
+                }
+            }
+            pf[rb] = __builtin_bit_cast(bf16x8, pv);
+        }
+        const bool partial = kq + 8 > c.k1;    // keys past the end: zero V too
+#pragma unroll
+        for (int b = 0; b < D / 16; b++) {
+            u16x8 v8 = vf[b];
+            if (partial)
+                for (int e = 0; e < 8; e++)
+                    if (kq + e >= c.k1) v8[e] = 0;
+            const bf16x8 va = __builtin_bit_cast(bf16x8, v8);
+#pragma unroll
+            for (int rb = 0; rb < NRB; rb++)
+                acc[rb][b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, pf[rb], acc[rb][b], 0, 0, 0);
+        }
+#pragma unroll
+        for (int b = 0; b < D / 16; b++) vf[b] = vn[b];
+#pragma unroll
+        for (int rb = 0; rb < NRB; rb++) af[rb] = an[rb];
+    }
+#pragma unroll
+    for (int rb = 0; rb < NRB; rb++) {
+        if (!vrow[rb]) continue;
+        float *orow = Op + (((size_t)c.gsplit * nkv + c.kvh) * kRows + rb * 16 + c16) * D;
+#pragma unroll
+        for (int b = 0; b < D / 16; b++)
+            *reinterpret_cast<float4 *>(orow + b * 16 + q4 * 4) =
+                make_float4(acc[rb][b][0], acc[rb][b][1], acc[rb][b][2], acc[rb][b][3]);
+    }
+}
+
+// ---- k_attn_combine: one block per (token, q head), d threads ----------
+__global__ __launch_bounds__(D) void k_attn_combine(
+    AttnSeqs sq, const int32_t *__restrict__ dmeta, const float *__restrict__ Op,
+    const uint16_t *__restrict__ qg, int nh, int nkv, uint16_t *__restrict__ y) {
+    const Meta mt = meta_of(sq, dmeta);
+    const int32_t *cu = mt.cu, *soff = mt.soff2;
+    const int tt = blockIdx.x / nh, h = blockIdx.x % nh;
+    const int s = seq_of(cu, sq.n, tt), t = tt - cu[s];
+    const int kvh = h / GRP, n = t * GRP + h % GRP;
+    const int dd = threadIdx.x;
+    float sum = 0.0f;
+    for (int p = soff[s]; p < soff[s + 1]; p++)
+        sum += Op[(((size_t)p * nkv + kvh) * kRows + n) * D + dd];
+    const float o = rndf(sum);
+    const float gt = rndf(sigmoid_cr(bf2f(qg[((size_t)tt * nh + h) * 2 * D + D + dd])));
+    y[((size_t)tt * nh + h) * D + dd] = f2bf(o * gt);
+}
+
+// ---- cache layout conversion (one sequence) ----------------------------
+__global__ void k_cache_pack(const uint16_t *__restrict__ kref, const uint16_t *__restrict__ vref,
+                             size_t ntok, int nkv, uint16_t *__restrict__ kc,
+                             uint16_t *__restrict__ vc, size_t max_seq) {
+    size_t e = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (e >= ntok * nkv * D) return;
+    size_t p = e / (nkv * D), r = e % (nkv * D);
+    int hk = (int)(r / D), dd = (int)(r % D);
+    kc[((size_t)hk * max_seq + p) * D + dd] = kref[e];
+    vc[(size_t)hk * D * max_seq + ((p / 32) * D + dd) * 32 + p % 32] = vref[e];
+}
+
+__global__ void k_cache_unpack(const uint16_t *__restrict__ kc, const uint16_t *__restrict__ vc,
+                               size_t ntok, int nkv, size_t max_seq,
+                               uint16_t *__restrict__ kref, uint16_t *__restrict__ vref) {
+    size_t e = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (e >= ntok * nkv * D) return;
+    size_t p = e / (nkv * D), r = e % (nkv * D);
+    int hk = (int)(r / D), dd = (int)(r % D);
+    kref[e] = kc[((size_t)hk * max_seq + p) * D + dd];
+    vref[e] = vc[(size_t)hk * D * max_seq + ((p / 32) * D + dd) * 32 + p % 32];
+}
+
+}  // namespace
+
+namespace apus {
+
+int attn_check_layer(const ApusHipAttnLayer *L) {
+    if (!L) return set_error(kErrArgument, "NULL layer");
+    if (L->d != (size_t)D || L->rot != (size_t)ROT || L->nkv == 0 ||
+        L->nh != (size_t)GRP * L->nkv)
+        return set_error(kErrUnsupported,
+                         "attention mixer supports d=256, rot=64, nh=8*nkv (got nh=%zu "
+                         "nkv=%zu d=%zu rot=%zu)", L->nh, L->nkv, L->d, L->rot);
+    return kOk;
+}
+
+// Fill the metadata (by value, or uploaded when B is large) and choose the
+// split sizes: each kernel's grid should be one round of resident waves
+// (occupancy x 4 SIMDs x CUs) so no straggler round is left; ks1 (scores)
+// is a multiple of 64 keys, ks2 (P.V) of 32.
+static int attn_meta(size_t B, const int32_t *cu, const int32_t *pos0, size_t max_seq,
+                     size_t nkv, AttnSeqs *sq, const int32_t **dmeta, size_t *nsplit1,
+                     size_t *nsplit2, size_t *max_tok) {
+    if (!cu || !pos0 || cu[0] != 0) return set_error(kErrArgument, "bad offsets");
+    if (max_seq % 32 != 0) return set_error(kErrArgument, "max_seq must be a multiple of 32");
+    size_t mt = 0, keys = 0;
+    for (size_t s = 0; s < B; s++) {
+        const int32_t tq = cu[s + 1] - cu[s];
+        if (tq < 1 || tq > kRows / GRP)
+            return set_error(kErrUnsupported, "decode takes 1..%d new tokens per sequence (got %d)",
+                             kRows / GRP, tq);
+        if (pos0[s] < 0 || (size_t)pos0[s] + (size_t)tq > max_seq)
+            return set_error(kErrArgument, "sequence %zu overflows the cache (%d+%d > %zu)", s,
+                             pos0[s], tq, max_seq);
+        keys += (size_t)pos0[s] + (size_t)tq;
+        if ((size_t)tq > mt) mt = (size_t)tq;
+    }
+    const size_t slots = 4 * (size_t)cu_count();
+    const size_t occ1 = mt <= 2 ? 3 : 2, occ2 = 2;
+    auto pick = [](size_t work, size_t waves, size_t gran) {
+        size_t k = (work + waves - 1) / waves;
+        k = (k + gran - 1) / gran * gran;
+        return k < 256 ? (size_t)256 : k > 16384 ? (size_t)16384 : k;
+    };
+    const size_t ks1 = pick(keys * nkv, occ1 * slots, 64), ks2 = pick(keys * nkv, occ2 * slots, 32);
+    std::vector<int32_t> soff(B + 1, 0), soff2(B + 1, 0);
+    for (size_t s = 0; s < B; s++) {
+        const size_t ctx = (size_t)pos0[s] + (size_t)(cu[s + 1] - cu[s]);
+        soff[s + 1] = soff[s] + (int32_t)((ctx + ks1 - 1) / ks1);
+        soff2[s + 1] = soff2[s] + (int32_t)((ctx + ks2 - 1) / ks2);
+    }
+    *nsplit1 = (size_t)soff[B];
+    *nsplit2 = (size_t)soff2[B];
+    *max_tok = mt;
+    sq->n = (int32_t)B;
+    sq->ks1 = (int32_t)ks1;
+    sq->ks2 = (int32_t)ks2;
+    *dmeta = nullptr;
+    if (B <= (size_t)kAttnInlineSeqs) {
+        memcpy(sq->cu, cu, (B + 1) * 4);
+        memcpy(sq->pos0, pos0, B * 4);
+        memcpy(sq->soff, soff.data(), (B + 1) * 4);
+        memcpy(sq->soff2, soff2.data(), (B + 1) * 4);
+    } else {
+        std::vector<int32_t> m(4 * B + 3);
+        memcpy(m.data(), cu, (B + 1) * 4);
+        memcpy(m.data() + B + 1, pos0, B * 4);
+        memcpy(m.data() + 2 * B + 1, soff.data(), (B + 1) * 4);
+        memcpy(m.data() + 3 * B + 2, soff2.data(), (B + 1) * 4);
+        *dmeta = (const int32_t *)upload_small(kScratchMeta2, m.data(), m.size() * 4);
+        if (!*dmeta) return kErrHip;
+    }
+    return kOk;
+}
+
+int attn_prep(const ApusHipAttnLayer *L, const AttnSeqs &sq, const int32_t *dmeta,
+              size_t Ttot, size_t max_pos, const uint16_t *qg, const uint16_t *k,
+              const uint16_t *v, uint16_t *kcache, uint16_t *vcache, size_t max_seq,
+              uint16_t *qn) {
+    const uint16_t *rope = rope_table(L->rot, L->theta, max_pos);
+    if (!rope) return kErrHip;
+    k_attn_prep<<<(unsigned)(Ttot * (L->nh + L->nkv)), D, 0, stream()>>>(
+        sq, dmeta, qg, k, v, L->qn_w, L->kn_w, rope, kcache, vcache, max_seq, qn,
+        (int)L->nh, (int)L->nkv);
+    return launch_check("k_attn_prep");
+}
+
+}  // namespace apus
+
+extern "C" {
+
+int apus_hip_attn_decode(const ApusHipAttnLayer *L, size_t B, const int32_t *cu,
+                         const int32_t *pos0, const uint16_t *qg, const uint16_t *k,
+                         const uint16_t *v, uint16_t *kcache, uint16_t *vcache,
+                         size_t max_seq, uint16_t *y) {
+    APUS_READY();
+    if (int r = attn_check_layer(L)) return r;
+    if (B == 0) return kOk;
+    AttnSeqs sq;
+    const int32_t *dmeta = nullptr;
+    size_t ns1 = 0, ns2 = 0, mt = 0;
+    if (int r = attn_meta(B, cu, pos0, max_seq, L->nkv, &sq, &dmeta, &ns1, &ns2, &mt)) return r;
+    const size_t Ttot = (size_t)cu[B];
+    size_t max_pos = 0;
+    for (size_t s = 0; s < B; s++)
+        max_pos = std::max(max_pos, (size_t)pos0[s] + (size_t)(cu[s + 1] - cu[s]));
+    uint16_t *qn = (uint16_t *)scratch(kScratchAttnQ, Ttot * L->nh * D * 2);
+    uint16_t *As = (uint16_t *)scratch(kScratchAttnA, ns1 * (size_t)sq.ks1 * L->nkv * kRows * 2);
+    float2 *st = (float2 *)scratch(kScratchAttnStat, ns1 * L->nkv * kRows * 8);
+    float *Op = (float *)scratch(kScratchAttnPart, ns2 * L->nkv * kRows * D * 4);
+    if (!qn || !As || !st || !Op) return kErrHip;
+    if (int r = attn_prep(L, sq, dmeta, Ttot, max_pos, qg, k, v, kcache, vcache, max_seq, qn))
+        return r;
+    const float scale = (float)(1.0 / sqrt((double)L->d));
+    const unsigned grid = (unsigned)(ns1 * L->nkv), grid2 = (unsigned)(ns2 * L->nkv);
+    // one 16-row block covers up to 2 new tokens per sequence (8 heads each)
+    if (mt <= 2) {
+        k_attn_scores<1><<<grid, 64, 0, stream()>>>(sq, dmeta, qn, kcache, max_seq, (int)L->nh,
+                                                     (int)L->nkv, scale, As, st);
+        APUS_LAUNCHED("k_attn_scores");
+        k_attn_pv<1><<<grid2, 64, 0, stream()>>>(sq, dmeta, vcache, max_seq, (int)L->nkv, As, st, Op);
+        APUS_LAUNCHED("k_attn_pv");
+    } else {
+        k_attn_scores<2><<<grid, 64, 0, stream()>>>(sq, dmeta, qn, kcache, max_seq, (int)L->nh,
+                                                     (int)L->nkv, scale, As, st);
+        APUS_LAUNCHED("k_attn_scores");
+        k_attn_pv<2><<<grid2, 64, 0, stream()>>>(sq, dmeta, vcache, max_seq, (int)L->nkv, As, st, Op);
+        APUS_LAUNCHED("k_attn_pv");
+    }
+    k_attn_combine<<<(unsigned)(Ttot * L->nh), D, 0, stream()>>>(sq, dmeta, Op, qg, (int)L->nh,
+                                                                  (int)L->nkv, y);
+    APUS_LAUNCHED("k_attn_combine");
+    return kOk;
+}
+
+int apus_hip_attn_cache_pack(const uint16_t *kc_ref, const uint16_t *vc_ref, size_t ntok,
+                             size_t nkv, size_t d, uint16_t *kcache, uint16_t *vcache,
+                             size_t max_seq) {
+    APUS_READY();
+    if (d != (size_t)D) return set_error(kErrUnsupported, "cache pack supports d=256");
+    if (ntok > max_seq || max_seq % 32) return set_error(kErrArgument, "bad ntok/max_seq");
+    if (ntok == 0) return kOk;
+    k_cache_pack<<<cdiv(ntok * nkv * D, 256), 256, 0, stream()>>>(kc_ref, vc_ref, ntok, (int)nkv,
+                                                                   kcache, vcache, max_seq);
+    APUS_LAUNCHED("k_cache_pack");
+    return kOk;
+}
+
+int apus_hip_attn_cache_unpack(const uint16_t *kcache, const uint16_t *vcache, size_t ntok,
+                               size_t nkv, size_t d, size_t max_seq, uint16_t *kc_ref,
+                               uint16_t *vc_ref) {
+    APUS_READY();
+    if (d != (size_t)D) return set_error(kErrUnsupported, "cache unpack supports d=256");
+    if (ntok > max_seq || max_seq % 32) return set_error(kErrArgument, "bad ntok/max_seq");
+    if (ntok == 0) return kOk;
+    k_cache_unpack<<<cdiv(ntok * nkv * D, 256), 256, 0, stream()>>>(kcache, vcache, ntok, (int)nkv,
+                                                                     max_seq, kc_ref, vc_ref);
+    APUS_LAUNCHED("k_cache_unpack");
+    return kOk;
+}
+
+}  // extern "C"

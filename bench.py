@@ -12,6 +12,7 @@ reported under "configs" with their own roofline fractions:
   c0   config 0   GDN decode, batch 1
   c0b  config 0'  GDN decode, batch 64 (HBM-bound decode)
   c1   config 1   GDN prefill T=4096 (headline)
+  c2   config 2   gated-GQA decode, 64 sequences x 32K-token bf16 KV cache
 Input buffer sets rotate so the 256 MB Infinity Cache cannot serve
 repeated reads. The CPU baseline is the reference's own scalar anchors
 (oracle/_ref, built from the reference sources) when present, else the
@@ -163,6 +164,54 @@ def gdn_prefill_flops(T, C=64):
     return per * (T // C) * HV
 
 
+ATTN = (16, 2, 256, 64, 1e7)
+NH, NKV, AD = 16, 2, 256
+
+
+def attn_decode_bytes(ctx, tq=1):
+    """Algorithmic HBM bytes of one sequence's decode step: the K and V
+    cache rows read (ctx keys x nkv x d x 2 B each), the new q|gate, k, v
+    read, the appended k, v written, and the gated output written."""
+    kv = ctx * NKV * AD * 2 * 2
+    per_tok = NH * 2 * AD * 2 + NKV * AD * 2 * 2 + NKV * AD * 2 * 2 + NH * AD * 2
+    return kv + tq * per_tok
+
+
+def bench_attn_decode(torch, B, ctx, steps, warmup, seed):
+    """Config 2: B sequences, each with ctx-1 cached tokens plus one new
+    token (so the new token attends ctx keys)."""
+    import apus_hip
+    dev = torch.device("cuda")
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed)
+
+    def bf(shape, std=1.0):
+        return (torch.randn(shape, generator=g, device=dev) * std).to(torch.bfloat16).view(torch.int16)
+
+    w = dict(qn_w=bf((AD,), 0.1), kn_w=bf((AD,), 0.1))
+    layer = apus_hip.attn_layer(ATTN, w)
+    max_seq = ctx
+    kc = bf((B, NKV, max_seq, AD))
+    vc = bf((B, NKV, max_seq // 32, AD, 32))
+    nsets = 2
+    sets = [dict(qg=bf((B, NH, 2 * AD)), k=bf((B, NKV, AD)), v=bf((B, NKV, AD)),
+                 y=torch.empty((B, NH * AD), dtype=torch.int16, device=dev)) for _ in range(nsets)]
+    cu = np.arange(B + 1, dtype=np.int32)
+    pos0 = np.full(B, ctx - 1, np.int32)
+
+    def step(i):
+        s = sets[i]
+        apus_hip.attn_decode(layer, cu, pos0, s["qg"], s["k"], s["v"], kc, vc, max_seq, s["y"])
+
+    total, per = time_steps(torch, step, steps, warmup, nsets)
+    kt = float(np.mean(per))
+    bytes_ = B * attn_decode_bytes(ctx) + 2 * AD * 2
+    flops = B * NH * 4 * AD * ctx
+    return dict(workload=f"attn_decode_b{B}_ctx{ctx}", tokens_per_step=B, ms_per_step=total / steps * 1e3,
+                kernel="k_attn_scores+k_attn_pv", kernel_ms=kt * 1e3, alg_bytes=bytes_, alg_flops=flops,
+                tok_s=B * steps / total, hbm_gbs=bytes_ / kt / 1e9, hbm_frac=bytes_ / kt / HBM_PEAK)
+
+
 # ---------------------------------------------------------------- CPU side
 def cpu_model():
     try:
@@ -221,7 +270,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--only", default="c0,c0b,c1")
+    ap.add_argument("--only", default="c0,c0b,c1,c2")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-tokens", type=int, default=512)
     ap.add_argument("--cpu-threads", type=int, default=CPU_THREADS)
@@ -251,6 +300,10 @@ def main():
     if "c1" in want:
         res["c1"] = bench_gdn_prefill(torch, 4096, args.steps, args.warmup, 12)
         log("c1", res["c1"])
+
+    if "c2" in want:
+        res["c2"] = bench_attn_decode(torch, 64, 32768, args.steps, args.warmup, 13)
+        log("c2", res["c2"])
 
     head = res.get("c1") or next(iter(res.values()))
     cpu = None if args.no_cpu else cpu_baseline(args.cpu_threads, args.cpu_tokens)

@@ -164,6 +164,42 @@ int apus_hip_gdn_decode(const ApusHipGdnLayer *L, size_t B,
                         const uint16_t *b, uint16_t *conv_state, float *S,
                         uint16_t *y);
 
+/* Full-attention layer weights + dims (hot fields of ApusLayerCfg/W,
+ * c/layer.h:113-157). Device pointers. */
+typedef struct {
+    size_t nh, nkv, d, rot;         /* 16, 2, 256, 64 */
+    double theta;                   /* 1e7 */
+    const uint16_t *qn_w, *kn_w;    /* [d] bf16, (1+w) storage */
+} ApusHipAttnLayer;
+
+/* Device KV-cache layout. Sequence s of a batch owns
+ *   K: kcache + s*nkv*max_seq*d, laid out [nkv][max_seq][d];
+ *   V: vcache + s*nkv*d*max_seq, laid out [nkv][max_seq/32][d][32]
+ *      (transposed in blocks of 32 positions),
+ * bf16, max_seq a multiple of 32. The reference keeps both as
+ * [max_seq][nkv][d] (c/layer.h:164-165); pack/unpack convert the first
+ * ntok positions of one sequence (device pointers). */
+int apus_hip_attn_cache_pack(const uint16_t *kc_ref, const uint16_t *vc_ref,
+                             size_t ntok, size_t nkv, size_t d,
+                             uint16_t *kcache, uint16_t *vcache, size_t max_seq);
+int apus_hip_attn_cache_unpack(const uint16_t *kcache, const uint16_t *vcache,
+                               size_t ntok, size_t nkv, size_t d, size_t max_seq,
+                               uint16_t *kc_ref, uint16_t *vc_ref);
+
+/* Full-attention decode / verify for B sequences (c/layer.h:300-322 per
+ * token: q/k (1+w) RMSNorm, partial RoPE at each token's position, cache
+ * append, causal GQA over the cache, sigmoid output gate). Sequence s has
+ * pos0[s] tokens cached (HOST array) and cu[s+1]-cu[s] in 1..4 new tokens;
+ * new token t sits at position pos0[s]+t and attends keys 0..pos0[s]+t.
+ *   qg [Ttot, nh, 2d] ([q|gate] per head), k, v [Ttot, nkv, d] bf16;
+ *   y [Ttot, nh*d] bf16 (feeds wo).
+ * Split-K over the context on MFMA. Supports d=256, rot=64, nh=8*nkv. */
+int apus_hip_attn_decode(const ApusHipAttnLayer *L, size_t B,
+                         const int32_t *cu, const int32_t *pos0,
+                         const uint16_t *qg, const uint16_t *k,
+                         const uint16_t *v, uint16_t *kcache,
+                         uint16_t *vcache, size_t max_seq, uint16_t *y);
+
 #ifdef __cplusplus
 }
 #endif

@@ -70,3 +70,19 @@ def f32_stats(c, r):
     r = np.asarray(r, np.float32).ravel()
     same = np.mean(c.view(np.uint32) == r.view(np.uint32)) if c.size else 1.0
     return dict(exact=float(same), rel=state_rel(c, r))
+
+
+def assert_bf16_esc(c, r, esc, rel=BF16_REL, what=""):
+    """Tolerance class for reordered reductions (the reference's own form,
+    tests/m4a/test_gdn.c:84-95): every element |c - r| <= rel*(|r| + esc),
+    esc the sum of |terms| of that output, plus ||c - r||_2/||r||_2 <= rel.
+    Outputs that are small through cancellation (|r| << esc) are judged
+    against the size of their terms, as the reference judges its own."""
+    st = bf16_stats(c, r)
+    cf = f32_of(np.asarray(c).ravel()).astype(np.float64)
+    rf = f32_of(np.asarray(r).ravel()).astype(np.float64)
+    e = np.asarray(esc, np.float64).ravel()
+    ratio = np.abs(cf - rf) / (np.abs(rf) + e + 1e-30)
+    st["esc_max"] = float(ratio.max()) if ratio.size else 0.0
+    assert st["rel"] <= rel and st["esc_max"] <= rel, f"{what}: {st}"
+    return st

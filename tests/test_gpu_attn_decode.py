@@ -1,0 +1,98 @@
+"""GPU parity: the batched gated-GQA decode mixer (apus_hip_attn_decode)
+against the oracle's mixer (c/layer.h:300-322 wiring) on identical inputs.
+
+Tolerance class: q.k and P.V accumulate on MFMA in a different order than
+the reference's sequential loops, so a score may round to the neighbouring
+bf16 code; bf16 outputs are held to 2e-3 relative (||.||_2 over the
+tensor) and, per element, to 2e-3 of (|out| + sum of |terms|), the
+reference's esc-normalised form (tests/numerics.py assert_bf16_esc). The cache rows
+the mixer appends (normed, roped k; raw v) must be bit-exact.
+"""
+import numpy as np
+import pytest
+
+import synth
+from numerics import assert_bf16_esc
+from synth import bf16_f32
+
+
+def attn_esc(qf, kc, vc, cu, pos0, nh, nkv, d):
+    """esc = sum_j P_j |V_jd| per output element, P from the roped q and
+    the cache in float64 (the magnitude of the terms each output sums)."""
+    T = int(cu[-1])
+    esc = np.zeros((T, nh, d))
+    grp = nh // nkv
+    for s in range(len(cu) - 1):
+        for t in range(cu[s], cu[s + 1]):
+            p = pos0[s] + t - cu[s]
+            q = bf16_f32(qf[t]).astype(np.float64).reshape(nh, d)
+            for hk in range(nkv):
+                K = bf16_f32(kc[s, :p + 1, hk]).astype(np.float64)
+                V = np.abs(bf16_f32(vc[s, :p + 1, hk]).astype(np.float64))
+                A = q[hk * grp:(hk + 1) * grp] @ K.T / np.sqrt(d)
+                P = np.exp(A - A.max(1, keepdims=True))
+                P /= P.sum(1, keepdims=True)
+                esc[t, hk * grp:(hk + 1) * grp] = P @ V
+    return esc.reshape(T, nh * d)
+
+pytestmark = pytest.mark.gpu
+
+
+def _run(hip, orc, rng, cu, pos0, max_seq):
+    import torch
+    dims = synth.ATTN_DIMS
+    nh, nkv, d, rot, theta = dims
+    B = len(cu) - 1
+    T = int(cu[-1])
+    w = synth.attn_weights(rng)
+    tok = synth.attn_tokens(rng, T)
+    kc = synth.normal_bf16(rng, (B, max_seq, nkv, d))
+    vc = synth.normal_bf16(rng, (B, max_seq, nkv, d))
+    k_o, v_o = kc.copy(), vc.copy()
+    y_o, qf, _ = orc.attn_mixer(dims, w, np.asarray(cu, np.int32), np.asarray(pos0, np.int32),
+                                tok["qg"], tok["k"], tok["v"], k_o, v_o, max_seq * nkv * d,
+                                capture=True)
+    esc = attn_esc(qf, k_o, v_o, np.asarray(cu), np.asarray(pos0), nh, nkv, d)
+    dev = torch.device("cuda")
+    td = lambda a: torch.from_numpy(np.ascontiguousarray(a).view(np.int16)).to(dev)
+    tw = {k: td(v) for k, v in w.items()}
+    layer = hip.attn_layer(dims, tw)
+    dk = torch.empty((B, nkv, max_seq, d), dtype=torch.int16, device=dev)
+    dv = torch.empty((B, nkv, max_seq // 32, d, 32), dtype=torch.int16, device=dev)
+    for s in range(B):
+        hip.attn_cache_pack(td(kc[s]), td(vc[s]), max_seq, nkv, d, dk[s], dv[s], max_seq)
+    y = torch.empty((T, nh * d), dtype=torch.int16, device=dev)
+    t = {k: td(v) for k, v in tok.items()}
+    hip.attn_decode(layer, cu, pos0, t["qg"], t["k"], t["v"], dk, dv, max_seq, y)
+    rk = torch.empty((max_seq, nkv, d), dtype=torch.int16, device=dev)
+    rv = torch.empty_like(rk)
+    for s in range(B):
+        hip.attn_cache_unpack(dk[s], dv[s], max_seq, nkv, d, max_seq, rk, rv)
+        torch.cuda.synchronize()
+        assert np.array_equal(rk.cpu().numpy().view(np.uint16), k_o[s]), f"k cache seq {s}"
+        assert np.array_equal(rv.cpu().numpy().view(np.uint16), v_o[s]), f"v cache seq {s}"
+    st = assert_bf16_esc(y.cpu().numpy().view(np.uint16), y_o, esc, what="attn_decode y")
+    print(st)
+    return st
+
+
+def test_decode_small(hip, orc):
+    _run(hip, orc, np.random.default_rng(1), [0, 3, 4], [5, 40], 64)
+
+
+def test_decode_verify4(hip, orc):
+    """Three and four verify tokens (two 16-row MFMA blocks per kv head)."""
+    _run(hip, orc, np.random.default_rng(5), [0, 4, 7], [100, 1500], 1536)
+
+
+def test_decode_split_boundaries(hip, orc):
+    """Contexts ending just before, at and after the 1024-key split edges,
+    with 1..4 verify tokens (the causal mask inside the last split)."""
+    cu = np.array([0, 4, 5, 7, 10, 11], np.int32)
+    _run(hip, orc, np.random.default_rng(2), cu, [1020, 1023, 1024, 2046, 3000], 3072)
+
+
+def test_decode_config2_shape(hip, orc):
+    """BASELINE config 2 per sequence: 32K-token cache, one new token
+    (two sequences here; the bench runs 64)."""
+    _run(hip, orc, np.random.default_rng(3), [0, 1, 2], [32767, 32767], 32768)
