@@ -40,6 +40,19 @@ __device__ __forceinline__ float softplus_cr(float x) {
     return x > 20.0f ? x : (float)log1p((double)exp_cr(x));
 }
 
+// exp(x) for x <= 0 in fp32 via the hardware exp2 with the rounding error
+// of x*log2(e) folded back in (a few ulp). For the tolerance-class paths
+// (attention scores, chunked GDN decay factors), not for rounding points
+// that must match the reference.
+__device__ __forceinline__ float exp_fast(float x) {
+    if (x == -INFINITY) return 0.0f;
+    const float L2E = 1.44269504088896341f;
+    const float t = x * L2E;
+    const float r = fmaf(x, L2E, -t) + x * 1.925963001e-8f;
+    const float e = __builtin_amdgcn_exp2f(t);
+    return fmaf(e, r * 0.693147180559945f, e);
+}
+
 // Value of `v` in lane `src` of the wavefront (src must be uniform).
 __device__ __forceinline__ float lane_bcast(float v, int src) {
     return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), src));

@@ -40,6 +40,7 @@ enum ScratchSlot { kScratchIn = 0, kScratchIn2, kScratchIn3, kScratchIn4,
                    // batched GDN mixer intermediates
                    kScratchGdnQK, kScratchGdnV, kScratchGdnGate, kScratchGdnOB,
                    kScratchGdnChunk, kScratchGdnChunk2, kScratchGdnChunk3,
+                   kScratchGdnChunk4, kScratchGdnChunk5,
                    // batched attention mixer intermediates
                    kScratchAttnQ, kScratchAttnA, kScratchAttnStat,
                    kScratchAttnPart,

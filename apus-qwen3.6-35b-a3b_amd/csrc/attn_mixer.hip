@@ -64,18 +64,6 @@ __device__ __forceinline__ int seq_of(const int32_t *off, int n, int x) {
     return lo;
 }
 
-// exp(x) for x <= 0 in fp32 via the hardware exp2 with the rounding error
-// of x*log2(e) folded back in (a few ulp; the score path is a tolerance
-// class, see the file comment).
-__device__ __forceinline__ float exp_fast(float x) {
-    if (x == -INFINITY) return 0.0f;
-    const float L2E = 1.44269504088896341f;
-    const float t = x * L2E;
-    const float r = fmaf(x, L2E, -t) + x * 1.925963001e-8f;
-    const float e = __builtin_amdgcn_exp2f(t);
-    return fmaf(e, r * 0.693147180559945f, e);
-}
-
 // Metadata views: by value (AttnSeqs) or, for large batches, a device
 // array cu[B+1] | pos0[B] | soff[B+1] | soff2[B+1].
 struct Meta {

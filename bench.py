@@ -144,14 +144,14 @@ def bench_gdn_prefill(torch, T, steps, warmup, seed):
         s = d.sets[i]
         s["conv"].zero_()
         s["S"].zero_()
-        apus_hip.gdn_decode(d.layer, d.cu, s["qkv"], s["z"], s["a"], s["b"], s["conv"], s["S"], s["y"])
+        apus_hip.gdn_prefill(d.layer, d.cu, s["qkv"], s["z"], s["a"], s["b"], s["conv"], s["S"], s["y"])
 
     total, per = time_steps(torch, step, steps, warmup, nsets)
     kt = float(np.mean(per))
     bytes_ = gdn_seq_bytes(T) + GDN_WEIGHT_BYTES
     flops = gdn_prefill_flops(T)
     return dict(workload=f"gdn_prefill_t{T}", tokens_per_step=T, ms_per_step=total / steps * 1e3,
-                kernel="k_gdn_decode", kernel_ms=kt * 1e3, alg_bytes=bytes_, alg_flops=flops,
+                kernel="gdn_prefill", kernel_ms=kt * 1e3, alg_bytes=bytes_, alg_flops=flops,
                 tok_s=T * steps / total, hbm_gbs=bytes_ / kt / 1e9, hbm_frac=bytes_ / kt / HBM_PEAK,
                 mfma_tflops=flops / kt / 1e12, mfma_frac=flops / kt / BF16_PEAK)
 

@@ -164,6 +164,21 @@ int apus_hip_gdn_decode(const ApusHipGdnLayer *L, size_t B,
                         const uint16_t *b, uint16_t *conv_state, float *S,
                         uint16_t *y);
 
+/* Chunked GDN prefill: the same layer and arguments as apus_hip_gdn_decode
+ * for sequences of any length (c/layer.h:427-492, the prompt path; the
+ * reference steps the recurrence token by token, c/gdn.h:627-635). The
+ * recurrence runs in chunks of 64 tokens in the WY/UT form on fp32 MFMA:
+ * conv_state and the token-parallel ops equal the reference anchors up to
+ * libm ulps; S and y are a tolerance class of the sequential recurrence
+ * (state within 1e-4 relative, y within bf16 rounding of the sequential
+ * result). Library scratch grows with the token count (about 80 KiB per
+ * chunk of 64 tokens per v-head). */
+int apus_hip_gdn_prefill(const ApusHipGdnLayer *L, size_t B,
+                         const int32_t *cu, const uint16_t *qkv,
+                         const uint16_t *z, const uint16_t *a,
+                         const uint16_t *b, uint16_t *conv_state, float *S,
+                         uint16_t *y);
+
 /* Full-attention layer weights + dims (hot fields of ApusLayerCfg/W,
  * c/layer.h:113-157). Device pointers. */
 typedef struct {
