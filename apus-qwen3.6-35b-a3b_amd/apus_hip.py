@@ -27,7 +27,7 @@ EXPORTS = [
     "apus_hip_init", "apus_hip_is_enabled", "apus_hip_last_error",
     "apus_hip_set_stream", "apus_hip_synchronize", "apus_hip_malloc",
     "apus_hip_free", "apus_hip_memcpy_h2d", "apus_hip_memcpy_d2h",
-    "apus_hip_memset",
+    "apus_hip_memset", "apus_hip_timing_enable", "apus_hip_timing_get",
     "apus_hip_gdn_conv1d", "apus_hip_gdn_conv1d_step", "apus_hip_gdn_decay",
     "apus_hip_gdn_beta", "apus_hip_gdn_l2norm", "apus_hip_gdn_step",
     "apus_hip_gdn_step_mt", "apus_hip_gdn_recurrent", "apus_hip_gdn_onorm",
@@ -129,6 +129,18 @@ def set_stream(stream_handle):
 
 def synchronize():
     _chk(load().apus_hip_synchronize())
+
+
+def timing_enable(on=True):
+    _chk(load().apus_hip_timing_enable(C.c_int(1 if on else 0)))
+
+
+def timing_get(kernel):
+    """(total milliseconds, launches) recorded for one kernel name."""
+    ms = C.c_double(0.0)
+    n = _sz(0)
+    _chk(load().apus_hip_timing_get(kernel.encode(), C.byref(ms), C.byref(n)))
+    return ms.value, n.value
 
 
 # ---------------------------------------------------------------- tier 1

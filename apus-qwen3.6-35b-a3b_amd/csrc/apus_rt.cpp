@@ -43,6 +43,35 @@ uint16_t host_bf16(float x) {
     return (uint16_t)((u + 0x7fffu + ((u >> 16) & 1u)) >> 16);
 }
 
+struct TimedKernel {
+    const char *name;
+    std::vector<std::pair<hipEvent_t, hipEvent_t>> ev;
+};
+bool g_timing = false;
+std::vector<TimedKernel> g_timed;
+std::vector<hipEvent_t> g_event_pool;
+int g_open = -1;
+
+hipEvent_t take_event() {
+    if (!g_event_pool.empty()) {
+        hipEvent_t e = g_event_pool.back();
+        g_event_pool.pop_back();
+        return e;
+    }
+    hipEvent_t e = nullptr;
+    if (hipEventCreate(&e) != hipSuccess) return nullptr;
+    return e;
+}
+
+void timing_clear() {
+    for (auto &k : g_timed)
+        for (auto &p : k.ev) {
+            g_event_pool.push_back(p.first);
+            g_event_pool.push_back(p.second);
+        }
+    g_timed.clear();
+}
+
 bool disabled_by_env() {
     const char *e = getenv("APUS_HIP_DISABLE");
     return e && *e && strcmp(e, "0") != 0;
@@ -183,6 +212,23 @@ const uint16_t *rope_table(size_t rot, double theta, size_t max_pos) {
     return g_rope.dev;
 }
 
+int timing_begin(const char *name) {
+    if (!g_timing) return -1;
+    size_t i = 0;
+    while (i < g_timed.size() && strcmp(g_timed[i].name, name) != 0) i++;
+    if (i == g_timed.size()) g_timed.push_back(TimedKernel{name, {}});
+    hipEvent_t a = take_event(), b = take_event();
+    if (!a || !b) return -1;
+    if (hipEventRecord(a, g_stream) != hipSuccess) return -1;
+    g_timed[i].ev.emplace_back(a, b);
+    return (int)i;
+}
+
+void timing_end(int slot) {
+    if (slot < 0 || (size_t)slot >= g_timed.size() || g_timed[slot].ev.empty()) return;
+    (void)hipEventRecord(g_timed[slot].ev.back().second, g_stream);
+}
+
 }  // namespace apus
 
 using namespace apus;
@@ -243,6 +289,32 @@ int apus_hip_memcpy_d2h(void *dst, const void *src, size_t bytes) {
     APUS_HIP_TRY(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost,
                                 g_stream));
     APUS_HIP_TRY(hipStreamSynchronize(g_stream));
+    return kOk;
+}
+
+int apus_hip_timing_enable(int on) {
+    APUS_READY();
+    APUS_HIP_TRY(hipStreamSynchronize(g_stream));
+    timing_clear();
+    g_timing = on != 0;
+    return kOk;
+}
+
+int apus_hip_timing_get(const char *name, double *total_ms, size_t *count) {
+    APUS_READY();
+    if (!name || !total_ms || !count) return set_error(kErrArgument, "NULL argument");
+    APUS_HIP_TRY(hipStreamSynchronize(g_stream));
+    *total_ms = 0.0;
+    *count = 0;
+    for (auto &k : g_timed) {
+        if (strcmp(k.name, name) != 0) continue;
+        for (auto &p : k.ev) {
+            float ms = 0.0f;
+            APUS_HIP_TRY(hipEventElapsedTime(&ms, p.first, p.second));
+            *total_ms += ms;
+        }
+        *count = k.ev.size();
+    }
     return kOk;
 }
 

@@ -57,7 +57,20 @@ const uint16_t *rope_table(size_t rot, double theta, size_t max_pos);
 // by the library; stream-ordered, valid until the next call with `slot`.
 void *upload_small(int slot, const void *host, size_t bytes);
 
+// Opt-in per-kernel timing: when enabled (apus_hip_timing_enable), a pair
+// of events is recorded on the library stream around each wrapped launch;
+// apus_hip_timing_get sums them per kernel name. Disabled: one branch.
+int timing_begin(const char *name);
+void timing_end(int slot);
+
 }  // namespace apus
+
+#define APUS_TIMED(name, ...)                                                \
+    do {                                                                     \
+        int ts_ = ::apus::timing_begin(name);                                \
+        __VA_ARGS__;                                                         \
+        ::apus::timing_end(ts_);                                             \
+    } while (0)
 
 #define APUS_HIP_TRY(expr)                                                   \
     do {                                                                     \

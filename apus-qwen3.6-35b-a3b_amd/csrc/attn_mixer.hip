@@ -514,9 +514,10 @@ int attn_prep(const ApusHipAttnLayer *L, const AttnSeqs &sq, const int32_t *dmet
               uint16_t *qn) {
     const uint16_t *rope = rope_table(L->rot, L->theta, max_pos);
     if (!rope) return kErrHip;
-    k_attn_prep<<<(unsigned)(Ttot * (L->nh + L->nkv)), D, 0, stream()>>>(
+    APUS_TIMED("k_attn_prep",
+               k_attn_prep<<<(unsigned)(Ttot * (L->nh + L->nkv)), D, 0, stream()>>>(
         sq, dmeta, qg, k, v, L->qn_w, L->kn_w, rope, kcache, vcache, max_seq, qn,
-        (int)L->nh, (int)L->nkv);
+        (int)L->nh, (int)L->nkv));
     return launch_check("k_attn_prep");
 }
 
@@ -550,20 +551,25 @@ int apus_hip_attn_decode(const ApusHipAttnLayer *L, size_t B, const int32_t *cu,
     const unsigned grid = (unsigned)(ns1 * L->nkv), grid2 = (unsigned)(ns2 * L->nkv);
     // one 16-row block covers up to 2 new tokens per sequence (8 heads each)
     if (mt <= 2) {
-        k_attn_scores<1><<<grid, 64, 0, stream()>>>(sq, dmeta, qn, kcache, max_seq, (int)L->nh,
-                                                     (int)L->nkv, scale, As, st);
+        APUS_TIMED("k_attn_scores",
+                   k_attn_scores<1><<<grid, 64, 0, stream()>>>(sq, dmeta, qn, kcache, max_seq, (int)L->nh,
+                                                     (int)L->nkv, scale, As, st));
         APUS_LAUNCHED("k_attn_scores");
-        k_attn_pv<1><<<grid2, 64, 0, stream()>>>(sq, dmeta, vcache, max_seq, (int)L->nkv, As, st, Op);
+        APUS_TIMED("k_attn_pv",
+                   k_attn_pv<1><<<grid2, 64, 0, stream()>>>(sq, dmeta, vcache, max_seq, (int)L->nkv, As, st, Op));
         APUS_LAUNCHED("k_attn_pv");
     } else {
-        k_attn_scores<2><<<grid, 64, 0, stream()>>>(sq, dmeta, qn, kcache, max_seq, (int)L->nh,
-                                                     (int)L->nkv, scale, As, st);
+        APUS_TIMED("k_attn_scores",
+                   k_attn_scores<2><<<grid, 64, 0, stream()>>>(sq, dmeta, qn, kcache, max_seq, (int)L->nh,
+                                                     (int)L->nkv, scale, As, st));
         APUS_LAUNCHED("k_attn_scores");
-        k_attn_pv<2><<<grid2, 64, 0, stream()>>>(sq, dmeta, vcache, max_seq, (int)L->nkv, As, st, Op);
+        APUS_TIMED("k_attn_pv",
+                   k_attn_pv<2><<<grid2, 64, 0, stream()>>>(sq, dmeta, vcache, max_seq, (int)L->nkv, As, st, Op));
         APUS_LAUNCHED("k_attn_pv");
     }
-    k_attn_combine<<<(unsigned)(Ttot * L->nh), D, 0, stream()>>>(sq, dmeta, Op, qg, (int)L->nh,
-                                                                  (int)L->nkv, y);
+    APUS_TIMED("k_attn_combine",
+               k_attn_combine<<<(unsigned)(Ttot * L->nh), D, 0, stream()>>>(sq, dmeta, Op, qg, (int)L->nh,
+                                                                  (int)L->nkv, y));
     APUS_LAUNCHED("k_attn_combine");
     return kOk;
 }

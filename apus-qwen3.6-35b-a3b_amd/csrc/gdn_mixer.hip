@@ -385,9 +385,10 @@ int gdn_prep(const ApusHipGdnLayer *L, size_t B, const int32_t *dcu,
     if (!w->qk || !w->vconv || !w->gate || !w->ob || (want_graw && !w->graw))
         return kErrHip;
     const float qscale = (float)pow((double)L->dk, -0.5);
-    k_gdn_prep<<<(unsigned)(Ttot * L->hk), 256, 0, stream()>>>(
+    APUS_TIMED("k_gdn_prep",
+               k_gdn_prep<<<(unsigned)(Ttot * L->hk), 256, 0, stream()>>>(
         dcu, (int)B, qkv, a, b, L->conv_w, L->A_log, L->dt_bias, conv_state,
-        w->qk, w->vconv, w->gate, w->graw, (int)L->hk, qscale);
+        w->qk, w->vconv, w->gate, w->graw, (int)L->hk, qscale));
     return launch_check("k_gdn_prep");
 }
 
@@ -396,9 +397,10 @@ int gdn_post(const ApusHipGdnLayer *L, size_t B, const int32_t *dcu,
              const uint16_t *qkv, uint16_t *conv_state, uint16_t *y) {
     const size_t cd = 2 * L->hk * DK + L->hv * DV;
     const size_t nblk = Ttot * L->hv + B * (cd / 128);
-    k_gdn_post<<<(unsigned)nblk, 128, 0, stream()>>>(
+    APUS_TIMED("k_gdn_post",
+               k_gdn_post<<<(unsigned)nblk, 128, 0, stream()>>>(
         dcu, (int)B, (int)Ttot, w->ob, z, L->onorm_w, y, qkv, conv_state,
-        (int)L->hk);
+        (int)L->hk));
     return launch_check("k_gdn_post");
 }
 
@@ -426,9 +428,10 @@ int apus_hip_gdn_decode(const ApusHipGdnLayer *L, size_t B, const int32_t *cu,
     const float qscale = (float)pow((double)L->dk, -0.5);
     const bool multi = (size_t)cu[B] != B;     // some sequence has != 1 token
     auto kern = multi ? k_gdn_decode<true> : k_gdn_decode<false>;
-    kern<<<(unsigned)(B * L->hk), 256, 0, stream()>>>(
+    APUS_TIMED("k_gdn_decode",
+               kern<<<(unsigned)(B * L->hk), 256, 0, stream()>>>(
         ca, dcu, qkv, z, a, b, L->conv_w, L->A_log, L->dt_bias, L->onorm_w,
-        conv_state, S, y, (int)L->hk, qscale);
+        conv_state, S, y, (int)L->hk, qscale));
     APUS_LAUNCHED("k_gdn_decode");
     return kOk;
 }

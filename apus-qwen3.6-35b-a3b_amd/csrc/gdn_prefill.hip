@@ -400,11 +400,13 @@ int apus_hip_gdn_prefill(const ApusHipGdnLayer *L, size_t B, const int32_t *cu,
     float *Ab = (float *)scratch(kScratchGdnChunk4, units * C * C * 4);
     float *Fb = (float *)scratch(kScratchGdnChunk5, units * 2 * C * 4);
     if (!Ub || !Wb || !Ab || !Fb) return kErrHip;
-    k_gdn_chunk_wy<<<(unsigned)units, 256, 0, stream()>>>(
-        sq, kmeta, w.qk, w.vconv, w.gate, w.graw, Ub, Wb, Ab, Fb, (int)L->hk);
+    APUS_TIMED("k_gdn_chunk_wy",
+               k_gdn_chunk_wy<<<(unsigned)units, 256, 0, stream()>>>(
+        sq, kmeta, w.qk, w.vconv, w.gate, w.graw, Ub, Wb, Ab, Fb, (int)L->hk));
     APUS_LAUNCHED("k_gdn_chunk_wy");
-    k_gdn_chunk_scan<<<(unsigned)(B * L->hv * NCB), 256, 0, stream()>>>(
-        sq, kmeta, w.qk, Ub, Wb, Ab, Fb, S, w.ob, (int)L->hk);
+    APUS_TIMED("k_gdn_chunk_scan",
+               k_gdn_chunk_scan<<<(unsigned)(B * L->hv * NCB), 256, 0, stream()>>>(
+        sq, kmeta, w.qk, Ub, Wb, Ab, Fb, S, w.ob, (int)L->hk));
     APUS_LAUNCHED("k_gdn_chunk_scan");
     return gdn_post(L, B, dmeta, Ttot, &w, z, qkv, conv_state, y);
 }

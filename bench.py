@@ -36,6 +36,7 @@ for p in (PKG, os.path.join(ROOT, "oracle")):
 
 HBM_PEAK = 8.0e12            # B/s, MI355X HBM3E
 BF16_PEAK = 2.5e15           # flop/s dense bf16 MFMA
+FP32_PEAK = 157.3e12         # flop/s dense fp32 MFMA
 CPU_THREADS = 16             # the GPU box's CPU share for one GPU
 
 GDN = (16, 32, 128, 128)
@@ -96,9 +97,13 @@ class Dev:
         self.zero_state = zero_state
 
 
-def time_steps(torch, fn, steps, warmup, nsets):
-    """Run warmup then `steps` timed steps; return (total_s, per-step
-    event times in s). Each step uses buffer set i % nsets."""
+def time_steps(torch, fn, steps, warmup, nsets, kernels=()):
+    """Run warmup then `steps` timed steps; return (total_s, per-step event
+    times in s, {kernel: average launch ms}). Each step uses buffer set
+    i % nsets. The wall-clock pass runs without kernel timing; a second
+    pass of the same steps records HIP events around each launch of the
+    named kernels on the library's stream (apus_hip_timing_*)."""
+    import apus_hip
     for i in range(warmup):
         fn(i % nsets)
     torch.cuda.synchronize()
@@ -112,7 +117,46 @@ def time_steps(torch, fn, steps, warmup, nsets):
     torch.cuda.synchronize()
     total = time.perf_counter() - t0
     per = [a.elapsed_time(b) * 1e-3 for a, b in ev]
-    return total, per
+    kt = {}
+    if kernels:
+        apus_hip.timing_enable(True)
+        for i in range(steps):
+            fn(i % nsets)
+        for k in kernels:
+            ms, n = apus_hip.timing_get(k)
+            if n:
+                kt[k] = ms / n
+        apus_hip.timing_enable(False)
+    return total, per, kt
+
+
+def measured_traffic(workload, kernel):
+    """HBM bytes per launch of `kernel` in `workload` from the committed
+    rocprofv3 FETCH_SIZE / WRITE_SIZE passes (profiles/hbm_traffic.json,
+    scaled by a 1 GiB copy), or None when not profiled."""
+    try:
+        with open(os.path.join(ROOT, "profiles", "hbm_traffic.json")) as f:
+            t = json.load(f)
+        return t[f"{workload}/{kernel}"]["bytes"]
+    except (OSError, KeyError, ValueError):
+        return None
+
+
+def kernel_roofline(kt, table, workload):
+    """Roofline of the dominant kernel: table maps kernel name to
+    (bound, algorithmic units per launch, peak per second); achieved =
+    units / that kernel's average launch time."""
+    name = max((k for k in table if k in kt), key=lambda k: kt[k])
+    bound, units, peak = table[name]
+    sec = kt[name] * 1e-3
+    traffic = measured_traffic(workload, name)
+    if bound == "mfma":
+        return dict(kernel=name, bound="mfma", achieved=units / sec / 1e12, peak=peak / 1e12,
+                    unit="TFLOP/s", frac=units / sec / peak, traffic=traffic, launch_ms=kt[name],
+                    per_launch=units)
+    return dict(kernel=name, bound="hbm", achieved=units / sec / 1e9, peak=peak / 1e9,
+                unit="GB/s", frac=units / sec / peak, traffic=traffic, launch_ms=kt[name],
+                per_launch=units)
 
 
 # ---------------------------------------------------------------- workloads
@@ -126,12 +170,14 @@ def bench_gdn_decode(torch, B, steps, warmup, seed):
         s = d.sets[i]
         apus_hip.gdn_decode(d.layer, d.cu, s["qkv"], s["z"], s["a"], s["b"], s["conv"], s["S"], s["y"])
 
-    total, per = time_steps(torch, step, steps, warmup, nsets)
-    kt = float(np.mean(per))
     bytes_ = B * gdn_seq_bytes(1) + GDN_WEIGHT_BYTES
-    return dict(workload=f"gdn_decode_b{B}", tokens_per_step=B, ms_per_step=total / steps * 1e3,
-                kernel="k_gdn_decode", kernel_ms=kt * 1e3, alg_bytes=bytes_,
-                tok_s=B * steps / total, hbm_gbs=bytes_ / kt / 1e9, hbm_frac=bytes_ / kt / HBM_PEAK)
+    table = {"k_gdn_decode": ("hbm", bytes_, HBM_PEAK)}
+    total, per, kt = time_steps(torch, step, steps, warmup, nsets, table)
+    st = float(np.mean(per))
+    wl = f"gdn_decode_b{B}"
+    return dict(workload=wl, tokens_per_step=B, ms_per_step=total / steps * 1e3,
+                step_event_ms=st * 1e3, kernels_ms=kt, alg_bytes=bytes_,
+                tok_s=B * steps / total, roofline=kernel_roofline(kt, table, wl))
 
 
 def bench_gdn_prefill(torch, T, steps, warmup, seed):
@@ -146,14 +192,40 @@ def bench_gdn_prefill(torch, T, steps, warmup, seed):
         s["S"].zero_()
         apus_hip.gdn_prefill(d.layer, d.cu, s["qkv"], s["z"], s["a"], s["b"], s["conv"], s["S"], s["y"])
 
-    total, per = time_steps(torch, step, steps, warmup, nsets)
-    kt = float(np.mean(per))
     bytes_ = gdn_seq_bytes(T) + GDN_WEIGHT_BYTES
     flops = gdn_prefill_flops(T)
-    return dict(workload=f"gdn_prefill_t{T}", tokens_per_step=T, ms_per_step=total / steps * 1e3,
-                kernel="gdn_prefill", kernel_ms=kt * 1e3, alg_bytes=bytes_, alg_flops=flops,
-                tok_s=T * steps / total, hbm_gbs=bytes_ / kt / 1e9, hbm_frac=bytes_ / kt / HBM_PEAK,
-                mfma_tflops=flops / kt / 1e12, mfma_frac=flops / kt / BF16_PEAK)
+    nu = (T // 64) * HV                       # (chunk, v-head) units
+    table = {"k_gdn_chunk_scan": ("mfma", nu * SCAN_FLOPS_PER_UNIT, FP32_PEAK),
+             "k_gdn_chunk_wy": ("mfma", nu * WY_FLOPS_PER_UNIT, FP32_PEAK),
+             "k_gdn_prep": ("hbm", gdn_prep_bytes(T), HBM_PEAK),
+             "k_gdn_post": ("hbm", gdn_post_bytes(T), HBM_PEAK)}
+    total, per, kt = time_steps(torch, step, steps, warmup, nsets, table)
+    st = float(np.mean(per))
+    wl = f"gdn_prefill_t{T}"
+    return dict(workload=wl, tokens_per_step=T, ms_per_step=total / steps * 1e3,
+                step_event_ms=st * 1e3, kernels_ms=kt, alg_bytes=bytes_, alg_flops=flops,
+                tok_s=T * steps / total, layer_hbm_frac=bytes_ / st / HBM_PEAK,
+                layer_tflops=flops / st / 1e12, roofline=kernel_roofline(kt, table, wl))
+
+
+# Algorithmic flops per (chunk of 64, v-head) of the two chunk kernels:
+# the scan does W S0, Q S0, K^T D (64x128x128 each) and A D (64x64x128);
+# the WY build does K K^T, Q K^T (64x64x128) and the two 64x64x128
+# triangular applications giving U and W, plus the triangular solve.
+SCAN_FLOPS_PER_UNIT = 3 * 2 * 64 * 128 * 128 + 2 * 64 * 64 * 128
+WY_FLOPS_PER_UNIT = 4 * 2 * 64 * 64 * 128 + (2 * 64 ** 3) // 3
+
+
+def gdn_prep_bytes(T):
+    """k_gdn_prep interface bytes: qkv, a, b in; fp32 l2-normed q and k,
+    conv+SiLU v (bf16), (exp g, beta) and g out; old conv state in."""
+    return T * (CD * 2 + HV * 2 * 2 + 2 * HK * DK * 4 + VD * 2 + HV * 8 + HV * 4) + CD * 3 * 2
+
+
+def gdn_post_bytes(T):
+    """k_gdn_post interface bytes: rnd(o) and z in, y out; conv state
+    rewritten from the last three qkv rows."""
+    return T * VD * 2 * 3 + CD * 3 * 2 * 2 + 3 * CD * 2
 
 
 def gdn_prefill_flops(T, C=64):
@@ -203,13 +275,38 @@ def bench_attn_decode(torch, B, ctx, steps, warmup, seed):
         s = sets[i]
         apus_hip.attn_decode(layer, cu, pos0, s["qg"], s["k"], s["v"], kc, vc, max_seq, s["y"])
 
-    total, per = time_steps(torch, step, steps, warmup, nsets)
-    kt = float(np.mean(per))
     bytes_ = B * attn_decode_bytes(ctx) + 2 * AD * 2
     flops = B * NH * 4 * AD * ctx
-    return dict(workload=f"attn_decode_b{B}_ctx{ctx}", tokens_per_step=B, ms_per_step=total / steps * 1e3,
-                kernel="k_attn_scores+k_attn_pv", kernel_ms=kt * 1e3, alg_bytes=bytes_, alg_flops=flops,
-                tok_s=B * steps / total, hbm_gbs=bytes_ / kt / 1e9, hbm_frac=bytes_ / kt / HBM_PEAK)
+    kbytes = B * ctx * NKV * AD * 2           # one of the K / V caches
+    table = {"k_attn_scores": ("hbm", kbytes, HBM_PEAK), "k_attn_pv": ("hbm", kbytes, HBM_PEAK),
+             "k_attn_prep": ("hbm", B * (NH * 2 * AD * 2 + NKV * AD * 2 * 4), HBM_PEAK),
+             "k_attn_combine": ("hbm", B * NH * AD * 2 * 2, HBM_PEAK)}
+    total, per, kt = time_steps(torch, step, steps, warmup, nsets, table)
+    st = float(np.mean(per))
+    wl = f"attn_decode_b{B}_ctx{ctx}"
+    return dict(workload=wl, tokens_per_step=B, ms_per_step=total / steps * 1e3,
+                step_event_ms=st * 1e3, kernels_ms=kt, alg_bytes=bytes_, alg_flops=flops,
+                tok_s=B * steps / total, layer_hbm_gbs=bytes_ / st / 1e9,
+                layer_hbm_frac=bytes_ / st / HBM_PEAK, roofline=kernel_roofline(kt, table, wl))
+
+
+def bench_copy(torch, steps, warmup):
+    """Calibration workload for HBM counters: a plain 1 GiB device copy
+    (reads 1 GiB, writes 1 GiB); rocprofv3 FETCH_SIZE / WRITE_SIZE of its
+    kernel against 1,048,576 KiB give the counter scale."""
+    n = 1 << 30
+    a = [torch.empty(n, dtype=torch.uint8, device="cuda") for _ in range(2)]
+    b = [torch.empty(n, dtype=torch.uint8, device="cuda") for _ in range(2)]
+    for x in a:
+        x.fill_(1)
+
+    def step(i):
+        b[i].copy_(a[i])
+
+    total, per, _ = time_steps(torch, step, steps, warmup, 2)
+    st = float(np.mean(per))
+    return dict(workload="copy_1GiB", ms_per_step=total / steps * 1e3, step_event_ms=st * 1e3,
+                alg_bytes=2 * n, hbm_gbs=2 * n / st / 1e9, tok_s=0.0)
 
 
 # ---------------------------------------------------------------- CPU side
@@ -264,6 +361,14 @@ def cpu_baseline(threads, tokens):
                         f" with {threads} pool threads on {cpu_model()} (nproc {os.cpu_count()})"))
 
 
+def _rounded(x):
+    if isinstance(x, dict):
+        return {k: _rounded(v) for k, v in x.items()}
+    if isinstance(x, float):
+        return float(f"{x:.6g}")
+    return x
+
+
 # ---------------------------------------------------------------- main
 def main():
     ap = argparse.ArgumentParser()
@@ -272,7 +377,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--only", default="c0,c0b,c1,c2")
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--cpu-tokens", type=int, default=512)
+    ap.add_argument("--cpu-tokens", type=int, default=8192)
     ap.add_argument("--cpu-threads", type=int, default=CPU_THREADS)
     ap.add_argument("--cpu-worker", action="store_true")
     args = ap.parse_args()
@@ -304,22 +409,24 @@ def main():
     if "c2" in want:
         res["c2"] = bench_attn_decode(torch, 64, 32768, args.steps, args.warmup, 13)
         log("c2", res["c2"])
+    if "copy" in want:
+        res["copy"] = bench_copy(torch, args.steps, args.warmup)
+        log("copy", res["copy"])
 
-    head = res.get("c1") or next(iter(res.values()))
+    head = res.get("c1") or next((v for v in res.values() if "roofline" in v), None)
+    if head is None:                       # calibration-only run
+        print(json.dumps(dict(metric="copy calibration", configs=_rounded(res))))
+        return
     cpu = None if args.no_cpu else cpu_baseline(args.cpu_threads, args.cpu_tokens)
-    roof = dict(bound="hbm", achieved=head["alg_bytes"] / (head["kernel_ms"] * 1e-3) / 1e9,
-                peak=HBM_PEAK / 1e9, unit="GB/s",
-                frac=head["alg_bytes"] / (head["kernel_ms"] * 1e-3) / HBM_PEAK,
-                traffic=None, kernel=head["kernel"])
+    roof = head["roofline"]
     line = dict(metric="attn-layer tok/s @1 GPU; decode HBM GB/s % peak; prefill MFMA TFLOP/s % peak",
                 value=head["tok_s"], unit="tok/s", n_gpus=1, steps=args.steps, warmup=args.warmup,
                 ms_per_step=head["ms_per_step"], higher_is_better=True, scaling="weak",
-                vs_baseline=None, dtype="bf16/fp32", data="synthetic",
+                vs_baseline=None, dtype="f32", data="synthetic (bf16 storage, fp32 arithmetic)",
                 config=dict(workload=head["workload"], global_batch=1,
                             seq_len=head["tokens_per_step"], parallelism="none (1 GPU)"),
                 roofline=roof, cpu_baseline=cpu,
-                configs={k: {kk: (round(vv, 6) if isinstance(vv, float) else vv)
-                             for kk, vv in v.items()} for k, v in res.items()})
+                configs=_rounded(res))
     print(json.dumps(line))
 
 

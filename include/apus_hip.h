@@ -57,6 +57,14 @@ int    apus_hip_free(void *dptr);
 int    apus_hip_memcpy_h2d(void *dst, const void *src, size_t bytes);
 int    apus_hip_memcpy_d2h(void *dst, const void *src, size_t bytes);
 int    apus_hip_memset(void *dst, int value, size_t bytes);
+/* Per-kernel timing (no counterpart in the reference; for benchmarks and
+ * profiling hosts). enable(1) clears and starts recording a pair of
+ * events on the library stream around every mixer kernel launch;
+ * enable(0) stops. get() synchronizes the stream and returns the summed
+ * milliseconds and launch count recorded for one kernel name (e.g.
+ * "k_gdn_chunk_scan"). */
+int    apus_hip_timing_enable(int on);
+int    apus_hip_timing_get(const char *kernel, double *total_ms, size_t *count);
 
 /* ---- Tier 1: GDN ops (c/gdn.h) -------------------------------------- */
 /* replaces apus_gdn_conv1d      (c/gdn.h:107-108, impl 314-318) */
