@@ -62,14 +62,6 @@ __device__ __forceinline__ float seq_sumsq(const float *x, int n) {
     return ss;
 }
 
-// Pre-conv input of channel c at token index ti of a sequence starting at
-// t0: from the activations, or from the old conv state for ti < t0.
-__device__ __forceinline__ float conv_in(const uint16_t *qkv,
-                                         const uint16_t *cst, size_t cd,
-                                         int ti, int t0, size_t c) {
-    uint16_t v = ti >= t0 ? qkv[(size_t)ti * cd + c] : cst[c * 3 + (ti - t0 + 3)];
-    return bf2f(v);
-}
 
 // ---- state layout conversion -------------------------------------------
 __device__ __forceinline__ size_t packed_index(int i, int j) {
@@ -255,61 +247,116 @@ void k_gdn_decode(
 }
 
 // ---- token-parallel pieces for the chunked prefill ------------------------
-// k_gdn_prep: per (token, K head), 256 threads. Conv + SiLU of the head's
-// q, k channels and its two v-heads' v channels (the first three tokens of
-// a sequence read their window from the old conv state), l2norm of q and
-// k, and (exp(g), beta) of the two v-heads; optionally the raw g.
+constexpr int PT = 16;       // tokens per k_gdn_prep tile
+constexpr int PR = 64;       // (token, v-head) rows per k_gdn_post tile
+constexpr int RS = DK + 1;   // LDS row stride: lane r reads row r, bank-free
+constexpr int PC = 4 * DK;   // pre-conv channels of one K head: q, k, 2 x v
+
+// k_gdn_prep: per (tile of 16 tokens, K head), 256 threads. The tile's
+// pre-conv inputs of the head (q, k and its two v-heads' channels) plus
+// three halo tokens are staged in LDS with 16-byte loads; thread c then
+// owns one q/k channel and one v channel and walks the tokens (a
+// sequence's first three tokens take their window from the old conv
+// state). One lane per (token, q|k) takes the ordered sum of squares for
+// the l2norm (c/gdn.h:402-416); 32 lanes evaluate the (exp(g), beta) gates
+// of the two v-heads, optionally with the raw g.
 __global__ __launch_bounds__(256) void k_gdn_prep(
-    const int32_t *__restrict__ cu, int B, const uint16_t *__restrict__ qkv,
+    const int32_t *__restrict__ cu, int B, int Ttot, const uint16_t *__restrict__ qkv,
     const uint16_t *__restrict__ a, const uint16_t *__restrict__ b,
     const uint16_t *__restrict__ conv_w, const float *__restrict__ A_log,
     const float *__restrict__ dt_bias, const uint16_t *__restrict__ conv_state,
     float *__restrict__ qk, uint16_t *__restrict__ vconv,
     float2 *__restrict__ gate, float *__restrict__ graw, int hk, float qscale) {
-    const int t = blockIdx.x / hk, kh = blockIdx.x % hk;
+    typedef unsigned short u16x8 __attribute__((ext_vector_type(8)));
+    const int tile = blockIdx.x / hk, kh = blockIdx.x % hk;
+    const int tb = tile * PT, nt = min(PT, Ttot - tb);
     const int tid = threadIdx.x;
     const int hv = hk * REP;
     const size_t kd = (size_t)hk * DK, vd = (size_t)hv * DV, cd = 2 * kd + vd;
-    const int s = seq_of(cu, B, t), t0 = cu[s];
-    const uint16_t *cst = conv_state + (size_t)s * cd * 3;
-    __shared__ __attribute__((aligned(16))) float raw[2 * DK];
-    __shared__ float rs[2];
+    __shared__ __attribute__((aligned(16))) uint16_t xin[(PT + 3) * PC];
+    // q rows at 0, k rows at PT*RS: the 32 summing lanes hit distinct banks
+    __shared__ float raw[2 * PT * RS];
+    __shared__ float rs[2][PT];
 
+    // stage rows tb-3 .. tb+nt-1 (those that exist); LDS channel order
+    // [q(128) | k(128) | v(256)]
+    for (int e = tid; e < (PT + 3) * PC / 8; e += 256) {
+        const int r = e / (PC / 8), c8 = (e % (PC / 8)) * 8;
+        const int t = tb - 3 + r;
+        if (t >= 0 && r < nt + 3) {
+            const size_t gc = c8 < DK ? (size_t)kh * DK + c8
+                            : c8 < 2 * DK ? kd + (size_t)kh * DK + (c8 - DK)
+                                          : 2 * kd + (size_t)kh * 2 * DV + (c8 - 2 * DK);
+            *reinterpret_cast<u16x8 *>(xin + r * PC + c8) =
+                *reinterpret_cast<const u16x8 *>(qkv + (size_t)t * cd + gc);
+        }
+    }
     const size_t cqk = tid < DK ? (size_t)kh * DK + tid : kd + (size_t)kh * DK + (tid - DK);
     const int h = kh * REP + tid / DV, j = tid % DV;
     const size_t cv = 2 * kd + (size_t)h * DV + j;
-    float wq[4], wv[4], xq[4], xv[4];
+    float wq[4], wv[4];
     for (int i = 0; i < 4; i++) {
         wq[i] = bf2f(conv_w[cqk * 4 + i]);
         wv[i] = bf2f(conv_w[cv * 4 + i]);
-        xq[i] = conv_in(qkv, cst, cd, t - 3 + i, t0, cqk);
-        xv[i] = conv_in(qkv, cst, cd, t - 3 + i, t0, cv);
-    }
-    raw[tid] = bf2f(conv_tap4(wq, xq[0], xq[1], xq[2], xq[3]));
-    vconv[(size_t)t * vd + (size_t)h * DV + j] = conv_tap4(wv, xv[0], xv[1], xv[2], xv[3]);
-    __syncthreads();
-    if (tid == 0 || tid == DK) {            // q sum (wave 0), k sum (wave 2)
-        rs[tid / DK] = 1.0f / sqrtf(seq_sumsq(raw + tid, DK) + kEps);
-    } else if (tid == 64 || tid == 64 + DV) {   // gates on waves 1 and 3
-        const int hh = kh * REP + tid / DV;
-        const float g = decay_of(a[(size_t)t * hv + hh], A_log[hh], dt_bias[hh]);
-        const float bt = rndf(sigmoid_cr(bf2f(b[(size_t)t * hv + hh])));
-        gate[(size_t)t * hv + hh] = make_float2(exp_cr(g), bt);
-        if (graw) graw[(size_t)t * hv + hh] = g;
     }
     __syncthreads();
-    float *qkt = qk + (size_t)t * 2 * kd;
-    if (tid < DK)
-        qkt[(size_t)kh * DK + tid] = (raw[tid] * rs[0]) * qscale;
-    else
-        qkt[kd + (size_t)kh * DK + (tid - DK)] = raw[tid] * rs[1];
+
+    float *rrow = raw + (tid < DK ? 0 : PT * RS) + (tid & (DK - 1));
+    int s = seq_of(cu, B, tb);
+    for (int i = 0; i < nt; i++) {
+        const int t = tb + i;
+        while (t >= cu[s + 1]) s++;
+        const int t0 = cu[s];
+        const uint16_t *cst = conv_state + (size_t)s * cd * 3;
+        float xq[4], xv[4];
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            const int ti = t - 3 + u;
+            if (ti >= t0) {
+                xq[u] = bf2f(xin[(i + u) * PC + tid]);
+                xv[u] = bf2f(xin[(i + u) * PC + 2 * DK + tid]);
+            } else {
+                xq[u] = bf2f(cst[cqk * 3 + (ti - t0 + 3)]);
+                xv[u] = bf2f(cst[cv * 3 + (ti - t0 + 3)]);
+            }
+        }
+        rrow[i * RS] = bf2f(conv_tap4(wq, xq[0], xq[1], xq[2], xq[3]));
+        vconv[(size_t)t * vd + (size_t)h * DV + j] = conv_tap4(wv, xv[0], xv[1], xv[2], xv[3]);
+    }
+    __syncthreads();
+    if (tid < 2 * PT) {                      // ordered sums, one lane per row
+        const int r = tid & (PT - 1), w = tid / PT;
+        if (r < nt) {
+            const float *row = raw + w * PT * RS + r * RS;
+            float ss = 0.0f;
+            for (int c = 0; c < DK; c++) ss = ss + row[c] * row[c];
+            rs[w][r] = 1.0f / sqrtf(ss + kEps);
+        }
+    } else if (tid >= 64 && tid < 64 + REP * PT) {   // gates of the two v-heads
+        const int r = (tid - 64) & (PT - 1), hh = kh * REP + (tid - 64) / PT;
+        if (r < nt) {
+            const size_t t = (size_t)(tb + r);
+            const float g = decay_of(a[t * hv + hh], A_log[hh], dt_bias[hh]);
+            const float bt = rndf(sigmoid_cr(bf2f(b[t * hv + hh])));
+            gate[t * hv + hh] = make_float2(exp_cr(g), bt);
+            if (graw) graw[t * hv + hh] = g;
+        }
+    }
+    __syncthreads();
+    const int w = tid < DK ? 0 : 1;
+    for (int i = 0; i < nt; i++) {
+        const float x = rrow[i * RS] * rs[w][i];
+        qk[(size_t)(tb + i) * 2 * kd + cqk] = w == 0 ? x * qscale : x;
+    }
 }
 
-// k_gdn_post: blocks [0, Ttot*hv) apply the gated RMSNorm to one (token,
-// v-head) of ob (c/gdn.h:639-661); the remaining blocks write each
-// sequence's new conv state (the last three pre-conv inputs of
+// k_gdn_post: blocks [0, ceil(Ttot*hv/64)) apply the gated RMSNorm
+// (c/gdn.h:639-661) to 64 consecutive (token, v-head) rows of ob: 16-byte
+// loads into LDS, one lane per row for the ordered sum of squares, then
+// elementwise with 16-byte z loads and y stores. The remaining blocks
+// write each sequence's new conv state (the last three pre-conv inputs of
 // [old state | tokens]) after every reader of the old one has finished.
-__global__ __launch_bounds__(128) void k_gdn_post(
+__global__ __launch_bounds__(256) void k_gdn_post(
     const int32_t *__restrict__ cu, int B, int Ttot,
     const uint16_t *__restrict__ ob, const uint16_t *__restrict__ z,
     const uint16_t *__restrict__ onorm_w, uint16_t *__restrict__ y,
@@ -318,26 +365,52 @@ __global__ __launch_bounds__(128) void k_gdn_post(
     const int hv = hk * REP;
     const size_t kd = (size_t)hk * DK, vd = (size_t)hv * DV, cd = 2 * kd + vd;
     const int tid = threadIdx.x;
-    const size_t nnorm = (size_t)Ttot * hv;
+    const size_t nrows = (size_t)Ttot * hv;
+    const size_t nnorm = (nrows + PR - 1) / PR;
+    typedef unsigned short u16x8 __attribute__((ext_vector_type(8)));
     if ((size_t)blockIdx.x < nnorm) {
-        const size_t t = blockIdx.x / hv, h = blockIdx.x % hv;
-        const size_t off = t * vd + h * DV;
-        __shared__ __attribute__((aligned(16))) float o_s[DV];
-        __shared__ float rs_s;
-        const float o = bf2f(ob[off + tid]);
-        o_s[tid] = o;
+        const size_t r0 = (size_t)blockIdx.x * PR;
+        const int nr = (int)min((size_t)PR, nrows - r0);
+        __shared__ float os[PR * RS];
+        __shared__ float rs[PR];
+        for (int e = tid; e < PR * DV / 8; e += 256) {
+            const int row = e / (DV / 8), c8 = (e % (DV / 8)) * 8;
+            if (row < nr) {
+                const u16x8 v = *reinterpret_cast<const u16x8 *>(ob + (r0 + row) * DV + c8);
+#pragma unroll
+                for (int i = 0; i < 8; i++) os[row * RS + c8 + i] = bf2f(v[i]);
+            }
+        }
         __syncthreads();
-        if (tid == 0) rs_s = 1.0f / sqrtf(seq_sumsq(o_s, DV) / (float)DV + kEps);
+        if (tid < nr) {
+            const float *row = os + tid * RS;
+            float ss = 0.0f;
+            for (int c = 0; c < DV; c++) ss = ss + row[c] * row[c];
+            rs[tid] = 1.0f / sqrtf(ss / (float)DV + kEps);
+        }
         __syncthreads();
-        const float x1 = rndf(o * rs_s);
-        const float x2 = rndf(x1 * bf2f(onorm_w[tid]));
-        const float zf = bf2f(z[off + tid]);
-        y[off + tid] = f2bf(x2 * (zf * sigmoid_cr(zf)));
+        for (int e = tid; e < PR * DV / 8; e += 256) {
+            const int row = e / (DV / 8), c8 = (e % (DV / 8)) * 8;
+            if (row < nr) {
+                const size_t off = (r0 + row) * DV + c8;
+                const u16x8 zv = *reinterpret_cast<const u16x8 *>(z + off);
+                const u16x8 wv = *reinterpret_cast<const u16x8 *>(onorm_w + c8);
+                u16x8 out;
+#pragma unroll
+                for (int i = 0; i < 8; i++) {
+                    const float x1 = rndf(os[row * RS + c8 + i] * rs[row]);
+                    const float x2 = rndf(x1 * bf2f(wv[i]));
+                    const float zf = bf2f(zv[i]);
+                    out[i] = f2bf(x2 * (zf * sigmoid_cr(zf)));
+                }
+                *reinterpret_cast<u16x8 *>(y + off) = out;
+            }
+        }
         return;
     }
     const size_t bb = blockIdx.x - nnorm;
-    const size_t per = cd / 128;
-    const size_t s = bb / per, c = (bb % per) * 128 + tid;
+    const size_t per = cd / 256;
+    const size_t s = bb / per, c = (bb % per) * 256 + tid;
     const int t0 = cu[s], n = cu[s + 1] - t0;
     if (n == 0) return;
     uint16_t *st = conv_state + s * cd * 3 + c * 3;
@@ -386,8 +459,8 @@ int gdn_prep(const ApusHipGdnLayer *L, size_t B, const int32_t *dcu,
         return kErrHip;
     const float qscale = (float)pow((double)L->dk, -0.5);
     APUS_TIMED("k_gdn_prep",
-               k_gdn_prep<<<(unsigned)(Ttot * L->hk), 256, 0, stream()>>>(
-        dcu, (int)B, qkv, a, b, L->conv_w, L->A_log, L->dt_bias, conv_state,
+               k_gdn_prep<<<(unsigned)(cdiv(Ttot, PT) * L->hk), 256, 0, stream()>>>(
+        dcu, (int)B, (int)Ttot, qkv, a, b, L->conv_w, L->A_log, L->dt_bias, conv_state,
         w->qk, w->vconv, w->gate, w->graw, (int)L->hk, qscale));
     return launch_check("k_gdn_prep");
 }
@@ -396,9 +469,9 @@ int gdn_post(const ApusHipGdnLayer *L, size_t B, const int32_t *dcu,
              size_t Ttot, const GdnScratch *w, const uint16_t *z,
              const uint16_t *qkv, uint16_t *conv_state, uint16_t *y) {
     const size_t cd = 2 * L->hk * DK + L->hv * DV;
-    const size_t nblk = Ttot * L->hv + B * (cd / 128);
+    const size_t nblk = cdiv(Ttot * L->hv, PR) + B * (cd / 256);
     APUS_TIMED("k_gdn_post",
-               k_gdn_post<<<(unsigned)nblk, 128, 0, stream()>>>(
+               k_gdn_post<<<(unsigned)nblk, 256, 0, stream()>>>(
         dcu, (int)B, (int)Ttot, w->ob, z, L->onorm_w, y, qkv, conv_state,
         (int)L->hk));
     return launch_check("k_gdn_post");

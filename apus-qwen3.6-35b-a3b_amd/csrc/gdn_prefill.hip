@@ -92,6 +92,12 @@ __device__ __forceinline__ float4 lds4(const float *p) {
     return *reinterpret_cast<const float4 *>(p);
 }
 
+// v if ok else 0, by value (a ternary between a register-array element
+// and a temporary can force the array to scratch memory)
+__device__ __forceinline__ float4 keep4(bool ok, float4 v) {
+    return make_float4(ok ? v.x : 0.f, ok ? v.y : 0.f, ok ? v.z : 0.f, ok ? v.w : 0.f);
+}
+
 __device__ __forceinline__ float4 ld4(const float *p) {
     return *reinterpret_cast<const float4 *>(p);
 }
@@ -117,10 +123,30 @@ __device__ __forceinline__ ChunkPos chunk_pos(const int32_t *cu, const int32_t *
     return p;
 }
 
-// Per (chunk, v-head) buffers written by k_gdn_chunk_wy:
-//   U [C][DV], W [C][DK], A [C][C] (rows t, lower triangle incl. diagonal
-//   valid), F [2][C]: F[0][t] = G_t, F[1][s] = exp(gamma_C - gamma_s).
-__global__ __launch_bounds__(256) void k_gdn_chunk_wy(
+// Per (chunk, v-head) buffers written by k_gdn_chunk_wy, stored in the
+// order k_gdn_chunk_scan's MFMA lanes consume them, so that every scan load
+// instruction reads 1 KiB of contiguous memory. "lane(r, q)" is r + 16*q,
+// the lane that holds row r and reduction quad q of a 16x16x4 operand.
+//   W  [4 row blocks][8 k-groups of 16][64 lanes][4]: element (t, c) at
+//      lane(t%16, (c%16)/4) of block (t/16, c/16), slot c%4;
+//   A  [4][4 k-groups][64][4]: element (t, s) likewise (s <= t valid);
+//   U  [8 column slices][4 row blocks][64][4]: element (t, j) at
+//      lane(j%16, (t%16)/4) of (j/16, t/16), slot t%4 -- the accumulator
+//      layout of the scan's D tile;
+//   F  [2][C]: F[0][t] = G_t, F[1][s] = exp(gamma_C - gamma_s).
+__device__ __forceinline__ size_t wy_w_index(int t, int c) {
+    return ((size_t)((t >> 4) * 8 + (c >> 4)) * 64 + ((c & 15) >> 2) * 16 + (t & 15)) * 4 + (c & 3);
+}
+__device__ __forceinline__ size_t wy_a_index(int t, int s) {
+    return ((size_t)((t >> 4) * 4 + (s >> 4)) * 64 + ((s & 15) >> 2) * 16 + (t & 15)) * 4 + (s & 3);
+}
+__device__ __forceinline__ size_t wy_u_index(int t, int j) {
+    return ((size_t)((j >> 4) * 4 + (t >> 4)) * 64 + ((t & 15) >> 2) * 16 + (j & 15)) * 4 + (t & 3);
+}
+
+// k_gdn_chunk_wy: one workgroup per (chunk, v-head), two per CU (Q's LDS
+// copy is reused for L once Q K^T is done).
+__global__ __launch_bounds__(256, 2) void k_gdn_chunk_wy(
     ChunkSeqs sq, const int32_t *__restrict__ dmeta, const float *__restrict__ qk,
     const uint16_t *__restrict__ vconv, const float2 *__restrict__ gate,
     const float *__restrict__ graw, float *__restrict__ Ub, float *__restrict__ Wb,
@@ -135,9 +161,8 @@ __global__ __launch_bounds__(256) void k_gdn_chunk_wy(
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
 
     __shared__ __attribute__((aligned(16))) float Ks[C * KP];
-    __shared__ __attribute__((aligned(16))) float Qs[C * KP];
-    __shared__ __attribute__((aligned(16))) float Ls[C * CP];
-    __shared__ float gam[C], bet[C], Gs[C];
+    __shared__ __attribute__((aligned(16))) float QL[C * KP];   // Q, then L [C][CP]
+    __shared__ float graw_s[C], gam[C], bet[C], Gs[C];
 
     // rows t >= nt are padding: q = k = 0, g = 0, beta = 0
     for (int e = tid; e < C * DK / 4; e += 256) {
@@ -148,21 +173,19 @@ __global__ __launch_bounds__(256) void k_gdn_chunk_wy(
             q = ld4(row);
             k = ld4(row + kd);
         }
-        *reinterpret_cast<float4 *>(Qs + t * KP + q4) = q;
+        *reinterpret_cast<float4 *>(QL + t * KP + q4) = q;
         *reinterpret_cast<float4 *>(Ks + t * KP + q4) = k;
     }
     if (tid < C) {
         const bool ok = tid < P.nt;
-        gam[tid] = ok ? graw[(size_t)(P.t0 + tid) * hv + h] : 0.0f;
+        graw_s[tid] = ok ? graw[(size_t)(P.t0 + tid) * hv + h] : 0.0f;
         bet[tid] = ok ? gate[(size_t)(P.t0 + tid) * hv + h].y : 0.0f;
     }
     __syncthreads();
-    if (tid == 0) {                    // cumulative log decay, in token order
+    if (tid < C) {                     // gamma_t = g_0 + .. + g_t, in token order
         float acc = 0.0f;
-        for (int t = 0; t < C; t++) {
-            acc = acc + gam[t];
-            gam[t] = acc;
-        }
+        for (int t = 0; t <= tid; t++) acc = acc + graw_s[t];
+        gam[tid] = acc;
     }
     __syncthreads();
     float *F = Fb + (size_t)blockIdx.x * 2 * C;
@@ -172,34 +195,55 @@ __global__ __launch_bounds__(256) void k_gdn_chunk_wy(
         F[C + tid] = exp_fast(gam[C - 1] - gam[tid]);
     }
 
-    // K K^T (row block w) and Q K^T (row block 3-w): lower-triangle tiles
     const int r16 = lane & 15, kq = (lane >> 4) * 4;
+    // Q K^T, row block 3-w: A = decayed lower triangle, to global
     float *A = Ab + (size_t)blockIdx.x * C * C;
-    for (int pass = 0; pass < 2; pass++) {
-        const int rb = pass == 0 ? wave : 3 - wave;
-        const float *X = pass == 0 ? Ks : Qs;
+    {
+        const int rb = 3 - wave;
         for (int cb = 0; cb <= rb; cb++) {
             f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int k0 = 0; k0 < DK; k0 += 16)
-                acc = mfma_k16(lds4(X + (rb * 16 + r16) * KP + k0 + kq),
+                acc = mfma_k16(lds4(QL + (rb * 16 + r16) * KP + k0 + kq),
                                lds4(Ks + (cb * 16 + r16) * KP + k0 + kq), acc);
             const int s = cb * 16 + r16;
 #pragma unroll
             for (int i = 0; i < 4; i++) {
                 const int t = rb * 16 + kq + i;
-                if (pass == 0) {
-                    Ls[t * CP + s] = s < t ? bet[t] * (exp_fast(gam[t] - gam[s]) * acc[i]) : 0.0f;
-                } else {
-                    A[t * C + s] = s <= t ? exp_fast(gam[t] - gam[s]) * acc[i] : 0.0f;
-                }
+                A[wy_a_index(t, s)] = s <= t ? exp_fast(gam[t] - gam[s]) * acc[i] : 0.0f;
+            }
+        }
+    }
+    // K K^T, row block w, kept in registers until Q's LDS copy is free
+    f32x4 g[4];
+#pragma unroll
+    for (int cb = 0; cb < 4; cb++) {
+        g[cb] = f32x4{0.f, 0.f, 0.f, 0.f};
+        if (cb <= wave) {
+#pragma unroll
+            for (int k0 = 0; k0 < DK; k0 += 16)
+                g[cb] = mfma_k16(lds4(Ks + (wave * 16 + r16) * KP + k0 + kq),
+                                 lds4(Ks + (cb * 16 + r16) * KP + k0 + kq), g[cb]);
+        }
+    }
+    __syncthreads();                   // every reader of Q is done
+    float *Ls = QL;
+#pragma unroll
+    for (int cb = 0; cb < 4; cb++) {
+        if (cb <= wave) {
+            const int s = cb * 16 + r16;
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int t = wave * 16 + kq + i;
+                Ls[t * CP + s] = s < t ? bet[t] * (exp_fast(gam[t] - gam[s]) * g[cb][i]) : 0.0f;
             }
         }
     }
     __syncthreads();
 
-    // forward substitution: X_t = R_t - sum_{s<t} L[t][s] X_s for the 256
-    // right-hand-side columns [b V | b G K], one per thread
+    // forward substitution X_t = R_t - sum_{s<t} L[t][s] X_s for the 256
+    // right-hand-side columns [b V | b G K], one per thread; four partial
+    // sums (s mod 4) shorten the dependent chain
     float x[C];
     if (tid < DV) {
         const uint16_t *vp = vconv + (size_t)P.t0 * vd + (size_t)h * DV + tid;
@@ -213,27 +257,78 @@ __global__ __launch_bounds__(256) void k_gdn_chunk_wy(
     }
 #pragma unroll
     for (int t = 1; t < C; t++) {
-        float acc = x[t];
+        float p0 = 0.f, p1 = 0.f, p2 = 0.f, p3 = 0.f;
 #pragma unroll
         for (int s0 = 0; s0 < t; s0 += 4) {
             const float4 l4 = lds4(Ls + t * CP + s0);
-            acc = fmaf(-l4.x, x[s0], acc);
-            if (s0 + 1 < t) acc = fmaf(-l4.y, x[s0 + 1], acc);
-            if (s0 + 2 < t) acc = fmaf(-l4.z, x[s0 + 2], acc);
-            if (s0 + 3 < t) acc = fmaf(-l4.w, x[s0 + 3], acc);
+            p0 = fmaf(l4.x, x[s0], p0);
+            if (s0 + 1 < t) p1 = fmaf(l4.y, x[s0 + 1], p1);
+            if (s0 + 2 < t) p2 = fmaf(l4.z, x[s0 + 2], p2);
+            if (s0 + 3 < t) p3 = fmaf(l4.w, x[s0 + 3], p3);
         }
-        x[t] = acc;
+        x[t] = x[t] - ((p0 + p1) + (p2 + p3));
     }
-    float *out = (tid < DV ? Ub : Wb) + (size_t)blockIdx.x * C * DV + (tid & (DV - 1));
+    const size_t ub = (size_t)blockIdx.x * C * DV;
+    if (tid < DV) {
 #pragma unroll
-    for (int t = 0; t < C; t++) out[t * DV] = x[t];
+        for (int t = 0; t < C; t++) Ub[ub + wy_u_index(t, tid)] = x[t];
+    } else {
+#pragma unroll
+        for (int t = 0; t < C; t++) Wb[ub + wy_w_index(t, tid - DV)] = x[t];
+    }
 }
 
 // Chunk-to-chunk scan of one 16-column slice of one head's state.
 // Block index = cb * (B*hv) + (s*hv + h): the 8 slices of a head share
 // their U/W/A/Q/K reads, and with B*hv a multiple of 8 they land on the
 // same XCD (blocks are dealt round-robin over the 8 XCDs) and so share
-// its L2.
+// its L2. The next chunk's operands are loaded into registers as soon as
+// the current chunk's copy has been consumed, so their latency overlaps
+// this chunk's work; W, A and U arrive in MFMA lane order (1 KiB per
+// load instruction), Q and K as whole rows into LDS.
+struct ScanOps {
+    float4 k[C * DK / 4 / 256];     // K rows
+    float4 q[C * DK / 4 / 256];     // Q rows
+    float4 w[DK / 16];              // W operand, row block w
+    float4 a[C / 16];               // A operand, row block w (causal part)
+    float4 u;                       // U in the D-tile layout
+    float f;                        // decay factors (threads < 2C)
+};
+
+// Q and K rows of one chunk (rows past its tokens are clamped to a valid
+// row; the consumer zeroes them -- a select right after the load would
+// wait for it, and the in-order load counter would then drain every
+// prefetch issued before it).
+__device__ __forceinline__ void scan_load_qk(ScanOps &nx, const float *__restrict__ qk,
+                                             const float *__restrict__ Fb, size_t u, int t0,
+                                             int nt, size_t kd, int kh, int tid) {
+#pragma unroll
+    for (int it = 0; it < C * DK / 4 / 256; it++) {
+        const int e = it * 256 + tid, t = e / (DK / 4), q4 = (e % (DK / 4)) * 4;
+        const float *row = qk + (size_t)(t0 + min(t, nt - 1)) * 2 * kd + (size_t)kh * DK + q4;
+        nx.q[it] = ld4(row);
+        nx.k[it] = ld4(row + kd);
+    }
+    nx.f = Fb[u * 2 * C + (tid & (2 * C - 1))];
+}
+
+__device__ __forceinline__ void scan_load_wu(ScanOps &nx, const float *__restrict__ Wb,
+                                             const float *__restrict__ Ub, size_t u, int wave,
+                                             int lane, int cb) {
+    const float *W = Wb + u * C * DK + (size_t)wave * 8 * 256 + lane * 4;
+#pragma unroll
+    for (int k = 0; k < DK / 16; k++) nx.w[k] = ld4(W + k * 256);
+    nx.u = ld4(Ub + u * C * DV + ((size_t)(cb * 4 + wave) * 64 + lane) * 4);
+}
+
+__device__ __forceinline__ void scan_load_a(ScanOps &nx, const float *__restrict__ Ab, size_t u,
+                                            int wave, int lane) {
+    const float *Ar = Ab + u * C * C + (size_t)wave * 4 * 256 + lane * 4;
+#pragma unroll
+    for (int k = 0; k < C / 16; k++)
+        if (k <= wave) nx.a[k] = ld4(Ar + k * 256);
+}
+
 __global__ __launch_bounds__(256) void k_gdn_chunk_scan(
     ChunkSeqs sq, const int32_t *__restrict__ dmeta, const float *__restrict__ qk,
     const float *__restrict__ Ub, const float *__restrict__ Wb,
@@ -249,8 +344,10 @@ __global__ __launch_bounds__(256) void k_gdn_chunk_scan(
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int r16 = lane & 15, kq = (lane >> 4) * 4;
+    const int rw = wave * 16;
 
-    __shared__ __attribute__((aligned(16))) float KT[DK * CP];     // K^T of the chunk
+    __shared__ __attribute__((aligned(16))) float Ks[C * KP];      // K rows of the chunk
+    __shared__ __attribute__((aligned(16))) float Qs[C * KP];      // Q rows
     __shared__ __attribute__((aligned(16))) float S0T[CB * KP];    // S slice, [col][row]
     __shared__ __attribute__((aligned(16))) float DT[CB * CP];     // D slice, [col][t]
     __shared__ __attribute__((aligned(16))) float DpT[CB * CP];    // decayed D
@@ -265,83 +362,88 @@ __global__ __launch_bounds__(256) void k_gdn_chunk_scan(
     }
 
     const int c0 = coff[s], c1 = coff[s + 1];
+    const int tS = cu[s], tE = cu[s + 1];
+    ScanOps nx;
+    if (c0 < c1) {
+        const size_t u = (size_t)c0 * hv + h;
+        scan_load_qk(nx, qk, Fb, u, tS, min(C, tE - tS), kd, kh, tid);
+        scan_load_wu(nx, Wb, Ub, u, wave, lane, cb);
+        scan_load_a(nx, Ab, u, wave, lane);
+    }
+
     for (int ci = c0; ci < c1; ci++) {
-        const int t0 = cu[s] + (ci - c0) * C, nt = min(C, cu[s + 1] - t0);
-        const size_t u = (size_t)ci * hv + h;
-        __syncthreads();               // previous step done with KT/Fs/S0T
-        for (int e = tid; e < C * DK / 4; e += 256) {
-            const int t = e % C, q4 = (e / C) * 4;
-            float4 k = make_float4(0.f, 0.f, 0.f, 0.f);
-            if (t < nt) k = ld4(qk + (size_t)(t0 + t) * 2 * kd + kd + (size_t)kh * DK + q4);
-            KT[(q4 + 0) * CP + t] = k.x;
-            KT[(q4 + 1) * CP + t] = k.y;
-            KT[(q4 + 2) * CP + t] = k.z;
-            KT[(q4 + 3) * CP + t] = k.w;
+        const int t0 = tS + (ci - c0) * C, nt = min(C, tE - t0);
+        const bool more = ci + 1 < c1;
+        const int t0n = t0 + C, ntn = min(C, tE - t0n);
+        const size_t un = (size_t)(ci + 1) * hv + h;
+        __syncthreads();               // previous step done with Ks/Qs/Fs/S0T
+#pragma unroll
+        for (int it = 0; it < C * DK / 4 / 256; it++) {
+            const int e = it * 256 + tid, t = e / (DK / 4), q4 = (e % (DK / 4)) * 4;
+            *reinterpret_cast<float4 *>(Ks + t * KP + q4) = keep4(t < nt, nx.k[it]);
+            *reinterpret_cast<float4 *>(Qs + t * KP + q4) = keep4(t < nt, nx.q[it]);
         }
-        if (tid < 2 * C) Fs[tid] = Fb[u * 2 * C + tid];
+        if (tid < 2 * C) Fs[tid] = nx.f;
+        if (more) scan_load_qk(nx, qk, Fb, un, t0n, ntn, kd, kh, tid);
         __syncthreads();
 
         // D rows [16w, 16w+16) of this slice: U - W S0
-        const int rw = wave * 16;
-        const float *W = Wb + (u * C + rw + r16) * DK;
         f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int k0 = 0; k0 < DK; k0 += 16)
-            acc = mfma_k16(ld4(W + k0 + kq), lds4(S0T + r16 * KP + k0 + kq), acc);
-        const float *U = Ub + u * C * DV + cb * CB + r16;
+        for (int k = 0; k < DK / 16; k++)
+            acc = mfma_k16(nx.w[k], lds4(S0T + r16 * KP + k * 16 + kq), acc);
+        const float uu[4] = {nx.u.x, nx.u.y, nx.u.z, nx.u.w};
 #pragma unroll
         for (int i = 0; i < 4; i++) {
             const int t = rw + kq + i;
-            const float d = U[(size_t)t * DV] - acc[i];
+            const float d = uu[i] - acc[i];
             DT[r16 * CP + t] = d;
             DpT[r16 * CP + t] = Fs[C + t] * d;
         }
+        if (more) scan_load_wu(nx, Wb, Ub, un, wave, lane, cb);
         // O rows: G_t (Q S0) ...
-        const int tq = rw + r16;
-        const float *Q = qk + (size_t)(t0 + tq) * 2 * kd + (size_t)kh * DK;
-        // (MFMA is a whole-wave operation: padding rows get zero operands,
-        // never a branch around the instruction)
-        float4 qa[DK / 16];
-#pragma unroll
-        for (int k = 0; k < DK / 16; k++)
-            qa[k] = tq < nt ? ld4(Q + k * 16 + kq) : make_float4(0.f, 0.f, 0.f, 0.f);
         f32x4 o = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int k = 0; k < DK / 16; k++)
-            o = mfma_k16(qa[k], lds4(S0T + r16 * KP + k * 16 + kq), o);
+            o = mfma_k16(lds4(Qs + (rw + r16) * KP + k * 16 + kq),
+                         lds4(S0T + r16 * KP + k * 16 + kq), o);
 #pragma unroll
         for (int i = 0; i < 4; i++) o[i] = Fs[rw + kq + i] * o[i];
         __syncthreads();               // D complete
 
         // ... + A D over the causal part s < 16(w+1)
-        const float *Ar = Ab + (u * C + rw + r16) * C;
-        for (int k0 = 0; k0 < rw + 16; k0 += 16)
-            o = mfma_k16(ld4(Ar + k0 + kq), lds4(DT + r16 * CP + k0 + kq), o);
+#pragma unroll
+        for (int k = 0; k < C / 16; k++)
+            if (k <= wave) o = mfma_k16(nx.a[k], lds4(DT + r16 * CP + k * 16 + kq), o);
+        if (more) scan_load_a(nx, Ab, un, wave, lane);
 #pragma unroll
         for (int i = 0; i < 4; i++) {
             const int t = rw + kq + i;
             if (t < nt) ob[(size_t)(t0 + t) * vd + (size_t)h * DV + cb * CB + r16] = f2bf(o[i]);
         }
 
-        // S1 rows [32w, 32w+32): G_C S0 + K^T Dp
+        // S1^T columns [32w, 32w+32): G_C S0^T + Dp^T K (rows n of the
+        // slice, columns i of the state; K read in place, row-major)
         const float gc = Fs[C - 1];
         f32x4 sn[2];
 #pragma unroll
         for (int r = 0; r < 2; r++) {
             const int i0 = wave * 32 + r * 16;
 #pragma unroll
-            for (int i = 0; i < 4; i++) sn[r][i] = gc * S0T[r16 * KP + i0 + kq + i];
+            for (int i = 0; i < 4; i++) sn[r][i] = gc * S0T[(kq + i) * KP + i0 + r16];
 #pragma unroll
-            for (int k0 = 0; k0 < C; k0 += 16)
-                sn[r] = mfma_k16(lds4(KT + (i0 + r16) * CP + k0 + kq),
-                                 lds4(DpT + r16 * CP + k0 + kq), sn[r]);
+            for (int k0 = 0; k0 < C; k0 += 16) {
+                const float *kc = Ks + (k0 + kq) * KP + i0 + r16;
+                sn[r] = mfma_k16(lds4(DpT + r16 * CP + k0 + kq),
+                                 make_float4(kc[0], kc[KP], kc[2 * KP], kc[3 * KP]), sn[r]);
+            }
         }
         __syncthreads();               // every reader of S0T is done
 #pragma unroll
         for (int r = 0; r < 2; r++) {
             const int i0 = wave * 32 + r * 16;
 #pragma unroll
-            for (int i = 0; i < 4; i++) S0T[r16 * KP + i0 + kq + i] = sn[r][i];
+            for (int i = 0; i < 4; i++) S0T[(kq + i) * KP + i0 + r16] = sn[r][i];
         }
     }
     __syncthreads();
