@@ -35,7 +35,7 @@ EXPORTS = [
     "apus_hip_attn_gqa_decode", "apus_hip_attn_gqa_mt",
     "apus_hip_attn_gqa_decode_mt", "apus_hip_attn_outgate",
     "apus_hip_gdn_decode", "apus_hip_gdn_prefill", "apus_hip_gdn_state_pack", "apus_hip_gdn_state_unpack",
-    "apus_hip_attn_cache_pack", "apus_hip_attn_cache_unpack", "apus_hip_attn_decode",
+    "apus_hip_attn_cache_pack", "apus_hip_attn_cache_unpack", "apus_hip_attn_decode", "apus_hip_attn_prefill",
 ]
 
 
@@ -262,11 +262,17 @@ def _cu_arr(cu):
 
 def gdn_layer(dims, w):
     """Build an ApusHipGdnLayer from dims (hk, hv, dk, dv) and a dict of
-    device tensors conv_w, A_log, dt_bias, onorm_w. Keep `w` alive."""
+    device tensors conv_w, A_log, dt_bias, onorm_w. The struct carries raw
+    device pointers, so it keeps a reference to the tensors: they stay
+    allocated as long as the layer object lives."""
     hk, hv, dk, dv = dims
-    return GdnLayer(hk, hv, dk, dv, w["conv_w"].data_ptr(),
-                    w["A_log"].data_ptr(), w["dt_bias"].data_ptr(),
-                    w["onorm_w"].data_ptr())
+    for k in ("conv_w", "A_log", "dt_bias", "onorm_w"):
+        assert w[k].is_cuda and w[k].is_contiguous(), k
+    layer = GdnLayer(hk, hv, dk, dv, w["conv_w"].data_ptr(),
+                     w["A_log"].data_ptr(), w["dt_bias"].data_ptr(),
+                     w["onorm_w"].data_ptr())
+    layer._tensors = dict(w)
+    return layer
 
 
 def gdn_decode(layer, cu, qkv, z, a, b, conv_state, S, y):
@@ -295,9 +301,13 @@ def gdn_state_unpack(S_dev, S_ref):
 
 def attn_layer(dims, w):
     """ApusHipAttnLayer from dims (nh, nkv, d, rot, theta) and device tensors
-    qn_w, kn_w. Keep `w` alive while the layer is used."""
+    qn_w, kn_w; the layer keeps a reference to them (raw device pointers)."""
     nh, nkv, d, rot, theta = dims
-    return AttnLayer(nh, nkv, d, rot, theta, w["qn_w"].data_ptr(), w["kn_w"].data_ptr())
+    for k in ("qn_w", "kn_w"):
+        assert w[k].is_cuda and w[k].is_contiguous(), k
+    layer = AttnLayer(nh, nkv, d, rot, theta, w["qn_w"].data_ptr(), w["kn_w"].data_ptr())
+    layer._tensors = dict(w)
+    return layer
 
 
 def attn_cache_pack(kc_ref, vc_ref, ntok, nkv, d, kcache, vcache, max_seq):
@@ -317,3 +327,13 @@ def attn_decode(layer, cu, pos0, qg, k, v, kcache, vcache, max_seq, y):
     _chk(load().apus_hip_attn_decode(C.byref(layer), _sz(B), cup, pos0.ctypes.data_as(_i32p),
                                      _dp(qg), _dp(k), _dp(v), _dp(kcache), _dp(vcache),
                                      _sz(max_seq), _dp(y)))
+
+
+def attn_prefill(layer, cu, pos0, qg, k, v, kcache, vcache, max_seq, y):
+    """Causal prefill of any number of new tokens per sequence; arguments
+    as attn_decode."""
+    cu, cup, B = _cu_arr(cu)
+    pos0 = np.ascontiguousarray(np.asarray(pos0, dtype=np.int32))
+    _chk(load().apus_hip_attn_prefill(C.byref(layer), _sz(B), cup, pos0.ctypes.data_as(_i32p),
+                                      _dp(qg), _dp(k), _dp(v), _dp(kcache), _dp(vcache),
+                                      _sz(max_seq), _dp(y)))

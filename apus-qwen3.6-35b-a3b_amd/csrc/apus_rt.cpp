@@ -50,7 +50,6 @@ struct TimedKernel {
 bool g_timing = false;
 std::vector<TimedKernel> g_timed;
 std::vector<hipEvent_t> g_event_pool;
-int g_open = -1;
 
 hipEvent_t take_event() {
     if (!g_event_pool.empty()) {

@@ -13,6 +13,7 @@ reported under "configs" with their own roofline fractions:
   c0b  config 0'  GDN decode, batch 64 (HBM-bound decode)
   c1   config 1   GDN prefill T=4096 (headline)
   c2   config 2   gated-GQA decode, 64 sequences x 32K-token bf16 KV cache
+  c3   config 3   gated-GQA causal prefill, T=8192 (cache fill + attention)
 Input buffer sets rotate so the 256 MB Infinity Cache cannot serve
 repeated reads. The CPU baseline is the reference's own scalar anchors
 (oracle/_ref, built from the reference sources) when present, else the
@@ -290,6 +291,50 @@ def bench_attn_decode(torch, B, ctx, steps, warmup, seed):
                 layer_hbm_frac=bytes_ / st / HBM_PEAK, roofline=kernel_roofline(kt, table, wl))
 
 
+def attn_prefill_flops(T):
+    """Causal GQA prefill, algorithmic: q.k and P.V over the keys each row
+    sees (16 heads x 256 dims x 2 flop x 2 matmuls x T(T+1)/2 rows-keys)."""
+    return NH * 4 * AD * (T * (T + 1) // 2)
+
+
+def bench_attn_prefill(torch, T, steps, warmup, seed):
+    """Config 3: one sequence, T new tokens from position 0: norm, RoPE,
+    cache fill and causal attention with the output gate."""
+    import apus_hip
+    dev = torch.device("cuda")
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed)
+
+    def bf(shape, std=1.0):
+        return (torch.randn(shape, generator=g, device=dev) * std).to(torch.bfloat16).view(torch.int16)
+
+    w = dict(qn_w=bf((AD,), 0.1), kn_w=bf((AD,), 0.1))
+    layer = apus_hip.attn_layer(ATTN, w)
+    nsets = 2
+    sets = [dict(qg=bf((T, NH, 2 * AD)), k=bf((T, NKV, AD)), v=bf((T, NKV, AD)),
+                 kc=torch.empty((1, NKV, T, AD), dtype=torch.int16, device=dev),
+                 vc=torch.empty((1, NKV, T // 32, AD, 32), dtype=torch.int16, device=dev),
+                 y=torch.empty((T, NH * AD), dtype=torch.int16, device=dev)) for _ in range(nsets)]
+    cu = np.array([0, T], np.int32)
+    pos0 = np.zeros(1, np.int32)
+
+    def step(i):
+        s = sets[i]
+        apus_hip.attn_prefill(layer, cu, pos0, s["qg"], s["k"], s["v"], s["kc"], s["vc"], T, s["y"])
+
+    flops = attn_prefill_flops(T)
+    bytes_ = T * (NH * 2 * AD * 2 + 2 * NKV * AD * 2 + 2 * NKV * AD * 2 + NH * AD * 2)
+    table = {"k_attn_fa": ("mfma", flops, BF16_PEAK),
+             "k_attn_prep": ("hbm", T * (NH * 2 * AD * 2 + NKV * AD * 2 * 4 + NH * AD * 2), HBM_PEAK)}
+    total, per, kt = time_steps(torch, step, steps, warmup, nsets, table)
+    st = float(np.mean(per))
+    wl = f"attn_prefill_t{T}"
+    return dict(workload=wl, tokens_per_step=T, ms_per_step=total / steps * 1e3,
+                step_event_ms=st * 1e3, kernels_ms=kt, alg_bytes=bytes_, alg_flops=flops,
+                tok_s=T * steps / total, layer_tflops=flops / st / 1e12,
+                layer_mfma_frac=flops / st / BF16_PEAK, roofline=kernel_roofline(kt, table, wl))
+
+
 def bench_copy(torch, steps, warmup):
     """Calibration workload for HBM counters: a plain 1 GiB device copy
     (reads 1 GiB, writes 1 GiB); rocprofv3 FETCH_SIZE / WRITE_SIZE of its
@@ -375,7 +420,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--only", default="c0,c0b,c1,c2")
+    ap.add_argument("--only", default="c0,c0b,c1,c2,c3")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-tokens", type=int, default=8192)
     ap.add_argument("--cpu-threads", type=int, default=CPU_THREADS)
@@ -409,6 +454,9 @@ def main():
     if "c2" in want:
         res["c2"] = bench_attn_decode(torch, 64, 32768, args.steps, args.warmup, 13)
         log("c2", res["c2"])
+    if "c3" in want:
+        res["c3"] = bench_attn_prefill(torch, 8192, args.steps, args.warmup, 14)
+        log("c3", res["c3"])
     if "copy" in want:
         res["copy"] = bench_copy(torch, args.steps, args.warmup)
         log("copy", res["copy"])

@@ -209,6 +209,20 @@ int apus_hip_attn_cache_unpack(const uint16_t *kcache, const uint16_t *vcache,
                                size_t ntok, size_t nkv, size_t d, size_t max_seq,
                                uint16_t *kc_ref, uint16_t *vc_ref);
 
+/* Full-attention causal prefill for B sequences of any length (c/layer.h:
+ * 498-564: per token q/k (1+w) RMSNorm, partial RoPE, cache append, then
+ * causal GQA of every new token over the cache, sigmoid output gate).
+ * Arguments as apus_hip_attn_decode with no limit on new tokens per
+ * sequence (pos0[s] + new tokens <= max_seq). The attention runs as an
+ * MFMA flash-attention kernel; y is a tolerance class of the reference
+ * (|c - r| <= 2e-3 (|r| + sum_j |P_j V_j|)). Supports d=256, rot=64,
+ * nh=8*nkv. */
+int apus_hip_attn_prefill(const ApusHipAttnLayer *L, size_t B,
+                          const int32_t *cu, const int32_t *pos0,
+                          const uint16_t *qg, const uint16_t *k,
+                          const uint16_t *v, uint16_t *kcache,
+                          uint16_t *vcache, size_t max_seq, uint16_t *y);
+
 /* Full-attention decode / verify for B sequences (c/layer.h:300-322 per
  * token: q/k (1+w) RMSNorm, partial RoPE at each token's position, cache
  * append, causal GQA over the cache, sigmoid output gate). Sequence s has

@@ -72,45 +72,26 @@ def f32_stats(c, r):
     return dict(exact=float(same), rel=state_rel(c, r))
 
 
-def assert_bf16_esc(c, r, esc, rel=BF16_REL, what=""):
+def assert_bf16_esc(c, r, esc, rel=BF16_REL, ulps=1, what=""):
     """Tolerance class for reordered reductions (the reference's own form,
-    tests/m4a/test_gdn.c:84-95): every element |c - r| <= rel*(|r| + esc),
-    esc the sum of |terms| of that output, plus ||c - r||_2/||r||_2 <= rel.
-    Outputs that are small through cancellation (|r| << esc) are judged
-    against the size of their terms, as the reference judges its own."""
+    tests/m4a/test_gdn.c:84-95): every element within `ulps` bf16 ulps of
+    the reference, or |c - r| <= rel*(|r| + esc) with esc the sum of |terms| of
+    that output; and ||c - r||_2/||r||_2 <= rel over the tensor. Outputs
+    that are small through cancellation (|r| << esc) are judged against the
+    size of their terms, as the reference judges its own; the one-ulp
+    allowance is the final bf16 rounding itself (a single ulp is already
+    2^-8..2^-7 relative, so an fp32 value within rel*esc of the reference's
+    can still round to the neighbouring code when one term dominates; a
+    later rounding point, such as the output gate's rnd(o * g), can carry
+    that one ulp of o into two ulps of its result)."""
     st = bf16_stats(c, r)
     cf = f32_of(np.asarray(c).ravel()).astype(np.float64)
     rf = f32_of(np.asarray(r).ravel()).astype(np.float64)
     e = np.asarray(esc, np.float64).ravel()
     ratio = np.abs(cf - rf) / (np.abs(rf) + e + 1e-30)
-    st["esc_max"] = float(ratio.max()) if ratio.size else 0.0
+    ud = ulp_diff(np.asarray(c).ravel(), np.asarray(r).ravel())
+    judged = ud > ulps
+    st["esc_max"] = float(ratio[judged].max()) if judged.any() else 0.0
+    st["esc_max_all"] = float(ratio.max()) if ratio.size else 0.0
     assert st["rel"] <= rel and st["esc_max"] <= rel, f"{what}: {st}"
-    return st
-
-
-def assert_bf16_rows(c, r, ncols, max_ulp=4, rel=BF16_REL, floor=BF16_REL, abs_floor=1e-5,
-                     what=""):
-    """Tolerance class for a reordered fp32 reduction feeding bf16 rounding
-    points and a per-row normalisation (the chunked GDN output: o from the
-    chunk form, rnd(o), then the gated RMSNorm's three roundings,
-    c/gdn.h:639-661). An fp32 ulp of o that crosses a bf16 boundary moves
-    rnd(o) by one ulp and each later rounding by at most one more, so an
-    element may sit up to 4 ulps away; elements small through cancellation
-    (|c - r| <= floor * rms of their row) are judged against the row's
-    scale instead. Rows whose recurrence output lies below the norm's eps
-    (a state decayed to ~0) are o * rs with rs up to 1/sqrt(1e-6): their
-    values are amplified fp32 noise of a near-zero o, so differences under
-    abs_floor * rms of the whole tensor are not counted either.
-    Normwise ||c - r||_2 / ||r||_2 <= rel over the tensor."""
-    st = bf16_stats(c, r)
-    c2 = np.asarray(c).reshape(-1, ncols)
-    r2 = np.asarray(r).reshape(-1, ncols)
-    cf = f32_of(c2).astype(np.float64)
-    rf = f32_of(r2).astype(np.float64)
-    rms = np.sqrt(np.mean(rf * rf, axis=1, keepdims=True))
-    grms = np.sqrt(np.mean(rf * rf)) if rf.size else 0.0
-    far = np.abs(cf - rf) > np.maximum(floor * rms, abs_floor * grms)
-    ud = ulp_diff(c2, r2)
-    st["max_ulp"] = int(ud[far].max()) if far.any() else 0
-    assert st["rel"] <= rel and st["max_ulp"] <= max_ulp, f"{what}: {st}"
     return st

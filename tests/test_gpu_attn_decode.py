@@ -5,35 +5,17 @@ Tolerance class: q.k and P.V accumulate on MFMA in a different order than
 the reference's sequential loops, so a score may round to the neighbouring
 bf16 code; bf16 outputs are held to 2e-3 relative (||.||_2 over the
 tensor) and, per element, to 2e-3 of (|out| + sum of |terms|), the
-reference's esc-normalised form (tests/numerics.py assert_bf16_esc). The cache rows
+reference's esc-normalised form, or to 2 bf16 ulps (one of rnd(o), carried
+through the gate's rnd(o * g)) (tests/numerics.py assert_bf16_esc). The cache rows
 the mixer appends (normed, roped k; raw v) must be bit-exact.
 """
 import numpy as np
 import pytest
 
 import synth
+from attn_util import attn_esc
 from numerics import assert_bf16_esc
-from synth import bf16_f32
 
-
-def attn_esc(qf, kc, vc, cu, pos0, nh, nkv, d):
-    """esc = sum_j P_j |V_jd| per output element, P from the roped q and
-    the cache in float64 (the magnitude of the terms each output sums)."""
-    T = int(cu[-1])
-    esc = np.zeros((T, nh, d))
-    grp = nh // nkv
-    for s in range(len(cu) - 1):
-        for t in range(cu[s], cu[s + 1]):
-            p = pos0[s] + t - cu[s]
-            q = bf16_f32(qf[t]).astype(np.float64).reshape(nh, d)
-            for hk in range(nkv):
-                K = bf16_f32(kc[s, :p + 1, hk]).astype(np.float64)
-                V = np.abs(bf16_f32(vc[s, :p + 1, hk]).astype(np.float64))
-                A = q[hk * grp:(hk + 1) * grp] @ K.T / np.sqrt(d)
-                P = np.exp(A - A.max(1, keepdims=True))
-                P /= P.sum(1, keepdims=True)
-                esc[t, hk * grp:(hk + 1) * grp] = P @ V
-    return esc.reshape(T, nh * d)
 
 pytestmark = pytest.mark.gpu
 
@@ -71,7 +53,7 @@ def _run(hip, orc, rng, cu, pos0, max_seq):
         torch.cuda.synchronize()
         assert np.array_equal(rk.cpu().numpy().view(np.uint16), k_o[s]), f"k cache seq {s}"
         assert np.array_equal(rv.cpu().numpy().view(np.uint16), v_o[s]), f"v cache seq {s}"
-    st = assert_bf16_esc(y.cpu().numpy().view(np.uint16), y_o, esc, what="attn_decode y")
+    st = assert_bf16_esc(y.cpu().numpy().view(np.uint16), y_o, esc, ulps=2, what="attn_decode y")
     print(st)
     return st
 
