@@ -95,3 +95,31 @@ def assert_bf16_esc(c, r, esc, rel=BF16_REL, ulps=1, what=""):
     st["esc_max_all"] = float(ratio.max()) if ratio.size else 0.0
     assert st["rel"] <= rel and st["esc_max"] <= rel, f"{what}: {st}"
     return st
+
+
+def assert_bf16_rows(c, r, ncols, max_ulp=4, rel=BF16_REL, floor=BF16_REL, abs_floor=1e-5,
+                     what=""):
+    """Tolerance class for a reordered fp32 reduction feeding bf16 rounding
+    points and a per-row normalisation (the chunked GDN output: o from the
+    chunk form, rnd(o), then the gated RMSNorm's three roundings,
+    c/gdn.h:639-661). An fp32 ulp of o that crosses a bf16 boundary moves
+    rnd(o) by one ulp and each later rounding by at most one more, so an
+    element may sit up to 4 ulps away; elements small through cancellation
+    (|c - r| <= floor * rms of their row) are judged against the row's
+    scale instead. Rows whose recurrence output lies below the norm's eps
+    (a state decayed to ~0) are o * rs with rs up to 1/sqrt(1e-6): their
+    values are amplified fp32 noise of a near-zero o, so differences under
+    abs_floor * rms of the whole tensor are not counted either.
+    Normwise ||c - r||_2 / ||r||_2 <= rel over the tensor."""
+    st = bf16_stats(c, r)
+    c2 = np.asarray(c).reshape(-1, ncols)
+    r2 = np.asarray(r).reshape(-1, ncols)
+    cf = f32_of(c2).astype(np.float64)
+    rf = f32_of(r2).astype(np.float64)
+    rms = np.sqrt(np.mean(rf * rf, axis=1, keepdims=True))
+    grms = np.sqrt(np.mean(rf * rf)) if rf.size else 0.0
+    far = np.abs(cf - rf) > np.maximum(floor * rms, abs_floor * grms)
+    ud = ulp_diff(c2, r2)
+    st["max_ulp"] = int(ud[far].max()) if far.any() else 0
+    assert st["rel"] <= rel and st["max_ulp"] <= max_ulp, f"{what}: {st}"
+    return st
