@@ -116,6 +116,7 @@ int ensure_ready() {
 }
 
 int cu_count() { return g_cus; }
+int current_device() { return g_device; }
 
 hipStream_t stream() { return g_stream; }
 void set_stream(hipStream_t s) { g_stream = s; }

@@ -29,6 +29,18 @@ int hip_fail(hipError_t e, const char *what, const char *file, int line);
 int ensure_ready();
 hipStream_t stream();
 int cu_count();     // compute units of the current device
+int current_device();
+
+// bf16-code activation tables (act_tables.hip): for every bf16 code c,
+// silu_bf[c] = rnd(x*sigmoid(x)), silu_f[c] = x*sigmoid(x) (fp32) and
+// sig_bf[c] = rnd(sigmoid(x)), x = the value of c. Device pointers, filled
+// on the library stream at the first call on a device.
+struct ActTables {
+    const uint16_t *silu_bf = nullptr;
+    const float *silu_f = nullptr;
+    const uint16_t *sig_bf = nullptr;
+};
+const ActTables *act_tables();
 void set_stream(hipStream_t s);
 
 // Grow-only device scratch, one buffer per slot. Valid until the next

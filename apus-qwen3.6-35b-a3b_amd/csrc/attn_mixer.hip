@@ -397,7 +397,8 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void k_
 // ---- k_attn_combine: one block per (token, q head), d threads ----------
 __global__ __launch_bounds__(D) void k_attn_combine(
     AttnSeqs sq, const int32_t *__restrict__ dmeta, const float *__restrict__ Op,
-    const uint16_t *__restrict__ qg, int nh, int nkv, uint16_t *__restrict__ y) {
+    const uint16_t *__restrict__ qg, int nh, int nkv, uint16_t *__restrict__ y,
+    const uint16_t *__restrict__ sig_bf) {
     const Meta mt = meta_of(sq, dmeta);
     const int32_t *cu = mt.cu, *soff = mt.soff2;
     const int tt = blockIdx.x / nh, h = blockIdx.x % nh;
@@ -408,7 +409,7 @@ __global__ __launch_bounds__(D) void k_attn_combine(
     for (int p = soff[s]; p < soff[s + 1]; p++)
         sum += Op[(((size_t)p * nkv + kvh) * kRows + n) * D + dd];
     const float o = rndf(sum);
-    const float gt = rndf(sigmoid_cr(bf2f(qg[((size_t)tt * nh + h) * 2 * D + D + dd])));
+    const float gt = bf2f(sig_bf[qg[((size_t)tt * nh + h) * 2 * D + D + dd]]);  // rnd(sigmoid)
     y[((size_t)tt * nh + h) * D + dd] = f2bf(o * gt);
 }
 
@@ -548,6 +549,8 @@ int apus_hip_attn_decode(const ApusHipAttnLayer *L, size_t B, const int32_t *cu,
     if (int r = attn_prep(L, sq, dmeta, Ttot, max_pos, qg, k, v, kcache, vcache, max_seq, qn))
         return r;
     const float scale = (float)(1.0 / sqrt((double)L->d));
+    const ActTables *tabs = act_tables();
+    if (!tabs) return kErrHip;
     const unsigned grid = (unsigned)(ns1 * L->nkv), grid2 = (unsigned)(ns2 * L->nkv);
     // one 16-row block covers up to 2 new tokens per sequence (8 heads each)
     if (mt <= 2) {
@@ -569,7 +572,7 @@ int apus_hip_attn_decode(const ApusHipAttnLayer *L, size_t B, const int32_t *cu,
     }
     APUS_TIMED("k_attn_combine",
                k_attn_combine<<<(unsigned)(Ttot * L->nh), D, 0, stream()>>>(sq, dmeta, Op, qg, (int)L->nh,
-                                                                  (int)L->nkv, y));
+                                                                  (int)L->nkv, y, tabs->sig_bf));
     APUS_LAUNCHED("k_attn_combine");
     return kOk;
 }

@@ -184,7 +184,7 @@ __global__ __launch_bounds__(256) void k_attn_fa(
     FaSeqs sq, const int32_t *__restrict__ dmeta, const uint16_t *__restrict__ qn,
     const uint16_t *__restrict__ qg, const uint16_t *__restrict__ kcache,
     const uint16_t *__restrict__ vcache, size_t max_seq, int nh, int nkv, float scale,
-    uint16_t *__restrict__ y) {
+    uint16_t *__restrict__ y, const uint16_t *__restrict__ sig_bf) {
     const int n = sq.n;
     const int32_t *cu = dmeta ? dmeta : sq.cu;
     const int32_t *pos0 = dmeta ? dmeta + n + 1 : sq.pos0;
@@ -344,7 +344,7 @@ __global__ __launch_bounds__(256) void k_attn_fa(
 #pragma unroll
                 for (int i = 0; i < 4; i++) {
                     const float ov = rndf(o[mt][4 * q4 + i]);
-                    const float gs = rndf(sigmoid_cr(bf2f(gv[i])));
+                    const float gs = bf2f(sig_bf[gv[i]]);     // rnd(sigmoid(gate))
                     out[i] = f2bf(ov * gs);
                 }
                 *reinterpret_cast<u16x4 *>(yr + d0) = out;
@@ -417,9 +417,12 @@ int apus_hip_attn_prefill(const ApusHipAttnLayer *L, size_t B, const int32_t *cu
     if (int r = attn_prep(L, as, adm, Ttot, max_pos, qg, k, v, kcache, vcache, max_seq, qn))
         return r;
     const float scale = (float)(1.0 / sqrt((double)L->d));
+    const ActTables *tabs = act_tables();
+    if (!tabs) return kErrHip;
     APUS_TIMED("k_attn_fa",
                k_attn_fa<<<(unsigned)(ntiles * L->nkv), 256, 0, stream()>>>(
-                   fs, fdm, qn, qg, kcache, vcache, max_seq, (int)L->nh, (int)L->nkv, scale, y));
+                   fs, fdm, qn, qg, kcache, vcache, max_seq, (int)L->nh, (int)L->nkv, scale, y,
+                   tabs->sig_bf));
     APUS_LAUNCHED("k_attn_fa");
     return kOk;
 }

@@ -266,7 +266,8 @@ __global__ __launch_bounds__(256) void k_gdn_prep(
     const uint16_t *__restrict__ conv_w, const float *__restrict__ A_log,
     const float *__restrict__ dt_bias, const uint16_t *__restrict__ conv_state,
     float *__restrict__ qk, uint16_t *__restrict__ vconv,
-    float2 *__restrict__ gate, float *__restrict__ graw, int hk, float qscale) {
+    float2 *__restrict__ gate, float *__restrict__ graw, int hk, float qscale,
+    const uint16_t *__restrict__ silu_bf, const uint16_t *__restrict__ sig_bf) {
     typedef unsigned short u16x8 __attribute__((ext_vector_type(8)));
     const int tile = blockIdx.x / hk, kh = blockIdx.x % hk;
     const int tb = tile * PT, nt = min(PT, Ttot - tb);
@@ -320,8 +321,9 @@ __global__ __launch_bounds__(256) void k_gdn_prep(
                 xv[u] = bf2f(cst[cv * 3 + (ti - t0 + 3)]);
             }
         }
-        rrow[i * RS] = bf2f(conv_tap4(wq, xq[0], xq[1], xq[2], xq[3]));
-        vconv[(size_t)t * vd + (size_t)h * DV + j] = conv_tap4(wv, xv[0], xv[1], xv[2], xv[3]);
+        rrow[i * RS] = bf2f(conv_tap4_tab(wq, xq[0], xq[1], xq[2], xq[3], silu_bf));
+        vconv[(size_t)t * vd + (size_t)h * DV + j] =
+            conv_tap4_tab(wv, xv[0], xv[1], xv[2], xv[3], silu_bf);
     }
     __syncthreads();
     if (tid < 2 * PT) {                      // ordered sums, one lane per row
@@ -337,7 +339,7 @@ __global__ __launch_bounds__(256) void k_gdn_prep(
         if (r < nt) {
             const size_t t = (size_t)(tb + r);
             const float g = decay_of(a[t * hv + hh], A_log[hh], dt_bias[hh]);
-            const float bt = rndf(sigmoid_cr(bf2f(b[t * hv + hh])));
+            const float bt = bf2f(sig_bf[b[t * hv + hh]]);
             gate[t * hv + hh] = make_float2(exp_cr(g), bt);
             if (graw) graw[t * hv + hh] = g;
         }
@@ -361,7 +363,7 @@ __global__ __launch_bounds__(256) void k_gdn_post(
     const uint16_t *__restrict__ ob, const uint16_t *__restrict__ z,
     const uint16_t *__restrict__ onorm_w, uint16_t *__restrict__ y,
     const uint16_t *__restrict__ qkv, uint16_t *__restrict__ conv_state,
-    int hk) {
+    int hk, const float *__restrict__ silu_f) {
     const int hv = hk * REP;
     const size_t kd = (size_t)hk * DK, vd = (size_t)hv * DV, cd = 2 * kd + vd;
     const int tid = threadIdx.x;
@@ -400,8 +402,7 @@ __global__ __launch_bounds__(256) void k_gdn_post(
                 for (int i = 0; i < 8; i++) {
                     const float x1 = rndf(os[row * RS + c8 + i] * rs[row]);
                     const float x2 = rndf(x1 * bf2f(wv[i]));
-                    const float zf = bf2f(zv[i]);
-                    out[i] = f2bf(x2 * (zf * sigmoid_cr(zf)));
+                    out[i] = f2bf(x2 * silu_f[zv[i]]);     // silu(z), fp32
                 }
                 *reinterpret_cast<u16x8 *>(y + off) = out;
             }
@@ -458,10 +459,12 @@ int gdn_prep(const ApusHipGdnLayer *L, size_t B, const int32_t *dcu,
     if (!w->qk || !w->vconv || !w->gate || !w->ob || (want_graw && !w->graw))
         return kErrHip;
     const float qscale = (float)pow((double)L->dk, -0.5);
+    const ActTables *tabs = act_tables();
+    if (!tabs) return kErrHip;
     APUS_TIMED("k_gdn_prep",
                k_gdn_prep<<<(unsigned)(cdiv(Ttot, PT) * L->hk), 256, 0, stream()>>>(
         dcu, (int)B, (int)Ttot, qkv, a, b, L->conv_w, L->A_log, L->dt_bias, conv_state,
-        w->qk, w->vconv, w->gate, w->graw, (int)L->hk, qscale));
+        w->qk, w->vconv, w->gate, w->graw, (int)L->hk, qscale, tabs->silu_bf, tabs->sig_bf));
     return launch_check("k_gdn_prep");
 }
 
@@ -470,10 +473,12 @@ int gdn_post(const ApusHipGdnLayer *L, size_t B, const int32_t *dcu,
              const uint16_t *qkv, uint16_t *conv_state, uint16_t *y) {
     const size_t cd = 2 * L->hk * DK + L->hv * DV;
     const size_t nblk = cdiv(Ttot * L->hv, PR) + B * (cd / 256);
+    const ActTables *tabs = act_tables();
+    if (!tabs) return kErrHip;
     APUS_TIMED("k_gdn_post",
                k_gdn_post<<<(unsigned)nblk, 256, 0, stream()>>>(
         dcu, (int)B, (int)Ttot, w->ob, z, L->onorm_w, y, qkv, conv_state,
-        (int)L->hk));
+        (int)L->hk, tabs->silu_f));
     return launch_check("k_gdn_post");
 }
 
