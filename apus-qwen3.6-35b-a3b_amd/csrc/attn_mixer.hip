@@ -75,67 +75,97 @@ __device__ __forceinline__ Meta meta_of(const AttnSeqs &sq, const int32_t *dmeta
     return Meta{dmeta, dmeta + n + 1, dmeta + 2 * n + 1, dmeta + 3 * n + 2};
 }
 
-// ---- k_attn_prep: one block per (token, head slot), 256 threads -------
-// slots 0..nh-1: q heads; nh..nh+nkv-1: kv heads (k normed+roped into the
-// K cache, v copied into the transposed V cache).
-__global__ __launch_bounds__(D) void k_attn_prep(
+// k_attn_prep: one block of 256 threads per rpb <= 32 rows (8 when there
+// are few rows, so small decode batches still spread over the chip), a
+// row being one (token, slot) with slots 0..nh-1 the q heads and
+// nh..nh+nkv-1 the kv heads. Rows are staged in LDS with 16-byte loads, the
+// rows' sequence, position and cos/sin codes alongside; lane r takes row
+// r's ascending sum of squares (c/attn.h:177-182); then thread i normalises
+// dim i of every row with (1+w) and one rounding, applies the partial NeoX
+// RoPE with the host-made cos/sin codes (c/attn.h:244-266) and writes q to
+// qn, or k to the K cache and v (raw) to the transposed V cache.
+constexpr int PRR = 32;          // rows per k_attn_prep block
+constexpr int PST = D + 4;       // LDS row stride: 16-byte aligned rows on distinct banks
+__global__ __launch_bounds__(256) void k_attn_prep(
     AttnSeqs sq, const int32_t *__restrict__ dmeta, const uint16_t *__restrict__ qg,
     const uint16_t *__restrict__ kin, const uint16_t *__restrict__ vin,
     const uint16_t *__restrict__ qn_w, const uint16_t *__restrict__ kn_w,
     const uint16_t *__restrict__ rope, uint16_t *__restrict__ kcache,
     uint16_t *__restrict__ vcache, size_t max_seq, uint16_t *__restrict__ qn,
-    int nh, int nkv) {
+    int nh, int nkv, int nrows, int rpb) {
+    typedef unsigned short u16x8v __attribute__((ext_vector_type(8)));
     const Meta mt = meta_of(sq, dmeta);
     const int32_t *cu = mt.cu, *pos0 = mt.pos0;
     const int nslot = nh + nkv;
-    const int tt = blockIdx.x / nslot, slot = blockIdx.x % nslot;
-    const int s = seq_of(cu, sq.n, tt);
-    const int pos = pos0[s] + (tt - cu[s]);
-    const int i = threadIdx.x;
-    const bool isq = slot < nh;
-    const int kvh = slot - nh;
-    const uint16_t *x = isq ? qg + ((size_t)tt * nh + slot) * 2 * D
-                            : kin + ((size_t)tt * nkv + kvh) * D;
-    const uint16_t *w = isq ? qn_w : kn_w;
-    __shared__ __attribute__((aligned(16))) float xs[D];
-    __shared__ float rs_s;
-    __shared__ float ns[D];
-    const float xf = bf2f(x[i]);
-    xs[i] = xf;
+    const int r0 = blockIdx.x * rpb, nr = min(rpb, nrows - r0);
+    const int tid = threadIdx.x;
+    __shared__ __attribute__((aligned(16))) float xs[PRR * PST];
+    __shared__ float rs[PRR];
+    __shared__ int rseq[PRR], rpos[PRR];
+    __shared__ uint16_t rcs[PRR * ROT];
+    for (int e = tid; e < nr * (D / 8); e += 256) {
+        const int r = e / (D / 8), c8 = (e % (D / 8)) * 8;
+        const int row = r0 + r, tt = row / nslot, slot = row % nslot;
+        const uint16_t *x = slot < nh ? qg + ((size_t)tt * nh + slot) * 2 * D
+                                      : kin + ((size_t)tt * nkv + (slot - nh)) * D;
+        const u16x8v v = *reinterpret_cast<const u16x8v *>(x + c8);
+#pragma unroll
+        for (int i = 0; i < 8; i++) xs[r * PST + c8 + i] = bf2f(v[i]);
+    }
+    if (tid >= 64 && tid < 64 + nr) {         // row metadata, one lane per row
+        const int r = tid - 64, tt = (r0 + r) / nslot;
+        const int sq_ = seq_of(cu, sq.n, tt);
+        rseq[r] = sq_;
+        rpos[r] = pos0[sq_] + (tt - cu[sq_]);
+    }
     __syncthreads();
-    if (i == 0) {                       // ascending sum of squares (c/attn.h:177-182)
+    if (tid < nr) {                           // ascending, 16-byte LDS reads
+        const float4 *x4 = reinterpret_cast<const float4 *>(xs + tid * PST);
         float ss = 0.0f;
-        for (int j = 0; j < D; j += 4) {
-            const float4 v4 = *reinterpret_cast<const float4 *>(xs + j);
-            ss = ss + v4.x * v4.x;
-            ss = ss + v4.y * v4.y;
-            ss = ss + v4.z * v4.z;
-            ss = ss + v4.w * v4.w;
+#pragma unroll 8
+        for (int j = 0; j < D / 4; j++) {
+            const float4 v = x4[j];
+            ss = ss + v.x * v.x;
+            ss = ss + v.y * v.y;
+            ss = ss + v.z * v.z;
+            ss = ss + v.w * v.w;
         }
-        rs_s = 1.0f / sqrtf(ss / (float)D + kEps);
+        rs[tid] = 1.0f / sqrtf(ss / (float)D + kEps);
+    }
+    for (int e = tid; e < nr * ROT; e += 256)  // the rows' cos/sin codes
+        rcs[e] = rope[(size_t)rpos[e / ROT] * ROT + e % ROT];
+    __syncthreads();
+    const float wq = 1.0f + bf2f(qn_w[tid]), wk = 1.0f + bf2f(kn_w[tid]);
+    for (int r = 0; r < nr; r++) {
+        const int slot = (r0 + r) % nslot;
+        float &x = xs[r * PST + tid];
+        x = rndf((x * rs[r]) * (slot < nh ? wq : wk));
     }
     __syncthreads();
-    const float nv = rndf((xf * rs_s) * (1.0f + bf2f(w[i])));
-    ns[i] = nv;
-    __syncthreads();
-    // partial NeoX RoPE with the host-made cos/sin codes (c/attn.h:244-266)
-    const uint16_t *cs = rope + (size_t)pos * ROT;
     constexpr int R = ROT / 2;
-    float out = nv;
-    if (i < R) {
-        const float c = bf2f(cs[i]), sn = bf2f(cs[R + i]);
-        out = rndf(rndf(nv * c) + rndf(-ns[i + R] * sn));
-    } else if (i < ROT) {
-        const float c = bf2f(cs[i - R]), sn = bf2f(cs[i]);
-        out = rndf(rndf(nv * c) + rndf(ns[i - R] * sn));
-    }
-    if (isq) {
-        qn[((size_t)tt * nh + slot) * D + i] = f2bf(out);
-    } else {
-        uint16_t *kc = kcache + ((size_t)s * nkv + kvh) * max_seq * D;
-        kc[(size_t)pos * D + i] = f2bf(out);
-        uint16_t *vc = vcache + ((size_t)s * nkv + kvh) * D * max_seq;
-        vc[((size_t)(pos / 32) * D + i) * 32 + pos % 32] = vin[((size_t)tt * nkv + kvh) * D + i];
+    for (int r = 0; r < nr; r++) {
+        const int row = r0 + r, tt = row / nslot, slot = row % nslot;
+        const int s = rseq[r], pos = rpos[r];
+        const float *ns = xs + r * PST;
+        const float nv = ns[tid];
+        float out = nv;
+        const uint16_t *cs = rcs + r * ROT;
+        if (tid < R) {
+            const float c = bf2f(cs[tid]), sn = bf2f(cs[R + tid]);
+            out = rndf(rndf(nv * c) + rndf(-ns[tid + R] * sn));
+        } else if (tid < ROT) {
+            const float c = bf2f(cs[tid - R]), sn = bf2f(cs[tid]);
+            out = rndf(rndf(nv * c) + rndf(ns[tid - R] * sn));
+        }
+        if (slot < nh) {
+            qn[((size_t)tt * nh + slot) * D + tid] = f2bf(out);
+        } else {
+            const int kvh = slot - nh;
+            uint16_t *kc = kcache + ((size_t)s * nkv + kvh) * max_seq * D;
+            kc[(size_t)pos * D + tid] = f2bf(out);
+            uint16_t *vc = vcache + ((size_t)s * nkv + kvh) * D * max_seq;
+            vc[((size_t)(pos / 32) * D + tid) * 32 + pos % 32] = vin[((size_t)tt * nkv + kvh) * D + tid];
+        }
     }
 }
 
@@ -515,10 +545,12 @@ int attn_prep(const ApusHipAttnLayer *L, const AttnSeqs &sq, const int32_t *dmet
               uint16_t *qn) {
     const uint16_t *rope = rope_table(L->rot, L->theta, max_pos);
     if (!rope) return kErrHip;
+    const size_t nrows = Ttot * (L->nh + L->nkv);
+    const int rpb = nrows < (size_t)64 * PRR * cu_count() ? 8 : PRR;
     APUS_TIMED("k_attn_prep",
-               k_attn_prep<<<(unsigned)(Ttot * (L->nh + L->nkv)), D, 0, stream()>>>(
+               k_attn_prep<<<cdiv(nrows, rpb), 256, 0, stream()>>>(
         sq, dmeta, qg, k, v, L->qn_w, L->kn_w, rope, kcache, vcache, max_seq, qn,
-        (int)L->nh, (int)L->nkv));
+        (int)L->nh, (int)L->nkv, (int)nrows, rpb));
     return launch_check("k_attn_prep");
 }
 

@@ -249,8 +249,24 @@ void k_gdn_decode(
 // ---- token-parallel pieces for the chunked prefill ------------------------
 constexpr int PT = 16;       // tokens per k_gdn_prep tile
 constexpr int PR = 64;       // (token, v-head) rows per k_gdn_post tile
-constexpr int RS = DK + 1;   // LDS row stride: lane r reads row r, bank-free
+constexpr int RS = DK + 4;   // LDS row stride: 16-byte aligned rows on distinct banks
 constexpr int PC = 4 * DK;   // pre-conv channels of one K head: q, k, 2 x v
+
+// Ascending sum of squares of one 128-float LDS row, one rounding per mul
+// and add, with 16-byte reads kept in flight ahead of the add chain.
+__device__ __forceinline__ float row_sumsq(const float *row) {
+    const float4 *x4 = reinterpret_cast<const float4 *>(row);
+    float ss = 0.0f;
+#pragma unroll 8
+    for (int j = 0; j < DK / 4; j++) {
+        const float4 v = x4[j];
+        ss = ss + v.x * v.x;
+        ss = ss + v.y * v.y;
+        ss = ss + v.z * v.z;
+        ss = ss + v.w * v.w;
+    }
+    return ss;
+}
 
 // k_gdn_prep: per (tile of 16 tokens, K head), 256 threads. The tile's
 // pre-conv inputs of the head (q, k and its two v-heads' channels) plus
@@ -275,8 +291,8 @@ __global__ __launch_bounds__(256) void k_gdn_prep(
     const int hv = hk * REP;
     const size_t kd = (size_t)hk * DK, vd = (size_t)hv * DV, cd = 2 * kd + vd;
     __shared__ __attribute__((aligned(16))) uint16_t xin[(PT + 3) * PC];
-    // q rows at 0, k rows at PT*RS: the 32 summing lanes hit distinct banks
-    __shared__ float raw[2 * PT * RS];
+    // q rows at 0, k rows at PT*RS (rows 16-byte aligned for the sums)
+    __shared__ __attribute__((aligned(16))) float raw[2 * PT * RS];
     __shared__ float rs[2][PT];
 
     // stage rows tb-3 .. tb+nt-1 (those that exist); LDS channel order
@@ -329,10 +345,7 @@ __global__ __launch_bounds__(256) void k_gdn_prep(
     if (tid < 2 * PT) {                      // ordered sums, one lane per row
         const int r = tid & (PT - 1), w = tid / PT;
         if (r < nt) {
-            const float *row = raw + w * PT * RS + r * RS;
-            float ss = 0.0f;
-            for (int c = 0; c < DK; c++) ss = ss + row[c] * row[c];
-            rs[w][r] = 1.0f / sqrtf(ss + kEps);
+            rs[w][r] = 1.0f / sqrtf(row_sumsq(raw + w * PT * RS + r * RS) + kEps);
         }
     } else if (tid >= 64 && tid < 64 + REP * PT) {   // gates of the two v-heads
         const int r = (tid - 64) & (PT - 1), hh = kh * REP + (tid - 64) / PT;
@@ -373,7 +386,7 @@ __global__ __launch_bounds__(256) void k_gdn_post(
     if ((size_t)blockIdx.x < nnorm) {
         const size_t r0 = (size_t)blockIdx.x * PR;
         const int nr = (int)min((size_t)PR, nrows - r0);
-        __shared__ float os[PR * RS];
+        __shared__ __attribute__((aligned(16))) float os[PR * RS];
         __shared__ float rs[PR];
         for (int e = tid; e < PR * DV / 8; e += 256) {
             const int row = e / (DV / 8), c8 = (e % (DV / 8)) * 8;
@@ -385,10 +398,7 @@ __global__ __launch_bounds__(256) void k_gdn_post(
         }
         __syncthreads();
         if (tid < nr) {
-            const float *row = os + tid * RS;
-            float ss = 0.0f;
-            for (int c = 0; c < DV; c++) ss = ss + row[c] * row[c];
-            rs[tid] = 1.0f / sqrtf(ss / (float)DV + kEps);
+            rs[tid] = 1.0f / sqrtf(row_sumsq(os + tid * RS) / (float)DV + kEps);
         }
         __syncthreads();
         for (int e = tid; e < PR * DV / 8; e += 256) {
