@@ -85,6 +85,13 @@ __device__ __forceinline__ uint32_t pack2(float lo, float hi) {
 }
 __device__ __forceinline__ float rnd_hw(float x) { return (float)(__bf16)x; }
 
+// e^x for the softmax, x <= 0: the hardware exp2 of x*log2(e) (about two
+// ulp; the result is rounded to a bf16 probability, so this stays inside
+// the tolerance class; exp2(-inf) = 0)
+__device__ __forceinline__ float exp_sm(float x) {
+    return __builtin_amdgcn_exp2f(x * 1.44269504088896341f);
+}
+
 // Key-tile staging: 16-byte pieces e = r*256 + tid, K rows (key e/32,
 // dims (e%32)*8..) and the V^T block ([d][32 keys], contiguous in the
 // cache: piece e is d = e/4, keys (e%4)*8..). Keys at or past nkeys are
@@ -137,17 +144,15 @@ __device__ __forceinline__ void fa_store_v(uint16_t *Vs, const u16x8 (&pv)[4], i
     }
 }
 
-// Scores of one key tile for this lane's query: S^T = K Q^T on MFMA, then
-// A = rnd(rnd(q.k) * scale) for keys kbase + 8*(i/4) + 4h + i%4 <= qpos,
-// -inf beyond.
-__device__ __forceinline__ void fa_scores(float (&a)[16], const uint16_t *Ks,
-                                          const bf16x8 (&qb)[D / 16], int kbase, int qpos,
-                                          float scale, int l32, int h) {
-    // two independent accumulation chains (even / odd 16-dim steps); the
-    // K operands of step pair p+1 are read while pair p is on the MFMA
-    // pipe (sched_group_barrier keeps that order: the LDS latency is then
-    // covered by the MFMAs instead of stalling each one)
-    f32x16 sc0, sc1;
+// Scores of one key tile for this lane's query, in two parts so the
+// callers can interleave them with other work: fa_qk runs S^T = K Q^T on
+// MFMA (two accumulation chains, even / odd 16-dim steps, the K operands
+// of step pair p+1 read while pair p is on the MFMA pipe), fa_round turns
+// it into A = rnd(rnd(q.k) * scale) for keys kbase + 8*(i/4) + 4h + i%4
+// <= qpos, -inf beyond (the compare only on tiles that reach the diagonal
+// of the wavefront's queries).
+__device__ __forceinline__ void fa_qk(f32x16 &sc0, f32x16 &sc1, const uint16_t *Ks,
+                                      const bf16x8 (&qb)[D / 16], int l32, int h) {
 #pragma unroll
     for (int i = 0; i < 16; i++) { sc0[i] = 0.0f; sc1[i] = 0.0f; }
     const uint16_t *kr = Ks + l32 * KSTR + h * 8;
@@ -165,19 +170,36 @@ __device__ __forceinline__ void fa_scores(float (&a)[16], const uint16_t *Ks,
         k0 = n0;
         k1 = n1;
     }
-    // order: reads of pairs 0 and 1, then (MFMA pair p, reads of pair p+2)
+}
+
+__device__ __forceinline__ void fa_round(float (&a)[16], const f32x16 &sc0, const f32x16 &sc1,
+                                         int kbase, int qpos, int qmin, float scale, int h) {
+    if (kbase + KT - 1 <= qmin) {      // wave-uniform: no key of the tile is masked
+#pragma unroll
+        for (int i = 0; i < 16; i++) a[i] = rnd_hw(rnd_hw(sc0[i] + sc1[i]) * scale);
+    } else {
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+            const int key = kbase + 8 * (i / 4) + 4 * h + (i % 4);
+            a[i] = key <= qpos ? rnd_hw(rnd_hw(sc0[i] + sc1[i]) * scale) : -INFINITY;
+        }
+    }
+}
+
+// order of one S^T computation: reads of pairs 0 and 1, then (MFMA pair p,
+// VALU from the caller, reads of pair p+2)
+template <int VALU_PER_PAIR>
+__device__ __forceinline__ void fa_qk_schedule() {
     __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);       // LDS reads
 #pragma unroll
     for (int g = 0; g < D / 32 - 2; g++) {
         __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);   // MFMA
+        __builtin_amdgcn_sched_group_barrier(0x002, VALU_PER_PAIR, 0);
         __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);   // LDS reads
     }
-    __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
-#pragma unroll
-    for (int i = 0; i < 16; i++) {
-        const int key = kbase + 8 * (i / 4) + 4 * h + (i % 4);
-        a[i] = key <= qpos ? rnd_hw(rnd_hw(sc0[i] + sc1[i]) * scale) : -INFINITY;
-    }
+    __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+    __builtin_amdgcn_sched_group_barrier(0x002, VALU_PER_PAIR, 0);
+    __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
 }
 
 __global__ __launch_bounds__(256) void k_attn_fa(
@@ -214,6 +236,7 @@ __global__ __launch_bounds__(256) void k_attn_fa(
     const bool qok = tk < nt;
     const int qtok = tb + min(tk, nt - 1);
     const int qpos = qpos0 + tk;
+    const int qmin = qpos0 + wave * 4;          // smallest query position of the wavefront
     bf16x8 qb[D / 16];
     {
         const uint16_t *qr = qn + ((size_t)qtok * nh + head) * D + h * 8;
@@ -228,12 +251,16 @@ __global__ __launch_bounds__(256) void k_attn_fa(
     // stages tile kb+1, then scores it on MFMA while the VALU folds tile
     // kb into (m, s).
     float m = -INFINITY, lsum = 0.0f;
-    float a[16], an[16];
+    float a[16];
     fa_load_k(pk, kc, 0, tid);
     fa_store_k(Ks[0], pk, 0, nkeys, tid);
     if (nkt > 1) fa_load_k(pk, kc, 1, tid);
     __syncthreads();
-    fa_scores(a, Ks[0], qb, 0, qpos, scale, l32, h);
+    {
+        f32x16 s0, s1;
+        fa_qk(s0, s1, Ks[0], qb, l32, h);
+        fa_round(a, s0, s1, 0, qpos, qmin, scale, h);
+    }
     for (int kb = 0; kb < nkt; kb++) {
         const bool more = kb + 1 < nkt;
         if (more) {
@@ -241,7 +268,10 @@ __global__ __launch_bounds__(256) void k_attn_fa(
             if (kb + 2 < nkt) fa_load_k(pk, kc, kb + 2, tid);
         }
         __syncthreads();
-        if (more) fa_scores(an, Ks[(kb + 1) & 1], qb, (kb + 1) * KT, qpos, scale, l32, h);
+        // next tile's S^T (past the last tile it reads a stale buffer and is
+        // discarded) interleaved with folding tile kb into (m, s)
+        f32x16 s0, s1;
+        fa_qk(s0, s1, Ks[(kb + 1) & 1], qb, l32, h);
         float mx = -INFINITY;
 #pragma unroll
         for (int i = 0; i < 16; i++) mx = fmaxf(mx, a[i]);
@@ -249,12 +279,12 @@ __global__ __launch_bounds__(256) void k_attn_fa(
         const float mn = fmaxf(m, mx);
         float ps = 0.0f;
 #pragma unroll
-        for (int i = 0; i < 16; i++) ps += exp_fast(a[i] - mn);
+        for (int i = 0; i < 16; i++) ps += exp_sm(a[i] - mn);
         ps += __shfl_xor(ps, 32);
-        lsum = lsum * exp_fast(m - mn) + ps;   // exp(-inf) = 0 on the first tile
+        lsum = lsum * exp_sm(m - mn) + ps;     // exp(-inf) = 0 on the first tile
         m = mn;
-#pragma unroll
-        for (int i = 0; i < 16; i++) a[i] = an[i];
+        fa_round(a, s0, s1, (kb + 1) * KT, qpos, qmin, scale, h);
+        fa_qk_schedule<10>();
     }
 
     // ---- pass 2: P = rnd(e^{A-m} / s), O^T += V^T P^T (e times 1/s: a
@@ -277,7 +307,11 @@ __global__ __launch_bounds__(256) void k_attn_fa(
         fa_load_v(pv, vc, 1, tid);
     }
     __syncthreads();
-    fa_scores(a, Ks[0], qb, 0, qpos, scale, l32, h);
+    {
+        f32x16 s0, s1;
+        fa_qk(s0, s1, Ks[0], qb, l32, h);
+        fa_round(a, s0, s1, 0, qpos, qmin, scale, h);
+    }
     for (int kb = 0; kb < nkt; kb++) {
         const bool more = kb + 1 < nkt;
         if (more) {
@@ -289,11 +323,15 @@ __global__ __launch_bounds__(256) void k_attn_fa(
             }
         }
         __syncthreads();
-        if (more) fa_scores(an, Ks[(kb + 1) & 1], qb, (kb + 1) * KT, qpos, scale, l32, h);
+        // next tile's S^T interleaved with tile kb's probabilities, then
+        // tile kb's P.V interleaved with the next tile's score rounding
+        f32x16 s0, s1;
+        fa_qk(s0, s1, Ks[(kb + 1) & 1], qb, l32, h);
         uint32_t pp[8];
 #pragma unroll
         for (int i = 0; i < 8; i++)
-            pp[i] = pack2(exp_fast(a[2 * i] - m) * inv_s, exp_fast(a[2 * i + 1] - m) * inv_s);
+            pp[i] = pack2(exp_sm(a[2 * i] - m) * inv_s, exp_sm(a[2 * i + 1] - m) * inv_s);
+        fa_qk_schedule<8>();
         const uint16_t *Vb = Vs[kb % 3];
         // step st covers keys st*16 + {4h..4h+3, 8+4h..8+4h+3}; the V^T
         // operand of MFMA j+1 is read while MFMA j runs
@@ -318,15 +356,15 @@ __global__ __launch_bounds__(256) void k_attn_fa(
             vlo = nlo;
             vhi = nhi;
         }
+        fa_round(a, s0, s1, (kb + 1) * KT, qpos, qmin, scale, h);
         __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);   // LDS reads
 #pragma unroll
         for (int j = 0; j < 2 * (D / 32) - 2; j++) {
             __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // MFMA
+            __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);   // VALU
             __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);   // LDS reads
         }
         __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
-#pragma unroll
-        for (int i = 0; i < 16; i++) a[i] = an[i];
     }
 
     // epilogue: o = rnd(O); y = rnd(o * rnd(sigmoid(gate)))
