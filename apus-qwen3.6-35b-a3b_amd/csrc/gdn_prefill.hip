@@ -92,12 +92,6 @@ __device__ __forceinline__ float4 lds4(const float *p) {
     return *reinterpret_cast<const float4 *>(p);
 }
 
-// v if ok else 0, by value (a ternary between a register-array element
-// and a temporary can force the array to scratch memory)
-__device__ __forceinline__ float4 keep4(bool ok, float4 v) {
-    return make_float4(ok ? v.x : 0.f, ok ? v.y : 0.f, ok ? v.z : 0.f, ok ? v.w : 0.f);
-}
-
 __device__ __forceinline__ float4 ld4(const float *p) {
     return *reinterpret_cast<const float4 *>(p);
 }
@@ -125,23 +119,45 @@ __device__ __forceinline__ ChunkPos chunk_pos(const int32_t *cu, const int32_t *
 
 // Per (chunk, v-head) buffers written by k_gdn_chunk_wy, stored in the
 // order k_gdn_chunk_scan's MFMA lanes consume them, so that every scan load
-// instruction reads 1 KiB of contiguous memory. "lane(r, q)" is r + 16*q,
-// the lane that holds row r and reduction quad q of a 16x16x4 operand.
-//   W  [4 row blocks][8 k-groups of 16][64 lanes][4]: element (t, c) at
-//      lane(t%16, (c%16)/4) of block (t/16, c/16), slot c%4;
-//   A  [4][4 k-groups][64][4]: element (t, s) likewise (s <= t valid);
-//   U  [8 column slices][4 row blocks][64][4]: element (t, j) at
-//      lane(j%16, (t%16)/4) of (j/16, t/16), slot t%4 -- the accumulator
-//      layout of the scan's D tile;
-//   F  [2][C]: F[0][t] = G_t, F[1][s] = exp(gamma_C - gamma_s).
-__device__ __forceinline__ size_t wy_w_index(int t, int c) {
-    return ((size_t)((t >> 4) * 8 + (c >> 4)) * 64 + ((c & 15) >> 2) * 16 + (t & 15)) * 4 + (c & 3);
+// instruction reads 1 KiB of contiguous memory. The scan multiplies on
+// the 16x16x32 bf16 MFMA in split precision: every fp32 operand x is held
+// as hi = rnd(x) and lo = rnd(x - hi) (bf16), and a product is
+// hi.hi + hi.lo + lo.hi with fp32 accumulation (about 2^-16 relative per
+// product; the dropped lo.lo term is below 2^-17). Matrix operands are
+// stored per 16 rows x 32 reduction columns: lane g*16 + r of block
+// (row block, 32-column block) holds row r, columns 8g..8g+7 as 8 hi then
+// 8 lo codes (32 bytes).
+//   W  [4 row blocks][4 column blocks][64 lanes][16] (rows t, columns c);
+//   A  [4 row blocks][2 column blocks][64][16] (rows t, columns s; zero for
+//      s > t inside the blocks the scan reads);
+//   U  fp32 [8 column slices][4 row blocks][64][4]: element (t, j) at lane
+//      (j%16) + 16*((t%16)/4) of (j/16, t/16), slot t%4 -- the
+//      accumulator layout of the scan's D tile;
+//   F  fp32 [2][C]: F[0][t] = G_t, F[1][s] = exp(gamma_C - gamma_s).
+// Per (chunk, K head), written by the v-head of even index (both v-heads
+// of a K head hold the same q and k):
+//   Q  in W's layout (the A operand of G_t (Q S0));
+//   K  [8 state-row blocks][2 column blocks][64][16] as a B operand: lane
+//      g*16 + i%16 holds key rows s = 8g..8g+7 of state row i.
+__device__ __forceinline__ size_t bx_a_index(int t, int c, int nkb) {
+    return ((size_t)((t >> 4) * nkb + (c >> 5)) * 64 + ((c & 31) >> 3) * 16 + (t & 15)) * 16 + (c & 7);
 }
-__device__ __forceinline__ size_t wy_a_index(int t, int s) {
-    return ((size_t)((t >> 4) * 4 + (s >> 4)) * 64 + ((s & 15) >> 2) * 16 + (t & 15)) * 4 + (s & 3);
+__device__ __forceinline__ size_t bx_b_index(int s, int i) {
+    return ((size_t)((i >> 4) * 2 + (s >> 5)) * 64 + ((s & 31) >> 3) * 16 + (i & 15)) * 16 + (s & 7);
 }
 __device__ __forceinline__ size_t wy_u_index(int t, int j) {
     return ((size_t)((j >> 4) * 4 + (t >> 4)) * 64 + ((t & 15) >> 2) * 16 + (j & 15)) * 4 + (t & 3);
+}
+
+// hi = rnd(x), lo = rnd(x - hi), as bf16 codes (hardware round to nearest
+// even)
+__device__ __forceinline__ void split_bf(float x, uint16_t &hi, uint16_t &lo) {
+    const __bf16 h = (__bf16)x;
+    hi = __builtin_bit_cast(uint16_t, h);
+    lo = __builtin_bit_cast(uint16_t, (__bf16)(x - (float)h));
+}
+__device__ __forceinline__ void put_split(uint16_t *p, float x) {
+    split_bf(x, p[0], p[8]);
 }
 
 // k_gdn_chunk_wy: one workgroup per (chunk, v-head), two per CU (Q's LDS
@@ -149,11 +165,15 @@ __device__ __forceinline__ size_t wy_u_index(int t, int j) {
 __global__ __launch_bounds__(256, 2) void k_gdn_chunk_wy(
     ChunkSeqs sq, const int32_t *__restrict__ dmeta, const float *__restrict__ qk,
     const uint16_t *__restrict__ vconv, const float2 *__restrict__ gate,
-    const float *__restrict__ graw, float *__restrict__ Ub, float *__restrict__ Wb,
-    float *__restrict__ Ab, float *__restrict__ Fb, int hk) {
+    const float *__restrict__ graw, float *__restrict__ Ub, uint16_t *__restrict__ Wb,
+    uint16_t *__restrict__ Ab, float *__restrict__ Fb, uint16_t *__restrict__ Qp,
+    uint16_t *__restrict__ Kp, int hk) {
     const int hv = hk * REP;
     const size_t kd = (size_t)hk * DK, vd = (size_t)hv * DV;
     const int ci = blockIdx.x / hv, h = blockIdx.x % hv, kh = h / REP;
+    const bool wqk = h % REP == 0;              // this v-head writes Qp / Kp
+    uint16_t *Qpu = Qp + ((size_t)ci * hk + kh) * C * DK * 2;
+    uint16_t *Kpu = Kp + ((size_t)ci * hk + kh) * C * DK * 2;
     const int32_t *cu = dmeta ? dmeta : sq.cu;
     const int32_t *coff = dmeta ? dmeta + sq.n + 1 : sq.coff;
     const ChunkPos P = chunk_pos(cu, coff, sq.n, ci);
@@ -175,6 +195,14 @@ __global__ __launch_bounds__(256, 2) void k_gdn_chunk_wy(
         }
         *reinterpret_cast<float4 *>(QL + t * KP + q4) = q;
         *reinterpret_cast<float4 *>(Ks + t * KP + q4) = k;
+        if (wqk) {
+            const float qv[4] = {q.x, q.y, q.z, q.w}, kv[4] = {k.x, k.y, k.z, k.w};
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                put_split(Qpu + bx_a_index(t, q4 + j, DK / 32), qv[j]);
+                put_split(Kpu + bx_b_index(t, q4 + j), kv[j]);
+            }
+        }
     }
     if (tid < C) {
         const bool ok = tid < P.nt;
@@ -197,9 +225,14 @@ __global__ __launch_bounds__(256, 2) void k_gdn_chunk_wy(
 
     const int r16 = lane & 15, kq = (lane >> 4) * 4;
     // Q K^T, row block 3-w: A = decayed lower triangle, to global
-    float *A = Ab + (size_t)blockIdx.x * C * C;
+    uint16_t *A = Ab + (size_t)blockIdx.x * C * C * 2;
     {
         const int rb = 3 - wave;
+        if ((rb & 1) == 0) {           // the upper tile the scan's 32-column block covers
+            const int s = (rb + 1) * 16 + r16;
+#pragma unroll
+            for (int i = 0; i < 4; i++) put_split(A + bx_a_index(rb * 16 + kq + i, s, C / 32), 0.0f);
+        }
         for (int cb = 0; cb <= rb; cb++) {
             f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -210,7 +243,8 @@ __global__ __launch_bounds__(256, 2) void k_gdn_chunk_wy(
 #pragma unroll
             for (int i = 0; i < 4; i++) {
                 const int t = rb * 16 + kq + i;
-                A[wy_a_index(t, s)] = s <= t ? exp_fast(gam[t] - gam[s]) * acc[i] : 0.0f;
+                put_split(A + bx_a_index(t, s, C / 32),
+                          s <= t ? exp_fast(gam[t] - gam[s]) * acc[i] : 0.0f);
             }
         }
     }
@@ -274,68 +308,100 @@ __global__ __launch_bounds__(256, 2) void k_gdn_chunk_wy(
         for (int t = 0; t < C; t++) Ub[ub + wy_u_index(t, tid)] = x[t];
     } else {
 #pragma unroll
-        for (int t = 0; t < C; t++) Wb[ub + wy_w_index(t, tid - DV)] = x[t];
+        for (int t = 0; t < C; t++) put_split(Wb + 2 * ub + bx_a_index(t, tid - DV, DK / 32), x[t]);
     }
 }
 
 // Chunk-to-chunk scan of one 16-column slice of one head's state.
 // Block index = cb * (B*hv) + (s*hv + h): the 8 slices of a head share
-// their U/W/A/Q/K reads, and with B*hv a multiple of 8 they land on the
-// same XCD (blocks are dealt round-robin over the 8 XCDs) and so share
-// its L2. The next chunk's operands are loaded into registers as soon as
-// the current chunk's copy has been consumed, so their latency overlaps
-// this chunk's work; W, A and U arrive in MFMA lane order (1 KiB per
-// load instruction), Q and K as whole rows into LDS.
+// their operand reads, and with B*hv a multiple of 8 they land on the same
+// XCD (blocks are dealt round-robin over the 8 XCDs) and so share its L2.
+// 512 threads in two roles, two wavefronts per SIMD:
+//   waves 0-3 carry the recurrence: D = U - W S0 (rows 16w..), then
+//             S1^T = G_C S0^T + Dp^T K (state rows 32w..);
+//   waves 4-7 produce the chunk's outputs meanwhile: G_t (Q S0), then
+//             + A D once D is complete, rnd(o) to ob.
+// Products run on the 16x16x32 bf16 MFMA in split precision (hi.hi +
+// hi.lo + lo.hi); the state slice is kept in fp32 and, for the MFMA, as
+// hi/lo codes made once when it is written. Each wavefront loads the next
+// chunk's operands it consumes into registers as soon as the current copy
+// is used.
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef unsigned short u16x8 __attribute__((ext_vector_type(8)));
+
+__device__ __forceinline__ bf16x8 as_bf(u16x8 v) { return __builtin_bit_cast(bf16x8, v); }
+__device__ __forceinline__ u16x8 ld8(const uint16_t *p) {
+    return *reinterpret_cast<const u16x8 *>(p);
+}
+// acc += a.b in split precision: (ah, al) and (bh, bl) the hi/lo operands
+__device__ __forceinline__ f32x4 mfma_x3(u16x8 ah, u16x8 al, u16x8 bh, u16x8 bl, f32x4 c) {
+    c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf(al), as_bf(bh), c, 0, 0, 0);
+    c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf(ah), as_bf(bl), c, 0, 0, 0);
+    c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf(ah), as_bf(bh), c, 0, 0, 0);
+    return c;
+}
+
+constexpr int SB = DK + 8;     // bf16 row stride of the state slice copies
+constexpr int DB = C + 8;      // bf16 row stride of the D copies
+
 struct ScanOps {
-    float4 k[C * DK / 4 / 256];     // K rows
-    float4 q[C * DK / 4 / 256];     // Q rows
-    float4 w[DK / 16];              // W operand, row block w
-    float4 a[C / 16];               // A operand, row block w (causal part)
-    float4 u;                       // U in the D-tile layout
+    u16x8 w[DK / 32][2];            // W operand, row block w (hi, lo)      (waves 0-3)
+    u16x8 k[2][C / 32][2];          // K operand, state-row blocks          (waves 0-3)
+    float4 u;                       // U in the D-tile layout               (waves 0-3)
+    u16x8 q[DK / 32][2];            // Q operand, row block w               (waves 4-7)
+    u16x8 a[C / 32][2];             // A operand, causal part               (waves 4-7)
     float f;                        // decay factors (threads < 2C)
 };
 
-// Q and K rows of one chunk (rows past its tokens are clamped to a valid
-// row; the consumer zeroes them -- a select right after the load would
-// wait for it, and the in-order load counter would then drain every
-// prefetch issued before it).
-__device__ __forceinline__ void scan_load_qk(ScanOps &nx, const float *__restrict__ qk,
-                                             const float *__restrict__ Fb, size_t u, int t0,
-                                             int nt, size_t kd, int kh, int tid) {
-#pragma unroll
-    for (int it = 0; it < C * DK / 4 / 256; it++) {
-        const int e = it * 256 + tid, t = e / (DK / 4), q4 = (e % (DK / 4)) * 4;
-        const float *row = qk + (size_t)(t0 + min(t, nt - 1)) * 2 * kd + (size_t)kh * DK + q4;
-        nx.q[it] = ld4(row);
-        nx.k[it] = ld4(row + kd);
-    }
-    nx.f = Fb[u * 2 * C + (tid & (2 * C - 1))];
-}
-
-__device__ __forceinline__ void scan_load_wu(ScanOps &nx, const float *__restrict__ Wb,
+__device__ __forceinline__ void scan_load_wu(ScanOps &nx, const uint16_t *__restrict__ Wb,
                                              const float *__restrict__ Ub, size_t u, int wave,
                                              int lane, int cb) {
-    const float *W = Wb + u * C * DK + (size_t)wave * 8 * 256 + lane * 4;
+    const uint16_t *W = Wb + u * C * DK * 2 + ((size_t)wave * (DK / 32) * 64 + lane) * 16;
 #pragma unroll
-    for (int k = 0; k < DK / 16; k++) nx.w[k] = ld4(W + k * 256);
+    for (int kb = 0; kb < DK / 32; kb++) {
+        nx.w[kb][0] = ld8(W + kb * 64 * 16);
+        nx.w[kb][1] = ld8(W + kb * 64 * 16 + 8);
+    }
     nx.u = ld4(Ub + u * C * DV + ((size_t)(cb * 4 + wave) * 64 + lane) * 4);
 }
 
-__device__ __forceinline__ void scan_load_a(ScanOps &nx, const float *__restrict__ Ab, size_t u,
-                                            int wave, int lane) {
-    const float *Ar = Ab + u * C * C + (size_t)wave * 4 * 256 + lane * 4;
+__device__ __forceinline__ void scan_load_k(ScanOps &nx, const uint16_t *__restrict__ Kp,
+                                            size_t uk, int wave, int lane) {
+    const uint16_t *K = Kp + uk * C * DK * 2 + ((size_t)wave * 2 * (C / 32) * 64 + lane) * 16;
 #pragma unroll
-    for (int k = 0; k < C / 16; k++)
-        if (k <= wave) nx.a[k] = ld4(Ar + k * 256);
+    for (int r = 0; r < 2; r++)
+#pragma unroll
+        for (int kb = 0; kb < C / 32; kb++) {
+            nx.k[r][kb][0] = ld8(K + (r * (C / 32) + kb) * 64 * 16);
+            nx.k[r][kb][1] = ld8(K + (r * (C / 32) + kb) * 64 * 16 + 8);
+        }
 }
 
-__global__ __launch_bounds__(256) void k_gdn_chunk_scan(
-    ChunkSeqs sq, const int32_t *__restrict__ dmeta, const float *__restrict__ qk,
-    const float *__restrict__ Ub, const float *__restrict__ Wb,
-    const float *__restrict__ Ab, const float *__restrict__ Fb, float *__restrict__ S,
-    uint16_t *__restrict__ ob, int hk) {
+__device__ __forceinline__ void scan_load_out(ScanOps &nx, const uint16_t *__restrict__ Qp,
+                                              const uint16_t *__restrict__ Ab, size_t u,
+                                              size_t uk, int ow, int lane) {
+    const uint16_t *Q = Qp + uk * C * DK * 2 + ((size_t)ow * (DK / 32) * 64 + lane) * 16;
+#pragma unroll
+    for (int kb = 0; kb < DK / 32; kb++) {
+        nx.q[kb][0] = ld8(Q + kb * 64 * 16);
+        nx.q[kb][1] = ld8(Q + kb * 64 * 16 + 8);
+    }
+    const uint16_t *Ar = Ab + u * C * C * 2 + ((size_t)ow * (C / 32) * 64 + lane) * 16;
+#pragma unroll
+    for (int kb = 0; kb < C / 32; kb++)
+        if (kb <= ow / 2) {
+            nx.a[kb][0] = ld8(Ar + kb * 64 * 16);
+            nx.a[kb][1] = ld8(Ar + kb * 64 * 16 + 8);
+        }
+}
+
+__global__ __launch_bounds__(512) void k_gdn_chunk_scan(
+    ChunkSeqs sq, const int32_t *__restrict__ dmeta, const uint16_t *__restrict__ Qp,
+    const uint16_t *__restrict__ Kp, const float *__restrict__ Ub,
+    const uint16_t *__restrict__ Wb, const uint16_t *__restrict__ Ab,
+    const float *__restrict__ Fb, float *__restrict__ S, uint16_t *__restrict__ ob, int hk) {
     const int hv = hk * REP;
-    const size_t kd = (size_t)hk * DK, vd = (size_t)hv * DV;
+    const size_t vd = (size_t)hv * DV;
     const int nsh = sq.n * hv;
     const int cb = blockIdx.x / nsh, sh = blockIdx.x % nsh;
     const int s = sh / hv, h = sh % hv, kh = h / REP;
@@ -343,111 +409,127 @@ __global__ __launch_bounds__(256) void k_gdn_chunk_scan(
     const int32_t *coff = dmeta ? dmeta + sq.n + 1 : sq.coff;
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int r16 = lane & 15, kq = (lane >> 4) * 4;
-    const int rw = wave * 16;
+    const bool rec = wave < 4;                  // recurrence or output role
+    const int wr = wave & 3;
+    const int rw = wr * 16;                     // the role's 16-row block
+    const int r16 = lane & 15, g4 = lane >> 4;  // MFMA row / column, lane group
+    const int kq = g4 * 4;
 
-    __shared__ __attribute__((aligned(16))) float Ks[C * KP];      // K rows of the chunk
-    __shared__ __attribute__((aligned(16))) float Qs[C * KP];      // Q rows
-    __shared__ __attribute__((aligned(16))) float S0T[CB * KP];    // S slice, [col][row]
-    __shared__ __attribute__((aligned(16))) float DT[CB * CP];     // D slice, [col][t]
-    __shared__ __attribute__((aligned(16))) float DpT[CB * CP];    // decayed D
+    __shared__ __attribute__((aligned(16))) float S0T[CB * KP];        // S slice [col][row]
+    __shared__ __attribute__((aligned(16))) uint16_t S0h[CB * SB];     // its hi / lo codes
+    __shared__ __attribute__((aligned(16))) uint16_t S0l[CB * SB];
+    __shared__ __attribute__((aligned(16))) uint16_t Dh[CB * DB];      // D [col][t], hi / lo
+    __shared__ __attribute__((aligned(16))) uint16_t Dl[CB * DB];
+    __shared__ __attribute__((aligned(16))) uint16_t Dph[CB * DB];     // decayed D
+    __shared__ __attribute__((aligned(16))) uint16_t Dpl[CB * DB];
     __shared__ float Fs[2 * C];
 
     // state slice in: packed layout ((j/64*32 + i/4)*64 + j%64)*4 + i%4
     float *Sm = S + (size_t)sh * DK * DV;
     const int jb = (cb * CB) / 64 * 32, jl = (cb * CB) % 64;
-    for (int e = tid; e < CB * DK; e += 256) {
+    for (int e = tid; e < CB * DK; e += 512) {
         const int q = e / 64, rem = e % 64, jj = rem / 4, r = rem % 4;
-        S0T[jj * KP + 4 * q + r] = Sm[((size_t)(jb + q) * 64 + jl + jj) * 4 + r];
+        const float x = Sm[((size_t)(jb + q) * 64 + jl + jj) * 4 + r];
+        S0T[jj * KP + 4 * q + r] = x;
+        split_bf(x, S0h[jj * SB + 4 * q + r], S0l[jj * SB + 4 * q + r]);
     }
 
     const int c0 = coff[s], c1 = coff[s + 1];
     const int tS = cu[s], tE = cu[s + 1];
     ScanOps nx;
     if (c0 < c1) {
-        const size_t u = (size_t)c0 * hv + h;
-        scan_load_qk(nx, qk, Fb, u, tS, min(C, tE - tS), kd, kh, tid);
-        scan_load_wu(nx, Wb, Ub, u, wave, lane, cb);
-        scan_load_a(nx, Ab, u, wave, lane);
+        const size_t u = (size_t)c0 * hv + h, uk = (size_t)c0 * hk + kh;
+        if (tid < 2 * C) Fs[tid] = Fb[u * 2 * C + tid];
+        if (rec) {
+            scan_load_wu(nx, Wb, Ub, u, wr, lane, cb);
+            scan_load_k(nx, Kp, uk, wr, lane);
+        } else {
+            scan_load_out(nx, Qp, Ab, u, uk, wr, lane);
+        }
     }
 
     for (int ci = c0; ci < c1; ci++) {
         const int t0 = tS + (ci - c0) * C, nt = min(C, tE - t0);
         const bool more = ci + 1 < c1;
-        const int t0n = t0 + C, ntn = min(C, tE - t0n);
-        const size_t un = (size_t)(ci + 1) * hv + h;
-        __syncthreads();               // previous step done with Ks/Qs/Fs/S0T
-#pragma unroll
-        for (int it = 0; it < C * DK / 4 / 256; it++) {
-            const int e = it * 256 + tid, t = e / (DK / 4), q4 = (e % (DK / 4)) * 4;
-            *reinterpret_cast<float4 *>(Ks + t * KP + q4) = keep4(t < nt, nx.k[it]);
-            *reinterpret_cast<float4 *>(Qs + t * KP + q4) = keep4(t < nt, nx.q[it]);
-        }
-        if (tid < 2 * C) Fs[tid] = nx.f;
-        if (more) scan_load_qk(nx, qk, Fb, un, t0n, ntn, kd, kh, tid);
-        __syncthreads();
+        const size_t un = (size_t)(ci + 1) * hv + h, ukn = (size_t)(ci + 1) * hk + kh;
+        if (more && tid < 2 * C) nx.f = Fb[un * 2 * C + tid];
+        __syncthreads();               // the state slice and Fs of this chunk are in place
 
-        // D rows [16w, 16w+16) of this slice: U - W S0
-        f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int k = 0; k < DK / 16; k++)
-            acc = mfma_k16(nx.w[k], lds4(S0T + r16 * KP + k * 16 + kq), acc);
-        const float uu[4] = {nx.u.x, nx.u.y, nx.u.z, nx.u.w};
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const int t = rw + kq + i;
-            const float d = uu[i] - acc[i];
-            DT[r16 * CP + t] = d;
-            DpT[r16 * CP + t] = Fs[C + t] * d;
-        }
-        if (more) scan_load_wu(nx, Wb, Ub, un, wave, lane, cb);
-        // O rows: G_t (Q S0) ...
         f32x4 o = {0.f, 0.f, 0.f, 0.f};
+        if (rec) {
+            // D rows [rw, rw+16) of this slice: U - W S0
+            f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int k = 0; k < DK / 16; k++)
-            o = mfma_k16(lds4(Qs + (rw + r16) * KP + k * 16 + kq),
-                         lds4(S0T + r16 * KP + k * 16 + kq), o);
+            for (int kb = 0; kb < DK / 32; kb++)
+                acc = mfma_x3(nx.w[kb][0], nx.w[kb][1], ld8(S0h + r16 * SB + kb * 32 + g4 * 8),
+                              ld8(S0l + r16 * SB + kb * 32 + g4 * 8), acc);
+            const float uu[4] = {nx.u.x, nx.u.y, nx.u.z, nx.u.w};
 #pragma unroll
-        for (int i = 0; i < 4; i++) o[i] = Fs[rw + kq + i] * o[i];
+            for (int i = 0; i < 4; i++) {
+                const int t = rw + kq + i;
+                const float d = uu[i] - acc[i];
+                split_bf(d, Dh[r16 * DB + t], Dl[r16 * DB + t]);
+                split_bf(Fs[C + t] * d, Dph[r16 * DB + t], Dpl[r16 * DB + t]);
+            }
+            if (more) scan_load_wu(nx, Wb, Ub, un, wr, lane, cb);
+        } else {
+            // O rows [rw, rw+16): G_t (Q S0)
+#pragma unroll
+            for (int kb = 0; kb < DK / 32; kb++)
+                o = mfma_x3(nx.q[kb][0], nx.q[kb][1], ld8(S0h + r16 * SB + kb * 32 + g4 * 8),
+                            ld8(S0l + r16 * SB + kb * 32 + g4 * 8), o);
+#pragma unroll
+            for (int i = 0; i < 4; i++) o[i] = Fs[rw + kq + i] * o[i];
+        }
         __syncthreads();               // D complete
 
-        // ... + A D over the causal part s < 16(w+1)
-#pragma unroll
-        for (int k = 0; k < C / 16; k++)
-            if (k <= wave) o = mfma_k16(nx.a[k], lds4(DT + r16 * CP + k * 16 + kq), o);
-        if (more) scan_load_a(nx, Ab, un, wave, lane);
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const int t = rw + kq + i;
-            if (t < nt) ob[(size_t)(t0 + t) * vd + (size_t)h * DV + cb * CB + r16] = f2bf(o[i]);
-        }
-
-        // S1^T columns [32w, 32w+32): G_C S0^T + Dp^T K (rows n of the
-        // slice, columns i of the state; K read in place, row-major)
-        const float gc = Fs[C - 1];
         f32x4 sn[2];
+        if (rec) {
+            // S1^T columns [32w, 32w+32): G_C S0^T + Dp^T K
+            const float gc = Fs[C - 1];
 #pragma unroll
-        for (int r = 0; r < 2; r++) {
-            const int i0 = wave * 32 + r * 16;
+            for (int r = 0; r < 2; r++) {
+                const int i0 = wr * 32 + r * 16;
 #pragma unroll
-            for (int i = 0; i < 4; i++) sn[r][i] = gc * S0T[(kq + i) * KP + i0 + r16];
+                for (int i = 0; i < 4; i++) sn[r][i] = gc * S0T[(kq + i) * KP + i0 + r16];
 #pragma unroll
-            for (int k0 = 0; k0 < C; k0 += 16) {
-                const float *kc = Ks + (k0 + kq) * KP + i0 + r16;
-                sn[r] = mfma_k16(lds4(DpT + r16 * CP + k0 + kq),
-                                 make_float4(kc[0], kc[KP], kc[2 * KP], kc[3 * KP]), sn[r]);
+                for (int kb = 0; kb < C / 32; kb++)
+                    sn[r] = mfma_x3(ld8(Dph + r16 * DB + kb * 32 + g4 * 8),
+                                    ld8(Dpl + r16 * DB + kb * 32 + g4 * 8), nx.k[r][kb][0],
+                                    nx.k[r][kb][1], sn[r]);
+            }
+            if (more) scan_load_k(nx, Kp, ukn, wr, lane);
+        } else {
+            // ... + A D over the causal part s < rw + 16, then rnd(o)
+#pragma unroll
+            for (int kb = 0; kb < C / 32; kb++)
+                if (kb <= wr / 2)
+                    o = mfma_x3(nx.a[kb][0], nx.a[kb][1], ld8(Dh + r16 * DB + kb * 32 + g4 * 8),
+                                ld8(Dl + r16 * DB + kb * 32 + g4 * 8), o);
+            if (more) scan_load_out(nx, Qp, Ab, un, ukn, wr, lane);
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int t = rw + kq + i;
+                if (t < nt) ob[(size_t)(t0 + t) * vd + (size_t)h * DV + cb * CB + r16] = f2bf(o[i]);
             }
         }
-        __syncthreads();               // every reader of S0T is done
+        __syncthreads();               // every reader of the state slice and Fs is done
+        if (rec) {
 #pragma unroll
-        for (int r = 0; r < 2; r++) {
-            const int i0 = wave * 32 + r * 16;
+            for (int r = 0; r < 2; r++) {
+                const int i0 = wr * 32 + r * 16;
 #pragma unroll
-            for (int i = 0; i < 4; i++) S0T[(kq + i) * KP + i0 + r16] = sn[r][i];
+                for (int i = 0; i < 4; i++) {
+                    const int n = kq + i, col = i0 + r16;
+                    S0T[n * KP + col] = sn[r][i];
+                    split_bf(sn[r][i], S0h[n * SB + col], S0l[n * SB + col]);
+                }
+            }
         }
+        if (more && tid < 2 * C) Fs[tid] = nx.f;
     }
     __syncthreads();
-    for (int e = tid; e < CB * DK; e += 256) {
+    for (int e = tid; e < CB * DK; e += 512) {
         const int q = e / 64, rem = e % 64, jj = rem / 4, r = rem % 4;
         Sm[((size_t)(jb + q) * 64 + jl + jj) * 4 + r] = S0T[jj * KP + 4 * q + r];
     }
@@ -498,17 +580,19 @@ int apus_hip_gdn_prefill(const ApusHipGdnLayer *L, size_t B, const int32_t *cu,
     if (int r = gdn_prep(L, B, dmeta, Ttot, qkv, a, b, conv_state, &w, true)) return r;
     const size_t units = nch * L->hv;
     float *Ub = (float *)scratch(kScratchGdnChunk, units * C * DV * 4);
-    float *Wb = (float *)scratch(kScratchGdnChunk2, units * C * DK * 4);
-    float *Ab = (float *)scratch(kScratchGdnChunk4, units * C * C * 4);
+    uint16_t *Wb = (uint16_t *)scratch(kScratchGdnChunk2, units * C * DK * 4);
+    uint16_t *Ab = (uint16_t *)scratch(kScratchGdnChunk4, units * C * C * 4);
     float *Fb = (float *)scratch(kScratchGdnChunk5, units * 2 * C * 4);
-    if (!Ub || !Wb || !Ab || !Fb) return kErrHip;
+    uint16_t *Qp = (uint16_t *)scratch(kScratchGdnChunk6, nch * L->hk * C * DK * 4);
+    uint16_t *Kp = (uint16_t *)scratch(kScratchGdnChunk7, nch * L->hk * C * DK * 4);
+    if (!Ub || !Wb || !Ab || !Fb || !Qp || !Kp) return kErrHip;
     APUS_TIMED("k_gdn_chunk_wy",
                k_gdn_chunk_wy<<<(unsigned)units, 256, 0, stream()>>>(
-        sq, kmeta, w.qk, w.vconv, w.gate, w.graw, Ub, Wb, Ab, Fb, (int)L->hk));
+        sq, kmeta, w.qk, w.vconv, w.gate, w.graw, Ub, Wb, Ab, Fb, Qp, Kp, (int)L->hk));
     APUS_LAUNCHED("k_gdn_chunk_wy");
     APUS_TIMED("k_gdn_chunk_scan",
-               k_gdn_chunk_scan<<<(unsigned)(B * L->hv * NCB), 256, 0, stream()>>>(
-        sq, kmeta, w.qk, Ub, Wb, Ab, Fb, S, w.ob, (int)L->hk));
+               k_gdn_chunk_scan<<<(unsigned)(B * L->hv * NCB), 512, 0, stream()>>>(
+        sq, kmeta, Qp, Kp, Ub, Wb, Ab, Fb, S, w.ob, (int)L->hk));
     APUS_LAUNCHED("k_gdn_chunk_scan");
     return gdn_post(L, B, dmeta, Ttot, &w, z, qkv, conv_state, y);
 }
