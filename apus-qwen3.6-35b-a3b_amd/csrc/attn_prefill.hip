@@ -3,23 +3,30 @@
 // causal GQA over the cache, sigmoid output gate) for B sequences of any
 // length, with the attention as an MFMA flash-attention kernel.
 //
-// k_attn_fa: one workgroup per (16-token query tile, kv head), tiles
-// dealt longest first. The 8 q heads of the kv head x 16 tokens are 128
-// query rows; wavefront w owns tokens 4w..4w+3 (32 rows: one MFMA N-tile).
-// Key tiles of 32 (K rows and the cache's 32-key transposed V block) are
-// staged in LDS, the next one prefetched into registers. Two passes over
-// the keys:
+// k_attn_fa: one workgroup of 8 wavefronts (two per SIMD) per (32-token
+// query tile, kv head), tiles dealt longest first. The 8 q heads of the
+// kv head x 32 tokens are 256 query rows; wavefront w owns tokens
+// 4w..4w+3 (32 rows: one MFMA N-tile), its Q rows held in registers.
+// Key tiles of 64 (K rows and the cache's two 32-key transposed V blocks)
+// are copied global -> LDS by the DMA path (global_load_lds, 16 bytes a
+// lane), the next tile's copy in flight while the current one is used;
+// one barrier per tile. Two passes over the keys:
 //   pass 1: S^T = K Q^T on MFMA 32x32x16 bf16 (fp32 accumulation); with
 //           keys on the M side each lane holds 16 keys of ONE query, so
-//           the row max / sum need one exchange between the lane halves.
-//           A = rnd(rnd(q.k) * scale) as the reference rounds it
-//           (c/attn.h:340-347), causal mask key <= query; running max m
-//           and sum s = sum_j e^{A_j - m} per query;
+//           the row max / sum need one exchange between the lane halves
+//           (v_permlane32_swap). A = rnd(rnd(q.k) * scale) as the
+//           reference rounds it (c/attn.h:340-347), causal mask key <=
+//           query; running max m and sum s = sum_j e^{A_j - m} per query;
 //   pass 2: S^T again, then the reference's normalised probabilities
 //           P = rnd(e^{A-m} / s) (c/attn.h:354-360) in bf16, straight from
-//           the S^T accumulator registers into O^T += V^T P^T on MFMA (the
-//           key order each lane half holds is the reduction order both
-//           operands use).
+//           the S^T accumulator registers into O^T += V^T P^T on MFMA.
+// The A-operand row m of S^T is key pi(m) = 16(m/16) + 8((m/4)%2) +
+// 4((m/8)%2) + m%4 of the 32-key step, chosen so that the 8 probabilities
+// a lane feeds to each P.V MFMA are 8 consecutive keys: the V^T operand
+// is then one 16-byte piece of the V block.
+// LDS pieces are XOR-swizzled (16-byte piece c of K row r at c ^ (r%16);
+// of V^T row r at c ^ ((r/4)%4)) so that the MFMA operand reads of 16
+// lanes hit 16 distinct 16-byte bank groups.
 // Epilogue: o = rnd(O), y = rnd(o * rnd(sigmoid(gate))) (c/attn.h:524-531).
 //
 // Numerics: P is the reference's rounding point, so only the MFMA
@@ -45,15 +52,16 @@ using namespace apus;
 namespace {
 
 constexpr int D = 256, GRP = 8;
-constexpr int TQ = 16;                 // query tokens per workgroup
-constexpr int KT = 32;                 // keys per tile
-constexpr int KSTR = D + 8;            // K tile row stride (bf16)
-constexpr int VSTR = KT + 4;           // V^T tile row stride (bf16)
+constexpr int NW = 8;                  // wavefronts per workgroup
+constexpr int TQ = 4 * NW;             // query tokens per workgroup
+constexpr int KT = 64;                 // keys per tile
+constexpr int VB = 32;                 // keys per V^T block of the cache
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef unsigned short u16x8 __attribute__((ext_vector_type(8)));
 typedef unsigned short u16x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) void lds_void;
 
 constexpr int kFaInline = 300;
 struct FaSeqs {
@@ -85,124 +93,129 @@ __device__ __forceinline__ uint32_t pack2(float lo, float hi) {
 }
 __device__ __forceinline__ float rnd_hw(float x) { return (float)(__bf16)x; }
 
-// e^x for the softmax, x <= 0: the hardware exp2 of x*log2(e) (about two
-// ulp; the result is rounded to a bf16 probability, so this stays inside
-// the tolerance class; exp2(-inf) = 0)
-__device__ __forceinline__ float exp_sm(float x) {
-    return __builtin_amdgcn_exp2f(x * 1.44269504088896341f);
+// max / sum of x over lanes l and l ^ 32, in both (v_permlane32_swap
+// exchanges one half of its two operands; with both = x the two results
+// hold x's two halves in some order, and max / + commute)
+__device__ __forceinline__ float max32(float x) {
+    const uint32_t u = __float_as_uint(x);
+    const auto p = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+    return fmaxf(__uint_as_float(p[0]), __uint_as_float(p[1]));
+}
+__device__ __forceinline__ float sum32(float x) {
+    const uint32_t u = __float_as_uint(x);
+    const auto p = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+    return __uint_as_float(p[0]) + __uint_as_float(p[1]);
 }
 
-// Key-tile staging: 16-byte pieces e = r*256 + tid, K rows (key e/32,
-// dims (e%32)*8..) and the V^T block ([d][32 keys], contiguous in the
-// cache: piece e is d = e/4, keys (e%4)*8..). Keys at or past nkeys are
-// zeroed in LDS (never read unwritten cache memory into the sums).
-__device__ __forceinline__ void fa_load_k(u16x8 (&pk)[4], const uint16_t *__restrict__ kc,
-                                          int kb, int tid) {
+// one 16-byte global -> LDS copy per lane through a buffer resource:
+// byte offset voff (per lane) + soff (uniform), LDS address = the
+// wave-uniform base plus 16 * lane. Offsets past the resource's size read
+// as zero.
+__device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, int voff, int soff,
+                                      uint16_t *lds_base) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void *)lds_base, 16, voff, soff, 0, 0);
+}
+
+// K rows of tile kb -> Kb: wavefront w copies rows 8w..8w+7, two rows of
+// 32 pieces per instruction. The resource ends at the last key, so rows
+// past it are zero (and their scores masked).
+__device__ __forceinline__ void fa_dma_k(uint16_t *Kb, __amdgpu_buffer_rsrc_t kr, int kb,
+                                         int wave, int lane) {
 #pragma unroll
-    for (int r = 0; r < 4; r++) {
-        const int e = r * 256 + tid;
-        const int key = e / (D / 8), c8 = (e % (D / 8)) * 8;
-        pk[r] = *reinterpret_cast<const u16x8 *>(kc + (size_t)(kb * KT + key) * D + c8);
+    for (int j = 0; j < 4; j++) {
+        const int r0 = 8 * wave + 2 * j, r = r0 + (lane >> 5);
+        const int c = (lane & 31) ^ (r & 15);
+        dma16(kr, (r * D + c * 8) * 2, kb * KT * D * 2, Kb + r0 * D);
     }
 }
 
-__device__ __forceinline__ void fa_load_v(u16x8 (&pv)[4], const uint16_t *__restrict__ vc,
-                                          int kb, int tid) {
+// V^T blocks 2kb, 2kb+1 -> Vb ([block][d][32 keys]): wavefront w copies
+// the 1 KiB groups 4w..4w+3 (16 d-rows of 4 pieces each). The resource
+// ends at the last key's block; keys past the last one inside that block
+// are zeroed in LDS before use.
+__device__ __forceinline__ void fa_dma_v(uint16_t *Vb, __amdgpu_buffer_rsrc_t vr, int kb,
+                                         int wave, int lane) {
 #pragma unroll
-    for (int r = 0; r < 4; r++)
-        pv[r] = *reinterpret_cast<const u16x8 *>(vc + (size_t)kb * D * KT + (size_t)(r * 256 + tid) * 8);
-}
-
-__device__ __forceinline__ void fa_store_k(uint16_t *Ks, const u16x8 (&pk)[4], int kbase,
-                                           int nkeys, int tid) {
-#pragma unroll
-    for (int r = 0; r < 4; r++) {
-        const int e = r * 256 + tid;
-        const int key = e / (D / 8), c8 = (e % (D / 8)) * 8;
-        u16x8 kv = pk[r];
-        if (kbase + key >= nkeys) kv = u16x8{0, 0, 0, 0, 0, 0, 0, 0};
-        *reinterpret_cast<u16x8 *>(Ks + key * KSTR + c8) = kv;
+    for (int j = 0; j < 4; j++) {
+        const int q = 4 * wave + j, bb = q >> 4, g = q & 15;
+        const int r = 16 * g + (lane >> 2);
+        const int c = (lane & 3) ^ ((r >> 2) & 3);
+        dma16(vr, (bb * D * VB + r * VB + c * 8) * 2, kb * KT * D * 2,
+              Vb + bb * D * VB + g * 16 * VB);
     }
 }
 
-__device__ __forceinline__ void fa_store_v(uint16_t *Vs, const u16x8 (&pv)[4], int kbase,
-                                           int nkeys, int tid) {
-#pragma unroll
-    for (int r = 0; r < 4; r++) {
-        const int e = r * 256 + tid;
-        const int d = e / 4, k8 = (e % 4) * 8;
-        u16x8 vv = pv[r];
-#pragma unroll
-        for (int i = 0; i < 8; i++)
-            if (kbase + k8 + i >= nkeys) vv[i] = 0;
-        uint32_t *dst = reinterpret_cast<uint32_t *>(Vs + d * VSTR + k8);
-        *reinterpret_cast<uint2 *>(dst) = make_uint2((uint32_t)vv[0] | ((uint32_t)vv[1] << 16),
-                                                     (uint32_t)vv[2] | ((uint32_t)vv[3] << 16));
-        *reinterpret_cast<uint2 *>(dst + 2) =
-            make_uint2((uint32_t)vv[4] | ((uint32_t)vv[5] << 16),
-                       (uint32_t)vv[6] | ((uint32_t)vv[7] << 16));
-    }
+// Per-lane LDS byte offsets of the MFMA operands. K operand of S^T step
+// ks: row pi(l32) of the 32-key step, piece (2ks + h) ^ (row % 16), i.e.
+// kbase ^ (ks << 5): the ks bits (5..8) are disjoint from the row bits
+// (9..) and the h bit (4), so one base and one XOR per read suffice.
+__device__ __forceinline__ int fa_kbase(int l32, int h) {
+    const int m = l32;
+    const int row = 16 * (m >> 4) + 8 * ((m >> 2) & 1) + 4 * ((m >> 3) & 1) + (m & 3);
+    const int sw = row & 15;
+    return row * D * 2 + (((h ^ sw) & 1) << 4) + ((sw & 14) << 4);
+}
+// V^T operand of P.V step st, d-tile mt: row 32mt + l32, piece
+// (2st + h) ^ ((row / 4) % 4): vbase ^ (st << 5), plus mt * 2 KiB
+__device__ __forceinline__ int fa_vbase(int l32, int h) {
+    const int sw = (l32 >> 2) & 3;
+    return l32 * VB * 2 + (((h ^ sw) & 1) << 4) + ((sw & 2) << 4);
 }
 
-// Scores of one key tile for this lane's query, in two parts so the
-// callers can interleave them with other work: fa_qk runs S^T = K Q^T on
-// MFMA (two accumulation chains, even / odd 16-dim steps, the K operands
-// of step pair p+1 read while pair p is on the MFMA pipe), fa_round turns
-// it into A = rnd(rnd(q.k) * scale) for keys kbase + 8*(i/4) + 4h + i%4
-// <= qpos, -inf beyond (the compare only on tiles that reach the diagonal
-// of the wavefront's queries).
-__device__ __forceinline__ void fa_qk(f32x16 &sc0, f32x16 &sc1, const uint16_t *Ks,
-                                      const bf16x8 (&qb)[D / 16], int l32, int h) {
+// S^T of the 32 keys at byte offset koff of the K tile for this lane's
+// query (element i <-> key 16(i/8) + 8h + i%8 of the step).
+__device__ __forceinline__ f32x16 fa_qk(const char *Kb, int kbase, const bf16x8 (&qb)[D / 16]) {
+    f32x16 sc;
 #pragma unroll
-    for (int i = 0; i < 16; i++) { sc0[i] = 0.0f; sc1[i] = 0.0f; }
-    const uint16_t *kr = Ks + l32 * KSTR + h * 8;
-    bf16x8 k0 = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u16x8 *>(kr));
-    bf16x8 k1 = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u16x8 *>(kr + 16));
+    for (int i = 0; i < 16; i++) sc[i] = 0.0f;
 #pragma unroll
-    for (int ks = 0; ks < D / 16; ks += 2) {
-        bf16x8 n0 = k0, n1 = k1;
-        if (ks + 2 < D / 16) {
-            n0 = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u16x8 *>(kr + (ks + 2) * 16));
-            n1 = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u16x8 *>(kr + (ks + 3) * 16));
-        }
-        sc0 = mfma32(k0, qb[ks], sc0);
-        sc1 = mfma32(k1, qb[ks + 1], sc1);
-        k0 = n0;
-        k1 = n1;
+    for (int ks = 0; ks < D / 16; ks++) {
+        const bf16x8 k =
+            __builtin_bit_cast(bf16x8, *reinterpret_cast<const u16x8 *>(Kb + (kbase ^ (ks << 5))));
+        sc = mfma32(k, qb[ks], sc);
     }
+    return sc;
 }
 
-__device__ __forceinline__ void fa_round(float (&a)[16], const f32x16 &sc0, const f32x16 &sc1,
-                                         int kbase, int qpos, int qmin, float scale, int h) {
-    if (kbase + KT - 1 <= qmin) {      // wave-uniform: no key of the tile is masked
+// rnd(q.k) with the causal mask (-inf past the query), keys
+// k0 + 16(i/8) + 8h + i%8; the compare only on steps that reach the
+// wavefront's first query
+__device__ __forceinline__ void fa_round(float (&r)[16], const f32x16 &sc, int k0, int qpos,
+                                         int qmin, int h) {
+    if (k0 + 31 <= qmin) {             // wave-uniform: no key of the step is masked
 #pragma unroll
-        for (int i = 0; i < 16; i++) a[i] = rnd_hw(rnd_hw(sc0[i] + sc1[i]) * scale);
+        for (int i = 0; i < 16; i++) r[i] = rnd_hw(sc[i]);
     } else {
 #pragma unroll
         for (int i = 0; i < 16; i++) {
-            const int key = kbase + 8 * (i / 4) + 4 * h + (i % 4);
-            a[i] = key <= qpos ? rnd_hw(rnd_hw(sc0[i] + sc1[i]) * scale) : -INFINITY;
+            const int key = k0 + 16 * (i >> 3) + 8 * h + (i & 7);
+            r[i] = key <= qpos ? rnd_hw(sc[i]) : -INFINITY;
         }
     }
 }
 
-// order of one S^T computation: reads of pairs 0 and 1, then (MFMA pair p,
-// VALU from the caller, reads of pair p+2)
-template <int VALU_PER_PAIR>
-__device__ __forceinline__ void fa_qk_schedule() {
-    __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);       // LDS reads
-#pragma unroll
-    for (int g = 0; g < D / 32 - 2; g++) {
-        __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);   // MFMA
-        __builtin_amdgcn_sched_group_barrier(0x002, VALU_PER_PAIR, 0);
-        __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);   // LDS reads
+// End of a step: this wavefront's copies have landed, then the barrier
+// that publishes them. When the tile just copied is the last one (`last`)
+// and the keys end inside a V block, its V entries past the last key are
+// zeroed (P is 0 there, but 0 * NaN from unwritten cache memory would not
+// be), behind a second barrier.
+__device__ __forceinline__ void fa_sync(uint16_t *Vn, bool last, int nkeys, int tid) {
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (last && nkeys % VB != 0) {
+        const int kbase = (nkeys - 1) / KT * KT;
+        for (int e = tid; e < KT * D; e += 64 * NW) {
+            const int bb = e / (D * VB), rem = e % (D * VB), row = rem / VB, kk = rem % VB;
+            if (kbase + bb * VB + kk >= nkeys) {
+                const int c = (kk >> 3) ^ ((row >> 2) & 3);
+                Vn[bb * D * VB + row * VB + c * 8 + (kk & 7)] = 0;
+            }
+        }
+        __syncthreads();
     }
-    __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
-    __builtin_amdgcn_sched_group_barrier(0x002, VALU_PER_PAIR, 0);
-    __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
 }
 
-__global__ __launch_bounds__(256) void k_attn_fa(
+__global__ __launch_bounds__(64 * NW) void k_attn_fa(
     FaSeqs sq, const int32_t *__restrict__ dmeta, const uint16_t *__restrict__ qn,
     const uint16_t *__restrict__ qg, const uint16_t *__restrict__ kcache,
     const uint16_t *__restrict__ vcache, size_t max_seq, int nh, int nkv, float scale,
@@ -214,29 +227,36 @@ __global__ __launch_bounds__(256) void k_attn_fa(
     const int ntiles = toff[n];
     const int g = ntiles - 1 - (int)(blockIdx.x / nkv);
     const int kvh = blockIdx.x % nkv;
-    const int s = seq_of(toff, n, g);
-    const int tb = cu[s] + (g - toff[s]) * TQ;             // first token of the tile
-    const int nt = min(TQ, cu[s + 1] - tb);
-    const int qpos0 = pos0[s] + (tb - cu[s]);              // its position
+    // workgroup-uniform (loaded values are not provably so: readfirstlane
+    // keeps the buffer resources in SGPRs)
+    const int s = __builtin_amdgcn_readfirstlane(seq_of(toff, n, g));
+    const int tb = __builtin_amdgcn_readfirstlane(cu[s] + (g - toff[s]) * TQ);  // first token
+    const int nt = __builtin_amdgcn_readfirstlane(min(TQ, cu[s + 1] - tb));
+    const int qpos0 = __builtin_amdgcn_readfirstlane(pos0[s] + (tb - cu[s]));  // its position
     const int nkeys = qpos0 + nt;
     const int tid = threadIdx.x, lane = tid & 63, h = lane >> 5, l32 = lane & 31;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
 
-    // K tiles double buffered, V tiles triple buffered: with one barrier
-    // per key tile (after the staging writes), a buffer is rewritten only
-    // after every wavefront has passed a later barrier than its last reader
-    __shared__ __attribute__((aligned(16))) uint16_t Ks[2][KT * KSTR];
-    __shared__ __attribute__((aligned(16))) uint16_t Vs[3][D * VSTR];
+    __shared__ __attribute__((aligned(16))) uint16_t Ks[2][KT * D];
+    __shared__ __attribute__((aligned(16))) uint16_t Vs[2][KT * D];
 
     const uint16_t *kc = kcache + ((size_t)s * nkv + kvh) * max_seq * D;
     const uint16_t *vc = vcache + ((size_t)s * nkv + kvh) * D * max_seq;
+    const int nkt = (nkeys + KT - 1) / KT;
+    const int nblk = (nkeys + VB - 1) / VB;
+    const __amdgpu_buffer_rsrc_t kr = buf_rsrc(kc, (uint32_t)nkeys * D * 2);
+    const __amdgpu_buffer_rsrc_t vr = buf_rsrc(vc, (uint32_t)nblk * D * VB * 2);
+
+    // first K tile in flight while Q is loaded
+    fa_dma_k(Ks[0], kr, 0, wave, lane);
 
     // query row of this lane: token 4w + l32/8, head l32%8 of the kv head
     const int tk = wave * 4 + l32 / GRP, head = kvh * GRP + l32 % GRP;
     const bool qok = tk < nt;
     const int qtok = tb + min(tk, nt - 1);
     const int qpos = qpos0 + tk;
-    const int qmin = qpos0 + wave * 4;          // smallest query position of the wavefront
+    const int qmin = qpos0 + wave * 4;          // the wavefront's first / last query position
+    const int qmax = qmin + 3;
     bf16x8 qb[D / 16];
     {
         const uint16_t *qr = qn + ((size_t)qtok * nh + head) * D + h * 8;
@@ -244,127 +264,92 @@ __global__ __launch_bounds__(256) void k_attn_fa(
         for (int ks = 0; ks < D / 16; ks++)
             qb[ks] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u16x8 *>(qr + ks * 16));
     }
-    const int nkt = (nkeys + KT - 1) / KT;
-    u16x8 pk[4], pv[4];
+    // (A - m) log2(e) = (rnd(q.k) - M) * scale * log2(e) with M = m / scale:
+    // scale is a power of two, so this is the reference's A - m scaled
+    const float c2 = scale * 1.44269504088896341f;
 
-    // ---- pass 1: per-query max m and sum s over all keys. Iteration kb
-    // stages tile kb+1, then scores it on MFMA while the VALU folds tile
-    // kb into (m, s).
-    float m = -INFINITY, lsum = 0.0f;
-    float a[16];
-    fa_load_k(pk, kc, 0, tid);
-    fa_store_k(Ks[0], pk, 0, nkeys, tid);
-    if (nkt > 1) fa_load_k(pk, kc, 1, tid);
-    __syncthreads();
-    {
-        f32x16 s0, s1;
-        fa_qk(s0, s1, Ks[0], qb, l32, h);
-        fa_round(a, s0, s1, 0, qpos, qmin, scale, h);
-    }
-    for (int kb = 0; kb < nkt; kb++) {
-        const bool more = kb + 1 < nkt;
-        if (more) {
-            fa_store_k(Ks[(kb + 1) & 1], pk, (kb + 1) * KT, nkeys, tid);
-            if (kb + 2 < nkt) fa_load_k(pk, kc, kb + 2, tid);
-        }
-        __syncthreads();
-        // next tile's S^T (past the last tile it reads a stale buffer and is
-        // discarded) interleaved with folding tile kb into (m, s)
-        f32x16 s0, s1;
-        fa_qk(s0, s1, Ks[(kb + 1) & 1], qb, l32, h);
-        float mx = -INFINITY;
-#pragma unroll
-        for (int i = 0; i < 16; i++) mx = fmaxf(mx, a[i]);
-        mx = fmaxf(mx, __shfl_xor(mx, 32));
-        const float mn = fmaxf(m, mx);
-        float ps = 0.0f;
-#pragma unroll
-        for (int i = 0; i < 16; i++) ps += exp_sm(a[i] - mn);
-        ps += __shfl_xor(ps, 32);
-        lsum = lsum * exp_sm(m - mn) + ps;     // exp(-inf) = 0 on the first tile
-        m = mn;
-        fa_round(a, s0, s1, (kb + 1) * KT, qpos, qmin, scale, h);
-        fa_qk_schedule<10>();
-    }
-
-    // ---- pass 2: P = rnd(e^{A-m} / s), O^T += V^T P^T (e times 1/s: a
-    // different fp32 quotient only when the two straddle a bf16 rounding
-    // boundary). Iteration kb stages tile kb+1, scores it, and turns tile
-    // kb's scores into P for the P.V MFMAs.
-    const float inv_s = 1.0f / lsum;
     f32x16 o[D / 32];
 #pragma unroll
     for (int mt = 0; mt < D / 32; mt++)
 #pragma unroll
         for (int i = 0; i < 16; i++) o[mt][i] = 0.0f;
-    __syncthreads();                   // pass 1 is done with Ks
-    fa_load_k(pk, kc, 0, tid);
-    fa_load_v(pv, vc, 0, tid);
-    fa_store_k(Ks[0], pk, 0, nkeys, tid);
-    fa_store_v(Vs[0], pv, 0, nkeys, tid);
-    if (nkt > 1) {
-        fa_load_k(pk, kc, 1, tid);
-        fa_load_v(pv, vc, 1, tid);
-    }
+    float M = -INFINITY, lsum = 0.0f;
+
+    __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
-    {
-        f32x16 s0, s1;
-        fa_qk(s0, s1, Ks[0], qb, l32, h);
-        fa_round(a, s0, s1, 0, qpos, qmin, scale, h);
-    }
+
+    // pass 1: per-query max M (in units of rnd(q.k)) and sum s over all
+    // keys; the last step also starts the copy of pass 2's first tile
     for (int kb = 0; kb < nkt; kb++) {
-        const bool more = kb + 1 < nkt;
-        if (more) {
-            fa_store_k(Ks[(kb + 1) & 1], pk, (kb + 1) * KT, nkeys, tid);
-            fa_store_v(Vs[(kb + 1) % 3], pv, (kb + 1) * KT, nkeys, tid);
-            if (kb + 2 < nkt) {
-                fa_load_k(pk, kc, kb + 2, tid);
-                fa_load_v(pv, vc, kb + 2, tid);
+        const int buf = kb & 1;
+        fa_dma_k(Ks[buf ^ 1], kr, kb + 1 < nkt ? kb + 1 : 0, wave, lane);
+        if (kb + 1 == nkt) fa_dma_v(Vs[buf ^ 1], vr, 0, wave, lane);
+        const char *Kb = reinterpret_cast<const char *>(Ks[buf]);
+#pragma unroll
+        for (int sub = 0; sub < KT / 32; sub++) {
+            const int k0 = kb * KT + sub * 32;
+            if (k0 <= qmax) {                  // wave-uniform: else every key is masked
+                int kbase = fa_kbase(l32, h);
+                asm volatile("" : "+v"(kbase));
+                const f32x16 sc = fa_qk(Kb + sub * 32 * D * 2, kbase, qb);
+                float r[16];
+                fa_round(r, sc, k0, qpos, qmin, h);
+                float mx = r[0];
+#pragma unroll
+                for (int i = 1; i < 16; i++) mx = fmaxf(mx, r[i]);
+                mx = max32(mx);
+                const float mn = fmaxf(M, mx);
+                float ps = 0.0f;
+#pragma unroll
+                for (int i = 0; i < 16; i++) ps += __builtin_amdgcn_exp2f((r[i] - mn) * c2);
+                ps = sum32(ps);
+                // first step: M = -inf, lsum = 0 (exp2(-inf) = 0)
+                lsum = lsum * __builtin_amdgcn_exp2f((M - mn) * c2) + ps;
+                M = mn;
             }
         }
-        __syncthreads();
-        // next tile's S^T interleaved with tile kb's probabilities, then
-        // tile kb's P.V interleaved with the next tile's score rounding
-        f32x16 s0, s1;
-        fa_qk(s0, s1, Ks[(kb + 1) & 1], qb, l32, h);
-        uint32_t pp[8];
+        fa_sync(Vs[buf ^ 1], kb + 1 == nkt && nkt == 1, nkeys, tid);
+    }
+    const float inv_s = 1.0f / lsum;
+
+    // pass 2: P = rnd(e^{A-m} / s), O^T += V^T P^T
+    for (int kb = 0; kb < nkt; kb++) {
+        const int buf = (nkt + kb) & 1;
+        if (kb + 1 < nkt) {
+            fa_dma_k(Ks[buf ^ 1], kr, kb + 1, wave, lane);
+            fa_dma_v(Vs[buf ^ 1], vr, kb + 1, wave, lane);
+        }
+        const char *Kb = reinterpret_cast<const char *>(Ks[buf]);
+        const char *Vb = reinterpret_cast<const char *>(Vs[buf]);
 #pragma unroll
-        for (int i = 0; i < 8; i++)
-            pp[i] = pack2(exp_sm(a[2 * i] - m) * inv_s, exp_sm(a[2 * i + 1] - m) * inv_s);
-        fa_qk_schedule<8>();
-        const uint16_t *Vb = Vs[kb % 3];
-        // step st covers keys st*16 + {4h..4h+3, 8+4h..8+4h+3}; the V^T
-        // operand of MFMA j+1 is read while MFMA j runs
-        const uint16_t *vr0 = Vb + l32 * VSTR + 4 * h;
-        uint2 vlo = *reinterpret_cast<const uint2 *>(vr0);
-        uint2 vhi = *reinterpret_cast<const uint2 *>(vr0 + 8);
+        for (int sub = 0; sub < KT / 32; sub++) {
+            const int k0 = kb * KT + sub * 32;
+            int kbase = fa_kbase(l32, h), vbase = fa_vbase(l32, h);
+            asm volatile("" : "+v"(kbase), "+v"(vbase));
+            const f32x16 sc = fa_qk(Kb + sub * 32 * D * 2, kbase, qb);
+            float r[16];
+            fa_round(r, sc, k0, qpos, qmin, h);
+            uint32_t pp[8];
 #pragma unroll
-        for (int j = 0; j < 2 * (D / 32); j++) {
-            const int st = j / (D / 32), mt = j % (D / 32);
-            uint2 nlo = vlo, nhi = vhi;
-            if (j + 1 < 2 * (D / 32)) {
-                const int st1 = (j + 1) / (D / 32), mt1 = (j + 1) % (D / 32);
-                const uint16_t *vr = vr0 + mt1 * 32 * VSTR + st1 * 16;
-                nlo = *reinterpret_cast<const uint2 *>(vr);
-                nhi = *reinterpret_cast<const uint2 *>(vr + 8);
+            for (int i = 0; i < 8; i++)
+                pp[i] = pack2(__builtin_amdgcn_exp2f((r[2 * i] - M) * c2) * inv_s,
+                              __builtin_amdgcn_exp2f((r[2 * i + 1] - M) * c2) * inv_s);
+            const char *Vsub = Vb + sub * D * VB * 2;
+#pragma unroll
+            for (int st = 0; st < 2; st++) {
+                const uint32_t w4[4] = {pp[4 * st], pp[4 * st + 1], pp[4 * st + 2],
+                                        pp[4 * st + 3]};
+                const bf16x8 pb = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u16x8 *>(w4));
+                const char *Vst = Vsub + (vbase ^ (st << 5));
+#pragma unroll
+                for (int mt = 0; mt < D / 32; mt++) {
+                    const bf16x8 va = __builtin_bit_cast(
+                        bf16x8, *reinterpret_cast<const u16x8 *>(Vst + mt * 32 * VB * 2));
+                    o[mt] = mfma32(va, pb, o[mt]);
+                }
             }
-            const uint32_t w4[4] = {pp[4 * st], pp[4 * st + 1], pp[4 * st + 2], pp[4 * st + 3]};
-            const bf16x8 pb = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u16x8 *>(w4));
-            const uint32_t v4[4] = {vlo.x, vlo.y, vhi.x, vhi.y};
-            const bf16x8 va = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u16x8 *>(v4));
-            o[mt] = mfma32(va, pb, o[mt]);
-            vlo = nlo;
-            vhi = nhi;
         }
-        fa_round(a, s0, s1, (kb + 1) * KT, qpos, qmin, scale, h);
-        __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);   // LDS reads
-#pragma unroll
-        for (int j = 0; j < 2 * (D / 32) - 2; j++) {
-            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // MFMA
-            __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);   // VALU
-            __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);   // LDS reads
-        }
-        __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+        if (kb + 1 < nkt) fa_sync(Vs[buf ^ 1], kb + 2 == nkt, nkeys, tid);
     }
 
     // epilogue: o = rnd(O); y = rnd(o * rnd(sigmoid(gate)))
@@ -403,7 +388,7 @@ int apus_hip_attn_prefill(const ApusHipAttnLayer *L, size_t B, const int32_t *cu
     if (int r = attn_check_layer(L)) return r;
     if (B == 0) return kOk;
     if (!cu || !pos0 || cu[0] != 0) return set_error(kErrArgument, "bad offsets");
-    if (max_seq % KT != 0) return set_error(kErrArgument, "max_seq must be a multiple of %d", KT);
+    if (max_seq % VB != 0) return set_error(kErrArgument, "max_seq must be a multiple of %d", VB);
     if (L->nh != GRP * L->nkv)
         return set_error(kErrUnsupported, "prefill supports nh = %d * nkv", GRP);
     size_t max_pos = 0;
@@ -458,7 +443,7 @@ int apus_hip_attn_prefill(const ApusHipAttnLayer *L, size_t B, const int32_t *cu
     const ActTables *tabs = act_tables();
     if (!tabs) return kErrHip;
     APUS_TIMED("k_attn_fa",
-               k_attn_fa<<<(unsigned)(ntiles * L->nkv), 256, 0, stream()>>>(
+               k_attn_fa<<<(unsigned)(ntiles * L->nkv), 64 * NW, 0, stream()>>>(
                    fs, fdm, qn, qg, kcache, vcache, max_seq, (int)L->nh, (int)L->nkv, scale, y,
                    tabs->sig_bf));
     APUS_LAUNCHED("k_attn_fa");
