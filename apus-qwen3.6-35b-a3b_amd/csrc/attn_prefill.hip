@@ -7,10 +7,8 @@
 // query tile, kv head), tiles dealt longest first. The 8 q heads of the
 // kv head x 32 tokens are 256 query rows; wavefront w owns tokens
 // 4w..4w+3 (32 rows: one MFMA N-tile), its Q rows held in registers.
-// Key tiles of 64 (K rows and the cache's two 32-key transposed V blocks)
-// are copied global -> LDS by the DMA path (global_load_lds, 16 bytes a
-// lane), the next tile's copy in flight while the current one is used;
-// one barrier per tile. Two passes over the keys:
+//
+// The attention runs over the keys twice:
 //   pass 1: S^T = K Q^T on MFMA 32x32x16 bf16 (fp32 accumulation); with
 //           keys on the M side each lane holds 16 keys of ONE query, so
 //           the row max / sum need one exchange between the lane halves
@@ -20,6 +18,22 @@
 //   pass 2: S^T again, then the reference's normalised probabilities
 //           P = rnd(e^{A-m} / s) (c/attn.h:354-360) in bf16, straight from
 //           the S^T accumulator registers into O^T += V^T P^T on MFMA.
+// Each pass is a software pipeline over 32-key steps that keeps the MFMA
+// pipe fed while the softmax runs on the VALU: in pass 1 step j issues
+// the MFMAs of S(j+1) interleaved with the max / sum fold of S(j); in
+// pass 2 step j computes S(j), then the MFMAs of P(j-1).V(j-1)
+// interleaved with forming P(j) (one set of scores and one of packed
+// probabilities live at a time: the O^T accumulators take half of the
+// wavefront's 256 registers).
+//
+// Keys arrive in tiles of 64 (K rows and the cache's two 32-key
+// transposed V blocks), copied global -> LDS by buffer DMA (16 bytes a
+// lane), one tile ahead, with one barrier per tile. A pass-2 tile's steps
+// read its K and V and the previous tile's V, so K is double and V triple
+// buffered (5 x 32 KiB, all of LDS). The DMA is issued as inline assembly
+// with explicit waits: the compiler would otherwise make every LDS read
+// wait for the copy in flight into another buffer.
+//
 // The A-operand row m of S^T is key pi(m) = 16(m/16) + 8((m/4)%2) +
 // 4((m/8)%2) + m%4 of the 32-key step, chosen so that the 8 probabilities
 // a lane feeds to each P.V MFMA are 8 consecutive keys: the V^T operand
@@ -52,15 +66,22 @@ using namespace apus;
 namespace {
 
 constexpr int D = 256, GRP = 8;
-constexpr int NW = 8;                  // wavefronts per workgroup
+constexpr int NW = 8;                  // wavefronts per workgroup, two per SIMD
 constexpr int TQ = 4 * NW;             // query tokens per workgroup
 constexpr int KT = 64;                 // keys per tile
 constexpr int VB = 32;                 // keys per V^T block of the cache
+constexpr int TILE_BYTES = KT * D * 2; // one K or V tile in the cache
+constexpr int KROW = D * 2 + 16;       // K row pitch in LDS (one 16-byte pad)
+constexpr int KBUF = KT * KROW;        // one K tile in LDS
+constexpr int KHALF = 32 * KROW;       // its second 32 keys
+constexpr int VHALF = 32 * D * 2;      // one 32-key V^T block in LDS
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef unsigned short u16x8 __attribute__((ext_vector_type(8)));
 typedef unsigned short u16x4 __attribute__((ext_vector_type(4)));
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x8_t __attribute__((ext_vector_type(8)));
 typedef __attribute__((address_space(3))) void lds_void;
 
 constexpr int kFaInline = 300;
@@ -107,112 +128,302 @@ __device__ __forceinline__ float sum32(float x) {
     return __uint_as_float(p[0]) + __uint_as_float(p[1]);
 }
 
-// one 16-byte global -> LDS copy per lane through a buffer resource:
-// byte offset voff (per lane) + soff (uniform), LDS address = the
-// wave-uniform base plus 16 * lane. Offsets past the resource's size read
-// as zero.
-__device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, int voff, int soff,
-                                      uint16_t *lds_base) {
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void *)lds_base, 16, voff, soff, 0, 0);
+// the lane index, opaque to the compiler: values derived from it are
+// formed where they are used rather than hoisted and held in registers
+// across the key loop (registers are the binding resource here)
+__device__ __forceinline__ int fa_lane() {
+    int l = __lane_id();
+    asm volatile("" : "+v"(l));
+    return l;
 }
 
-// K rows of tile kb -> Kb: wavefront w copies rows 8w..8w+7, two rows of
-// 32 pieces per instruction. The resource ends at the last key, so rows
-// past it are zero (and their scores masked).
-__device__ __forceinline__ void fa_dma_k(uint16_t *Kb, __amdgpu_buffer_rsrc_t kr, int kb,
-                                         int wave, int lane) {
+// Buffer resource (SGPRs) over `bytes` bytes at base; offsets past the
+// end read as zero.
+__device__ __forceinline__ i32x4 fa_rsrc(const void *base, uint32_t bytes) {
+    const uint64_t a = (uint64_t)base;
+    return i32x4{__builtin_amdgcn_readfirstlane((int)(uint32_t)a),
+                 __builtin_amdgcn_readfirstlane((int)(uint32_t)(a >> 32) & 0xffff),
+                 __builtin_amdgcn_readfirstlane((int)bytes), 0x00020000};
+}
+
+// one 16-byte global -> LDS copy per lane: byte offset voff (per lane) +
+// soff (uniform); LDS byte address lds (uniform) + 16 * lane. Counted by
+// vmcnt; the caller waits before the barrier that publishes the tile.
+__device__ __forceinline__ void dma16(i32x4 r, int voff, int soff, uint32_t lds) {
+    soff = __builtin_amdgcn_readfirstlane(soff);
+    lds = __builtin_amdgcn_readfirstlane(lds);
+    asm volatile("s_mov_b32 m0, %3\n\tbuffer_load_dwordx4 %0, %1, %2 offen lds"
+                 :: "v"(voff), "s"(r), "s"(soff), "s"(lds) : "memory", "m0");
+}
+
+// K rows of key tile kt -> the K buffer at LDS address kb (row pitch
+// KROW): wavefront w copies rows 8w..8w+7, one row (32 pieces, lanes
+// 0..31) per instruction. The resource ends at the last key, so rows past
+// it are zero (and their scores masked).
+__device__ __forceinline__ void fa_dma_k(uint32_t kb, i32x4 kr, int kt, int wave) {
+    const int lane = fa_lane();
+    if (lane < 32) {
 #pragma unroll
-    for (int j = 0; j < 4; j++) {
-        const int r0 = 8 * wave + 2 * j, r = r0 + (lane >> 5);
-        const int c = (lane & 31) ^ (r & 15);
-        dma16(kr, (r * D + c * 8) * 2, kb * KT * D * 2, Kb + r0 * D);
+        for (int j = 0; j < 8; j++) {
+            const int r = 8 * wave + j;
+            dma16(kr, (r * D + lane * 8) * 2, kt * TILE_BYTES, kb + r * KROW);
+        }
     }
 }
 
-// V^T blocks 2kb, 2kb+1 -> Vb ([block][d][32 keys]): wavefront w copies
-// the 1 KiB groups 4w..4w+3 (16 d-rows of 4 pieces each). The resource
-// ends at the last key's block; keys past the last one inside that block
-// are zeroed in LDS before use.
-__device__ __forceinline__ void fa_dma_v(uint16_t *Vb, __amdgpu_buffer_rsrc_t vr, int kb,
-                                         int wave, int lane) {
+// V^T blocks 2kt, 2kt+1 -> the LDS blocks at vb0, vb1 ([d][32 keys]):
+// wavefront w copies the 1 KiB groups 4w..4w+3 of block w / 4 (16 d-rows
+// of 4 pieces each). The resource ends at the last key's block; keys past
+// the last one inside that block are zeroed in LDS before use.
+__device__ __forceinline__ void fa_dma_v(uint32_t vb0, uint32_t vb1, i32x4 vr, int kt, int wave) {
+    const int lane = fa_lane();
 #pragma unroll
     for (int j = 0; j < 4; j++) {
         const int q = 4 * wave + j, bb = q >> 4, g = q & 15;
         const int r = 16 * g + (lane >> 2);
         const int c = (lane & 3) ^ ((r >> 2) & 3);
-        dma16(vr, (bb * D * VB + r * VB + c * 8) * 2, kb * KT * D * 2,
-              Vb + bb * D * VB + g * 16 * VB);
+        dma16(vr, (bb * D * VB + r * VB + c * 8) * 2, kt * TILE_BYTES,
+              (bb ? vb1 : vb0) + g * 16 * VB * 2);
     }
 }
 
 // Per-lane LDS byte offsets of the MFMA operands. K operand of S^T step
-// ks: row pi(l32) of the 32-key step, piece (2ks + h) ^ (row % 16), i.e.
-// kbase ^ (ks << 5): the ks bits (5..8) are disjoint from the row bits
-// (9..) and the h bit (4), so one base and one XOR per read suffice.
-__device__ __forceinline__ int fa_kbase(int l32, int h) {
+// ks: row pi(l32) of the 32-key step, piece 2ks + h: kbase + 32 ks (an
+// immediate offset). The 16-byte pad per K row puts the 16 rows one read
+// covers in 16 distinct 16-byte bank groups.
+__device__ __forceinline__ int fa_kbase() {
+    const int lane = fa_lane(), l32 = lane & 31, h = lane >> 5;
     const int m = l32;
     const int row = 16 * (m >> 4) + 8 * ((m >> 2) & 1) + 4 * ((m >> 3) & 1) + (m & 3);
-    const int sw = row & 15;
-    return row * D * 2 + (((h ^ sw) & 1) << 4) + ((sw & 14) << 4);
+    return row * KROW + h * 16;
 }
 // V^T operand of P.V step st, d-tile mt: row 32mt + l32, piece
 // (2st + h) ^ ((row / 4) % 4): vbase ^ (st << 5), plus mt * 2 KiB
-__device__ __forceinline__ int fa_vbase(int l32, int h) {
+__device__ __forceinline__ int fa_vbase() {
+    const int lane = fa_lane(), l32 = lane & 31, h = lane >> 5;
     const int sw = (l32 >> 2) & 3;
     return l32 * VB * 2 + (((h ^ sw) & 1) << 4) + ((sw & 2) << 4);
 }
 
-// S^T of the 32 keys at byte offset koff of the K tile for this lane's
-// query (element i <-> key 16(i/8) + 8h + i%8 of the step).
-__device__ __forceinline__ f32x16 fa_qk(const char *Kb, int kbase, const bf16x8 (&qb)[D / 16]) {
+__device__ __forceinline__ u16x8 lds16(const char *p) {
+    return *reinterpret_cast<const u16x8 *>(p);
+}
+
+// the LDS tile buffers: K tiles 0..1, then a ring of five 32-key V^T
+// blocks (tile u's block h in slot (2u + h) % 5: a step reads the block of
+// the step before it, so at most five are live or in flight)
+__shared__ __attribute__((aligned(16))) char fa_lds[2 * KBUF + 5 * VHALF];
+
+struct FaCtx {
+    i32x4 kr, vr;                      // this (sequence, kv head)'s K rows / V^T blocks
+    int nkt, nkeys;                    // key tiles, keys
+    int tid, wave, lane, l32, h;
+    float c2;                          // scale * log2(e)
+    uint32_t lds;                      // LDS address of fa_lds
+};
+
+// running softmax state of one query row (per lane)
+struct FaRow {
+    int qpos;                          // query position
+    float M, lsum;                     // max (units of rnd(q.k)), sum of e^{A - m}
+    float K2;                          // pass 2: M * scale * log2(e) + log2(sum)
+};
+
+// Instruction order. Each phase below is its own basic block (fa_split:
+// a uniform branch on a runtime value the compiler cannot fold), so the
+// scheduler cannot mix the K reads of an S block with the V reads of a
+// P.V block or pull a later step's reads forward; inside a block,
+// scheduling-group barriers lay out (operand read DEPTH ahead, MFMA,
+// VALU slice) groups. Left free, the scheduler issues all operand reads of
+// a step first and spills Q.
+__device__ __forceinline__ void fa_split(int opaque) {
+    if (__builtin_expect(opaque == -12345, 0)) asm volatile("s_nop 0");
+}
+
+// DEPTH LDS reads, then (1 MFMA, NVALU VALU, 1 read) x (16 - DEPTH), then
+// (1 MFMA, NVALU VALU) x DEPTH
+template <int DEPTH, int NVALU>
+__device__ __forceinline__ void fa_groups16() {
+    __builtin_amdgcn_sched_group_barrier(0x100, DEPTH, 0);   // LDS reads
+#pragma unroll
+    for (int i = 0; i < 16 - DEPTH; i++) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // MFMA
+        if (NVALU) __builtin_amdgcn_sched_group_barrier(0x002, NVALU, 0);
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+    }
+#pragma unroll
+    for (int i = 0; i < DEPTH; i++) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        if (NVALU) __builtin_amdgcn_sched_group_barrier(0x002, NVALU, 0);
+    }
+}
+
+// The softmax arithmetic per score, on the VALU, kept to a few
+// instructions because it is only partly hidden under the MFMAs:
+//   r   = rnd(q.k)                       v_cvt_pk_bf16_f32 (two scores),
+//                                        then a shift / mask to fp32
+//   arg = r * c2 - K                     v_fma_f32 (c2 = scale * log2(e),
+//                                        a power of two times log2(e))
+//   e   = exp2(arg)                      v_exp_f32
+// pass 1 (K = m * c2): the running sum of e; the row max is taken on the
+// unrounded scores (rnd is monotone: max rnd(x) = rnd(max x));
+// pass 2 (K = m * c2 + log2(s)): P = rnd(e) = rnd(e^{A-m} / s), the
+// reference's normalised probability (c/attn.h:354-360) with the division
+// folded into the exponent: a relative difference of a few 1e-7 from the
+// quotient, which moves P by one bf16 ulp only when e / s lies that close
+// to a rounding boundary -- the tolerance class of the hardware exp2.
+// Scores past the query (key kj + 16(i/8) + 8h + i%8 > qpos) are masked
+// only on steps that reach the diagonal (MASK).
+__device__ __forceinline__ bool fa_keep(int i, int lim) {
+    return 16 * (i >> 3) + (i & 7) <= lim;
+}
+// e_i = exp2(rnd(sc_i) * c2 - K), 0 where masked
+template <bool MASK>
+__device__ __forceinline__ void fa_exp16(float (&e)[16], const f32x16 &sc, float c2, float K,
+                                         int lim) {
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+        const uint32_t pk = pack2(sc[2 * j], sc[2 * j + 1]);
+        e[2 * j] = __builtin_amdgcn_exp2f(fmaf(__uint_as_float(pk << 16), c2, -K));
+        e[2 * j + 1] = __builtin_amdgcn_exp2f(fmaf(__uint_as_float(pk & 0xffff0000u), c2, -K));
+    }
+    if (MASK) {
+#pragma unroll
+        for (int i = 0; i < 16; i++) e[i] = fa_keep(i, lim) ? e[i] : 0.0f;
+    }
+}
+
+// the K operand address of S^T step ks
+__device__ __forceinline__ const char *fa_kaddr(const char *Kp, int kbase, int ks) {
+    return Kp + kbase + ks * 32;
+}
+// the V^T operand address of P.V MFMA jj (step jj/8, d-tile jj%8)
+__device__ __forceinline__ const char *fa_vaddr(const char *Vp, int vbase, int jj) {
+    return Vp + (vbase ^ ((jj >> 3) << 5)) + (jj & 7) * 32 * VB * 2;
+}
+
+// S^T of the 32-key K block at byte offset Kn of fa_lds for this lane's
+// query (element i <-> key 16(i/8) + 8h + i%8 of the block), operands
+// read 4 ahead; no other work.
+__device__ __forceinline__ f32x16 fa_s(const FaCtx &c, int Kn, const bf16x8 (&q)[D / 16]) {
+    const int kbase = fa_kbase();
+    const char *Kp = fa_lds + Kn;
     f32x16 sc;
 #pragma unroll
     for (int i = 0; i < 16; i++) sc[i] = 0.0f;
+    u16x8 kq[3];
+#pragma unroll
+    for (int i = 0; i < 3; i++) kq[i] = lds16(fa_kaddr(Kp, kbase, i));
 #pragma unroll
     for (int ks = 0; ks < D / 16; ks++) {
-        const bf16x8 k =
-            __builtin_bit_cast(bf16x8, *reinterpret_cast<const u16x8 *>(Kb + (kbase ^ (ks << 5))));
-        sc = mfma32(k, qb[ks], sc);
+        const bf16x8 k = __builtin_bit_cast(bf16x8, kq[ks % 3]);
+        if (ks + 3 < D / 16) kq[ks % 3] = lds16(fa_kaddr(Kp, kbase, ks + 3));
+        sc = mfma32(k, q[ks], sc);
     }
+    fa_groups16<3, 0>();
+    fa_split(c.nkeys);
     return sc;
 }
 
-// rnd(q.k) with the causal mask (-inf past the query), keys
-// k0 + 16(i/8) + 8h + i%8; the compare only on steps that reach the
-// wavefront's first query
-__device__ __forceinline__ void fa_round(float (&r)[16], const f32x16 &sc, int k0, int qpos,
-                                         int qmin, int h) {
-    if (k0 + 31 <= qmin) {             // wave-uniform: no key of the step is masked
+// pass-1 step j: S(j+1) from the K block at Kn (when NEXT), interleaved
+// with folding S(j) = sc (keys from kj) into the row's running max / sum.
+template <bool NEXT, bool MASK>
+__device__ __forceinline__ void fa_p1_step(const FaCtx &c, int Kn, int kj,
+                                           const bf16x8 (&q)[D / 16], f32x16 &sc, FaRow &w) {
+    const int lim = w.qpos - kj - 8 * (fa_lane() >> 5);
+    f32x16 nx;
+    if (NEXT) {
+        const int kbase = fa_kbase();
+        const char *Kp = fa_lds + Kn;
 #pragma unroll
-        for (int i = 0; i < 16; i++) r[i] = rnd_hw(sc[i]);
-    } else {
+        for (int i = 0; i < 16; i++) nx[i] = 0.0f;
+        u16x8 kq[4];
 #pragma unroll
-        for (int i = 0; i < 16; i++) {
-            const int key = k0 + 16 * (i >> 3) + 8 * h + (i & 7);
-            r[i] = key <= qpos ? rnd_hw(sc[i]) : -INFINITY;
+        for (int i = 0; i < 4; i++) kq[i] = lds16(fa_kaddr(Kp, kbase, i));
+#pragma unroll
+        for (int ks = 0; ks < D / 16; ks++) {
+            const bf16x8 k = __builtin_bit_cast(bf16x8, kq[ks & 3]);
+            if (ks + 4 < D / 16) kq[ks & 3] = lds16(fa_kaddr(Kp, kbase, ks + 4));
+            nx = mfma32(k, q[ks], nx);
         }
+    }
+    float mx = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < 16; i++) mx = fmaxf(mx, !MASK || fa_keep(i, lim) ? sc[i] : -INFINITY);
+    const float mn = fmaxf(w.M, rnd_hw(max32(mx)));
+    float e[16];
+    fa_exp16<MASK>(e, sc, c.c2, mn * c.c2, lim);
+    float ps = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 16; i++) ps += e[i];
+    // first step: M = -inf, lsum = 0 (exp2(-inf) = 0); key 0 is in every
+    // row's first step, so M is finite from then on
+    w.lsum = w.lsum * __builtin_amdgcn_exp2f((w.M - mn) * c.c2) + sum32(ps);
+    w.M = mn;
+    if (NEXT) {
+        fa_groups16<4, 4>();
+        sc = nx;
+    }
+    fa_split(c.nkeys);
+}
+
+// pass-2 step j: S(j) from the K block at Kn; then (when PV) the MFMAs of
+// P(j-1).V(j-1) from the V block at Vp, interleaved with forming P(j)
+// (keys from kj). pp holds P(j-1) on entry and P(j) on
+// return, as the B operands of the two P.V steps (keys 8h..8h+7 and
+// 16 + 8h..).
+template <bool PV, bool MASK>
+__device__ __forceinline__ void fa_p2_step(const FaCtx &c, int Kn, int Vp, int kj,
+                                           const bf16x8 (&q)[D / 16], const FaRow &w,
+                                           bf16x8 (&pp)[2], f32x16 (&o)[D / 32]) {
+    const f32x16 sc = fa_s(c, Kn, q);
+    const int lim = w.qpos - kj - 8 * (fa_lane() >> 5);
+    if (PV) {
+        const int vbase = fa_vbase();
+        const char *Vb = fa_lds + Vp;
+        u16x8 vq[2];
+#pragma unroll
+        for (int i = 0; i < 2; i++) vq[i] = lds16(fa_vaddr(Vb, vbase, i));
+#pragma unroll
+        for (int jj = 0; jj < 2 * (D / 32); jj++) {
+            const bf16x8 va = __builtin_bit_cast(bf16x8, vq[jj & 1]);
+            if (jj + 2 < 2 * (D / 32)) vq[jj & 1] = lds16(fa_vaddr(Vb, vbase, jj + 2));
+            o[jj & 7] = mfma32(va, pp[jj >> 3], o[jj & 7]);
+        }
+    }
+    float e[16];
+    fa_exp16<MASK>(e, sc, c.c2, w.K2, lim);
+    uint32_t pw[8];
+#pragma unroll
+    for (int i = 0; i < 8; i++) pw[i] = pack2(e[2 * i], e[2 * i + 1]);
+    if (PV) fa_groups16<2, 4>();
+    // keep P(j) in this block (else it is sunk past the next step's S)
+    asm volatile("" : "+v"(pw[0]), "+v"(pw[1]), "+v"(pw[2]), "+v"(pw[3]), "+v"(pw[4]),
+                 "+v"(pw[5]), "+v"(pw[6]), "+v"(pw[7]));
+#pragma unroll
+    for (int st = 0; st < 2; st++) {
+        const uint32_t w4[4] = {pw[4 * st], pw[4 * st + 1], pw[4 * st + 2], pw[4 * st + 3]};
+        pp[st] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u16x8 *>(w4));
+    }
+    fa_split(c.nkeys);
+}
+
+// the last P.V (no S after it)
+__device__ __forceinline__ void fa_pv_last(const FaCtx &c, int Vp, const bf16x8 (&pp)[2],
+                                           f32x16 (&o)[D / 32]) {
+    const int vbase = fa_vbase();
+    const char *Vb = fa_lds + Vp;
+#pragma unroll
+    for (int jj = 0; jj < 2 * (D / 32); jj++) {
+        const bf16x8 va = __builtin_bit_cast(bf16x8, lds16(fa_vaddr(Vb, vbase, jj)));
+        o[jj & 7] = mfma32(va, pp[jj >> 3], o[jj & 7]);
     }
 }
 
-// End of a step: this wavefront's copies have landed, then the barrier
-// that publishes them. When the tile just copied is the last one (`last`)
-// and the keys end inside a V block, its V entries past the last key are
-// zeroed (P is 0 there, but 0 * NaN from unwritten cache memory would not
-// be), behind a second barrier.
-__device__ __forceinline__ void fa_sync(uint16_t *Vn, bool last, int nkeys, int tid) {
-    __builtin_amdgcn_s_waitcnt(0);
+// wait for this wavefront's copies, then the barrier that publishes them
+__device__ __forceinline__ void fa_publish() {
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
-    if (last && nkeys % VB != 0) {
-        const int kbase = (nkeys - 1) / KT * KT;
-        for (int e = tid; e < KT * D; e += 64 * NW) {
-            const int bb = e / (D * VB), rem = e % (D * VB), row = rem / VB, kk = rem % VB;
-            if (kbase + bb * VB + kk >= nkeys) {
-                const int c = (kk >> 3) ^ ((row >> 2) & 3);
-                Vn[bb * D * VB + row * VB + c * 8 + (kk & 7)] = 0;
-            }
-        }
-        __syncthreads();
-    }
 }
 
 __global__ __launch_bounds__(64 * NW) void k_attn_fa(
@@ -228,140 +439,135 @@ __global__ __launch_bounds__(64 * NW) void k_attn_fa(
     const int g = ntiles - 1 - (int)(blockIdx.x / nkv);
     const int kvh = blockIdx.x % nkv;
     // workgroup-uniform (loaded values are not provably so: readfirstlane
-    // keeps the buffer resources in SGPRs)
+    // keeps them in SGPRs)
     const int s = __builtin_amdgcn_readfirstlane(seq_of(toff, n, g));
     const int tb = __builtin_amdgcn_readfirstlane(cu[s] + (g - toff[s]) * TQ);  // first token
     const int nt = __builtin_amdgcn_readfirstlane(min(TQ, cu[s + 1] - tb));
     const int qpos0 = __builtin_amdgcn_readfirstlane(pos0[s] + (tb - cu[s]));  // its position
-    const int nkeys = qpos0 + nt;
-    const int tid = threadIdx.x, lane = tid & 63, h = lane >> 5, l32 = lane & 31;
-    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
 
-    __shared__ __attribute__((aligned(16))) uint16_t Ks[2][KT * D];
-    __shared__ __attribute__((aligned(16))) uint16_t Vs[2][KT * D];
-
+    FaCtx c;
+    c.nkeys = qpos0 + nt;
+    c.tid = threadIdx.x;
+    c.lane = c.tid & 63;
+    c.h = c.lane >> 5;
+    c.l32 = c.lane & 31;
+    c.wave = __builtin_amdgcn_readfirstlane(c.tid >> 6);
     const uint16_t *kc = kcache + ((size_t)s * nkv + kvh) * max_seq * D;
     const uint16_t *vc = vcache + ((size_t)s * nkv + kvh) * D * max_seq;
-    const int nkt = (nkeys + KT - 1) / KT;
-    const int nblk = (nkeys + VB - 1) / VB;
-    const __amdgpu_buffer_rsrc_t kr = buf_rsrc(kc, (uint32_t)nkeys * D * 2);
-    const __amdgpu_buffer_rsrc_t vr = buf_rsrc(vc, (uint32_t)nblk * D * VB * 2);
+    c.nkt = (c.nkeys + KT - 1) / KT;
+    const int nblk = (c.nkeys + VB - 1) / VB;
+    c.kr = fa_rsrc(kc, (uint32_t)c.nkeys * D * 2);
+    c.vr = fa_rsrc(vc, (uint32_t)nblk * D * VB * 2);
+    c.lds = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(lds_void *)fa_lds);
+    c.c2 = scale * 1.44269504088896341f;
+    const int nkt = c.nkt;
+    // byte offsets of tile u's buffers in fa_lds
+    auto kbuf = [&](int u) { return (u & 1) * KBUF; };
+    auto vbuf = [&](int u, int half) { return 2 * KBUF + ((2 * u + half) % 5) * VHALF; };
 
-    // first K tile in flight while Q is loaded
-    fa_dma_k(Ks[0], kr, 0, wave, lane);
+    // tile u = 0 .. 2nkt-1 of the key stream: pass u / nkt, key tile u % nkt
+    fa_dma_k(c.lds + kbuf(0), c.kr, 0, c.wave);
 
     // query row of this lane: token 4w + l32/8, head l32%8 of the kv head
-    const int tk = wave * 4 + l32 / GRP, head = kvh * GRP + l32 % GRP;
-    const bool qok = tk < nt;
-    const int qtok = tb + min(tk, nt - 1);
-    const int qpos = qpos0 + tk;
-    const int qmin = qpos0 + wave * 4;          // the wavefront's first / last query position
-    const int qmax = qmin + 3;
-    bf16x8 qb[D / 16];
+    const int tk = c.wave * 4 + c.l32 / GRP, head = kvh * GRP + c.l32 % GRP;
+    bf16x8 q[D / 16];
     {
-        const uint16_t *qr = qn + ((size_t)qtok * nh + head) * D + h * 8;
+        const uint16_t *qr = qn + ((size_t)(tb + min(tk, nt - 1)) * nh + head) * D + c.h * 8;
 #pragma unroll
         for (int ks = 0; ks < D / 16; ks++)
-            qb[ks] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u16x8 *>(qr + ks * 16));
+            q[ks] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u16x8 *>(qr + ks * 16));
     }
-    // (A - m) log2(e) = (rnd(q.k) - M) * scale * log2(e) with M = m / scale:
-    // scale is a power of two, so this is the reference's A - m scaled
-    const float c2 = scale * 1.44269504088896341f;
+    FaRow w{qpos0 + tk, -INFINITY, 0.0f, 0.0f};
 
+    // Tile u = 0 .. 2nkt-1 of the key stream: pass u / nkt, key tile
+    // u % nkt. begin_tile(u) publishes tile u and starts the copy of u+1.
+    auto begin_tile = [&](int u) {
+        fa_publish();
+        if (u + 1 < 2 * nkt) {
+            fa_dma_k(c.lds + kbuf(u + 1), c.kr, (u + 1) % nkt, c.wave);
+            if (u + 1 >= nkt)
+                fa_dma_v(c.lds + vbuf(u + 1, 0), c.lds + vbuf(u + 1, 1), c.vr, u + 1 - nkt, c.wave);
+        }
+        // the last tile's V keys past nkeys: zero (P is 0 there, but
+        // 0 * NaN from unwritten cache memory would not be)
+        if (u == 2 * nkt - 1 && c.nkeys % VB != 0) {
+            const int kbase = (nkt - 1) * KT;
+            for (int e = c.tid; e < KT * D; e += 64 * NW) {
+                const int bb = e / (D * VB), rem = e % (D * VB), row = rem / VB, kk = rem % VB;
+                if (kbase + bb * VB + kk >= c.nkeys) {
+                    uint16_t *Vn = reinterpret_cast<uint16_t *>(fa_lds + vbuf(u, bb));
+                    const int cc = (kk >> 3) ^ ((row >> 2) & 3);
+                    Vn[row * VB + cc * 8 + (kk & 7)] = 0;
+                }
+            }
+            __syncthreads();
+        }
+    };
+    constexpr int HALF = KHALF;
+    // a step with keys from kj needs the causal mask when it reaches past
+    // this wavefront's first query
+    const int qminw = qpos0 + 4 * c.wave;
+#define FA_P1(NEXT, Kn, kj)                                                    \
+    do {                                                                       \
+        const int kj_ = (kj);                                                  \
+        if (kj_ + 31 > qminw) fa_p1_step<NEXT, true>(c, Kn, kj_, q, sc, w);    \
+        else fa_p1_step<NEXT, false>(c, Kn, kj_, q, sc, w);                    \
+    } while (0)
+
+    // pass 1 (steps j = 0 .. 2nkt-1; step j folds S(j) while S(j+1) is
+    // formed)
+    begin_tile(0);
+    f32x16 sc = fa_s(c, kbuf(0), q);
+    FA_P1(true, kbuf(0) + HALF, 0);
+    for (int u = 1; u < nkt; u++) {
+        begin_tile(u);
+        FA_P1(true, kbuf(u), (u - 1) * KT + 32);
+        FA_P1(true, kbuf(u) + HALF, u * KT);
+    }
+    begin_tile(nkt);                     // pass 2's key tile 0 (and its V)
+    FA_P1(false, 0, (nkt - 1) * KT + 32);
+    w.K2 = w.M * c.c2 + __builtin_amdgcn_logf(w.lsum);     // v_log_f32: log2
+
+    // pass 2 (step j = 2kt + half of key tile kt, in stream tile nkt + kt)
     f32x16 o[D / 32];
 #pragma unroll
     for (int mt = 0; mt < D / 32; mt++)
 #pragma unroll
         for (int i = 0; i < 16; i++) o[mt][i] = 0.0f;
-    float M = -INFINITY, lsum = 0.0f;
-
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
-
-    // pass 1: per-query max M (in units of rnd(q.k)) and sum s over all
-    // keys; the last step also starts the copy of pass 2's first tile
-    for (int kb = 0; kb < nkt; kb++) {
-        const int buf = kb & 1;
-        fa_dma_k(Ks[buf ^ 1], kr, kb + 1 < nkt ? kb + 1 : 0, wave, lane);
-        if (kb + 1 == nkt) fa_dma_v(Vs[buf ^ 1], vr, 0, wave, lane);
-        const char *Kb = reinterpret_cast<const char *>(Ks[buf]);
-#pragma unroll
-        for (int sub = 0; sub < KT / 32; sub++) {
-            const int k0 = kb * KT + sub * 32;
-            if (k0 <= qmax) {                  // wave-uniform: else every key is masked
-                int kbase = fa_kbase(l32, h);
-                asm volatile("" : "+v"(kbase));
-                const f32x16 sc = fa_qk(Kb + sub * 32 * D * 2, kbase, qb);
-                float r[16];
-                fa_round(r, sc, k0, qpos, qmin, h);
-                float mx = r[0];
-#pragma unroll
-                for (int i = 1; i < 16; i++) mx = fmaxf(mx, r[i]);
-                mx = max32(mx);
-                const float mn = fmaxf(M, mx);
-                float ps = 0.0f;
-#pragma unroll
-                for (int i = 0; i < 16; i++) ps += __builtin_amdgcn_exp2f((r[i] - mn) * c2);
-                ps = sum32(ps);
-                // first step: M = -inf, lsum = 0 (exp2(-inf) = 0)
-                lsum = lsum * __builtin_amdgcn_exp2f((M - mn) * c2) + ps;
-                M = mn;
-            }
-        }
-        fa_sync(Vs[buf ^ 1], kb + 1 == nkt && nkt == 1, nkeys, tid);
+    bf16x8 pp[2];
+    // Key tiles below nmf need no mask for any query of the workgroup; the
+    // rest (one or two) are masked. Two loops rather than a branch per
+    // step: a branch around the O^T updates makes the register allocator
+    // spill. Key tile 0 is always run masked.
+    const int nmf = (qpos0 + 1) / KT;
+    fa_p2_step<false, true>(c, kbuf(nkt), 0, 0, q, w, pp, o);
+    fa_p2_step<true, true>(c, kbuf(nkt) + HALF, vbuf(nkt, 0), 32, q, w, pp, o);
+    int u = nkt + 1;
+    for (; u < nkt + nmf; u++) {
+        const int kt = u - nkt;
+        begin_tile(u);
+        fa_p2_step<true, false>(c, kbuf(u), vbuf(u - 1, 1), kt * KT, q, w, pp, o);
+        fa_p2_step<true, false>(c, kbuf(u) + HALF, vbuf(u, 0), kt * KT + 32, q, w, pp, o);
     }
-    const float inv_s = 1.0f / lsum;
-
-    // pass 2: P = rnd(e^{A-m} / s), O^T += V^T P^T
-    for (int kb = 0; kb < nkt; kb++) {
-        const int buf = (nkt + kb) & 1;
-        if (kb + 1 < nkt) {
-            fa_dma_k(Ks[buf ^ 1], kr, kb + 1, wave, lane);
-            fa_dma_v(Vs[buf ^ 1], vr, kb + 1, wave, lane);
-        }
-        const char *Kb = reinterpret_cast<const char *>(Ks[buf]);
-        const char *Vb = reinterpret_cast<const char *>(Vs[buf]);
-#pragma unroll
-        for (int sub = 0; sub < KT / 32; sub++) {
-            const int k0 = kb * KT + sub * 32;
-            int kbase = fa_kbase(l32, h), vbase = fa_vbase(l32, h);
-            asm volatile("" : "+v"(kbase), "+v"(vbase));
-            const f32x16 sc = fa_qk(Kb + sub * 32 * D * 2, kbase, qb);
-            float r[16];
-            fa_round(r, sc, k0, qpos, qmin, h);
-            uint32_t pp[8];
-#pragma unroll
-            for (int i = 0; i < 8; i++)
-                pp[i] = pack2(__builtin_amdgcn_exp2f((r[2 * i] - M) * c2) * inv_s,
-                              __builtin_amdgcn_exp2f((r[2 * i + 1] - M) * c2) * inv_s);
-            const char *Vsub = Vb + sub * D * VB * 2;
-#pragma unroll
-            for (int st = 0; st < 2; st++) {
-                const uint32_t w4[4] = {pp[4 * st], pp[4 * st + 1], pp[4 * st + 2],
-                                        pp[4 * st + 3]};
-                const bf16x8 pb = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u16x8 *>(w4));
-                const char *Vst = Vsub + (vbase ^ (st << 5));
-#pragma unroll
-                for (int mt = 0; mt < D / 32; mt++) {
-                    const bf16x8 va = __builtin_bit_cast(
-                        bf16x8, *reinterpret_cast<const u16x8 *>(Vst + mt * 32 * VB * 2));
-                    o[mt] = mfma32(va, pb, o[mt]);
-                }
-            }
-        }
-        if (kb + 1 < nkt) fa_sync(Vs[buf ^ 1], kb + 2 == nkt, nkeys, tid);
+    for (; u < 2 * nkt; u++) {
+        const int kt = u - nkt;
+        begin_tile(u);
+        fa_p2_step<true, true>(c, kbuf(u), vbuf(u - 1, 1), kt * KT, q, w, pp, o);
+        fa_p2_step<true, true>(c, kbuf(u) + HALF, vbuf(u, 0), kt * KT + 32, q, w, pp, o);
     }
+    fa_pv_last(c, vbuf(2 * nkt - 1, 1), pp, o);
 
+#undef FA_P1
     // epilogue: o = rnd(O); y = rnd(o * rnd(sigmoid(gate)))
-    if (qok) {
-        const size_t row = (size_t)qtok * nh + head;
+    if (tk < nt) {
+        const size_t row = (size_t)(tb + tk) * nh + head;
         const uint16_t *gr = qg + row * 2 * D + D;
         uint16_t *yr = y + row * D;
 #pragma unroll
         for (int mt = 0; mt < D / 32; mt++) {
 #pragma unroll
             for (int q4 = 0; q4 < 4; q4++) {
-                const int d0 = mt * 32 + 8 * q4 + 4 * h;
+                const int d0 = mt * 32 + 8 * q4 + 4 * c.h;
                 const u16x4 gv = *reinterpret_cast<const u16x4 *>(gr + d0);
                 u16x4 out;
 #pragma unroll
