@@ -24,10 +24,14 @@ int attn_check_layer(const ApusHipAttnLayer *L);
 // q/k (1+w) RMSNorm, RoPE at each token's position, append k and v to the
 // device caches; writes the roped q into qn [Ttot, nh, d].
 // dmeta: device copy of the metadata when it does not fit by value (else
-// NULL); max_pos: one past the largest position written (RoPE table size).
+// NULL); max_pos: one past the largest position written (RoPE table size);
+// maxnb: attn_max_vblocks of the call.
 int attn_prep(const ApusHipAttnLayer *L, const AttnSeqs &sq, const int32_t *dmeta,
-              size_t Ttot, size_t max_pos, const uint16_t *qg, const uint16_t *k,
+              size_t Ttot, size_t max_pos, int maxnb, const uint16_t *qg, const uint16_t *k,
               const uint16_t *v, uint16_t *kcache, uint16_t *vcache, size_t max_seq,
               uint16_t *qn);
+
+// the most 32-position V-cache blocks one sequence's new tokens touch
+int attn_max_vblocks(size_t B, const int32_t *cu, const int32_t *pos0);
 
 }  // namespace apus

@@ -31,6 +31,7 @@
 #include <stdint.h>
 #include <string.h>
 
+#include <algorithm>
 #include <vector>
 
 #include "../../include/apus_hip.h"
@@ -75,97 +76,181 @@ __device__ __forceinline__ Meta meta_of(const AttnSeqs &sq, const int32_t *dmeta
     return Meta{dmeta, dmeta + n + 1, dmeta + 2 * n + 1, dmeta + 3 * n + 2};
 }
 
-// k_attn_prep: one block of 256 threads per rpb <= 32 rows (8 when there
-// are few rows, so small decode batches still spread over the chip), a
-// row being one (token, slot) with slots 0..nh-1 the q heads and
-// nh..nh+nkv-1 the kv heads. Rows are staged in LDS with 16-byte loads, the
-// rows' sequence, position and cos/sin codes alongside; lane r takes row
-// r's ascending sum of squares (c/attn.h:177-182); then thread i normalises
-// dim i of every row with (1+w) and one rounding, applies the partial NeoX
-// RoPE with the host-made cos/sin codes (c/attn.h:244-266) and writes q to
-// qn, or k to the K cache and v (raw) to the transposed V cache.
-constexpr int PRR = 32;          // rows per k_attn_prep block
-constexpr int PST = D + 4;       // LDS row stride: 16-byte aligned rows on distinct banks
+// k_attn_prep: one block of 256 threads per rpb <= 64 rows, a row being one
+// (token, slot) with slots 0..nh-1 the q heads and nh..nh+nkv-1 the kv
+// heads. Rows are staged in LDS as bf16 with 16-byte loads; lane r of the
+// first wavefront takes row r's ascending sum of squares (c/attn.h:177-182,
+// the reference's order, so rs is bit-exact); then each thread takes one
+// 16-byte piece (8 dims) of a row at a time: (1+w) RMSNorm with one
+// rounding, the partial NeoX RoPE with the host-made cos/sin codes
+// (c/attn.h:244-266, the partner dims +-32 read from the staged row), and
+// a 16-byte store of q to qn or of k to the K cache. V is appended by
+// k_attn_vappend.
+constexpr int PRB = 64;                  // rows per k_attn_prep block
+constexpr int PRS = D + 8;               // LDS row pitch (bf16): rows on distinct banks
 __global__ __launch_bounds__(256) void k_attn_prep(
     AttnSeqs sq, const int32_t *__restrict__ dmeta, const uint16_t *__restrict__ qg,
-    const uint16_t *__restrict__ kin, const uint16_t *__restrict__ vin,
-    const uint16_t *__restrict__ qn_w, const uint16_t *__restrict__ kn_w,
-    const uint16_t *__restrict__ rope, uint16_t *__restrict__ kcache,
-    uint16_t *__restrict__ vcache, size_t max_seq, uint16_t *__restrict__ qn,
-    int nh, int nkv, int nrows, int rpb) {
-    typedef unsigned short u16x8v __attribute__((ext_vector_type(8)));
+    const uint16_t *__restrict__ kin, const uint16_t *__restrict__ qn_w,
+    const uint16_t *__restrict__ kn_w, const uint16_t *__restrict__ rope,
+    uint16_t *__restrict__ kcache, size_t max_seq, uint16_t *__restrict__ qn, int nh,
+    int nkv, int nrows, int rpb) {
     const Meta mt = meta_of(sq, dmeta);
     const int32_t *cu = mt.cu, *pos0 = mt.pos0;
     const int nslot = nh + nkv;
     const int r0 = blockIdx.x * rpb, nr = min(rpb, nrows - r0);
     const int tid = threadIdx.x;
-    __shared__ __attribute__((aligned(16))) float xs[PRR * PST];
-    __shared__ float rs[PRR];
-    __shared__ int rseq[PRR], rpos[PRR];
-    __shared__ uint16_t rcs[PRR * ROT];
-    for (int e = tid; e < nr * (D / 8); e += 256) {
-        const int r = e / (D / 8), c8 = (e % (D / 8)) * 8;
-        const int row = r0 + r, tt = row / nslot, slot = row % nslot;
-        const uint16_t *x = slot < nh ? qg + ((size_t)tt * nh + slot) * 2 * D
-                                      : kin + ((size_t)tt * nkv + (slot - nh)) * D;
-        const u16x8v v = *reinterpret_cast<const u16x8v *>(x + c8);
+    __shared__ __attribute__((aligned(16))) uint16_t xs[PRB * PRS];
+    __shared__ __attribute__((aligned(16))) uint16_t rcs[PRB * ROT];   // cos / sin codes
+    __shared__ float rs[PRB];
+    __shared__ int rseq[PRB], rpos[PRB];
+    // every load of the block in flight at once: 8 row pieces and 2 code
+    // pieces per thread
+    auto row_pos = [&](int r, int &s) {
+        const int tt = (r0 + r) / nslot;
+        s = seq_of(cu, sq.n, tt);
+        return pos0[s] + (tt - cu[s]);
+    };
+    u16x8 xv8[PRB * (D / 8) / 256], cv2[PRB * (ROT / 8) / 256];
 #pragma unroll
-        for (int i = 0; i < 8; i++) xs[r * PST + c8 + i] = bf2f(v[i]);
+    for (int k = 0; k < PRB * (D / 8) / 256; k++) {
+        const int e = tid + 256 * k, r = e / (D / 8), pc = e % (D / 8);
+        if (r < nr) {
+            const int row = r0 + r, tt = row / nslot, slot = row % nslot;
+            const uint16_t *x = slot < nh ? qg + ((size_t)tt * nh + slot) * 2 * D
+                                          : kin + ((size_t)tt * nkv + (slot - nh)) * D;
+            xv8[k] = *reinterpret_cast<const u16x8 *>(x + pc * 8);
+        }
     }
-    if (tid >= 64 && tid < 64 + nr) {         // row metadata, one lane per row
-        const int r = tid - 64, tt = (r0 + r) / nslot;
-        const int sq_ = seq_of(cu, sq.n, tt);
-        rseq[r] = sq_;
-        rpos[r] = pos0[sq_] + (tt - cu[sq_]);
+#pragma unroll
+    for (int k = 0; k < PRB * (ROT / 8) / 256; k++) {
+        const int e = tid + 256 * k, r = e / (ROT / 8), pc = e % (ROT / 8);
+        if (r < nr) {
+            int s;
+            cv2[k] = *reinterpret_cast<const u16x8 *>(rope + (size_t)row_pos(r, s) * ROT + pc * 8);
+        }
+    }
+    if (tid < nr) {                           // row metadata, one lane per row
+        int s;
+        rpos[tid] = row_pos(tid, s);
+        rseq[tid] = s;
+    }
+#pragma unroll
+    for (int k = 0; k < PRB * (D / 8) / 256; k++) {
+        const int e = tid + 256 * k, r = e / (D / 8), pc = e % (D / 8);
+        if (r < nr) *reinterpret_cast<u16x8 *>(xs + r * PRS + pc * 8) = xv8[k];
+    }
+#pragma unroll
+    for (int k = 0; k < PRB * (ROT / 8) / 256; k++) {
+        const int e = tid + 256 * k, r = e / (ROT / 8), pc = e % (ROT / 8);
+        if (r < nr) *reinterpret_cast<u16x8 *>(rcs + r * ROT + pc * 8) = cv2[k];
     }
     __syncthreads();
-    if (tid < nr) {                           // ascending, 16-byte LDS reads
-        const float4 *x4 = reinterpret_cast<const float4 *>(xs + tid * PST);
+    if (tid < nr) {                           // ascending, as the reference sums
+        const u16x8 *xr = reinterpret_cast<const u16x8 *>(xs + tid * PRS);
         float ss = 0.0f;
-#pragma unroll 8
-        for (int j = 0; j < D / 4; j++) {
-            const float4 v = x4[j];
-            ss = ss + v.x * v.x;
-            ss = ss + v.y * v.y;
-            ss = ss + v.z * v.z;
-            ss = ss + v.w * v.w;
+#pragma unroll 4
+        for (int j = 0; j < D / 8; j++) {
+            const u16x8 v = xr[j];
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                const float f = bf2f(v[i]);
+                ss = ss + f * f;
+            }
         }
         rs[tid] = 1.0f / sqrtf(ss / (float)D + kEps);
     }
-    for (int e = tid; e < nr * ROT; e += 256)  // the rows' cos/sin codes
-        rcs[e] = rope[(size_t)rpos[e / ROT] * ROT + e % ROT];
-    __syncthreads();
-    const float wq = 1.0f + bf2f(qn_w[tid]), wk = 1.0f + bf2f(kn_w[tid]);
-    for (int r = 0; r < nr; r++) {
-        const int slot = (r0 + r) % nslot;
-        float &x = xs[r * PST + tid];
-        x = rndf((x * rs[r]) * (slot < nh ? wq : wk));
-    }
     __syncthreads();
     constexpr int R = ROT / 2;
-    for (int r = 0; r < nr; r++) {
+    const int p = tid & 31;                   // this thread's piece: dims 8p..8p+7
+    const int pp = p ^ (R / 8);               // partner piece (dims +-32) of a rotary pair
+    // the (1+w) weights of the piece and of its partner, for q and for k
+    const u16x8 wq = *reinterpret_cast<const u16x8 *>(qn_w + p * 8);
+    const u16x8 wk = *reinterpret_cast<const u16x8 *>(kn_w + p * 8);
+    const u16x8 wqp = *reinterpret_cast<const u16x8 *>(qn_w + pp * 8);
+    const u16x8 wkp = *reinterpret_cast<const u16x8 *>(kn_w + pp * 8);
+    const int i0 = (p & (R / 8 - 1)) * 8;     // pair index of dim 0 of a rotary piece
+    for (int it = 0; it < (nr + 7) / 8; it++) {
+        const int r = it * 8 + (tid >> 5);
+        if (r >= nr) break;
         const int row = r0 + r, tt = row / nslot, slot = row % nslot;
-        const int s = rseq[r], pos = rpos[r];
-        const float *ns = xs + r * PST;
-        const float nv = ns[tid];
-        float out = nv;
-        const uint16_t *cs = rcs + r * ROT;
-        if (tid < R) {
-            const float c = bf2f(cs[tid]), sn = bf2f(cs[R + tid]);
-            out = rndf(rndf(nv * c) + rndf(-ns[tid + R] * sn));
-        } else if (tid < ROT) {
-            const float c = bf2f(cs[tid - R]), sn = bf2f(cs[tid]);
-            out = rndf(rndf(nv * c) + rndf(ns[tid - R] * sn));
-        }
-        if (slot < nh) {
-            qn[((size_t)tt * nh + slot) * D + tid] = f2bf(out);
+        const bool isq = slot < nh;
+        const u16x8 wv = isq ? wq : wk;
+        const float rr = rs[r];
+        const u16x8 xv = *reinterpret_cast<const u16x8 *>(xs + r * PRS + p * 8);
+        float n[8];
+#pragma unroll
+        for (int i = 0; i < 8; i++) n[i] = rndf((bf2f(xv[i]) * rr) * (1.0f + bf2f(wv[i])));
+        u16x8 out;
+        if (p < ROT / 8) {
+            const u16x8 xp = *reinterpret_cast<const u16x8 *>(xs + r * PRS + pp * 8);
+            const u16x8 wpv = isq ? wqp : wkp;
+            const uint16_t *cs = rcs + r * ROT;
+            const u16x8 cv = *reinterpret_cast<const u16x8 *>(cs + i0);
+            const u16x8 sv = *reinterpret_cast<const u16x8 *>(cs + R + i0);
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                const float np = rndf((bf2f(xp[i]) * rr) * (1.0f + bf2f(wpv[i])));
+                const float c = bf2f(cv[i]), sn = bf2f(sv[i]);
+                out[i] = p < R / 8 ? f2bf(rndf(n[i] * c) + rndf(-np * sn))
+                                   : f2bf(rndf(n[i] * c) + rndf(np * sn));
+            }
         } else {
-            const int kvh = slot - nh;
-            uint16_t *kc = kcache + ((size_t)s * nkv + kvh) * max_seq * D;
-            kc[(size_t)pos * D + tid] = f2bf(out);
-            uint16_t *vc = vcache + ((size_t)s * nkv + kvh) * D * max_seq;
-            vc[((size_t)(pos / 32) * D + tid) * 32 + pos % 32] = vin[((size_t)tt * nkv + kvh) * D + tid];
+#pragma unroll
+            for (int i = 0; i < 8; i++) out[i] = f2bf(n[i]);
         }
+        uint16_t *dst = isq ? qn + ((size_t)tt * nh + slot) * D
+                            : kcache + (((size_t)rseq[r] * nkv + (slot - nh)) * max_seq +
+                                        rpos[r]) * D;
+        *reinterpret_cast<u16x8 *>(dst + p * 8) = out;
+    }
+}
+
+// k_attn_vappend: the new tokens' v rows (raw, c/layer.h:315-316) into the
+// transposed V cache [seq][kv head][position / 32][d][32]. One block per
+// (sequence, kv head, 32-position block the new tokens touch): the rows are
+// staged in LDS, then thread d writes its 32 keys -- one 64-byte run, so
+// the block is written as contiguous 16 KiB (a block only partly covered
+// by new tokens keeps its other keys: element stores for those).
+__global__ __launch_bounds__(256) void k_attn_vappend(
+    AttnSeqs sq, const int32_t *__restrict__ dmeta, const uint16_t *__restrict__ vin,
+    uint16_t *__restrict__ vcache, size_t max_seq, int nkv, int maxnb) {
+    const Meta mt = meta_of(sq, dmeta);
+    const int s = blockIdx.x / (nkv * maxnb), rem = blockIdx.x % (nkv * maxnb);
+    const int kvh = rem / maxnb, bi = rem % maxnb;
+    const int t0 = mt.cu[s], ns = mt.cu[s + 1] - t0, p0 = mt.pos0[s];
+    if (ns <= 0) return;
+    const int b = p0 / 32 + bi;
+    if (b > (p0 + ns - 1) / 32) return;
+    const int klo = max(p0, b * 32) - b * 32, khi = min(p0 + ns, b * 32 + 32) - b * 32;
+    __shared__ __attribute__((aligned(16))) uint16_t vt[32 * PRS];
+    const int tid = threadIdx.x;
+    u16x8 v4[32 * (D / 8) / 256];               // every load in flight at once
+#pragma unroll
+    for (int j = 0; j < 32 * (D / 8) / 256; j++) {
+        const int e = tid + 256 * j, k = e / (D / 8), pc = e % (D / 8);
+        if (k >= klo && k < khi) {
+            const int t = t0 + (b * 32 + k - p0);
+            v4[j] = *reinterpret_cast<const u16x8 *>(vin + ((size_t)t * nkv + kvh) * D + pc * 8);
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < 32 * (D / 8) / 256; j++) {
+        const int e = tid + 256 * j, k = e / (D / 8), pc = e % (D / 8);
+        if (k >= klo && k < khi) *reinterpret_cast<u16x8 *>(vt + k * PRS + pc * 8) = v4[j];
+    }
+    __syncthreads();
+    uint16_t *blk = vcache + (((size_t)s * nkv + kvh) * (max_seq / 32) + b) * D * 32;
+    const int d = tid;
+    if (klo == 0 && khi == 32) {
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            u16x8 v;
+#pragma unroll
+            for (int i = 0; i < 8; i++) v[i] = vt[(q * 8 + i) * PRS + d];
+            *reinterpret_cast<u16x8 *>(blk + d * 32 + q * 8) = v;
+        }
+    } else {
+        for (int k = klo; k < khi; k++) blk[d * 32 + k] = vt[k * PRS + d];
     }
 }
 
@@ -540,18 +625,33 @@ static int attn_meta(size_t B, const int32_t *cu, const int32_t *pos0, size_t ma
 }
 
 int attn_prep(const ApusHipAttnLayer *L, const AttnSeqs &sq, const int32_t *dmeta,
-              size_t Ttot, size_t max_pos, const uint16_t *qg, const uint16_t *k,
+              size_t Ttot, size_t max_pos, int maxnb, const uint16_t *qg, const uint16_t *k,
               const uint16_t *v, uint16_t *kcache, uint16_t *vcache, size_t max_seq,
               uint16_t *qn) {
     const uint16_t *rope = rope_table(L->rot, L->theta, max_pos);
     if (!rope) return kErrHip;
     const size_t nrows = Ttot * (L->nh + L->nkv);
-    const int rpb = nrows < (size_t)64 * PRR * cu_count() ? 8 : PRR;
+    // few rows (decode): small blocks, so they spread over the chip
+    const int rpb = nrows < (size_t)8 * PRB * cu_count() ? 8 : PRB;
     APUS_TIMED("k_attn_prep",
                k_attn_prep<<<cdiv(nrows, rpb), 256, 0, stream()>>>(
-        sq, dmeta, qg, k, v, L->qn_w, L->kn_w, rope, kcache, vcache, max_seq, qn,
-        (int)L->nh, (int)L->nkv, (int)nrows, rpb));
-    return launch_check("k_attn_prep");
+        sq, dmeta, qg, k, L->qn_w, L->kn_w, rope, kcache, max_seq, qn, (int)L->nh,
+        (int)L->nkv, (int)nrows, rpb));
+    if (int r = launch_check("k_attn_prep")) return r;
+    APUS_TIMED("k_attn_vappend",
+               k_attn_vappend<<<(unsigned)(sq.n * L->nkv * maxnb), 256, 0, stream()>>>(
+        sq, dmeta, v, vcache, max_seq, (int)L->nkv, maxnb));
+    return launch_check("k_attn_vappend");
+}
+
+// the most 32-position V blocks one sequence's new tokens touch
+int attn_max_vblocks(size_t B, const int32_t *cu, const int32_t *pos0) {
+    int m = 1;
+    for (size_t s = 0; s < B; s++) {
+        const int ns = cu[s + 1] - cu[s];
+        if (ns > 0) m = std::max(m, (pos0[s] + ns - 1) / 32 - pos0[s] / 32 + 1);
+    }
+    return m;
 }
 
 }  // namespace apus
@@ -578,7 +678,8 @@ int apus_hip_attn_decode(const ApusHipAttnLayer *L, size_t B, const int32_t *cu,
     float2 *st = (float2 *)scratch(kScratchAttnStat, ns1 * L->nkv * kRows * 8);
     float *Op = (float *)scratch(kScratchAttnPart, ns2 * L->nkv * kRows * D * 4);
     if (!qn || !As || !st || !Op) return kErrHip;
-    if (int r = attn_prep(L, sq, dmeta, Ttot, max_pos, qg, k, v, kcache, vcache, max_seq, qn))
+    if (int r = attn_prep(L, sq, dmeta, Ttot, max_pos, attn_max_vblocks(B, cu, pos0), qg, k, v,
+                          kcache, vcache, max_seq, qn))
         return r;
     const float scale = (float)(1.0 / sqrt((double)L->d));
     const ActTables *tabs = act_tables();

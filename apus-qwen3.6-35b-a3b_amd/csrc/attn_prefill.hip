@@ -643,7 +643,8 @@ int apus_hip_attn_prefill(const ApusHipAttnLayer *L, size_t B, const int32_t *cu
     }
     uint16_t *qn = (uint16_t *)scratch(kScratchAttnQ, Ttot * L->nh * D * 2);
     if (!qn) return kErrHip;
-    if (int r = attn_prep(L, as, adm, Ttot, max_pos, qg, k, v, kcache, vcache, max_seq, qn))
+    if (int r = attn_prep(L, as, adm, Ttot, max_pos, attn_max_vblocks(B, cu, pos0), qg, k, v,
+                          kcache, vcache, max_seq, qn))
         return r;
     const float scale = (float)(1.0 / sqrt((double)L->d));
     const ActTables *tabs = act_tables();

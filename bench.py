@@ -280,7 +280,8 @@ def bench_attn_decode(torch, B, ctx, steps, warmup, seed):
     flops = B * NH * 4 * AD * ctx
     kbytes = B * ctx * NKV * AD * 2           # one of the K / V caches
     table = {"k_attn_scores": ("hbm", kbytes, HBM_PEAK), "k_attn_pv": ("hbm", kbytes, HBM_PEAK),
-             "k_attn_prep": ("hbm", B * (NH * 2 * AD * 2 + NKV * AD * 2 * 4), HBM_PEAK),
+             "k_attn_prep": ("hbm", B * (NH * AD * 2 * 2 + NKV * AD * 2 * 2), HBM_PEAK),
+             "k_attn_vappend": ("hbm", B * NKV * AD * 2 * 2, HBM_PEAK),
              "k_attn_combine": ("hbm", B * NH * AD * 2 * 2, HBM_PEAK)}
     total, per, kt = time_steps(torch, step, steps, warmup, nsets, table)
     st = float(np.mean(per))
@@ -325,7 +326,9 @@ def bench_attn_prefill(torch, T, steps, warmup, seed):
     flops = attn_prefill_flops(T)
     bytes_ = T * (NH * 2 * AD * 2 + 2 * NKV * AD * 2 + 2 * NKV * AD * 2 + NH * AD * 2)
     table = {"k_attn_fa": ("mfma", flops, BF16_PEAK),
-             "k_attn_prep": ("hbm", T * (NH * 2 * AD * 2 + NKV * AD * 2 * 4 + NH * AD * 2), HBM_PEAK)}
+             # q and k rows read and written (normed, roped), v rows appended
+             "k_attn_prep": ("hbm", T * (NH * AD * 2 * 2 + NKV * AD * 2 * 2), HBM_PEAK),
+             "k_attn_vappend": ("hbm", T * NKV * AD * 2 * 2, HBM_PEAK)}
     total, per, kt = time_steps(torch, step, steps, warmup, nsets, table)
     st = float(np.mean(per))
     wl = f"attn_prefill_t{T}"
