@@ -50,6 +50,8 @@ constexpr float kEps = 1e-6f;
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x8 __attribute__((ext_vector_type(8)));
+constexpr float kL2E = 1.44269504088896341f;
 typedef unsigned short u16x8 __attribute__((ext_vector_type(8)));
 
 __device__ __forceinline__ bf16x8 ld_bf16x8(const uint16_t *p) {
@@ -404,8 +406,10 @@ __global__ __launch_bounds__(64) void k_attn_scores(
 // O^T[d][row] = sum_key V^T[d][key] P^T[key][row] on MFMA 16x16x32: the
 // transposed V cache is the A operand (4 lanes read 64 contiguous bytes of
 // one d row), the probabilities the B operand.
+// (two row blocks hold 2 x 64 accumulators and the next step's operands:
+// one wavefront per SIMD, so they stay in registers)
 template <int NRB>
-__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void k_attn_pv(
+__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(NRB == 1 ? 2 : 1))) void k_attn_pv(
     AttnSeqs sq, const int32_t *__restrict__ dmeta, const uint16_t *__restrict__ vcache,
     size_t max_seq, int nkv, const uint16_t *__restrict__ As,
     const float2 *__restrict__ stats, float *__restrict__ Op) {
@@ -434,8 +438,12 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void k_
                 mm = mn;
             }
         }
+        // P = rnd(e^{A - m} / s) formed as rnd(exp2(A log2(e) - K)), K =
+        // m log2(e) + log2(s): the division folded into the exponent (a
+        // relative difference of a few 1e-7 from the quotient, the
+        // tolerance class of the hardware exp2)
         m[rb] = mm;
-        rsum[rb] = ss;
+        rsum[rb] = mm * kL2E + __builtin_amdgcn_logf(ss);
     }
     const uint16_t *Vb = vcache + ((size_t)c.s * nkv + c.kvh) * D * max_seq;
     const size_t cap = (size_t)(soff[c.s + 1] - soff[c.s]) * sq.ks1;
@@ -470,16 +478,14 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void k_
         bf16x8 pf[NRB];
 #pragma unroll
         for (int rb = 0; rb < NRB; rb++) {
-            u16x8 pv = {};
-            if (vrow[rb]) {
+            f32x8 e8;
 #pragma unroll
-                for (int e = 0; e < 8; e++) {
-                    const int kk = kq + e;
-                    if (kk <= lim[rb] && kk < c.k1)
-                        pv[e] = f2bf(exp_fast(bf2f(af[rb][e]) - m[rb]) / rsum[rb]);
-                }
+            for (int e = 0; e < 8; e++) {
+                const int kk = kq + e;
+                const float p = __builtin_amdgcn_exp2f(fmaf(bf2f(af[rb][e]), kL2E, -rsum[rb]));
+                e8[e] = vrow[rb] && kk <= lim[rb] && kk < c.k1 ? p : 0.0f;
             }
-            pf[rb] = __builtin_bit_cast(bf16x8, pv);
+            pf[rb] = __builtin_convertvector(e8, bf16x8);     // hardware RNE
         }
         const bool partial = kq + 8 > c.k1;    // keys past the end: zero V too
 #pragma unroll

@@ -14,6 +14,8 @@ reported under "configs" with their own roofline fractions:
   c1   config 1   GDN prefill T=4096 (headline)
   c2   config 2   gated-GQA decode, 64 sequences x 32K-token bf16 KV cache
   c3   config 3   gated-GQA causal prefill, T=8192 (cache fill + attention)
+  c4   config 4   hybrid decode block, 3 GDN + 1 GQA layers, 128 sequences
+                  verifying 1..4 tokens each at log-normal cached contexts
 Input buffer sets rotate so the 256 MB Infinity Cache cannot serve
 repeated reads. The CPU baseline is the reference's own scalar anchors
 (oracle/_ref, built from the reference sources) when present, else the
@@ -338,6 +340,82 @@ def bench_attn_prefill(torch, T, steps, warmup, seed):
                 layer_mfma_frac=flops / st / BF16_PEAK, roofline=kernel_roofline(kt, table, wl))
 
 
+def mixed_block_shape(B, seed):
+    """Config 4's ragged batch: cached context lengths log-normal around
+    4096 (mu = ln 4096, sigma = 1.0), clipped to [256, 65536], and 1..4
+    verify tokens per sequence, from a fixed seed."""
+    rng = np.random.default_rng(seed)
+    ctx = np.clip(np.exp(rng.normal(np.log(4096.0), 1.0, B)), 256, 65536).astype(np.int64)
+    k = rng.integers(1, 5, B)
+    ctx = np.minimum(ctx, 65536 - k)          # cached + new tokens stay within 65536
+    return ctx.astype(np.int32), k.astype(np.int32)
+
+
+def bench_mixed_block(torch, B, steps, warmup, seed):
+    """Config 4: one hybrid decode block in the model's 3:1 ratio -- three
+    Gated DeltaNet layers (each with its own weights, conv state and
+    recurrent state per sequence) and one gated-GQA layer (a bf16 KV cache
+    per sequence) -- over B sequences that each verify 1..4 tokens at a
+    log-normal cached context. value = verified tokens per second through
+    the block."""
+    import apus_hip
+    dev = torch.device("cuda")
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed)
+
+    def bf(shape, std=1.0, mean=0.0):
+        x = torch.randn(shape, generator=g, device=dev, dtype=torch.float32) * std + mean
+        return x.to(torch.bfloat16).view(torch.int16)
+
+    ctx, k = mixed_block_shape(B, seed)
+    cu = np.concatenate([[0], np.cumsum(k)]).astype(np.int32)
+    T = int(cu[-1])
+    gdn = []
+    for _ in range(3):
+        w = dict(conv_w=bf((CD, 4), 0.1), A_log=torch.rand(HV, generator=g, device=dev) * 2.7,
+                 dt_bias=torch.ones(HV, device=dev), onorm_w=bf((DV,), 0.1, 1.0))
+        gdn.append(dict(layer=apus_hip.gdn_layer(GDN, w), w=w, qkv=bf((T, CD)), z=bf((T, VD)),
+                        a=bf((T, HV)), b=bf((T, HV)), conv=bf((B, CD * 3)),
+                        S=torch.randn((B, HV, DK, DV), generator=g, device=dev) * 0.02,
+                        y=torch.empty((T, VD), dtype=torch.int16, device=dev)))
+    aw = dict(qn_w=bf((AD,), 0.1), kn_w=bf((AD,), 0.1))
+    alayer = apus_hip.attn_layer(ATTN, aw)
+    max_seq = int(-(-int((ctx + k).max()) // 32) * 32)
+    # caches filled with finite random bf16 codes (|x| < 1) without an fp32
+    # temporary of the caches' size
+    kc = torch.randint(-16000, 16000, (B, NKV, max_seq, AD), dtype=torch.int16, device=dev, generator=g)
+    vc = torch.randint(-16000, 16000, (B, NKV, max_seq // 32, AD, 32), dtype=torch.int16, device=dev,
+                       generator=g)
+    att = dict(qg=bf((T, NH, 2 * AD)), k=bf((T, NKV, AD)), v=bf((T, NKV, AD)),
+               y=torch.empty((T, NH * AD), dtype=torch.int16, device=dev))
+
+    def step(i):
+        for L in gdn:
+            apus_hip.gdn_decode(L["layer"], cu, L["qkv"], L["z"], L["a"], L["b"], L["conv"],
+                                L["S"], L["y"])
+        apus_hip.attn_decode(alayer, cu, ctx, att["qg"], att["k"], att["v"], kc, vc, max_seq,
+                             att["y"])
+
+    gdn_bytes = sum(gdn_seq_bytes(int(x)) for x in k) + GDN_WEIGHT_BYTES
+    attn_bytes = sum(attn_decode_bytes(int(c) + int(x), int(x)) for c, x in zip(ctx, k)) + 2 * AD * 2
+    bytes_ = 3 * gdn_bytes + attn_bytes
+    kv1 = int(sum((int(c) + int(x)) * NKV * AD * 2 for c, x in zip(ctx, k)))   # one of K / V
+    table = {"k_gdn_decode": ("hbm", gdn_bytes, HBM_PEAK),
+             "k_attn_scores": ("hbm", kv1, HBM_PEAK), "k_attn_pv": ("hbm", kv1, HBM_PEAK),
+             "k_attn_prep": ("hbm", T * (NH * AD * 2 * 2 + NKV * AD * 2 * 2), HBM_PEAK),
+             "k_attn_vappend": ("hbm", T * NKV * AD * 2 * 2, HBM_PEAK),
+             "k_attn_combine": ("hbm", T * NH * AD * 2 * 2, HBM_PEAK)}
+    total, per, kt = time_steps(torch, step, steps, warmup, 1, table)
+    st = float(np.mean(per))
+    wl = f"mixed_block_3gdn_1gqa_b{B}"
+    return dict(workload=wl, tokens_per_step=T, ms_per_step=total / steps * 1e3,
+                step_event_ms=st * 1e3, kernels_ms=kt, alg_bytes=bytes_,
+                ctx_mean=float(ctx.mean()), ctx_max=int(ctx.max()), verify_tokens=T,
+                tok_s=T * steps / total, layer_hbm_gbs=bytes_ / st / 1e9,
+                layer_hbm_frac=bytes_ / st / HBM_PEAK,
+                roofline=kernel_roofline(kt, table, wl))
+
+
 def bench_copy(torch, steps, warmup):
     """Calibration workload for HBM counters: a plain 1 GiB device copy
     (reads 1 GiB, writes 1 GiB); rocprofv3 FETCH_SIZE / WRITE_SIZE of its
@@ -423,7 +501,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--only", default="c0,c0b,c1,c2,c3")
+    ap.add_argument("--only", default="c0,c0b,c1,c2,c3,c4")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-tokens", type=int, default=8192)
     ap.add_argument("--cpu-threads", type=int, default=CPU_THREADS)
@@ -460,6 +538,9 @@ def main():
     if "c3" in want:
         res["c3"] = bench_attn_prefill(torch, 8192, args.steps, args.warmup, 14)
         log("c3", res["c3"])
+    if "c4" in want:
+        res["c4"] = bench_mixed_block(torch, 128, args.steps, args.warmup, 15)
+        log("c4", res["c4"])
     if "copy" in want:
         res["copy"] = bench_copy(torch, args.steps, args.warmup)
         log("copy", res["copy"])
