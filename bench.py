@@ -198,7 +198,10 @@ def bench_gdn_prefill(torch, T, steps, warmup, seed):
     bytes_ = gdn_seq_bytes(T) + GDN_WEIGHT_BYTES
     flops = gdn_prefill_flops(T)
     nu = (T // 64) * HV                       # (chunk, v-head) units
-    table = {"k_gdn_chunk_scan": ("mfma", nu * SCAN_FLOPS_PER_UNIT, FP32_PEAK),
+    # the scan multiplies fp32 operands on the bf16 MFMA in split precision
+    # (hi*hi + hi*lo + lo*hi: three bf16 MFMAs per fp32 product), so its roof
+    # for the fp32 algorithm is a third of the bf16 peak
+    table = {"k_gdn_chunk_scan": ("mfma", nu * SCAN_FLOPS_PER_UNIT, BF16_PEAK / 3),
              "k_gdn_chunk_wy": ("mfma", nu * WY_FLOPS_PER_UNIT, FP32_PEAK),
              "k_gdn_prep": ("hbm", gdn_prep_bytes(T), HBM_PEAK),
              "k_gdn_post": ("hbm", gdn_post_bytes(T), HBM_PEAK)}
