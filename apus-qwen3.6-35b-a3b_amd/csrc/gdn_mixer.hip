@@ -296,17 +296,27 @@ __global__ __launch_bounds__(256) void k_gdn_prep(
     __shared__ float rs[2][PT];
 
     // stage rows tb-3 .. tb+nt-1 (those that exist); LDS channel order
-    // [q(128) | k(128) | v(256)]
-    for (int e = tid; e < (PT + 3) * PC / 8; e += 256) {
-        const int r = e / (PC / 8), c8 = (e % (PC / 8)) * 8;
+    // [q(128) | k(128) | v(256)]. Every load of the tile is issued before
+    // the first LDS store (a store right after its load would wait for it).
+    constexpr int NPC = ((PT + 3) * PC / 8 + 255) / 256;
+    u16x8 pc[NPC];
+#pragma unroll
+    for (int k = 0; k < NPC; k++) {
+        const int e = tid + 256 * k, r = e / (PC / 8), c8 = (e % (PC / 8)) * 8;
         const int t = tb - 3 + r;
-        if (t >= 0 && r < nt + 3) {
+        if (e < (PT + 3) * PC / 8 && t >= 0 && r < nt + 3) {
             const size_t gc = c8 < DK ? (size_t)kh * DK + c8
                             : c8 < 2 * DK ? kd + (size_t)kh * DK + (c8 - DK)
                                           : 2 * kd + (size_t)kh * 2 * DV + (c8 - 2 * DK);
-            *reinterpret_cast<u16x8 *>(xin + r * PC + c8) =
-                *reinterpret_cast<const u16x8 *>(qkv + (size_t)t * cd + gc);
+            pc[k] = *reinterpret_cast<const u16x8 *>(qkv + (size_t)t * cd + gc);
         }
+    }
+#pragma unroll
+    for (int k = 0; k < NPC; k++) {
+        const int e = tid + 256 * k, r = e / (PC / 8), c8 = (e % (PC / 8)) * 8;
+        const int t = tb - 3 + r;
+        if (e < (PT + 3) * PC / 8 && t >= 0 && r < nt + 3)
+            *reinterpret_cast<u16x8 *>(xin + r * PC + c8) = pc[k];
     }
     const size_t cqk = tid < DK ? (size_t)kh * DK + tid : kd + (size_t)kh * DK + (tid - DK);
     const int h = kh * REP + tid / DV, j = tid % DV;
@@ -388,12 +398,23 @@ __global__ __launch_bounds__(256) void k_gdn_post(
         const int nr = (int)min((size_t)PR, nrows - r0);
         __shared__ __attribute__((aligned(16))) float os[PR * RS];
         __shared__ float rs[PR];
-        for (int e = tid; e < PR * DV / 8; e += 256) {
-            const int row = e / (DV / 8), c8 = (e % (DV / 8)) * 8;
-            if (row < nr) {
-                const u16x8 v = *reinterpret_cast<const u16x8 *>(ob + (r0 + row) * DV + c8);
+        // every load of the block (the rows and their z) in flight at once
+        constexpr int NPC = PR * DV / 8 / 256;
+        u16x8 ov[NPC], zv8[NPC];
 #pragma unroll
-                for (int i = 0; i < 8; i++) os[row * RS + c8 + i] = bf2f(v[i]);
+        for (int k = 0; k < NPC; k++) {
+            const int e = tid + 256 * k, row = e / (DV / 8), c8 = (e % (DV / 8)) * 8;
+            if (row < nr) {
+                ov[k] = *reinterpret_cast<const u16x8 *>(ob + (r0 + row) * DV + c8);
+                zv8[k] = *reinterpret_cast<const u16x8 *>(z + (r0 + row) * DV + c8);
+            }
+        }
+#pragma unroll
+        for (int k = 0; k < NPC; k++) {
+            const int e = tid + 256 * k, row = e / (DV / 8), c8 = (e % (DV / 8)) * 8;
+            if (row < nr) {
+#pragma unroll
+                for (int i = 0; i < 8; i++) os[row * RS + c8 + i] = bf2f(ov[k][i]);
             }
         }
         __syncthreads();
@@ -401,11 +422,12 @@ __global__ __launch_bounds__(256) void k_gdn_post(
             rs[tid] = 1.0f / sqrtf(row_sumsq(os + tid * RS) / (float)DV + kEps);
         }
         __syncthreads();
-        for (int e = tid; e < PR * DV / 8; e += 256) {
-            const int row = e / (DV / 8), c8 = (e % (DV / 8)) * 8;
+#pragma unroll
+        for (int k = 0; k < NPC; k++) {
+            const int e = tid + 256 * k, row = e / (DV / 8), c8 = (e % (DV / 8)) * 8;
             if (row < nr) {
                 const size_t off = (r0 + row) * DV + c8;
-                const u16x8 zv = *reinterpret_cast<const u16x8 *>(z + off);
+                const u16x8 zv = zv8[k];
                 const u16x8 wv = *reinterpret_cast<const u16x8 *>(onorm_w + c8);
                 u16x8 out;
 #pragma unroll

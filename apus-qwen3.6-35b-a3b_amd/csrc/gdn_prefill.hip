@@ -159,6 +159,21 @@ __device__ __forceinline__ void split_bf(float x, uint16_t &hi, uint16_t &lo) {
 __device__ __forceinline__ void put_split(uint16_t *p, float x) {
     split_bf(x, p[0], p[8]);
 }
+// the 8 hi codes then the 8 lo codes of x[0..7]: one 32-byte unit of the
+// packed operand layouts, written with two 16-byte stores
+__device__ __forceinline__ void put_split8(uint16_t *p, const float (&x)[8]) {
+    typedef unsigned short u16x8_t __attribute__((ext_vector_type(8)));
+    u16x8_t hi, lo;
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        uint16_t h, l;
+        split_bf(x[i], h, l);
+        hi[i] = h;
+        lo[i] = l;
+    }
+    *reinterpret_cast<u16x8_t *>(p) = hi;
+    *reinterpret_cast<u16x8_t *>(p + 8) = lo;
+}
 
 // k_gdn_chunk_wy: one workgroup per (chunk, v-head), two per CU (Q's LDS
 // copy is reused for L once Q K^T is done).
@@ -185,24 +200,24 @@ __global__ __launch_bounds__(256, 2) void k_gdn_chunk_wy(
     __shared__ float graw_s[C], gam[C], bet[C], Gs[C];
 
     // rows t >= nt are padding: q = k = 0, g = 0, beta = 0
-    for (int e = tid; e < C * DK / 4; e += 256) {
-        const int t = e / (DK / 4), q4 = (e % (DK / 4)) * 4;
-        float4 q = make_float4(0.f, 0.f, 0.f, 0.f), k = q;
+    // (every load issued before the first LDS store)
+    constexpr int NQ = C * DK / 4 / 256;
+    float4 qv[NQ], kv[NQ];
+#pragma unroll
+    for (int u = 0; u < NQ; u++) {
+        const int e = tid + 256 * u, t = e / (DK / 4), q4 = (e % (DK / 4)) * 4;
+        qv[u] = kv[u] = make_float4(0.f, 0.f, 0.f, 0.f);
         if (t < P.nt) {
             const float *row = qk + (size_t)(P.t0 + t) * 2 * kd + (size_t)kh * DK + q4;
-            q = ld4(row);
-            k = ld4(row + kd);
+            qv[u] = ld4(row);
+            kv[u] = ld4(row + kd);
         }
-        *reinterpret_cast<float4 *>(QL + t * KP + q4) = q;
-        *reinterpret_cast<float4 *>(Ks + t * KP + q4) = k;
-        if (wqk) {
-            const float qv[4] = {q.x, q.y, q.z, q.w}, kv[4] = {k.x, k.y, k.z, k.w};
+    }
 #pragma unroll
-            for (int j = 0; j < 4; j++) {
-                put_split(Qpu + bx_a_index(t, q4 + j, DK / 32), qv[j]);
-                put_split(Kpu + bx_b_index(t, q4 + j), kv[j]);
-            }
-        }
+    for (int u = 0; u < NQ; u++) {
+        const int e = tid + 256 * u, t = e / (DK / 4), q4 = (e % (DK / 4)) * 4;
+        *reinterpret_cast<float4 *>(QL + t * KP + q4) = qv[u];
+        *reinterpret_cast<float4 *>(Ks + t * KP + q4) = kv[u];
     }
     if (tid < C) {
         const bool ok = tid < P.nt;
@@ -210,6 +225,29 @@ __global__ __launch_bounds__(256, 2) void k_gdn_chunk_wy(
         bet[tid] = ok ? gate[(size_t)(P.t0 + tid) * hv + h].y : 0.0f;
     }
     __syncthreads();
+    if (wqk) {
+        // the scan's packed Q (rows t, 8 consecutive dims a unit) and K
+        // (dim i, 8 consecutive keys a unit) from the LDS copies
+#pragma unroll
+        for (int u = 0; u < C * DK / 8 / 256; u++) {
+            const int e = tid + 256 * u;
+            {
+                const int t = e / (DK / 8), c0 = (e % (DK / 8)) * 8;
+                float x[8];
+                const float4 a0 = lds4(QL + t * KP + c0), a1 = lds4(QL + t * KP + c0 + 4);
+                x[0] = a0.x; x[1] = a0.y; x[2] = a0.z; x[3] = a0.w;
+                x[4] = a1.x; x[5] = a1.y; x[6] = a1.z; x[7] = a1.w;
+                put_split8(Qpu + bx_a_index(t, c0, DK / 32), x);
+            }
+            {
+                const int i = e % DK, s0 = (e / DK) * 8;
+                float x[8];
+#pragma unroll
+                for (int j = 0; j < 8; j++) x[j] = Ks[(s0 + j) * KP + i];
+                put_split8(Kpu + bx_b_index(s0, i), x);
+            }
+        }
+    }
     if (tid < C) {                     // gamma_t = g_0 + .. + g_t, in token order
         float acc = 0.0f;
         for (int t = 0; t <= tid; t++) acc = acc + graw_s[t];
@@ -224,28 +262,44 @@ __global__ __launch_bounds__(256, 2) void k_gdn_chunk_wy(
     }
 
     const int r16 = lane & 15, kq = (lane >> 4) * 4;
-    // Q K^T, row block 3-w: A = decayed lower triangle, to global
+    // Q K^T, row block 3-w: A = decayed lower triangle, to global. The
+    // product is formed transposed (K Q^T) so each lane holds 4 consecutive
+    // key columns s of one row t: 4 hi and 4 lo codes, two 8-byte stores.
     uint16_t *A = Ab + (size_t)blockIdx.x * C * C * 2;
     {
+        typedef unsigned short u16x4_t __attribute__((ext_vector_type(4)));
         const int rb = 3 - wave;
-        if ((rb & 1) == 0) {           // the upper tile the scan's 32-column block covers
-            const int s = (rb + 1) * 16 + r16;
+        const int t = rb * 16 + r16;
+        auto put4 = [&](int s0, const float (&v)[4]) {
+            u16x4_t hi, lo;
 #pragma unroll
-            for (int i = 0; i < 4; i++) put_split(A + bx_a_index(rb * 16 + kq + i, s, C / 32), 0.0f);
+            for (int i = 0; i < 4; i++) {
+                uint16_t h, l;
+                split_bf(v[i], h, l);
+                hi[i] = h;
+                lo[i] = l;
+            }
+            uint16_t *p = A + bx_a_index(t, s0, C / 32);
+            *reinterpret_cast<u16x4_t *>(p) = hi;
+            *reinterpret_cast<u16x4_t *>(p + 8) = lo;
+        };
+        if ((rb & 1) == 0) {           // the upper tile the scan's 32-column block covers
+            const float z[4] = {0.f, 0.f, 0.f, 0.f};
+            put4((rb + 1) * 16 + kq, z);
         }
         for (int cb = 0; cb <= rb; cb++) {
             f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int k0 = 0; k0 < DK; k0 += 16)
-                acc = mfma_k16(lds4(QL + (rb * 16 + r16) * KP + k0 + kq),
-                               lds4(Ks + (cb * 16 + r16) * KP + k0 + kq), acc);
-            const int s = cb * 16 + r16;
+                acc = mfma_k16(lds4(Ks + (cb * 16 + r16) * KP + k0 + kq),
+                               lds4(QL + (rb * 16 + r16) * KP + k0 + kq), acc);
+            float v[4];
 #pragma unroll
             for (int i = 0; i < 4; i++) {
-                const int t = rb * 16 + kq + i;
-                put_split(A + bx_a_index(t, s, C / 32),
-                          s <= t ? exp_fast(gam[t] - gam[s]) * acc[i] : 0.0f);
+                const int s = cb * 16 + kq + i;
+                v[i] = s <= t ? exp_fast(gam[t] - gam[s]) * acc[i] : 0.0f;
             }
+            put4(cb * 16 + kq, v);
         }
     }
     // K K^T, row block w, kept in registers until Q's LDS copy is free
@@ -303,12 +357,29 @@ __global__ __launch_bounds__(256, 2) void k_gdn_chunk_wy(
         x[t] = x[t] - ((p0 + p1) + (p2 + p3));
     }
     const size_t ub = (size_t)blockIdx.x * C * DV;
-    if (tid < DV) {
+    if (tid < DV) {                    // U: 4 consecutive t of column tid are 16 contiguous bytes
 #pragma unroll
-        for (int t = 0; t < C; t++) Ub[ub + wy_u_index(t, tid)] = x[t];
-    } else {
+        for (int t = 0; t < C; t += 4)
+            *reinterpret_cast<float4 *>(Ub + ub + wy_u_index(t, tid)) =
+                make_float4(x[t], x[t + 1], x[t + 2], x[t + 3]);
+    }
+    // W through LDS (L is no longer read): column tid - DV of every row in,
+    // then 32-byte units of 8 consecutive columns of one row out
+    __syncthreads();
+    float *Wl = QL;
+    if (tid >= DV) {
 #pragma unroll
-        for (int t = 0; t < C; t++) put_split(Wb + 2 * ub + bx_a_index(t, tid - DV, DK / 32), x[t]);
+        for (int t = 0; t < C; t++) Wl[t * KP + (tid - DV)] = x[t];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int u = 0; u < C * DK / 8 / 256; u++) {
+        const int e = tid + 256 * u, t = e / (DK / 8), c0 = (e % (DK / 8)) * 8;
+        float w8[8];
+        const float4 a0 = lds4(Wl + t * KP + c0), a1 = lds4(Wl + t * KP + c0 + 4);
+        w8[0] = a0.x; w8[1] = a0.y; w8[2] = a0.z; w8[3] = a0.w;
+        w8[4] = a1.x; w8[5] = a1.y; w8[6] = a1.z; w8[7] = a1.w;
+        put_split8(Wb + 2 * ub + bx_a_index(t, c0, DK / 32), w8);
     }
 }
 
