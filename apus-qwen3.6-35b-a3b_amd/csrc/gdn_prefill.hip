@@ -415,13 +415,22 @@ __device__ __forceinline__ f32x4 mfma_x3(u16x8 ah, u16x8 al, u16x8 bh, u16x8 bl,
 constexpr int SB = DK + 8;     // bf16 row stride of the state slice copies
 constexpr int DB = C + 8;      // bf16 row stride of the D copies
 
+// One chunk step's operands in registers. A wavefront uses one role's
+// fields only, so the two roles share the storage:
+//   recurrence: ScanOps b = W (row block w: 4 column blocks x hi/lo), u = U;
+//               ScanOps2 b = K (2 state-row blocks x 2 key blocks x hi/lo);
+//   output:     ScanOps b = Q (row block w); ScanOps2 b[0..3] = A (causal part).
+// The operands a step needs first (W / Q, U, the decay factors) form a
+// two-slot ring: step ci reads slot ci % 2 and, once they are consumed,
+// reloads them with step ci + 2's, so those loads have two chunk steps to
+// arrive; K / A (needed late in a step) are loaded one step ahead.
 struct ScanOps {
-    u16x8 w[DK / 32][2];            // W operand, row block w (hi, lo)      (waves 0-3)
-    u16x8 k[2][C / 32][2];          // K operand, state-row blocks          (waves 0-3)
-    float4 u;                       // U in the D-tile layout               (waves 0-3)
-    u16x8 q[DK / 32][2];            // Q operand, row block w               (waves 4-7)
-    u16x8 a[C / 32][2];             // A operand, causal part               (waves 4-7)
+    u16x8 b[8];
+    float4 u;
     float f;                        // decay factors (threads < 2C)
+};
+struct ScanOps2 {
+    u16x8 b[8];                     // K (recurrence) or A (output), one step ahead
 };
 
 __device__ __forceinline__ void scan_load_wu(ScanOps &nx, const uint16_t *__restrict__ Wb,
@@ -430,39 +439,42 @@ __device__ __forceinline__ void scan_load_wu(ScanOps &nx, const uint16_t *__rest
     const uint16_t *W = Wb + u * C * DK * 2 + ((size_t)wave * (DK / 32) * 64 + lane) * 16;
 #pragma unroll
     for (int kb = 0; kb < DK / 32; kb++) {
-        nx.w[kb][0] = ld8(W + kb * 64 * 16);
-        nx.w[kb][1] = ld8(W + kb * 64 * 16 + 8);
+        nx.b[2 * kb] = ld8(W + kb * 64 * 16);
+        nx.b[2 * kb + 1] = ld8(W + kb * 64 * 16 + 8);
     }
     nx.u = ld4(Ub + u * C * DV + ((size_t)(cb * 4 + wave) * 64 + lane) * 4);
 }
 
-__device__ __forceinline__ void scan_load_k(ScanOps &nx, const uint16_t *__restrict__ Kp,
+__device__ __forceinline__ void scan_load_k(ScanOps2 &nx, const uint16_t *__restrict__ Kp,
                                             size_t uk, int wave, int lane) {
     const uint16_t *K = Kp + uk * C * DK * 2 + ((size_t)wave * 2 * (C / 32) * 64 + lane) * 16;
 #pragma unroll
     for (int r = 0; r < 2; r++)
 #pragma unroll
         for (int kb = 0; kb < C / 32; kb++) {
-            nx.k[r][kb][0] = ld8(K + (r * (C / 32) + kb) * 64 * 16);
-            nx.k[r][kb][1] = ld8(K + (r * (C / 32) + kb) * 64 * 16 + 8);
+            nx.b[4 * r + 2 * kb] = ld8(K + (r * (C / 32) + kb) * 64 * 16);
+            nx.b[4 * r + 2 * kb + 1] = ld8(K + (r * (C / 32) + kb) * 64 * 16 + 8);
         }
 }
 
-__device__ __forceinline__ void scan_load_out(ScanOps &nx, const uint16_t *__restrict__ Qp,
-                                              const uint16_t *__restrict__ Ab, size_t u,
-                                              size_t uk, int ow, int lane) {
+__device__ __forceinline__ void scan_load_q(ScanOps &nx, const uint16_t *__restrict__ Qp,
+                                            size_t uk, int ow, int lane) {
     const uint16_t *Q = Qp + uk * C * DK * 2 + ((size_t)ow * (DK / 32) * 64 + lane) * 16;
 #pragma unroll
     for (int kb = 0; kb < DK / 32; kb++) {
-        nx.q[kb][0] = ld8(Q + kb * 64 * 16);
-        nx.q[kb][1] = ld8(Q + kb * 64 * 16 + 8);
+        nx.b[2 * kb] = ld8(Q + kb * 64 * 16);
+        nx.b[2 * kb + 1] = ld8(Q + kb * 64 * 16 + 8);
     }
+}
+
+__device__ __forceinline__ void scan_load_a(ScanOps2 &nx, const uint16_t *__restrict__ Ab,
+                                            size_t u, int ow, int lane) {
     const uint16_t *Ar = Ab + u * C * C * 2 + ((size_t)ow * (C / 32) * 64 + lane) * 16;
 #pragma unroll
     for (int kb = 0; kb < C / 32; kb++)
         if (kb <= ow / 2) {
-            nx.a[kb][0] = ld8(Ar + kb * 64 * 16);
-            nx.a[kb][1] = ld8(Ar + kb * 64 * 16 + 8);
+            nx.b[2 * kb] = ld8(Ar + kb * 64 * 16);
+            nx.b[2 * kb + 1] = ld8(Ar + kb * 64 * 16 + 8);
         }
 }
 
@@ -507,23 +519,29 @@ __global__ __launch_bounds__(512) void k_gdn_chunk_scan(
 
     const int c0 = coff[s], c1 = coff[s + 1];
     const int tS = cu[s], tE = cu[s + 1];
-    ScanOps nx;
+    auto load_first = [&](ScanOps &nx, int ci) {
+        const size_t u = (size_t)ci * hv + h, uk = (size_t)ci * hk + kh;
+        if (tid < 2 * C) nx.f = Fb[u * 2 * C + tid];
+        if (rec) scan_load_wu(nx, Wb, Ub, u, wr, lane, cb);
+        else scan_load_q(nx, Qp, uk, wr, lane);
+    };
+    ScanOps ring0, ring1;
+    ScanOps2 late;
     if (c0 < c1) {
-        const size_t u = (size_t)c0 * hv + h, uk = (size_t)c0 * hk + kh;
-        if (tid < 2 * C) Fs[tid] = Fb[u * 2 * C + tid];
-        if (rec) {
-            scan_load_wu(nx, Wb, Ub, u, wr, lane, cb);
-            scan_load_k(nx, Kp, uk, wr, lane);
-        } else {
-            scan_load_out(nx, Qp, Ab, u, uk, wr, lane);
-        }
+        load_first(ring0, c0);
+        if (tid < 2 * C) Fs[tid] = ring0.f;
+        if (rec) scan_load_k(late, Kp, (size_t)c0 * hk + kh, wr, lane);
+        else scan_load_a(late, Ab, (size_t)c0 * hv + h, wr, lane);
     }
+    if (c0 + 1 < c1) load_first(ring1, c0 + 1);
 
-    for (int ci = c0; ci < c1; ci++) {
+    // chunk step ci from slot cur (the other slot holds step ci + 1)
+    auto step = [&](ScanOps &cur, const ScanOps &oth, int ci) {
         const int t0 = tS + (ci - c0) * C, nt = min(C, tE - t0);
-        const bool more = ci + 1 < c1;
-        const size_t un = (size_t)(ci + 1) * hv + h, ukn = (size_t)(ci + 1) * hk + kh;
-        if (more && tid < 2 * C) nx.f = Fb[un * 2 * C + tid];
+        const bool more = ci + 1 < c1, more2 = ci + 2 < c1;
+        const size_t u2 = (size_t)(ci + 2) * hv + h, uk2 = (size_t)(ci + 2) * hk + kh;
+        const size_t u1 = (size_t)(ci + 1) * hv + h, uk1 = (size_t)(ci + 1) * hk + kh;
+        if (more2 && tid < 2 * C) cur.f = Fb[u2 * 2 * C + tid];
         __syncthreads();               // the state slice and Fs of this chunk are in place
 
         f32x4 o = {0.f, 0.f, 0.f, 0.f};
@@ -532,9 +550,10 @@ __global__ __launch_bounds__(512) void k_gdn_chunk_scan(
             f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int kb = 0; kb < DK / 32; kb++)
-                acc = mfma_x3(nx.w[kb][0], nx.w[kb][1], ld8(S0h + r16 * SB + kb * 32 + g4 * 8),
+                acc = mfma_x3(cur.b[2 * kb], cur.b[2 * kb + 1],
+                              ld8(S0h + r16 * SB + kb * 32 + g4 * 8),
                               ld8(S0l + r16 * SB + kb * 32 + g4 * 8), acc);
-            const float uu[4] = {nx.u.x, nx.u.y, nx.u.z, nx.u.w};
+            const float uu[4] = {cur.u.x, cur.u.y, cur.u.z, cur.u.w};
 #pragma unroll
             for (int i = 0; i < 4; i++) {
                 const int t = rw + kq + i;
@@ -542,15 +561,17 @@ __global__ __launch_bounds__(512) void k_gdn_chunk_scan(
                 split_bf(d, Dh[r16 * DB + t], Dl[r16 * DB + t]);
                 split_bf(Fs[C + t] * d, Dph[r16 * DB + t], Dpl[r16 * DB + t]);
             }
-            if (more) scan_load_wu(nx, Wb, Ub, un, wr, lane, cb);
+            if (more2) scan_load_wu(cur, Wb, Ub, u2, wr, lane, cb);
         } else {
             // O rows [rw, rw+16): G_t (Q S0)
 #pragma unroll
             for (int kb = 0; kb < DK / 32; kb++)
-                o = mfma_x3(nx.q[kb][0], nx.q[kb][1], ld8(S0h + r16 * SB + kb * 32 + g4 * 8),
+                o = mfma_x3(cur.b[2 * kb], cur.b[2 * kb + 1],
+                            ld8(S0h + r16 * SB + kb * 32 + g4 * 8),
                             ld8(S0l + r16 * SB + kb * 32 + g4 * 8), o);
 #pragma unroll
             for (int i = 0; i < 4; i++) o[i] = Fs[rw + kq + i] * o[i];
+            if (more2) scan_load_q(cur, Qp, uk2, wr, lane);
         }
         __syncthreads();               // D complete
 
@@ -566,18 +587,19 @@ __global__ __launch_bounds__(512) void k_gdn_chunk_scan(
 #pragma unroll
                 for (int kb = 0; kb < C / 32; kb++)
                     sn[r] = mfma_x3(ld8(Dph + r16 * DB + kb * 32 + g4 * 8),
-                                    ld8(Dpl + r16 * DB + kb * 32 + g4 * 8), nx.k[r][kb][0],
-                                    nx.k[r][kb][1], sn[r]);
+                                    ld8(Dpl + r16 * DB + kb * 32 + g4 * 8),
+                                    late.b[4 * r + 2 * kb], late.b[4 * r + 2 * kb + 1], sn[r]);
             }
-            if (more) scan_load_k(nx, Kp, ukn, wr, lane);
+            if (more) scan_load_k(late, Kp, uk1, wr, lane);
         } else {
             // ... + A D over the causal part s < rw + 16, then rnd(o)
 #pragma unroll
             for (int kb = 0; kb < C / 32; kb++)
                 if (kb <= wr / 2)
-                    o = mfma_x3(nx.a[kb][0], nx.a[kb][1], ld8(Dh + r16 * DB + kb * 32 + g4 * 8),
+                    o = mfma_x3(late.b[2 * kb], late.b[2 * kb + 1],
+                                ld8(Dh + r16 * DB + kb * 32 + g4 * 8),
                                 ld8(Dl + r16 * DB + kb * 32 + g4 * 8), o);
-            if (more) scan_load_out(nx, Qp, Ab, un, ukn, wr, lane);
+            if (more) scan_load_a(late, Ab, u1, wr, lane);
 #pragma unroll
             for (int i = 0; i < 4; i++) {
                 const int t = rw + kq + i;
@@ -597,7 +619,11 @@ __global__ __launch_bounds__(512) void k_gdn_chunk_scan(
                 }
             }
         }
-        if (more && tid < 2 * C) Fs[tid] = nx.f;
+        if (more && tid < 2 * C) Fs[tid] = oth.f;
+    };
+    for (int ci = c0; ci < c1; ci += 2) {
+        step(ring0, ring1, ci);
+        if (ci + 1 < c1) step(ring1, ring0, ci + 1);
     }
     __syncthreads();
     for (int e = tid; e < CB * DK; e += 512) {
