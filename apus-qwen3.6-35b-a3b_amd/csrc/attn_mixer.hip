@@ -51,7 +51,13 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x8 __attribute__((ext_vector_type(8)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 constexpr float kL2E = 1.44269504088896341f;
+// two fp32 values as bf16 codes (hardware round-to-nearest-even), lo first
+__device__ __forceinline__ uint32_t pack2(float lo, float hi) {
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{lo, hi}, bf16x2));
+}
 typedef unsigned short u16x8 __attribute__((ext_vector_type(8)));
 
 __device__ __forceinline__ bf16x8 ld_bf16x8(const uint16_t *p) {
@@ -262,11 +268,12 @@ struct SplitCtx {
     int s, kvh, sp, gsplit, tq, pos0, ctx, k0, k1;
 };
 
-__device__ __forceinline__ SplitCtx split_ctx(const int32_t *cu, const int32_t *pos0,
-                                              const int32_t *soff, int nseq, int nkv, int ks) {
+__device__ __forceinline__ SplitCtx split_ctx_of(const int32_t *cu, const int32_t *pos0,
+                                                 const int32_t *soff, int nseq, int nkv, int ks,
+                                                 int item) {
     SplitCtx c;
-    c.kvh = blockIdx.x % nkv;
-    c.gsplit = blockIdx.x / nkv;
+    c.kvh = item % nkv;
+    c.gsplit = item / nkv;
     c.s = seq_of(soff, nseq, c.gsplit);
     c.sp = c.gsplit - soff[c.s];
     c.tq = cu[c.s + 1] - cu[c.s];
@@ -277,26 +284,85 @@ __device__ __forceinline__ SplitCtx split_ctx(const int32_t *cu, const int32_t *
     return c;
 }
 
-// ---- k_attn_scores: one wavefront per (split, kv head) -----------------
-// MFMA 16x16x32 bf16 (A: lane l holds row l%16, k (l/16)*8..+8; B: col
-// l%16, same k; D: rows (l/16)*4+i, col l%16). S^T[key][row] = K Q^T: the
-// four lanes of a key row read 64 contiguous bytes of it per instruction.
-// NRB row blocks of 16 (NRB = 2 when a sequence has more than 2 tokens).
-template <int NRB>
-__global__ __launch_bounds__(64) void k_attn_scores(
-    AttnSeqs sq, const int32_t *__restrict__ dmeta, const uint16_t *__restrict__ qn,
-    const uint16_t *__restrict__ kcache, size_t max_seq, int nh, int nkv, float scale,
-    uint16_t *__restrict__ As, float2 *__restrict__ stats) {
-    const Meta mt = meta_of(sq, dmeta);
-    const int32_t *cu = mt.cu;
-    const SplitCtx c = split_ctx(cu, mt.pos0, mt.soff, sq.n, nkv, sq.ks1);
-    const int l = threadIdx.x, c16 = l & 15, q4 = l >> 4;
+// item = blockIdx.x (one wavefront per item)
+__device__ __forceinline__ SplitCtx split_ctx(const int32_t *cu, const int32_t *pos0,
+                                              const int32_t *soff, int nseq, int nkv, int ks) {
+    return split_ctx_of(cu, pos0, soff, nseq, nkv, ks, blockIdx.x);
+}
 
-    bf16x8 qf[NRB][D / 32];
-    int lim[NRB];
-    bool vrow[NRB];
+// ---- k_attn_scores: W streaming wavefronts + 1 writer per workgroup ------
+// Each streaming wavefront owns one (split, kv head) item. MFMA 16x16x32
+// bf16 (A: lane l holds row l%16, k (l/16)*8..+8; B: col l%16, same k; D:
+// rows (l/16)*4+i, col l%16). S^T[key][row] = K Q^T: the four lanes of a key
+// row read 64 contiguous bytes of it per instruction. NRB row blocks of 16
+// (NRB = 2 when a sequence has more than 2 tokens).
+//
+// The streaming wavefronts issue no global stores. The vector memory
+// counter is shared by loads and stores and retires in order, and a store
+// issued into a saturated read stream is acknowledged microseconds late, so
+// any later wait on a K load would stall behind it (measured: a 3% store mix
+// costs ~20% of the stream, whether or not the stores reach HBM). Instead
+// each 64-key group's scores go into a per-wavefront LDS ring of kScRing
+// slots, a "ready" count in LDS publishes them, and the workgroup's last
+// wavefront copies published slots to global memory and returns them with
+// a "done" count. A wavefront's DS instructions execute in issue order, so a count written after its data is never seen before that data.
+constexpr int kScRing = 4;
+template <int NRB> struct ScoresShape {
+    static constexpr int W = NRB == 1 ? 11 : 7;   // streaming wavefronts (+1 writer)
+    static constexpr int SLOT = 2 * NRB * 64;     // uint4 per slot: 16*NRB rows x 64 keys
+};
+template <int NRB> constexpr int scores_items_per_block() { return ScoresShape<NRB>::W; }
+
+// relaxed workgroup-scope atomics: no cached values, and (unlike volatile)
+// no wait on the vector memory counter
+__device__ __forceinline__ int lds_count_load(int *p) {
+    return __builtin_amdgcn_readfirstlane(
+        __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP));
+}
+__device__ __forceinline__ void lds_count_store(int *p, int v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+__device__ __forceinline__ void compiler_fence() { asm volatile("" ::: "memory"); }
+
+// the K-cache score rows of item (split, kv head): [row][cap], absolute keys
+struct ScItem {
+    SplitCtx c;
+    uint16_t *Ab;
+    size_t cap;
+    int ngroups;
+};
+__device__ __forceinline__ ScItem scores_item(const Meta &mt, const AttnSeqs &sq, int nkv, int item,
+                                              int nitems, uint16_t *As) {
+    ScItem it;
+    if (item >= nitems) {
+        it.ngroups = 0;
+        return it;
+    }
+    it.c = split_ctx_of(mt.cu, mt.pos0, mt.soff, sq.n, nkv, sq.ks1, item);
+    it.cap = (size_t)(mt.soff[it.c.s + 1] - mt.soff[it.c.s]) * sq.ks1;
+    it.Ab = As + (size_t)mt.soff[it.c.s] * sq.ks1 * nkv * kRows + (size_t)it.c.kvh * kRows * it.cap;
+    it.ngroups = (it.c.k1 - it.c.k0 + 63) / 64;
+    return it;
+}
+
+// The streaming wavefront of k_attn_scores for an item whose sequence has
+// NR row blocks of queries (its ring slots, SLOT uint4 each, and counters
+// given).
+template <int NR, int SLOT>
+__device__ __forceinline__ void scores_stream(const Meta &mt, const SplitCtx &c,
+                                              const uint16_t *__restrict__ qn,
+                                              const uint16_t *__restrict__ kcache, size_t max_seq,
+                                              int nh, int nkv, float scale,
+                                              float2 *__restrict__ stats, uint4 *ringw,
+                                              int *readyw, int *donew) {
+    const int32_t *cu = mt.cu;
+    const int l = threadIdx.x & 63, c16 = l & 15, q4 = l >> 4;
+
+    bf16x8 qf[NR][D / 32];
+    int lim[NR];
+    bool vrow[NR];
 #pragma unroll
-    for (int rb = 0; rb < NRB; rb++) {
+    for (int rb = 0; rb < NR; rb++) {
         const int n = rb * 16 + c16, t = n / GRP, g = n % GRP;
         vrow[rb] = t < c.tq;
         lim[rb] = c.pos0 + t;
@@ -309,86 +375,117 @@ __global__ __launch_bounds__(64) void k_attn_scores(
         }
     }
     const uint16_t *Kb = kcache + ((size_t)c.s * nkv + c.kvh) * max_seq * D;
-    // score rows of this (sequence, kv head): [row][cap] with absolute keys
-    const size_t cap = (size_t)(mt.soff[c.s + 1] - mt.soff[c.s]) * sq.ks1;
-    uint16_t *Ab = As + (size_t)mt.soff[c.s] * sq.ks1 * nkv * kRows + (size_t)c.kvh * kRows * cap;
-    float mrun[NRB], lrun[NRB];
+    float mrun[NR], lrun[NR];
 #pragma unroll
-    for (int rb = 0; rb < NRB; rb++) { mrun[rb] = -INFINITY; lrun[rb] = 0.0f; }
+    for (int rb = 0; rb < NR; rb++) { mrun[rb] = -INFINITY; lrun[rb] = 0.0f; }
 
-    // K fragments of the next 16-key block are loaded while the current
-    // block is multiplied (double buffering keeps 16 loads per lane in flight)
     // Keys are processed in groups of 64 as four MFMA blocks j = 0..3. MFMA
     // row m of block j is key g0 + (m/4)*16 + 4*j + m%4, so the lane whose
     // output rows are m = 4*q4 .. 4*q4+3 ends a group holding the 16
-    // consecutive scores g0 + 16*q4 .. +15 of its row: one 32-byte store per
-    // lane and 128 contiguous bytes per row. K rows past the split end are
-    // clamped to a valid row, never zeroed (touching a loaded value on issue
-    // would wait for it); their scores are never stored or counted.
-    bf16x8 kf[D / 32];
-    auto load_k = [&](int g0, int j, bf16x8 *f) {
+    // consecutive scores g0 + 16*q4 .. +15 of its row: 32 bytes per lane and
+    // 128 contiguous bytes per row. K rows past the split end are clamped to
+    // a valid row, never zeroed (touching a loaded value on issue would wait
+    // for it); their scores are never stored or counted.
+    auto load_k = [&](int g0, int j, bf16x8 (&f)[D / 32]) {
         const int key = min(g0 + (c16 >> 2) * 16 + 4 * j + (c16 & 3), c.k1 - 1);
         const uint16_t *kr = Kb + (size_t)key * D + q4 * 8;
 #pragma unroll
         for (int ds = 0; ds < D / 32; ds++) f[ds] = ld_bf16x8(kr + ds * 32);
+        // keep the loads here: the scheduler would otherwise sink them to
+        // their first use and leave nothing in flight
+        __builtin_amdgcn_sched_barrier(0);
     };
-    load_k(c.k0, 0, kf);
-    for (int g0 = c.k0; g0 < c.k1; g0 += 64) {
-        uint16_t sc[NRB][16];
+    // the first key past which some row's scores are masked
+    int kmask = c.k1;
 #pragma unroll
-        for (int j = 0; j < 4; j++) {
-            bf16x8 kn[D / 32];
-            const bool more = j < 3 || g0 + 64 < c.k1;
-            if (more) load_k(j < 3 ? g0 : g0 + 64, (j + 1) & 3, kn);
-            f32x4 acc[NRB];
+    for (int rb = 0; rb < NR; rb++)
+        if (vrow[rb]) kmask = min(kmask, lim[rb] + 1);
+    kmask = __builtin_amdgcn_readfirstlane(min(kmask, c.pos0 + 1));
+    // Double buffering: while one 16-key block is multiplied the next one's
+    // 8 loads are in flight (the loads are unconditional: the prefetch past
+    // the split's end re-reads its last row), so the stream never drains
+    // between groups.
+    bf16x8 kA[D / 32], kB[D / 32];
+    load_k(c.k0, 0, kA);
+    for (int g0 = c.k0, grp = 0; g0 < c.k1; g0 += 64, grp++) {
+        // the writer must have drained this group's ring slot (read early;
+        // it is normally long done)
+        const int dn = lds_count_load(donew);
+        uint32_t sc[NR][8];                  // bf16 score codes, two per word
+        auto mma = [&](int j, const bf16x8 *kf) {
+            f32x4 acc[NR];
 #pragma unroll
-            for (int rb = 0; rb < NRB; rb++) acc[rb] = f32x4{};
+            for (int rb = 0; rb < NR; rb++) acc[rb] = f32x4{};
 #pragma unroll
             for (int ds = 0; ds < D / 32; ds++)
 #pragma unroll
-                for (int rb = 0; rb < NRB; rb++)
+                for (int rb = 0; rb < NR; rb++)
                     acc[rb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf[ds], qf[rb][ds], acc[rb], 0, 0, 0);
+            // A = rnd(rnd(q.k) * scale) = rnd(q.k * scale): scale = 1/sqrt(256)
+            // is a power of two (hardware RNE, two scores per instruction)
 #pragma unroll
-            for (int rb = 0; rb < NRB; rb++)
+            for (int rb = 0; rb < NR; rb++)
 #pragma unroll
-                for (int e = 0; e < 4; e++) sc[rb][4 * j + e] = f2bf(rndf(acc[rb][e]) * scale);
+                for (int e = 0; e < 4; e += 2)
+                    sc[rb][2 * j + e / 2] = pack2(acc[rb][e] * scale, acc[rb][e + 1] * scale);
+        };
+        load_k(g0, 1, kB);
+        mma(0, kA);
+        load_k(g0, 2, kA);
+        mma(1, kB);
+        load_k(g0, 3, kB);
+        mma(2, kA);
+        load_k(g0 + 64, 0, kA);
+        mma(3, kB);
+
+        // publish the group's scores to the writer through the ring
+        if (grp >= kScRing && dn <= grp - kScRing)
+            while (lds_count_load(donew) <= grp - kScRing) __builtin_amdgcn_s_sleep(1);
+        compiler_fence();
+        uint4 *sl = ringw + (grp % kScRing) * SLOT;
 #pragma unroll
-            for (int ds = 0; ds < D / 32; ds++) kf[ds] = kn[ds];
+        for (int rb = 0; rb < NR; rb++) {          // row rb*16 + c16, keys 16*q4..+15
+            uint4 *r = sl + (rb * 16 + c16) * 8 + 2 * q4;
+            r[0] = make_uint4(sc[rb][0], sc[rb][1], sc[rb][2], sc[rb][3]);
+            r[1] = make_uint4(sc[rb][4], sc[rb][5], sc[rb][6], sc[rb][7]);
         }
+        compiler_fence();
+        if (l == 0) lds_count_store(readyw, grp + 1);
+
         const int kq = g0 + 16 * q4;           // this lane's 16 keys
 #pragma unroll
-        for (int rb = 0; rb < NRB; rb++) {
+        for (int rb = 0; rb < NR; rb++) {
             if (!vrow[rb]) continue;
-            if (kq < c.k1) {
-                u16x8 lo, hi;
+            float a[16];
 #pragma unroll
-                for (int e = 0; e < 8; e++) { lo[e] = sc[rb][e]; hi[e] = sc[rb][8 + e]; }
-                u16x8 *dst = reinterpret_cast<u16x8 *>(Ab + (size_t)(rb * 16 + c16) * cap + kq);
-                dst[0] = lo;
-                dst[1] = hi;
+            for (int e = 0; e < 8; e++) {
+                a[2 * e] = __uint_as_float(sc[rb][e] << 16);
+                a[2 * e + 1] = __uint_as_float(sc[rb][e] & 0xffff0000u);
             }
-            float bmax = -INFINITY;
-#pragma unroll
-            for (int e = 0; e < 16; e++) {
-                const int kk = kq + e;
-                if (kk <= lim[rb] && kk < c.k1) bmax = fmaxf(bmax, bf2f(sc[rb][e]));
-            }
-            if (bmax > -INFINITY) {
-                const float mn = fmaxf(mrun[rb], bmax);
-                float add = 0.0f;
+            if (g0 + 64 > kmask) {             // (wave-uniform) keys past a query or the split
 #pragma unroll
                 for (int e = 0; e < 16; e++) {
                     const int kk = kq + e;
-                    if (kk <= lim[rb] && kk < c.k1) add += exp_fast(bf2f(sc[rb][e]) - mn);
+                    if (!(kk <= lim[rb] && kk < c.k1)) a[e] = -INFINITY;
                 }
-                lrun[rb] = lrun[rb] * exp_fast(mrun[rb] - mn) + add;
+            }
+            float bmax = a[0];
+#pragma unroll
+            for (int e = 1; e < 16; e++) bmax = fmaxf(bmax, a[e]);
+            if (bmax > -INFINITY) {
+                // running (max, sum of e^{A - m}) with the hardware exp2
+                const float mn = fmaxf(mrun[rb], bmax), kn = mn * kL2E;
+                float add = 0.0f;
+#pragma unroll
+                for (int e = 0; e < 16; e++) add += __builtin_amdgcn_exp2f(fmaf(a[e], kL2E, -kn));
+                lrun[rb] = lrun[rb] * __builtin_amdgcn_exp2f((mrun[rb] - mn) * kL2E) + add;
                 mrun[rb] = mn;
             }
         }
     }
     // the four lanes l%16 + {0,16,32,48} hold the key quarters of one row
 #pragma unroll
-    for (int rb = 0; rb < NRB; rb++) {
+    for (int rb = 0; rb < NR; rb++) {
         float m = mrun[rb], ls = lrun[rb];
 #pragma unroll
         for (int off = 16; off < 64; off <<= 1) {
@@ -402,29 +499,115 @@ __global__ __launch_bounds__(64) void k_attn_scores(
     }
 }
 
+template <int NRB>
+__global__ __launch_bounds__(64 * (ScoresShape<NRB>::W + 1)) void k_attn_scores(
+    AttnSeqs sq, const int32_t *__restrict__ dmeta, const uint16_t *__restrict__ qn,
+    const uint16_t *__restrict__ kcache, size_t max_seq, int nh, int nkv, float scale,
+    uint16_t *__restrict__ As, float2 *__restrict__ stats, int nitems) {
+    constexpr int W = ScoresShape<NRB>::W, SLOT = ScoresShape<NRB>::SLOT;
+    __shared__ uint4 ring[W][kScRing][SLOT];
+    __shared__ int ready[W], done[W];
+    const int wave = threadIdx.x >> 6, l = threadIdx.x & 63, c16 = l & 15, q4 = l >> 4;
+    if (threadIdx.x < W) {
+        ready[threadIdx.x] = 0;
+        done[threadIdx.x] = 0;
+    }
+    __syncthreads();
+    const Meta mt = meta_of(sq, dmeta);
+
+    if (wave == W) {
+        // ---- writer: copy published slots of the W items to global memory.
+        // Item parameters are computed once, before any store is issued: a
+        // load after a store would wait for the store's acknowledgement.
+        int nxt[W], ng[W], k0[W], k1[W], tq[W];
+        uint16_t *Ab[W];
+        size_t cap[W];
+#pragma unroll
+        for (int w = 0; w < W; w++) {
+            const ScItem it = scores_item(mt, sq, nkv, blockIdx.x * W + w, nitems, As);
+            nxt[w] = 0;
+            ng[w] = it.ngroups;
+            if (ng[w] > 0) {
+                k0[w] = it.c.k0;
+                k1[w] = it.c.k1;
+                tq[w] = it.c.tq;
+                Ab[w] = it.Ab;
+                cap[w] = it.cap;
+            } else {
+                k0[w] = k1[w] = tq[w] = 0;
+                Ab[w] = nullptr;
+                cap[w] = 0;
+            }
+        }
+        for (;;) {
+            bool left = false, moved = false;
+#pragma unroll
+            for (int w = 0; w < W; w++) {
+                if (nxt[w] >= ng[w]) continue;
+                left = true;
+                const int rd = lds_count_load(&ready[w]);
+                if (rd <= nxt[w]) continue;
+                compiler_fence();
+                // slot layout [row][64 keys]: lane l stores 16 bytes (8 keys)
+                // of row 8*i + l/8, so a row's 128 bytes are whole lines
+                for (int g = nxt[w]; g < rd; g++) {
+                    const uint4 *sl = ring[w][g % kScRing];
+                    const int kq = k0[w] + 64 * g + 8 * (l & 7);
+#pragma unroll
+                    for (int i = 0; i < 2 * NRB; i++) {
+                        const int row = 8 * i + (l >> 3);
+                        if (row / GRP < tq[w] && kq < k1[w])
+                            *reinterpret_cast<uint4 *>(Ab[w] + (size_t)row * cap[w] + kq) = sl[i * 64 + l];
+                    }
+                }
+                compiler_fence();
+                nxt[w] = rd;
+                if (l == 0) lds_count_store(&done[w], rd);
+                moved = true;
+            }
+            if (!left) break;
+            if (!moved) __builtin_amdgcn_s_sleep(2);
+        }
+        return;
+    }
+
+    // ---- streaming wavefront
+    const int item = blockIdx.x * W + wave;
+    if (item >= nitems) return;
+    const SplitCtx c = split_ctx_of(mt.cu, mt.pos0, mt.soff, sq.n, nkv, sq.ks1, item);
+    // a sequence with at most 2 tokens fills one row block
+    if (NRB == 2 && c.tq <= 2)
+        scores_stream<1, SLOT>(mt, c, qn, kcache, max_seq, nh, nkv, scale, stats, ring[wave][0],
+                               &ready[wave], &done[wave]);
+    else
+        scores_stream<NRB, SLOT>(mt, c, qn, kcache, max_seq, nh, nkv, scale, stats, ring[wave][0],
+                                 &ready[wave], &done[wave]);
+}
+
 // ---- k_attn_pv: one wavefront per (split, kv head) ---------------------
 // O^T[d][row] = sum_key V^T[d][key] P^T[key][row] on MFMA 16x16x32: the
 // transposed V cache is the A operand (4 lanes read 64 contiguous bytes of
 // one d row), the probabilities the B operand.
-// (two row blocks hold 2 x 64 accumulators and the next step's operands:
-// one wavefront per SIMD, so they stay in registers)
-template <int NRB>
-__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(NRB == 1 ? 2 : 1))) void k_attn_pv(
-    AttnSeqs sq, const int32_t *__restrict__ dmeta, const uint16_t *__restrict__ vcache,
-    size_t max_seq, int nkv, const uint16_t *__restrict__ As,
-    const float2 *__restrict__ stats, float *__restrict__ Op) {
-    const Meta mt = meta_of(sq, dmeta);
+// DH wavefronts share an item, each owning D/DH of the d rows (DH = 2 for two
+// row blocks: 2 x 64 accumulators and the next step's V operands would not
+// fit in registers at two wavefronts per SIMD otherwise).
+// P.V over one item for a sequence with NR row blocks of queries; this
+// wavefront owns d blocks hb*NB .. +NB
+template <int NR, int NB>
+__device__ __forceinline__ void pv_item(const Meta &mt, const SplitCtx &c, int hb,
+                                        const AttnSeqs &sq, const uint16_t *__restrict__ vcache,
+                                        size_t max_seq, int nkv, const uint16_t *__restrict__ As,
+                                        const float2 *__restrict__ stats, float *__restrict__ Op) {
     const int32_t *soff = mt.soff;
-    const SplitCtx c = split_ctx(mt.cu, mt.pos0, mt.soff2, sq.n, nkv, sq.ks2);
     const int l = threadIdx.x, c16 = l & 15, q4 = l >> 4;
 
     // global (max, sum) of each row over every split of this (seq, kv head)
-    float m[NRB], rsum[NRB];
-    bool vrow[NRB];
-    int lim[NRB];
+    float m[NR], rsum[NR];
+    bool vrow[NR];
+    int lim[NR];
     const int ns = soff[c.s + 1] - soff[c.s];
 #pragma unroll
-    for (int rb = 0; rb < NRB; rb++) {
+    for (int rb = 0; rb < NR; rb++) {
         const int n = rb * 16 + c16, t = n / GRP;
         vrow[rb] = t < c.tq;
         lim[rb] = c.pos0 + t;
@@ -448,71 +631,91 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(NRB == 1 ? 2
     const uint16_t *Vb = vcache + ((size_t)c.s * nkv + c.kvh) * D * max_seq;
     const size_t cap = (size_t)(soff[c.s + 1] - soff[c.s]) * sq.ks1;
     const uint16_t *Ab = As + (size_t)soff[c.s] * sq.ks1 * nkv * kRows + (size_t)c.kvh * kRows * cap;
-    f32x4 acc[NRB][D / 16];
+    f32x4 acc[NR][NB];
 #pragma unroll
-    for (int rb = 0; rb < NRB; rb++)
+    for (int rb = 0; rb < NR; rb++)
 #pragma unroll
-        for (int b = 0; b < D / 16; b++) acc[rb][b] = f32x4{};
+        for (int b = 0; b < NB; b++) acc[rb][b] = f32x4{};
 
     // V^T and score fragments of the next 32-key step are loaded while the
     // current step is multiplied. Loads never touch their value on issue
     // (that would wait for them): addresses are clamped into the cache's
     // valid 8-key groups and the out-of-range keys are masked at use.
     const int kclamp = ((c.k1 - 1) / 8) * 8;   // last aligned group holding a valid key
-    u16x8 vf[D / 16], af[NRB];
+    const int kmask = min(c.k1, c.pos0 + 1);   // the first key masked for some row
+    u16x8 vf[NB], af[NR];
     auto load_step = [&](int kb, u16x8 *fv, u16x8 *fa) {
         const int kq = min(kb + q4 * 8, kclamp);
 #pragma unroll
-        for (int b = 0; b < D / 16; b++)
+        for (int b = 0; b < NB; b++)
             fv[b] = *reinterpret_cast<const u16x8 *>(
-                Vb + ((size_t)(kq / 32) * D + b * 16 + c16) * 32 + kq % 32);
+                Vb + ((size_t)(kq / 32) * D + (hb * NB + b) * 16 + c16) * 32 + kq % 32);
 #pragma unroll
-        for (int rb = 0; rb < NRB; rb++)
+        for (int rb = 0; rb < NR; rb++)
             fa[rb] = *reinterpret_cast<const u16x8 *>(Ab + (size_t)(rb * 16 + c16) * cap + kq);
     };
     load_step(c.k0, vf, af);
     for (int kb = c.k0; kb < c.k1; kb += 32) {
-        u16x8 vn[D / 16], an[NRB];
+        u16x8 vn[NB], an[NR];
         if (kb + 32 < c.k1) load_step(kb + 32, vn, an);
         const int kq = kb + q4 * 8;            // this lane's 8 keys
-        bf16x8 pf[NRB];
+        bf16x8 pf[NR];
 #pragma unroll
-        for (int rb = 0; rb < NRB; rb++) {
+        for (int rb = 0; rb < NR; rb++) {
+            // (rows of absent tokens are left unmasked: never written out)
             f32x8 e8;
 #pragma unroll
-            for (int e = 0; e < 8; e++) {
-                const int kk = kq + e;
-                const float p = __builtin_amdgcn_exp2f(fmaf(bf2f(af[rb][e]), kL2E, -rsum[rb]));
-                e8[e] = vrow[rb] && kk <= lim[rb] && kk < c.k1 ? p : 0.0f;
+            for (int e = 0; e < 8; e++)
+                e8[e] = __builtin_amdgcn_exp2f(fmaf(bf2f(af[rb][e]), kL2E, -rsum[rb]));
+            if (kb + 32 > kmask) {             // (wave-uniform) keys past a query or the split
+#pragma unroll
+                for (int e = 0; e < 8; e++)
+                    if (!(kq + e <= lim[rb] && kq + e < c.k1)) e8[e] = 0.0f;
             }
             pf[rb] = __builtin_convertvector(e8, bf16x8);     // hardware RNE
         }
         const bool partial = kq + 8 > c.k1;    // keys past the end: zero V too
 #pragma unroll
-        for (int b = 0; b < D / 16; b++) {
+        for (int b = 0; b < NB; b++) {
             u16x8 v8 = vf[b];
             if (partial)
                 for (int e = 0; e < 8; e++)
                     if (kq + e >= c.k1) v8[e] = 0;
             const bf16x8 va = __builtin_bit_cast(bf16x8, v8);
 #pragma unroll
-            for (int rb = 0; rb < NRB; rb++)
+            for (int rb = 0; rb < NR; rb++)
                 acc[rb][b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, pf[rb], acc[rb][b], 0, 0, 0);
         }
 #pragma unroll
-        for (int b = 0; b < D / 16; b++) vf[b] = vn[b];
+        for (int b = 0; b < NB; b++) vf[b] = vn[b];
 #pragma unroll
-        for (int rb = 0; rb < NRB; rb++) af[rb] = an[rb];
+        for (int rb = 0; rb < NR; rb++) af[rb] = an[rb];
     }
 #pragma unroll
-    for (int rb = 0; rb < NRB; rb++) {
+    for (int rb = 0; rb < NR; rb++) {
         if (!vrow[rb]) continue;
         float *orow = Op + (((size_t)c.gsplit * nkv + c.kvh) * kRows + rb * 16 + c16) * D;
 #pragma unroll
-        for (int b = 0; b < D / 16; b++)
-            *reinterpret_cast<float4 *>(orow + b * 16 + q4 * 4) =
+        for (int b = 0; b < NB; b++)
+            *reinterpret_cast<float4 *>(orow + (hb * NB + b) * 16 + q4 * 4) =
                 make_float4(acc[rb][b][0], acc[rb][b][1], acc[rb][b][2], acc[rb][b][3]);
     }
+}
+
+template <int NRB, int DH>
+__global__ __launch_bounds__(64) void k_attn_pv(
+    AttnSeqs sq, const int32_t *__restrict__ dmeta, const uint16_t *__restrict__ vcache,
+    size_t max_seq, int nkv, const uint16_t *__restrict__ As,
+    const float2 *__restrict__ stats, float *__restrict__ Op) {
+    const Meta mt = meta_of(sq, dmeta);
+    constexpr int NB = D / 16 / DH;            // 16-row d blocks of this wavefront
+    const int hb = DH == 1 ? 0 : (int)(blockIdx.x % DH);
+    const SplitCtx c = split_ctx_of(mt.cu, mt.pos0, mt.soff2, sq.n, nkv, sq.ks2, blockIdx.x / DH);
+    // a sequence with at most 2 tokens fills one row block
+    if (NRB == 2 && c.tq <= 2)
+        pv_item<1, NB>(mt, c, hb, sq, vcache, max_seq, nkv, As, stats, Op);
+    else
+        pv_item<NRB, NB>(mt, c, hb, sq, vcache, max_seq, nkv, As, stats, Op);
 }
 
 // ---- k_attn_combine: one block per (token, q head), d threads ----------
@@ -573,8 +776,9 @@ int attn_check_layer(const ApusHipAttnLayer *L) {
 
 // Fill the metadata (by value, or uploaded when B is large) and choose the
 // split sizes: each kernel's grid should be one round of resident waves
-// (occupancy x 4 SIMDs x CUs) so no straggler round is left; ks1 (scores)
-// is a multiple of 64 keys, ks2 (P.V) of 32.
+// (scores: one workgroup of W streaming wavefronts per CU; P.V: occupancy x
+// 4 SIMDs x CUs) so no straggler round is left; ks1 (scores) is a multiple
+// of 64 keys, ks2 (P.V) of 32.
 static int attn_meta(size_t B, const int32_t *cu, const int32_t *pos0, size_t max_seq,
                      size_t nkv, AttnSeqs *sq, const int32_t **dmeta, size_t *nsplit1,
                      size_t *nsplit2, size_t *max_tok) {
@@ -593,13 +797,24 @@ static int attn_meta(size_t B, const int32_t *cu, const int32_t *pos0, size_t ma
         if ((size_t)tq > mt) mt = (size_t)tq;
     }
     const size_t slots = 4 * (size_t)cu_count();
-    const size_t occ1 = mt <= 2 ? 3 : 2, occ2 = 2;
-    auto pick = [](size_t work, size_t waves, size_t gran) {
-        size_t k = (work + waves - 1) / waves;
-        k = (k + gran - 1) / gran * gran;
-        return k < 256 ? (size_t)256 : k > 16384 ? (size_t)16384 : k;
+    // scores: one workgroup per CU, W streaming wavefronts each
+    const size_t w1 = mt <= 2 ? scores_items_per_block<1>() : scores_items_per_block<2>(), occ2 = 2;
+    // the smallest split (a multiple of gran, 256..16384 keys) whose items
+    // -- each sequence's last split partial -- fit in one round of waves
+    auto pick = [&](size_t waves, size_t gran) {
+        size_t k = (keys * nkv + waves - 1) / waves;
+        k = std::min<size_t>(std::max<size_t>((k + gran - 1) / gran * gran, 256), 16384);
+        for (; k < 16384; k += gran) {
+            size_t items = 0;
+            for (size_t s = 0; s < B; s++)
+                items += ((size_t)pos0[s] + (size_t)(cu[s + 1] - cu[s]) + k - 1) / k * nkv;
+            if (items <= waves) break;
+        }
+        return k;
     };
-    const size_t ks1 = pick(keys * nkv, occ1 * slots, 64), ks2 = pick(keys * nkv, occ2 * slots, 32);
+    // P.V: two wavefronts per item (halves of d) when a sequence has more
+    // than 2 tokens
+    const size_t ks1 = pick(w1 * cu_count(), 64), ks2 = pick(occ2 * slots / (mt <= 2 ? 1 : 2), 32);
     std::vector<int32_t> soff(B + 1, 0), soff2(B + 1, 0);
     for (size_t s = 0; s < B; s++) {
         const size_t ctx = (size_t)pos0[s] + (size_t)(cu[s + 1] - cu[s]);
@@ -694,19 +909,23 @@ int apus_hip_attn_decode(const ApusHipAttnLayer *L, size_t B, const int32_t *cu,
     // one 16-row block covers up to 2 new tokens per sequence (8 heads each)
     if (mt <= 2) {
         APUS_TIMED("k_attn_scores",
-                   k_attn_scores<1><<<grid, 64, 0, stream()>>>(sq, dmeta, qn, kcache, max_seq, (int)L->nh,
-                                                     (int)L->nkv, scale, As, st));
+                   k_attn_scores<1><<<cdiv(grid, scores_items_per_block<1>()),
+                                      64 * (scores_items_per_block<1>() + 1), 0, stream()>>>(
+                       sq, dmeta, qn, kcache, max_seq, (int)L->nh, (int)L->nkv, scale, As, st,
+                       (int)grid));
         APUS_LAUNCHED("k_attn_scores");
         APUS_TIMED("k_attn_pv",
-                   k_attn_pv<1><<<grid2, 64, 0, stream()>>>(sq, dmeta, vcache, max_seq, (int)L->nkv, As, st, Op));
+                   k_attn_pv<1, 1><<<grid2, 64, 0, stream()>>>(sq, dmeta, vcache, max_seq, (int)L->nkv, As, st, Op));
         APUS_LAUNCHED("k_attn_pv");
     } else {
         APUS_TIMED("k_attn_scores",
-                   k_attn_scores<2><<<grid, 64, 0, stream()>>>(sq, dmeta, qn, kcache, max_seq, (int)L->nh,
-                                                     (int)L->nkv, scale, As, st));
+                   k_attn_scores<2><<<cdiv(grid, scores_items_per_block<2>()),
+                                      64 * (scores_items_per_block<2>() + 1), 0, stream()>>>(
+                       sq, dmeta, qn, kcache, max_seq, (int)L->nh, (int)L->nkv, scale, As, st,
+                       (int)grid));
         APUS_LAUNCHED("k_attn_scores");
         APUS_TIMED("k_attn_pv",
-                   k_attn_pv<2><<<grid2, 64, 0, stream()>>>(sq, dmeta, vcache, max_seq, (int)L->nkv, As, st, Op));
+                   k_attn_pv<2, 2><<<2 * grid2, 64, 0, stream()>>>(sq, dmeta, vcache, max_seq, (int)L->nkv, As, st, Op));
         APUS_LAUNCHED("k_attn_pv");
     }
     APUS_TIMED("k_attn_combine",
