@@ -284,11 +284,6 @@ __device__ __forceinline__ SplitCtx split_ctx_of(const int32_t *cu, const int32_
     return c;
 }
 
-// item = blockIdx.x (one wavefront per item)
-__device__ __forceinline__ SplitCtx split_ctx(const int32_t *cu, const int32_t *pos0,
-                                              const int32_t *soff, int nseq, int nkv, int ks) {
-    return split_ctx_of(cu, pos0, soff, nseq, nkv, ks, blockIdx.x);
-}
 
 // ---- k_attn_scores: W streaming wavefronts + 1 writer per workgroup ------
 // Each streaming wavefront owns one (split, kv head) item. MFMA 16x16x32
@@ -507,7 +502,7 @@ __global__ __launch_bounds__(64 * (ScoresShape<NRB>::W + 1)) void k_attn_scores(
     constexpr int W = ScoresShape<NRB>::W, SLOT = ScoresShape<NRB>::SLOT;
     __shared__ uint4 ring[W][kScRing][SLOT];
     __shared__ int ready[W], done[W];
-    const int wave = threadIdx.x >> 6, l = threadIdx.x & 63, c16 = l & 15, q4 = l >> 4;
+    const int wave = threadIdx.x >> 6, l = threadIdx.x & 63;
     if (threadIdx.x < W) {
         ready[threadIdx.x] = 0;
         done[threadIdx.x] = 0;

@@ -5,6 +5,30 @@
 
 namespace apus {
 
+// rnd(co * sigmoid(co)) for a bf16 value co, with the sigmoid as the
+// reference forms it (exp correctly rounded, fp32 add and divide, fp32
+// product; c/gdn.h:19-33). An fp32 evaluation through the hardware exp2 and
+// reciprocal lands within ~11 ulp of that product for |co| <= 16 (x log2(e)
+// rounding ~5.5 ulp through exp2, exp2 and rcp 1 ulp each, the remaining
+// roundings), so its bf16 rounding is the reference's unless the product
+// lies within 16 ulp of a rounding midpoint (every finite code is checked
+// against the reference formula by the conv1d op's test). ok = false for
+// those, for |co| outside [2^-60, 16] and for non-finite co: the caller
+// then takes the reference formula (or the bf16-code table).
+__device__ __forceinline__ uint16_t silu_fast(float co, bool &ok) {
+    const float ax = fabsf(co);
+    const float e = __builtin_amdgcn_exp2f(co * -1.44269504088896341f);
+    const float p = co * __builtin_amdgcn_rcpf(1.0f + e);
+    const uint32_t b = __float_as_uint(p), lo = b & 0xffffu;
+    ok = ax <= 16.0f && ax >= 0x1p-60f && (lo > 0x8000u + 16u || lo + 16u < 0x8000u);
+    return (uint16_t)((b + 0x7fffu + ((b >> 16) & 1u)) >> 16);
+}
+__device__ __forceinline__ uint16_t silu_bf16(float co) {
+    bool ok;
+    const uint16_t r = silu_fast(co, ok);
+    return ok ? r : f2bf(co * sigmoid_cr(co));
+}
+
 // Causal conv1d k=4 + SiLU for one channel (c/gdn.h:19-33, 220-228): the
 // four taps accumulate oldest first with one rounding per mul and add,
 // then rnd (point 1), SiLU in fp32, rnd (point 2).
@@ -15,8 +39,18 @@ __device__ __forceinline__ uint16_t conv_tap4(const float w[4], float s0,
     acc = acc + w[1] * s1;
     acc = acc + w[2] * s2;
     acc = acc + w[3] * x;
-    float co = rndf(acc);
-    return f2bf(co * sigmoid_cr(co));
+    return silu_bf16(rndf(acc));
+}
+
+// The 4-tap conv sum in tap order, as a bf16 code (the SiLU table's index).
+__device__ __forceinline__ uint16_t conv_sum4_code(const float w[4], float s0, float s1, float s2,
+                                                   float x) {
+    float acc = 0.0f;
+    acc = acc + w[0] * s0;
+    acc = acc + w[1] * s1;
+    acc = acc + w[2] * s2;
+    acc = acc + w[3] * x;
+    return f2bf(acc);
 }
 
 // The same with the SiLU taken from the bf16-code table (act_tables.hip):
@@ -25,12 +59,7 @@ __device__ __forceinline__ uint16_t conv_tap4(const float w[4], float s0,
 __device__ __forceinline__ uint16_t conv_tap4_tab(const float w[4], float s0, float s1,
                                                   float s2, float x,
                                                   const uint16_t *__restrict__ silu_bf) {
-    float acc = 0.0f;
-    acc = acc + w[0] * s0;
-    acc = acc + w[1] * s1;
-    acc = acc + w[2] * s2;
-    acc = acc + w[3] * x;
-    return silu_bf[f2bf(acc)];
+    return silu_bf[conv_sum4_code(w, s0, s1, s2, x)];
 }
 
 // Decay gate g = -exp(A_log) * softplus(a + dt_bias) (c/gdn.h:34-40).

@@ -290,10 +290,15 @@ __global__ __launch_bounds__(256) void k_gdn_prep(
     const int tid = threadIdx.x;
     const int hv = hk * REP;
     const size_t kd = (size_t)hk * DK, vd = (size_t)hv * DV, cd = 2 * kd + vd;
-    __shared__ __attribute__((aligned(16))) uint16_t xin[(PT + 3) * PC];
-    // q rows at 0, k rows at PT*RS (rows 16-byte aligned for the sums)
-    __shared__ __attribute__((aligned(16))) float raw[2 * PT * RS];
+    // The staged inputs, then (once every conv tap has been read) the conv
+    // outputs of q and k for the ordered sums: q rows at 0, k rows at PT*RS
+    // (rows 16-byte aligned). Sharing the space keeps 8 blocks per CU.
+    constexpr int XIN_B = (PT + 3) * PC * 2, RAW_B = 2 * PT * RS * 4;
+    __shared__ __attribute__((aligned(16))) char prep_lds[XIN_B > RAW_B ? XIN_B : RAW_B];
+    uint16_t *xin = reinterpret_cast<uint16_t *>(prep_lds);
+    float *raw = reinterpret_cast<float *>(prep_lds);
     __shared__ float rs[2][PT];
+    __shared__ int2 tseq[PT];                 // (sequence, its first token) per tile token
 
     // stage rows tb-3 .. tb+nt-1 (those that exist); LDS channel order
     // [q(128) | k(128) | v(256)]. Every load of the tile is issued before
@@ -318,6 +323,10 @@ __global__ __launch_bounds__(256) void k_gdn_prep(
         if (e < (PT + 3) * PC / 8 && t >= 0 && r < nt + 3)
             *reinterpret_cast<u16x8 *>(xin + r * PC + c8) = pc[k];
     }
+    if (tid < nt) {
+        const int sq = seq_of(cu, B, tb + tid);
+        tseq[tid] = make_int2(sq, cu[sq]);
+    }
     const size_t cqk = tid < DK ? (size_t)kh * DK + tid : kd + (size_t)kh * DK + (tid - DK);
     const int h = kh * REP + tid / DV, j = tid % DV;
     const size_t cv = 2 * kd + (size_t)h * DV + j;
@@ -329,27 +338,76 @@ __global__ __launch_bounds__(256) void k_gdn_prep(
     __syncthreads();
 
     float *rrow = raw + (tid < DK ? 0 : PT * RS) + (tid & (DK - 1));
-    int s = seq_of(cu, B, tb);
-    for (int i = 0; i < nt; i++) {
-        const int t = tb + i;
-        while (t >= cu[s + 1]) s++;
-        const int t0 = cu[s];
-        const uint16_t *cst = conv_state + (size_t)s * cd * 3;
-        float xq[4], xv[4];
+    // The tile's conv sums (bf16 codes) first, then SiLU, then the stores.
+    // Tokens past the tile's end use code 0.
+    uint16_t sq[PT], sv[PT];
+    const int2 ts0 = tseq[0], tsl = tseq[nt - 1];
+    if (ts0.y <= tb - 3 && ts0.x == tsl.x) {
+        // (tile-uniform) one sequence, its 3 preceding tokens staged too:
+        // every tap comes from the staged rows, read once, all in flight
+        // (rows past the tile's tokens give unused codes)
+        float xq[PT + 3], xv[PT + 3];
 #pragma unroll
-        for (int u = 0; u < 4; u++) {
-            const int ti = t - 3 + u;
-            if (ti >= t0) {
-                xq[u] = bf2f(xin[(i + u) * PC + tid]);
-                xv[u] = bf2f(xin[(i + u) * PC + 2 * DK + tid]);
-            } else {
-                xq[u] = bf2f(cst[cqk * 3 + (ti - t0 + 3)]);
-                xv[u] = bf2f(cst[cv * 3 + (ti - t0 + 3)]);
-            }
+        for (int r = 0; r < PT + 3; r++) {
+            xq[r] = bf2f(xin[r * PC + tid]);
+            xv[r] = bf2f(xin[r * PC + 2 * DK + tid]);
         }
-        rrow[i * RS] = bf2f(conv_tap4_tab(wq, xq[0], xq[1], xq[2], xq[3], silu_bf));
-        vconv[(size_t)t * vd + (size_t)h * DV + j] =
-            conv_tap4_tab(wv, xv[0], xv[1], xv[2], xv[3], silu_bf);
+#pragma unroll
+        for (int i = 0; i < PT; i++) {
+            sq[i] = conv_sum4_code(wq, xq[i], xq[i + 1], xq[i + 2], xq[i + 3]);
+            sv[i] = conv_sum4_code(wv, xv[i], xv[i + 1], xv[i + 2], xv[i + 3]);
+        }
+    } else {
+#pragma unroll
+    for (int i = 0; i < PT; i++) {
+        sq[i] = sv[i] = 0;
+        if (i < nt) {
+            const int2 ts = tseq[i];
+            const int t = tb + i, t0 = ts.y;
+            const uint16_t *cst = conv_state + (size_t)ts.x * cd * 3;
+            float xq[4], xv[4];
+#pragma unroll
+            for (int u = 0; u < 4; u++) {
+                const int ti = t - 3 + u;
+                if (ti >= t0) {
+                    xq[u] = bf2f(xin[(i + u) * PC + tid]);
+                    xv[u] = bf2f(xin[(i + u) * PC + 2 * DK + tid]);
+                } else {
+                    xq[u] = bf2f(cst[cqk * 3 + (ti - t0 + 3)]);
+                    xv[u] = bf2f(cst[cv * 3 + (ti - t0 + 3)]);
+                }
+            }
+            sq[i] = conv_sum4_code(wq, xq[0], xq[1], xq[2], xq[3]);
+            sv[i] = conv_sum4_code(wv, xv[0], xv[1], xv[2], xv[3]);
+        }
+    }
+    }
+    // SiLU through the fp32 fast path; the few results it cannot vouch for
+    // come from the bf16-code table (gathers with few lanes active), all
+    // issued before the first use (code 0 past the tile's tokens)
+    uint32_t redo = 0;
+#pragma unroll
+    for (int i = 0; i < PT; i++) {
+        bool okq, okv;
+        const uint16_t rq = silu_fast(bf2f(sq[i]), okq), rv = silu_fast(bf2f(sv[i]), okv);
+        redo |= (okq ? 0u : 1u << i) | (okv ? 0u : 1u << (PT + i));
+        if (okq) sq[i] = rq;
+        if (okv) sv[i] = rv;
+    }
+    if (redo) {
+#pragma unroll
+        for (int i = 0; i < PT; i++) {
+            if (redo >> i & 1u) sq[i] = silu_bf[sq[i]];
+            if (redo >> (PT + i) & 1u) sv[i] = silu_bf[sv[i]];
+        }
+    }
+    __syncthreads();                          // every tap read: raw may overwrite xin
+#pragma unroll
+    for (int i = 0; i < PT; i++) {
+        if (i < nt) {
+            rrow[i * RS] = bf2f(sq[i]);
+            vconv[(size_t)(tb + i) * vd + (size_t)h * DV + j] = sv[i];
+        }
     }
     __syncthreads();
     if (tid < 2 * PT) {                      // ordered sums, one lane per row

@@ -156,9 +156,6 @@ __device__ __forceinline__ void split_bf(float x, uint16_t &hi, uint16_t &lo) {
     hi = __builtin_bit_cast(uint16_t, h);
     lo = __builtin_bit_cast(uint16_t, (__bf16)(x - (float)h));
 }
-__device__ __forceinline__ void put_split(uint16_t *p, float x) {
-    split_bf(x, p[0], p[8]);
-}
 // the 8 hi codes then the 8 lo codes of x[0..7]: one 32-byte unit of the
 // packed operand layouts, written with two 16-byte stores
 __device__ __forceinline__ void put_split8(uint16_t *p, const float (&x)[8]) {

@@ -31,6 +31,35 @@ def test_conv1d(hip, orc, rng, C, T):
     assert np.array_equal(s1, s2)          # state = exact input codes
 
 
+def _silu_bf16_reference(codes):
+    """rnd(co * sigmoid(co)) with the reference's sigmoid (exp correctly
+    rounded to fp32, fp32 add, divide and product; c/gdn.h:19-33)."""
+    co = (codes.astype(np.uint32) << 16).view(np.float32)
+    with np.errstate(over="ignore"):
+        e = np.exp(-co.astype(np.float64)).astype(np.float32)
+        sg = np.float32(1.0) / (np.float32(1.0) + e)
+    p = (co * sg).view(np.uint32)
+    return ((p + 0x7FFF + ((p >> 16) & 1)) >> 16).astype(np.uint16)
+
+
+def test_conv1d_silu_every_code(hip):
+    """The conv's SiLU over every finite bf16 code (taps 0,0,0,1 on a zero
+    state pass the input code through the sum unchanged), bit-exact: its
+    fp32 fast path must hand every near-midpoint product to the reference
+    formula."""
+    codes = np.arange(65536, dtype=np.uint32)
+    finite = ((codes >> 7) & 0xFF) != 0xFF
+    x = codes[finite].astype(np.uint16)
+    x = x[x != 0x8000][None, :]             # -0 sums to +0
+    C = x.shape[1]
+    w = np.tile(np.array([0, 0, 0, 0x3F80], np.uint16), (C, 1))
+    st = np.zeros(C * 3, np.uint16)
+    out = hip.gdn_conv1d(x, w, st)
+    exp = _silu_bf16_reference(x[0])
+    bad = np.flatnonzero(out[0] != exp)
+    assert bad.size == 0, f"{bad.size} codes differ, e.g. {[(hex(x[0][i]), hex(out[0][i]), hex(exp[i])) for i in bad[:5]]}"
+
+
 def test_decay_beta(hip, orc, rng):
     H = 4099
     a = synth.normal_bf16(rng, (H,), 3.0)
