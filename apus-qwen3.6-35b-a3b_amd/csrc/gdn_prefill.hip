@@ -468,11 +468,10 @@ __device__ __forceinline__ void scan_load_a(ScanOps2 &nx, const uint16_t *__rest
                                             size_t u, int ow, int lane) {
     const uint16_t *Ar = Ab + u * C * C * 2 + ((size_t)ow * (C / 32) * 64 + lane) * 16;
 #pragma unroll
-    for (int kb = 0; kb < C / 32; kb++)
-        if (kb <= ow / 2) {
-            nx.b[2 * kb] = ld8(Ar + kb * 64 * 16);
-            nx.b[2 * kb + 1] = ld8(Ar + kb * 64 * 16 + 8);
-        }
+    for (int kb = 0; kb < C / 32; kb++) {      // (the block past the diagonal is unused)
+        nx.b[2 * kb] = ld8(Ar + kb * 64 * 16);
+        nx.b[2 * kb + 1] = ld8(Ar + kb * 64 * 16 + 8);
+    }
 }
 
 __global__ __launch_bounds__(512) void k_gdn_chunk_scan(
@@ -516,34 +515,28 @@ __global__ __launch_bounds__(512) void k_gdn_chunk_scan(
 
     const int c0 = coff[s], c1 = coff[s + 1];
     const int tS = cu[s], tE = cu[s + 1];
-    auto load_first = [&](ScanOps &nx, int ci) {
-        const size_t u = (size_t)ci * hv + h, uk = (size_t)ci * hk + kh;
-        if (tid < 2 * C) nx.f = Fb[u * 2 * C + tid];
-        if (rec) scan_load_wu(nx, Wb, Ub, u, wr, lane, cb);
-        else scan_load_q(nx, Qp, uk, wr, lane);
-    };
-    ScanOps ring0, ring1;
-    ScanOps2 late;
-    if (c0 < c1) {
-        load_first(ring0, c0);
+    // Prefetches are unconditional, their chunk clamped to the sequence's
+    // last (re-read, unused): with no branch around them, and the two roles
+    // in loops of their own, every wait on a prefetch counts exactly the
+    // loads and stores issued after it instead of draining them all.
+    auto cl = [&](int ci) { return (size_t)min(ci, c1 - 1); };
+    if (c0 < c1 && rec) {
+        // ---- recurrence role: D = U - W S0 and S1 = G_C S0 + Dp^T K
+        ScanOps ring0, ring1;
+        ScanOps2 kf;
+        auto load_wu = [&](ScanOps &nx, int ci) {
+            const size_t u = cl(ci) * hv + h;
+            if (tid < 2 * C) nx.f = Fb[u * 2 * C + tid];
+            scan_load_wu(nx, Wb, Ub, u, wr, lane, cb);
+        };
+        load_wu(ring0, c0);
         if (tid < 2 * C) Fs[tid] = ring0.f;
-        if (rec) scan_load_k(late, Kp, (size_t)c0 * hk + kh, wr, lane);
-        else scan_load_a(late, Ab, (size_t)c0 * hv + h, wr, lane);
-    }
-    if (c0 + 1 < c1) load_first(ring1, c0 + 1);
-
-    // chunk step ci from slot cur (the other slot holds step ci + 1)
-    auto step = [&](ScanOps &cur, const ScanOps &oth, int ci) {
-        const int t0 = tS + (ci - c0) * C, nt = min(C, tE - t0);
-        const bool more = ci + 1 < c1, more2 = ci + 2 < c1;
-        const size_t u2 = (size_t)(ci + 2) * hv + h, uk2 = (size_t)(ci + 2) * hk + kh;
-        const size_t u1 = (size_t)(ci + 1) * hv + h, uk1 = (size_t)(ci + 1) * hk + kh;
-        if (more2 && tid < 2 * C) cur.f = Fb[u2 * 2 * C + tid];
-        __syncthreads();               // the state slice and Fs of this chunk are in place
-
-        f32x4 o = {0.f, 0.f, 0.f, 0.f};
-        if (rec) {
-            // D rows [rw, rw+16) of this slice: U - W S0
+        scan_load_k(kf, Kp, cl(c0) * hk + kh, wr, lane);
+        load_wu(ring1, c0 + 1);
+        auto step = [&](ScanOps &cur, const ScanOps &oth, int ci) {
+            const bool more = ci + 1 < c1;
+            if (tid < 2 * C) cur.f = Fb[(cl(ci + 2) * hv + h) * 2 * C + tid];
+            __syncthreads();           // the state slice and Fs of this chunk are in place
             f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int kb = 0; kb < DK / 32; kb++)
@@ -558,23 +551,9 @@ __global__ __launch_bounds__(512) void k_gdn_chunk_scan(
                 split_bf(d, Dh[r16 * DB + t], Dl[r16 * DB + t]);
                 split_bf(Fs[C + t] * d, Dph[r16 * DB + t], Dpl[r16 * DB + t]);
             }
-            if (more2) scan_load_wu(cur, Wb, Ub, u2, wr, lane, cb);
-        } else {
-            // O rows [rw, rw+16): G_t (Q S0)
-#pragma unroll
-            for (int kb = 0; kb < DK / 32; kb++)
-                o = mfma_x3(cur.b[2 * kb], cur.b[2 * kb + 1],
-                            ld8(S0h + r16 * SB + kb * 32 + g4 * 8),
-                            ld8(S0l + r16 * SB + kb * 32 + g4 * 8), o);
-#pragma unroll
-            for (int i = 0; i < 4; i++) o[i] = Fs[rw + kq + i] * o[i];
-            if (more2) scan_load_q(cur, Qp, uk2, wr, lane);
-        }
-        __syncthreads();               // D complete
-
-        f32x4 sn[2];
-        if (rec) {
-            // S1^T columns [32w, 32w+32): G_C S0^T + Dp^T K
+            scan_load_wu(cur, Wb, Ub, cl(ci + 2) * hv + h, wr, lane, cb);
+            __syncthreads();           // D complete
+            f32x4 sn[2];
             const float gc = Fs[C - 1];
 #pragma unroll
             for (int r = 0; r < 2; r++) {
@@ -585,26 +564,10 @@ __global__ __launch_bounds__(512) void k_gdn_chunk_scan(
                 for (int kb = 0; kb < C / 32; kb++)
                     sn[r] = mfma_x3(ld8(Dph + r16 * DB + kb * 32 + g4 * 8),
                                     ld8(Dpl + r16 * DB + kb * 32 + g4 * 8),
-                                    late.b[4 * r + 2 * kb], late.b[4 * r + 2 * kb + 1], sn[r]);
+                                    kf.b[4 * r + 2 * kb], kf.b[4 * r + 2 * kb + 1], sn[r]);
             }
-            if (more) scan_load_k(late, Kp, uk1, wr, lane);
-        } else {
-            // ... + A D over the causal part s < rw + 16, then rnd(o)
-#pragma unroll
-            for (int kb = 0; kb < C / 32; kb++)
-                if (kb <= wr / 2)
-                    o = mfma_x3(late.b[2 * kb], late.b[2 * kb + 1],
-                                ld8(Dh + r16 * DB + kb * 32 + g4 * 8),
-                                ld8(Dl + r16 * DB + kb * 32 + g4 * 8), o);
-            if (more) scan_load_a(late, Ab, u1, wr, lane);
-#pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const int t = rw + kq + i;
-                if (t < nt) ob[(size_t)(t0 + t) * vd + (size_t)h * DV + cb * CB + r16] = f2bf(o[i]);
-            }
-        }
-        __syncthreads();               // every reader of the state slice and Fs is done
-        if (rec) {
+            scan_load_k(kf, Kp, cl(ci + 1) * hk + kh, wr, lane);
+            __syncthreads();           // every reader of the state slice and Fs is done
 #pragma unroll
             for (int r = 0; r < 2; r++) {
                 const int i0 = wr * 32 + r * 16;
@@ -615,12 +578,51 @@ __global__ __launch_bounds__(512) void k_gdn_chunk_scan(
                     split_bf(sn[r][i], S0h[n * SB + col], S0l[n * SB + col]);
                 }
             }
+            if (more && tid < 2 * C) Fs[tid] = oth.f;
+        };
+        for (int ci = c0; ci < c1; ci += 2) {
+            step(ring0, ring1, ci);
+            if (ci + 1 < c1) step(ring1, ring0, ci + 1);
         }
-        if (more && tid < 2 * C) Fs[tid] = oth.f;
-    };
-    for (int ci = c0; ci < c1; ci += 2) {
-        step(ring0, ring1, ci);
-        if (ci + 1 < c1) step(ring1, ring0, ci + 1);
+    } else if (c0 < c1) {
+        // ---- output role: O = G Q S0 + A D, then rnd(o) out
+        ScanOps ring0, ring1;
+        ScanOps2 af;
+        scan_load_q(ring0, Qp, cl(c0) * hk + kh, wr, lane);
+        scan_load_a(af, Ab, cl(c0) * hv + h, wr, lane);
+        scan_load_q(ring1, Qp, cl(c0 + 1) * hk + kh, wr, lane);
+        auto step = [&](ScanOps &cur, int ci) {
+            const int t0 = tS + (ci - c0) * C, nt = min(C, tE - t0);
+            __syncthreads();           // the state slice and Fs of this chunk are in place
+            f32x4 o = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int kb = 0; kb < DK / 32; kb++)
+                o = mfma_x3(cur.b[2 * kb], cur.b[2 * kb + 1],
+                            ld8(S0h + r16 * SB + kb * 32 + g4 * 8),
+                            ld8(S0l + r16 * SB + kb * 32 + g4 * 8), o);
+#pragma unroll
+            for (int i = 0; i < 4; i++) o[i] = Fs[rw + kq + i] * o[i];
+            scan_load_q(cur, Qp, cl(ci + 2) * hk + kh, wr, lane);
+            __syncthreads();           // D complete
+            // ... + A D over the causal part s < rw + 16
+#pragma unroll
+            for (int kb = 0; kb < C / 32; kb++)
+                if (kb <= wr / 2)
+                    o = mfma_x3(af.b[2 * kb], af.b[2 * kb + 1],
+                                ld8(Dh + r16 * DB + kb * 32 + g4 * 8),
+                                ld8(Dl + r16 * DB + kb * 32 + g4 * 8), o);
+            scan_load_a(af, Ab, cl(ci + 1) * hv + h, wr, lane);
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int t = rw + kq + i;
+                if (t < nt) ob[(size_t)(t0 + t) * vd + (size_t)h * DV + cb * CB + r16] = f2bf(o[i]);
+            }
+            __syncthreads();           // every reader of the state slice and Fs is done
+        };
+        for (int ci = c0; ci < c1; ci += 2) {
+            step(ring0, ci);
+            if (ci + 1 < c1) step(ring1, ci + 1);
+        }
     }
     __syncthreads();
     for (int e = tid; e < CB * DK; e += 512) {
