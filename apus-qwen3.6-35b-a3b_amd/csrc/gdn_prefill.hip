@@ -179,10 +179,18 @@ __global__ __launch_bounds__(256, 2) void k_gdn_chunk_wy(
     const uint16_t *__restrict__ vconv, const float2 *__restrict__ gate,
     const float *__restrict__ graw, float *__restrict__ Ub, uint16_t *__restrict__ Wb,
     uint16_t *__restrict__ Ab, float *__restrict__ Fb, uint16_t *__restrict__ Qp,
-    uint16_t *__restrict__ Kp, int hk) {
+    uint16_t *__restrict__ Kp, int hk, int pair_map) {
     const int hv = hk * REP;
     const size_t kd = (size_t)hk * DK, vd = (size_t)hv * DV;
-    const int ci = blockIdx.x / hv, h = blockIdx.x % hv, kh = h / REP;
+    // unit = ci * hv + h. With pair_map the two v-heads of one K head (units
+    // 2P, 2P+1) run as blocks 8 apart: blocks are dealt round-robin over the
+    // 8 XCDs, so both land on one XCD and the second reads q, k from its L2.
+    int unit = blockIdx.x;
+    if (pair_map) {
+        const int b = blockIdx.x;
+        unit = ((b >> 4) * 8 + (b & 7)) * 2 + ((b >> 3) & 1);
+    }
+    const int ci = unit / hv, h = unit % hv, kh = h / REP;
     const bool wqk = h % REP == 0;              // this v-head writes Qp / Kp
     uint16_t *Qpu = Qp + ((size_t)ci * hk + kh) * C * DK * 2;
     uint16_t *Kpu = Kp + ((size_t)ci * hk + kh) * C * DK * 2;
@@ -196,6 +204,15 @@ __global__ __launch_bounds__(256, 2) void k_gdn_chunk_wy(
     __shared__ __attribute__((aligned(16))) float QL[C * KP];   // Q, then L [C][CP]
     __shared__ float graw_s[C], gam[C], bet[C], Gs[C];
 
+    // The V right-hand sides of the forward substitution (threads < DV, one
+    // column each) are loaded first: loaded after this kernel's stores,
+    // their wait would also wait for every store's acknowledgement.
+    uint16_t vpre[C];
+    if (tid < DV) {
+        const uint16_t *vp = vconv + (size_t)P.t0 * vd + (size_t)h * DV + tid;
+#pragma unroll
+        for (int t = 0; t < C; t++) vpre[t] = t < P.nt ? vp[(size_t)t * vd] : 0;
+    }
     // rows t >= nt are padding: q = k = 0, g = 0, beta = 0
     // (every load issued before the first LDS store)
     constexpr int NQ = C * DK / 4 / 256;
@@ -251,7 +268,7 @@ __global__ __launch_bounds__(256, 2) void k_gdn_chunk_wy(
         gam[tid] = acc;
     }
     __syncthreads();
-    float *F = Fb + (size_t)blockIdx.x * 2 * C;
+    float *F = Fb + (size_t)unit * 2 * C;
     if (tid < C) {
         Gs[tid] = exp_fast(gam[tid]);
         F[tid] = Gs[tid];
@@ -262,7 +279,7 @@ __global__ __launch_bounds__(256, 2) void k_gdn_chunk_wy(
     // Q K^T, row block 3-w: A = decayed lower triangle, to global. The
     // product is formed transposed (K Q^T) so each lane holds 4 consecutive
     // key columns s of one row t: 4 hi and 4 lo codes, two 8-byte stores.
-    uint16_t *A = Ab + (size_t)blockIdx.x * C * C * 2;
+    uint16_t *A = Ab + (size_t)unit * C * C * 2;
     {
         typedef unsigned short u16x4_t __attribute__((ext_vector_type(4)));
         const int rb = 3 - wave;
@@ -331,10 +348,8 @@ __global__ __launch_bounds__(256, 2) void k_gdn_chunk_wy(
     // sums (s mod 4) shorten the dependent chain
     float x[C];
     if (tid < DV) {
-        const uint16_t *vp = vconv + (size_t)P.t0 * vd + (size_t)h * DV + tid;
 #pragma unroll
-        for (int t = 0; t < C; t++)
-            x[t] = t < P.nt ? bet[t] * bf2f(vp[(size_t)t * vd]) : 0.0f;
+        for (int t = 0; t < C; t++) x[t] = bet[t] * bf2f(vpre[t]);   // (bet = 0 past nt)
     } else {
 #pragma unroll
         for (int t = 0; t < C; t++)
@@ -353,7 +368,7 @@ __global__ __launch_bounds__(256, 2) void k_gdn_chunk_wy(
         }
         x[t] = x[t] - ((p0 + p1) + (p2 + p3));
     }
-    const size_t ub = (size_t)blockIdx.x * C * DV;
+    const size_t ub = (size_t)unit * C * DV;
     if (tid < DV) {                    // U: 4 consecutive t of column tid are 16 contiguous bytes
 #pragma unroll
         for (int t = 0; t < C; t += 4)
@@ -684,7 +699,8 @@ int apus_hip_gdn_prefill(const ApusHipGdnLayer *L, size_t B, const int32_t *cu,
     if (!Ub || !Wb || !Ab || !Fb || !Qp || !Kp) return kErrHip;
     APUS_TIMED("k_gdn_chunk_wy",
                k_gdn_chunk_wy<<<(unsigned)units, 256, 0, stream()>>>(
-        sq, kmeta, w.qk, w.vconv, w.gate, w.graw, Ub, Wb, Ab, Fb, Qp, Kp, (int)L->hk));
+        sq, kmeta, w.qk, w.vconv, w.gate, w.graw, Ub, Wb, Ab, Fb, Qp, Kp, (int)L->hk,
+        units % 16 == 0 ? 1 : 0));
     APUS_LAUNCHED("k_gdn_chunk_wy");
     APUS_TIMED("k_gdn_chunk_scan",
                k_gdn_chunk_scan<<<(unsigned)(B * L->hv * NCB), 512, 0, stream()>>>(
