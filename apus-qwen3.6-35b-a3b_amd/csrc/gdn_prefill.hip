@@ -204,14 +204,20 @@ __global__ __launch_bounds__(256, 2) void k_gdn_chunk_wy(
     __shared__ __attribute__((aligned(16))) float QL[C * KP];   // Q, then L [C][CP]
     __shared__ float graw_s[C], gam[C], bet[C], Gs[C];
 
-    // The V right-hand sides of the forward substitution (threads < DV, one
-    // column each) are loaded first: loaded after this kernel's stores,
-    // their wait would also wait for every store's acknowledgement.
-    uint16_t vpre[C];
-    if (tid < DV) {
-        const uint16_t *vp = vconv + (size_t)P.t0 * vd + (size_t)h * DV + tid;
+    // The chunk's V rows (the right-hand sides b V of the forward
+    // substitution) in 16-byte pieces, loaded first: loaded after this
+    // kernel's stores, their wait would also wait for every store's
+    // acknowledgement. They go to LDS once Q's copy is free.
+    typedef unsigned short u16x8_t __attribute__((ext_vector_type(8)));
+    constexpr int NV = C * DV / 8 / 256;
+    u16x8_t vreg[NV];
 #pragma unroll
-        for (int t = 0; t < C; t++) vpre[t] = t < P.nt ? vp[(size_t)t * vd] : 0;
+    for (int k = 0; k < NV; k++) {
+        const int t = tid / (DV / 8) + k * (256 / (DV / 8)), c8 = (tid % (DV / 8)) * 8;
+        vreg[k] = u16x8_t{0, 0, 0, 0, 0, 0, 0, 0};
+        if (t < P.nt)
+            vreg[k] = *reinterpret_cast<const u16x8_t *>(vconv + (size_t)(P.t0 + t) * vd +
+                                                         (size_t)h * DV + c8);
     }
     // rows t >= nt are padding: q = k = 0, g = 0, beta = 0
     // (every load issued before the first LDS store)
@@ -330,6 +336,14 @@ __global__ __launch_bounds__(256, 2) void k_gdn_chunk_wy(
     }
     __syncthreads();                   // every reader of Q is done
     float *Ls = QL;
+    // V rows [C][DV] bf16 in the 16 KiB of Q's copy that L ([C][CP]) leaves
+    uint16_t *Vs = reinterpret_cast<uint16_t *>(QL + C * CP);
+    static_assert(C * CP * 4 + C * DV * 2 <= C * KP * 4, "V does not fit beside L");
+#pragma unroll
+    for (int k = 0; k < NV; k++) {
+        const int t = tid / (DV / 8) + k * (256 / (DV / 8)), c8 = (tid % (DV / 8)) * 8;
+        *reinterpret_cast<u16x8_t *>(Vs + t * DV + c8) = vreg[k];
+    }
 #pragma unroll
     for (int cb = 0; cb < 4; cb++) {
         if (cb <= wave) {
@@ -349,7 +363,7 @@ __global__ __launch_bounds__(256, 2) void k_gdn_chunk_wy(
     float x[C];
     if (tid < DV) {
 #pragma unroll
-        for (int t = 0; t < C; t++) x[t] = bet[t] * bf2f(vpre[t]);   // (bet = 0 past nt)
+        for (int t = 0; t < C; t++) x[t] = bet[t] * bf2f(Vs[t * DV + tid]);   // (bet = 0 past nt)
     } else {
 #pragma unroll
         for (int t = 0; t < C; t++)
