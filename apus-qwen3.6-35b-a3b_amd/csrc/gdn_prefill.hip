@@ -531,6 +531,7 @@ __global__ __launch_bounds__(512) void k_gdn_chunk_scan(
     __shared__ __attribute__((aligned(16))) uint16_t Dph[CB * DB];     // decayed D
     __shared__ __attribute__((aligned(16))) uint16_t Dpl[CB * DB];
     __shared__ float Fs[2 * C];
+    __shared__ __attribute__((aligned(16))) uint16_t Ost[4][16 * CB];   // output role: rnd(o) tiles
 
     // state slice in: packed layout ((j/64*32 + i/4)*64 + j%64)*4 + i%4
     float *Sm = S + (size_t)sh * DK * DV;
@@ -615,12 +616,15 @@ __global__ __launch_bounds__(512) void k_gdn_chunk_scan(
         }
     } else if (c0 < c1) {
         // ---- output role: O = G Q S0 + A D, then rnd(o) out
+        // Q and A both in two-slot rings (two steps ahead): the first wait
+        // issued behind a step's output stores then comes three steps later
         ScanOps ring0, ring1;
-        ScanOps2 af;
+        ScanOps2 af0, af1;
         scan_load_q(ring0, Qp, cl(c0) * hk + kh, wr, lane);
-        scan_load_a(af, Ab, cl(c0) * hv + h, wr, lane);
+        scan_load_a(af0, Ab, cl(c0) * hv + h, wr, lane);
         scan_load_q(ring1, Qp, cl(c0 + 1) * hk + kh, wr, lane);
-        auto step = [&](ScanOps &cur, int ci) {
+        scan_load_a(af1, Ab, cl(c0 + 1) * hv + h, wr, lane);
+        auto step = [&](ScanOps &cur, ScanOps2 &af, int ci) {
             const int t0 = tS + (ci - c0) * C, nt = min(C, tE - t0);
             __syncthreads();           // the state slice and Fs of this chunk are in place
             f32x4 o = {0.f, 0.f, 0.f, 0.f};
@@ -640,17 +644,25 @@ __global__ __launch_bounds__(512) void k_gdn_chunk_scan(
                     o = mfma_x3(af.b[2 * kb], af.b[2 * kb + 1],
                                 ld8(Dh + r16 * DB + kb * 32 + g4 * 8),
                                 ld8(Dl + r16 * DB + kb * 32 + g4 * 8), o);
-            scan_load_a(af, Ab, cl(ci + 1) * hv + h, wr, lane);
+            scan_load_a(af, Ab, cl(ci + 2) * hv + h, wr, lane);
+            // rnd(o) through a wave-private LDS tile, so that 32 lanes store
+            // the 16 rows as 16-byte pieces (2-byte stores run ~20x slower)
+            uint16_t *Ow = Ost[wr];
 #pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const int t = rw + kq + i;
-                if (t < nt) ob[(size_t)(t0 + t) * vd + (size_t)h * DV + cb * CB + r16] = f2bf(o[i]);
+            for (int i = 0; i < 4; i++) Ow[(kq + i) * CB + r16] = f2bf(o[i]);
+            __builtin_amdgcn_wave_barrier();
+            if (lane < 32) {
+                const int rr = lane >> 1, half = lane & 1, t = rw + rr;
+                const u16x8 v8 = *reinterpret_cast<const u16x8 *>(Ow + rr * CB + half * 8);
+                if (t < nt)
+                    *reinterpret_cast<u16x8 *>(ob + (size_t)(t0 + t) * vd + (size_t)h * DV +
+                                               cb * CB + half * 8) = v8;
             }
             __syncthreads();           // every reader of the state slice and Fs is done
         };
         for (int ci = c0; ci < c1; ci += 2) {
-            step(ring0, ci);
-            if (ci + 1 < c1) step(ring1, ci + 1);
+            step(ring0, af0, ci);
+            if (ci + 1 < c1) step(ring1, af1, ci + 1);
         }
     }
     __syncthreads();
