@@ -172,6 +172,41 @@ __device__ __forceinline__ void put_split8(uint16_t *p, const float (&x)[8]) {
     *reinterpret_cast<u16x8_t *>(p + 8) = lo;
 }
 
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef unsigned short u16x8 __attribute__((ext_vector_type(8)));
+
+__device__ __forceinline__ bf16x8 as_bf(u16x8 v) { return __builtin_bit_cast(bf16x8, v); }
+__device__ __forceinline__ u16x8 ld8(const uint16_t *p) {
+    return *reinterpret_cast<const u16x8 *>(p);
+}
+// acc += a.b in split precision: (ah, al) and (bh, bl) the hi/lo operands
+__device__ __forceinline__ f32x4 mfma_x3(u16x8 ah, u16x8 al, u16x8 bh, u16x8 bl, f32x4 c) {
+    c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf(al), as_bf(bh), c, 0, 0, 0);
+    c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf(ah), as_bf(bl), c, 0, 0, 0);
+    c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf(ah), as_bf(bh), c, 0, 0, 0);
+    return c;
+}
+
+__device__ __forceinline__ float4 lds4_(const float *p) {
+    return *reinterpret_cast<const float4 *>(p);
+}
+// hi/lo bf16 codes of 8 fp32 values: one split-precision MFMA operand
+__device__ __forceinline__ void split8(const float (&x)[8], u16x8 &hi, u16x8 &lo) {
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        uint16_t h, l;
+        split_bf(x[i], h, l);
+        hi[i] = h;
+        lo[i] = l;
+    }
+}
+// the same for 8 consecutive fp32 values in LDS
+__device__ __forceinline__ void lds_split8(const float *p, u16x8 &hi, u16x8 &lo) {
+    const float4 a0 = lds4_(p), a1 = lds4_(p + 4);
+    const float v[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+    split8(v, hi, lo);
+}
+
 // k_gdn_chunk_wy: one workgroup per (chunk, v-head), two per CU (Q's LDS
 // copy is reused for L once Q K^T is done).
 __global__ __launch_bounds__(256, 2) void k_gdn_chunk_wy(
@@ -281,7 +316,9 @@ __global__ __launch_bounds__(256, 2) void k_gdn_chunk_wy(
         F[C + tid] = exp_fast(gam[C - 1] - gam[tid]);
     }
 
-    const int r16 = lane & 15, kq = (lane >> 4) * 4;
+    // products on the split-precision MFMA 16x16x32 (lane: row / column
+    // r16, reduction indices g8 .. g8+7; result rows kq .. kq+3)
+    const int r16 = lane & 15, kq = (lane >> 4) * 4, g8 = (lane >> 4) * 8;
     // Q K^T, row block 3-w: A = decayed lower triangle, to global. The
     // product is formed transposed (K Q^T) so each lane holds 4 consecutive
     // key columns s of one row t: 4 hi and 4 lo codes, two 8-byte stores.
@@ -307,6 +344,9 @@ __global__ __launch_bounds__(256, 2) void k_gdn_chunk_wy(
             const float z[4] = {0.f, 0.f, 0.f, 0.f};
             put4((rb + 1) * 16 + kq, z);
         }
+        // (fp32 MFMA: q.k cancels, and A feeds the outputs directly; the
+        // split-precision product's error, relative to sum |q_i k_i|, shows
+        // as several output ulps)
         for (int cb = 0; cb <= rb; cb++) {
             f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -324,14 +364,21 @@ __global__ __launch_bounds__(256, 2) void k_gdn_chunk_wy(
     }
     // K K^T, row block w, kept in registers until Q's LDS copy is free
     f32x4 g[4];
+    {
+        u16x8 wh[DK / 32], wl[DK / 32];
 #pragma unroll
-    for (int cb = 0; cb < 4; cb++) {
-        g[cb] = f32x4{0.f, 0.f, 0.f, 0.f};
-        if (cb <= wave) {
+        for (int ks = 0; ks < DK / 32; ks++) lds_split8(Ks + (wave * 16 + r16) * KP + ks * 32 + g8, wh[ks], wl[ks]);
 #pragma unroll
-            for (int k0 = 0; k0 < DK; k0 += 16)
-                g[cb] = mfma_k16(lds4(Ks + (wave * 16 + r16) * KP + k0 + kq),
-                                 lds4(Ks + (cb * 16 + r16) * KP + k0 + kq), g[cb]);
+        for (int cb = 0; cb < 4; cb++) {
+            g[cb] = f32x4{0.f, 0.f, 0.f, 0.f};
+            if (cb <= wave) {
+#pragma unroll
+                for (int ks = 0; ks < DK / 32; ks++) {
+                    u16x8 kh, kl;
+                    lds_split8(Ks + (cb * 16 + r16) * KP + ks * 32 + g8, kh, kl);
+                    g[cb] = mfma_x3(wh[ks], wl[ks], kh, kl, g[cb]);
+                }
+            }
         }
     }
     __syncthreads();                   // every reader of Q is done
@@ -357,45 +404,137 @@ __global__ __launch_bounds__(256, 2) void k_gdn_chunk_wy(
     }
     __syncthreads();
 
-    // forward substitution X_t = R_t - sum_{s<t} L[t][s] X_s for the 256
-    // right-hand-side columns [b V | b G K], one per thread; four partial
-    // sums (s mod 4) shorten the dependent chain
-    float x[C];
-    if (tid < DV) {
+    // X = (I + L)^-1 R for the 256 right-hand-side columns R = [b V | b G K]
+    // as T R, T = (I + L)^-1, in 32x32 blocks: T00 = (I + L00)^-1 and T11 =
+    // (I + L11)^-1 by substitution (wavefront w < 2, lane j < 32 substitutes
+    // the unit vector e_j: x_t = e_j[t] - sum_{s<t} L[t][s] x_s, four partial
+    // sums shortening the dependent chain), written over their L blocks;
+    // then T10 = -T11 (L10 T00) as two split-precision MFMA products (the
+    // intermediate in the unused upper-right block), and T R on the MFMA
+    // (T's blocks above the diagonal are skipped).
+    constexpr int H = C / 2;
+    if (wave < 2) {
+        const int o = wave * H;                  // this diagonal block's first row / column
+        float x[H];
 #pragma unroll
-        for (int t = 0; t < C; t++) x[t] = bet[t] * bf2f(Vs[t * DV + tid]);   // (bet = 0 past nt)
-    } else {
+        for (int t = 0; t < H; t++) x[t] = t == lane ? 1.0f : 0.0f;
 #pragma unroll
-        for (int t = 0; t < C; t++)
-            x[t] = (bet[t] * Gs[t]) * Ks[t * KP + (tid - DV)];
-    }
+        for (int t = 1; t < H; t++) {
+            float p0 = 0.f, p1 = 0.f, p2 = 0.f, p3 = 0.f;
 #pragma unroll
-    for (int t = 1; t < C; t++) {
-        float p0 = 0.f, p1 = 0.f, p2 = 0.f, p3 = 0.f;
-#pragma unroll
-        for (int s0 = 0; s0 < t; s0 += 4) {
-            const float4 l4 = lds4(Ls + t * CP + s0);
-            p0 = fmaf(l4.x, x[s0], p0);
-            if (s0 + 1 < t) p1 = fmaf(l4.y, x[s0 + 1], p1);
-            if (s0 + 2 < t) p2 = fmaf(l4.z, x[s0 + 2], p2);
-            if (s0 + 3 < t) p3 = fmaf(l4.w, x[s0 + 3], p3);
+            for (int s0 = 0; s0 < t; s0 += 4) {
+                const float4 l4 = lds4(Ls + (o + t) * CP + o + s0);
+                p0 = fmaf(l4.x, x[s0], p0);
+                if (s0 + 1 < t) p1 = fmaf(l4.y, x[s0 + 1], p1);
+                if (s0 + 2 < t) p2 = fmaf(l4.z, x[s0 + 2], p2);
+                if (s0 + 3 < t) p3 = fmaf(l4.w, x[s0 + 3], p3);
+            }
+            x[t] = x[t] - ((p0 + p1) + (p2 + p3));
         }
-        x[t] = x[t] - ((p0 + p1) + (p2 + p3));
+        // (this wavefront's reads of L are all issued: DS operations run in order)
+        if (lane < H) {
+#pragma unroll
+            for (int t = 0; t < H; t++) Ls[(o + t) * CP + o + lane] = x[t];
+        }
+    }
+    __syncthreads();
+    {
+        // wavefront w: output tile (w / 2, w % 2) of the 32x32 products
+        const int tr = (wave >> 1) * 16, tc = (wave & 1) * 16;
+        const int rr = lane & 15, kk = (lane >> 4) * 8;
+        // Y = L10 T00: A = L rows H + tr + rr, k = kk..; B = T00 column tc + rr
+        u16x8 ah, al, bh, bl;
+        {
+            const float4 a0 = lds4(Ls + (H + tr + rr) * CP + kk), a1 = lds4(Ls + (H + tr + rr) * CP + kk + 4);
+            const float va[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+            split8(va, ah, al);
+            float vb[8];
+#pragma unroll
+            for (int j = 0; j < 8; j++) vb[j] = Ls[(kk + j) * CP + tc + rr];
+            split8(vb, bh, bl);
+        }
+        f32x4 y = mfma_x3(ah, al, bh, bl, f32x4{0.f, 0.f, 0.f, 0.f});
+        // Y to the upper-right block [k = row][n]: rows tr + 4(l/16) + i, column tc + rr
+#pragma unroll
+        for (int i = 0; i < 4; i++) Ls[(tr + (lane >> 4) * 4 + i) * CP + H + tc + rr] = y[i];
+        __syncthreads();
+        // T10 = -T11 Y: A = T11 rows H + tr + rr, k = H + kk..; B = Y column tc + rr
+        {
+            const float4 a0 = lds4(Ls + (H + tr + rr) * CP + H + kk), a1 = lds4(Ls + (H + tr + rr) * CP + H + kk + 4);
+            const float va[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+            split8(va, ah, al);
+            float vb[8];
+#pragma unroll
+            for (int j = 0; j < 8; j++) vb[j] = Ls[(kk + j) * CP + H + tc + rr];
+            split8(vb, bh, bl);
+        }
+        const f32x4 t10 = mfma_x3(ah, al, bh, bl, f32x4{0.f, 0.f, 0.f, 0.f});
+        __syncthreads();                         // every read of L10 and Y is done
+#pragma unroll
+        for (int i = 0; i < 4; i++) Ls[(H + tr + (lane >> 4) * 4 + i) * CP + tc + rr] = -t10[i];
+        // the upper-right block back to zero (T is lower triangular; T R reads
+        // only k below its row block, but keep the matrix clean)
+#pragma unroll
+        for (int i = 0; i < 4; i++) Ls[(tr + (lane >> 4) * 4 + i) * CP + H + tc + rr] = 0.0f;
+    }
+    __syncthreads();
+    const int g4 = kq;
+    const int cbase = wave * 64;                // this wavefront's 64 columns of R
+    const bool isv = cbase < DV;
+    f32x4 xacc[4][4];
+#pragma unroll
+    for (int rt = 0; rt < 4; rt++)
+#pragma unroll
+        for (int ct = 0; ct < 4; ct++) xacc[rt][ct] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int ks = 0; ks < C / 32; ks++) {
+        const int k0 = ks * 32 + g8;             // this lane's 8 reduction indices
+        u16x8 ah[4], al[4], bh[4], bl[4];
+#pragma unroll
+        for (int rt = 2 * ks; rt < 4; rt++) {    // T rows 16 rt + r16
+            const float4 a0 = lds4(Ls + (rt * 16 + r16) * CP + k0);
+            const float4 a1 = lds4(Ls + (rt * 16 + r16) * CP + k0 + 4);
+            const float v[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+            split8(v, ah[rt], al[rt]);
+        }
+#pragma unroll
+        for (int ct = 0; ct < 4; ct++) {         // R column n, rows k0 .. k0 + 7
+            const int n = cbase + ct * 16 + r16;
+            float v[8];
+#pragma unroll
+            for (int j = 0; j < 8; j++) {
+                const int t = k0 + j;
+                v[j] = isv ? bet[t] * bf2f(Vs[t * DV + n]) : (bet[t] * Gs[t]) * Ks[t * KP + (n - DV)];
+            }
+            split8(v, bh[ct], bl[ct]);
+        }
+#pragma unroll
+        for (int rt = 2 * ks; rt < 4; rt++)
+#pragma unroll
+            for (int ct = 0; ct < 4; ct++)
+                xacc[rt][ct] = mfma_x3(ah[rt], al[rt], bh[ct], bl[ct], xacc[rt][ct]);
     }
     const size_t ub = (size_t)unit * C * DV;
-    if (tid < DV) {                    // U: 4 consecutive t of column tid are 16 contiguous bytes
+    if (isv) {                         // U: the accumulator order is U's layout
 #pragma unroll
-        for (int t = 0; t < C; t += 4)
-            *reinterpret_cast<float4 *>(Ub + ub + wy_u_index(t, tid)) =
-                make_float4(x[t], x[t + 1], x[t + 2], x[t + 3]);
+        for (int rt = 0; rt < 4; rt++)
+#pragma unroll
+            for (int ct = 0; ct < 4; ct++)
+                *reinterpret_cast<float4 *>(Ub + ub + wy_u_index(rt * 16 + g4, cbase + ct * 16 + r16)) =
+                    make_float4(xacc[rt][ct][0], xacc[rt][ct][1], xacc[rt][ct][2], xacc[rt][ct][3]);
     }
     // W through LDS (L is no longer read): column tid - DV of every row in,
     // then 32-byte units of 8 consecutive columns of one row out
-    __syncthreads();
+    __syncthreads();                   // every reader of T and V is done
     float *Wl = QL;
-    if (tid >= DV) {
+    if (!isv) {
 #pragma unroll
-        for (int t = 0; t < C; t++) Wl[t * KP + (tid - DV)] = x[t];
+        for (int rt = 0; rt < 4; rt++)
+#pragma unroll
+            for (int ct = 0; ct < 4; ct++)
+#pragma unroll
+                for (int i = 0; i < 4; i++)
+                    Wl[(rt * 16 + g4 + i) * KP + (cbase - DV + ct * 16 + r16)] = xacc[rt][ct][i];
     }
     __syncthreads();
 #pragma unroll
@@ -423,21 +562,6 @@ __global__ __launch_bounds__(256, 2) void k_gdn_chunk_wy(
 // hi/lo codes made once when it is written. Each wavefront loads the next
 // chunk's operands it consumes into registers as soon as the current copy
 // is used.
-typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
-typedef unsigned short u16x8 __attribute__((ext_vector_type(8)));
-
-__device__ __forceinline__ bf16x8 as_bf(u16x8 v) { return __builtin_bit_cast(bf16x8, v); }
-__device__ __forceinline__ u16x8 ld8(const uint16_t *p) {
-    return *reinterpret_cast<const u16x8 *>(p);
-}
-// acc += a.b in split precision: (ah, al) and (bh, bl) the hi/lo operands
-__device__ __forceinline__ f32x4 mfma_x3(u16x8 ah, u16x8 al, u16x8 bh, u16x8 bl, f32x4 c) {
-    c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf(al), as_bf(bh), c, 0, 0, 0);
-    c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf(ah), as_bf(bl), c, 0, 0, 0);
-    c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf(ah), as_bf(bh), c, 0, 0, 0);
-    return c;
-}
-
 constexpr int SB = DK + 8;     // bf16 row stride of the state slice copies
 constexpr int DB = C + 8;      // bf16 row stride of the D copies
 
