@@ -80,13 +80,6 @@ __device__ __forceinline__ int seq_of(const int32_t *off, int n, int x) {
 // indices k0 + 4*(l/16) + 0..3 (a 16-byte read each); step j feeds index
 // 4*(l/16) + j, so A and B see the same permutation of k and the sum is
 // the plain 16-term dot product per output element.
-__device__ __forceinline__ f32x4 mfma_k16(float4 a, float4 b, f32x4 c) {
-    c = __builtin_amdgcn_mfma_f32_16x16x4f32(a.x, b.x, c, 0, 0, 0);
-    c = __builtin_amdgcn_mfma_f32_16x16x4f32(a.y, b.y, c, 0, 0, 0);
-    c = __builtin_amdgcn_mfma_f32_16x16x4f32(a.z, b.z, c, 0, 0, 0);
-    c = __builtin_amdgcn_mfma_f32_16x16x4f32(a.w, b.w, c, 0, 0, 0);
-    return c;
-}
 
 __device__ __forceinline__ float4 lds4(const float *p) {
     return *reinterpret_cast<const float4 *>(p);
@@ -205,6 +198,35 @@ __device__ __forceinline__ void lds_split8(const float *p, u16x8 &hi, u16x8 &lo)
     const float4 a0 = lds4_(p), a1 = lds4_(p + 4);
     const float v[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
     split8(v, hi, lo);
+}
+
+// Three-way split: x = hi + mid + lo to 24 bits (hi = rnd(x), mid =
+// rnd(x - hi), lo = rnd(x - hi - mid)), and the product keeping every
+// term down to 2^-16 relative (hh, hm, mh, hl, lh, mm; the dropped terms
+// are below 2^-24), smallest first.
+__device__ __forceinline__ void lds_split8x3(const float *p, u16x8 &hi, u16x8 &mid, u16x8 &lo) {
+    const float4 a0 = lds4_(p), a1 = lds4_(p + 4);
+    const float v[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        const __bf16 h = (__bf16)v[i];
+        const float r = v[i] - (float)h;
+        const __bf16 m = (__bf16)r;
+        const __bf16 l = (__bf16)(r - (float)m);
+        hi[i] = __builtin_bit_cast(uint16_t, h);
+        mid[i] = __builtin_bit_cast(uint16_t, m);
+        lo[i] = __builtin_bit_cast(uint16_t, l);
+    }
+}
+__device__ __forceinline__ f32x4 mfma_x6(u16x8 ah, u16x8 am, u16x8 al, u16x8 bh, u16x8 bm,
+                                         u16x8 bl, f32x4 c) {
+    c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf(am), as_bf(bm), c, 0, 0, 0);
+    c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf(al), as_bf(bh), c, 0, 0, 0);
+    c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf(ah), as_bf(bl), c, 0, 0, 0);
+    c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf(am), as_bf(bh), c, 0, 0, 0);
+    c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf(ah), as_bf(bm), c, 0, 0, 0);
+    c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf(ah), as_bf(bh), c, 0, 0, 0);
+    return c;
 }
 
 // k_gdn_chunk_wy: one workgroup per (chunk, v-head), two per CU (Q's LDS
@@ -344,15 +366,21 @@ __global__ __launch_bounds__(256, 2) void k_gdn_chunk_wy(
             const float z[4] = {0.f, 0.f, 0.f, 0.f};
             put4((rb + 1) * 16 + kq, z);
         }
-        // (fp32 MFMA: q.k cancels, and A feeds the outputs directly; the
-        // split-precision product's error, relative to sum |q_i k_i|, shows
-        // as several output ulps)
+        // q.k cancels and A feeds the outputs directly, so this product
+        // takes the three-way split (24 bits, fp32's error class): the
+        // two-way split's error, relative to sum |q_i k_i|, shows as
+        // several output ulps. Q rows of this block as B operands, once.
+        u16x8 qh[DK / 32], qm[DK / 32], ql[DK / 32];
+#pragma unroll
+        for (int ks = 0; ks < DK / 32; ks++) lds_split8x3(QL + (rb * 16 + r16) * KP + ks * 32 + g8, qh[ks], qm[ks], ql[ks]);
         for (int cb = 0; cb <= rb; cb++) {
             f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-            for (int k0 = 0; k0 < DK; k0 += 16)
-                acc = mfma_k16(lds4(Ks + (cb * 16 + r16) * KP + k0 + kq),
-                               lds4(QL + (rb * 16 + r16) * KP + k0 + kq), acc);
+            for (int ks = 0; ks < DK / 32; ks++) {
+                u16x8 kh, km, kl;
+                lds_split8x3(Ks + (cb * 16 + r16) * KP + ks * 32 + g8, kh, km, kl);
+                acc = mfma_x6(kh, km, kl, qh[ks], qm[ks], ql[ks], acc);
+            }
             float v[4];
 #pragma unroll
             for (int i = 0; i < 4; i++) {
