@@ -21,17 +21,19 @@
 //
 // Kernels (after k_gdn_prep, before k_gdn_post of gdn_mixer.hip):
 //   k_gdn_chunk_wy    one workgroup per (chunk, v-head), all chunks in
-//                     parallel: K K^T and Q K^T on fp32 MFMA, L and A with
-//                     their decay factors, then U and W by forward
-//                     substitution (one thread per right-hand-side column).
+//                     parallel: K K^T and Q K^T, L and A with their decay
+//                     factors, then U and W as T [b V | b G K] with
+//                     T = (I+L)^-1 built in 32x32 blocks.
 //   k_gdn_chunk_scan  one workgroup per (sequence, v-head, 16-column block
 //                     of S): the delta rule is separable by value column,
 //                     so the chunk-to-chunk carry of S runs in 8 independent
 //                     column slices per head, each walking its sequence's
-//                     chunks in order on fp32 MFMA (D, O, S1 above).
-// All products run on fp32 MFMA with fp32 accumulation: the recurrent
-// state must stay within 1e-4 of the sequential fp32 recurrence, which
-// bf16 operands (8-bit mantissa) cannot hold. The chunk form sums in a
+//                     chunks in order (D, O, S1 above).
+// The recurrent state must stay within 1e-4 of the sequential fp32
+// recurrence, which bf16 operands (8-bit mantissa) cannot hold: products
+// run on the bf16 MFMA with each fp32 operand split into bf16 parts (two
+// parts, hi + lo, for 16 bits; three for Q K^T, which cancels and feeds the
+// outputs directly) and fp32 accumulation. The chunk form sums in a
 // different order from the reference's token loop -- a tolerance class,
 // checked against the sequential oracle.
 #include <math.h>
