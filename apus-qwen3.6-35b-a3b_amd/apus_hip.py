@@ -34,7 +34,7 @@ EXPORTS = [
     "apus_hip_attn_rmsnorm", "apus_hip_attn_rope", "apus_hip_attn_gqa",
     "apus_hip_attn_gqa_decode", "apus_hip_attn_gqa_mt",
     "apus_hip_attn_gqa_decode_mt", "apus_hip_attn_outgate",
-    "apus_hip_gdn_decode", "apus_hip_gdn_prefill", "apus_hip_gdn_state_pack", "apus_hip_gdn_state_unpack",
+    "apus_hip_gdn_decode", "apus_hip_gdn_decode_into", "apus_hip_gdn_prefill", "apus_hip_gdn_state_pack", "apus_hip_gdn_state_unpack",
     "apus_hip_attn_cache_pack", "apus_hip_attn_cache_unpack", "apus_hip_attn_decode", "apus_hip_attn_prefill",
 ]
 
@@ -280,6 +280,16 @@ def gdn_decode(layer, cu, qkv, z, a, b, conv_state, S, y):
     _chk(load().apus_hip_gdn_decode(C.byref(layer), _sz(B), cup, _dp(qkv),
                                     _dp(z), _dp(a), _dp(b), _dp(conv_state),
                                     _dp(S), _dp(y)))
+
+
+def gdn_decode_into(layer, cu, qkv, z, a, b, conv_in, S_in, conv_out, S_out, y):
+    """Out-of-place decode/verify: states read from (conv_in, S_in), written
+    to (conv_out, S_out); sequences with no tokens are left untouched."""
+    cu, cup, B = _cu_arr(cu)
+    _chk(load().apus_hip_gdn_decode_into(C.byref(layer), _sz(B), cup, _dp(qkv),
+                                         _dp(z), _dp(a), _dp(b), _dp(conv_in),
+                                         _dp(S_in), _dp(conv_out), _dp(S_out),
+                                         _dp(y)))
 
 
 def gdn_prefill(layer, cu, qkv, z, a, b, conv_state, S, y):

@@ -105,7 +105,8 @@ void k_gdn_decode(
     CuArgs ca, const int32_t *dcu, const uint16_t *qkv, const uint16_t *z,
     const uint16_t *a, const uint16_t *b, const uint16_t *conv_w,
     const float *A_log, const float *dt_bias, const uint16_t *onorm_w,
-    uint16_t *conv_state, float *S, uint16_t *y, int hk, float qscale) {
+    const uint16_t *conv_state, const float *S, uint16_t *conv_out, float *S_out,
+    uint16_t *y, int hk, float qscale) {
     // (no __restrict__ on the small operands: it would let the compiler sink
     // their loads past the ordering barrier below the state loads)
     const int s = blockIdx.x / hk, kh = blockIdx.x % hk;
@@ -128,8 +129,8 @@ void k_gdn_decode(
 
     const size_t cqk = tid < DK ? (size_t)kh * DK + tid : kd + (size_t)kh * DK + (tid - DK);
     const size_t cv = 2 * kd + (size_t)h * DV + j;
-    uint16_t *stq = conv_state + (size_t)s * cd * 3 + cqk * 3;
-    uint16_t *stv = conv_state + (size_t)s * cd * 3 + cv * 3;
+    const uint16_t *stq = conv_state + (size_t)s * cd * 3 + cqk * 3;
+    const uint16_t *stv = conv_state + (size_t)s * cd * 3 + cv * 3;
     // Small per-token operands, loaded as raw bits before the state tile.
     uint32_t cwq_lo, cwq_hi, cwv_lo, cwv_hi;          // 4 bf16 conv taps each
     {
@@ -154,7 +155,7 @@ void k_gdn_decode(
     asm volatile("" ::: "memory");
     __builtin_amdgcn_sched_barrier(0);
     // this wave's 128x64 state tile: 32 x 16-byte loads per lane
-    const auto Sr = buf_rsrc(S + ((size_t)s * hv + h) * DK * DV, DK * DV * 4);
+    const auto Sr = buf_rsrc(const_cast<float *>(S) + ((size_t)s * hv + h) * DK * DV, DK * DV * 4);
     const int voff = (half * 32 * 64 + lane) * 16;
     float sr[DK];
 #pragma unroll
@@ -238,12 +239,15 @@ void k_gdn_decode(
         const float x2 = rndf(x1 * wo);
         y[(size_t)t * vd + (size_t)h * DV + j] = f2bf(x2 * zg);
     }
+    const auto Sw = buf_rsrc(S_out + ((size_t)s * hv + h) * DK * DV, DK * DV * 4);
 #pragma unroll
     for (int q = 0; q < DK / 4; q++)
-        buf_st4(Sr, voff, q * 1024,
+        buf_st4(Sw, voff, q * 1024,
                 f32x4_t{sr[4 * q + 0], sr[4 * q + 1], sr[4 * q + 2], sr[4 * q + 3]});
-    stq[0] = q0; stq[1] = q1; stq[2] = q2;
-    stv[0] = v0; stv[1] = v1; stv[2] = v2;
+    uint16_t *otq = conv_out + (size_t)s * cd * 3 + cqk * 3;
+    uint16_t *otv = conv_out + (size_t)s * cd * 3 + cv * 3;
+    otq[0] = q0; otq[1] = q1; otq[2] = q2;
+    otv[0] = v0; otv[1] = v1; otv[2] = v2;
 }
 
 // ---- token-parallel pieces for the chunked prefill ------------------------
@@ -576,15 +580,25 @@ int gdn_post(const ApusHipGdnLayer *L, size_t B, const int32_t *dcu,
 
 extern "C" {
 
-int apus_hip_gdn_decode(const ApusHipGdnLayer *L, size_t B, const int32_t *cu,
-                        const uint16_t *qkv, const uint16_t *z,
-                        const uint16_t *a, const uint16_t *b,
-                        uint16_t *conv_state, float *S, uint16_t *y) {
+int apus_hip_gdn_decode_into(const ApusHipGdnLayer *L, size_t B, const int32_t *cu,
+                             const uint16_t *qkv, const uint16_t *z,
+                             const uint16_t *a, const uint16_t *b,
+                             const uint16_t *conv_in, const float *S_in,
+                             uint16_t *conv_out, float *S_out, uint16_t *y) {
     APUS_READY();
     if (int r = gdn_check_layer(L)) return r;
     if (B == 0) return kOk;
     if (int r = gdn_check_offsets(B, cu)) return r;
     if (cu[B] == 0) return kOk;
+    // in place, or two disjoint state sets: a partial overlap would let one
+    // workgroup's writes land in another's inputs
+    const size_t nS = B * L->hv * DK * DV * 4, nC = B * (2 * L->hk * DK + L->hv * DV) * 3 * 2;
+    auto overlap = [](const void *p, const void *q, size_t n) {
+        const char *x = (const char *)p, *w = (const char *)q;
+        return x != w && x < w + n && w < x + n;
+    };
+    if (overlap(S_in, S_out, nS) || overlap(conv_in, conv_out, nC))
+        return set_error(kErrArgument, "state in/out must be the same buffer or disjoint");
     CuArgs ca;
     const int32_t *dcu = nullptr;
     if (B <= (size_t)kInlineSeqs) {
@@ -599,9 +613,17 @@ int apus_hip_gdn_decode(const ApusHipGdnLayer *L, size_t B, const int32_t *cu,
     APUS_TIMED("k_gdn_decode",
                kern<<<(unsigned)(B * L->hk), 256, 0, stream()>>>(
         ca, dcu, qkv, z, a, b, L->conv_w, L->A_log, L->dt_bias, L->onorm_w,
-        conv_state, S, y, (int)L->hk, qscale));
+        conv_in, S_in, conv_out, S_out, y, (int)L->hk, qscale));
     APUS_LAUNCHED("k_gdn_decode");
     return kOk;
+}
+
+int apus_hip_gdn_decode(const ApusHipGdnLayer *L, size_t B, const int32_t *cu,
+                        const uint16_t *qkv, const uint16_t *z,
+                        const uint16_t *a, const uint16_t *b,
+                        uint16_t *conv_state, float *S, uint16_t *y) {
+    return apus_hip_gdn_decode_into(L, B, cu, qkv, z, a, b, conv_state, S,
+                                    conv_state, S, y);
 }
 
 int apus_hip_gdn_state_pack(const float *S_ref, float *S_dev, size_t nmat) {

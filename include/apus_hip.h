@@ -172,6 +172,25 @@ int apus_hip_gdn_decode(const ApusHipGdnLayer *L, size_t B,
                         const uint16_t *b, uint16_t *conv_state, float *S,
                         uint16_t *y);
 
+/* GDN decode / verify out of place: as apus_hip_gdn_decode, reading each
+ * sequence's conv state and S from conv_in / S_in and writing the updated
+ * ones to conv_out / S_out (the same buffers, or disjoint ones). A sequence
+ * with no tokens in cu is skipped and its output state left untouched.
+ * This is the device form of the MTP snapshot/rollback of c/mtp.h:36-75
+ * (snapshot S and conv state, verify, on a partial reject restore the
+ * snapshot and re-feed the accepted prefix): with the input set kept as the
+ * snapshot, a verify writes the output set, and a rollback re-feeds the
+ * accepted prefix of the rejected sequences from the same input set into
+ * the output set; no state is copied. Full-attention layers roll back by
+ * their position alone (pos0 of the next call; rows past it are never
+ * read, c/mtp.h:64-68). */
+int apus_hip_gdn_decode_into(const ApusHipGdnLayer *L, size_t B,
+                             const int32_t *cu, const uint16_t *qkv,
+                             const uint16_t *z, const uint16_t *a,
+                             const uint16_t *b, const uint16_t *conv_in,
+                             const float *S_in, uint16_t *conv_out,
+                             float *S_out, uint16_t *y);
+
 /* Chunked GDN prefill: the same layer and arguments as apus_hip_gdn_decode
  * for sequences of any length (c/layer.h:427-492, the prompt path; the
  * reference steps the recurrence token by token, c/gdn.h:627-635). The

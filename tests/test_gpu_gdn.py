@@ -203,3 +203,100 @@ def test_state_pack_roundtrip(hip):
     for (m, i, j) in [(0, 0, 0), (1, 5, 70), (2, 127, 127), (0, 64, 63)]:
         off = ((j // 64 * 32 + i // 4) * 64 + j % 64) * 4 + i % 4
         assert Ph[m, off] == float(m * 16384 + i * 128 + j)
+
+
+def test_gdn_decode_into_rollback(hip, orc):
+    """Out-of-place verify plus rollback (the device form of the reference's
+    MTP snapshot/restore, c/mtp.h:36-75): every sequence verifies 4 tokens
+    from the snapshot set into the output set, then the sequences that
+    rejected a draft re-feed their accepted prefix from the same snapshot.
+    The output set must equal an in-place decode of the accepted prefixes
+    (same kernel, so bitwise), the snapshot must be unchanged, fully
+    accepted sequences keep their verify state, and the verify outputs
+    match the oracle."""
+    import torch
+    rng = np.random.default_rng(36)
+    dims = synth.GDN_DIMS
+    B, k = 12, 4
+    w = synth.gdn_weights(rng)
+    cu = np.arange(0, (B + 1) * k, k, dtype=np.int32)
+    tok = synth.gdn_tokens(rng, B * k)
+    conv, S = synth.gdn_state(rng, B)
+    acc = rng.integers(1, k + 1, B)            # accepted tokens per sequence
+    acc[0], acc[1] = k, 1
+    dev = torch.device("cuda")
+    tw = {n: torch.from_numpy(v.view(np.int16) if v.dtype == np.uint16 else v).to(dev)
+          for n, v in w.items()}
+    layer = hip.gdn_layer(dims, tw)
+    t = {n: torch.from_numpy(v.view(np.int16)).to(dev) for n, v in tok.items()}
+    vd = dims[1] * dims[3]
+    c_in = torch.from_numpy(conv.view(np.int16)).to(dev)
+    S_ref = torch.from_numpy(S).to(dev)
+    S_in = torch.empty_like(S_ref)
+    hip.gdn_state_pack(S_ref, S_in)
+    c_snap, S_snap = c_in.clone(), S_in.clone()
+    c_out, S_out = torch.zeros_like(c_in), torch.zeros_like(S_in)
+    y = torch.empty((B * k, vd), dtype=torch.int16, device=dev)
+    # verify: all k tokens, snapshot -> output set
+    hip.gdn_decode_into(layer, cu, t["qkv"], t["z"], t["a"], t["b"], c_in, S_in, c_out, S_out, y)
+    c_o, S_o = conv.copy(), S.copy()
+    y_o = orc.gdn_mixer(dims, w, cu, tok["qkv"], tok["z"], tok["a"], tok["b"], c_o, S_o)
+    torch.cuda.synchronize()
+    assert_bf16_close(y.cpu().numpy().view(np.uint16), y_o, what="verify y")
+    assert torch.equal(c_in, c_snap) and torch.equal(S_in, S_snap), "snapshot modified"
+    S_full = S_out.clone()
+    # rollback: re-feed the accepted prefix of rejected sequences only
+    rej = [s for s in range(B) if acc[s] < k]
+    ncu = np.zeros(B + 1, np.int32)
+    rows = []
+    for s in range(B):
+        n = acc[s] if acc[s] < k else 0
+        ncu[s + 1] = ncu[s] + n
+        rows += list(range(s * k, s * k + n))
+    idx = torch.tensor(rows, device=dev, dtype=torch.long)
+    y2 = torch.empty((len(rows), vd), dtype=torch.int16, device=dev)
+    hip.gdn_decode_into(layer, ncu, t["qkv"][idx].contiguous(), t["z"][idx].contiguous(),
+                        t["a"][idx].contiguous(), t["b"][idx].contiguous(),
+                        c_in, S_in, c_out, S_out, y2)
+    # expected: in-place decode of every accepted prefix from the snapshot
+    pcu = np.concatenate([[0], np.cumsum(acc)]).astype(np.int32)
+    prow = torch.tensor([s * k + i for s in range(B) for i in range(acc[s])],
+                        device=dev, dtype=torch.long)
+    c_e, S_e = c_snap.clone(), S_snap.clone()
+    y3 = torch.empty((int(pcu[-1]), vd), dtype=torch.int16, device=dev)
+    hip.gdn_decode(layer, pcu, t["qkv"][prow].contiguous(), t["z"][prow].contiguous(),
+                   t["a"][prow].contiguous(), t["b"][prow].contiguous(), c_e, S_e, y3)
+    torch.cuda.synchronize()
+    assert torch.equal(c_out, c_e), "rolled-back conv state"
+    assert torch.equal(S_out, S_e), "rolled-back S"
+    assert torch.equal(c_in, c_snap) and torch.equal(S_in, S_snap), "snapshot modified"
+    for s in range(B):
+        if acc[s] == k:
+            assert torch.equal(S_out[s], S_full[s])
+    # the re-fed rows' outputs equal the prefix decode's
+    prow_l = prow.tolist()
+    pos = {r: i for i, r in enumerate(prow_l)}
+    sel = torch.tensor([pos[r] for r in rows], device=dev, dtype=torch.long)
+    assert torch.equal(y2, y3[sel])
+    assert rej, "seed gives at least one rejected sequence"
+
+
+def test_gdn_decode_into_rejects_partial_overlap(hip):
+    """In/out state sets must be the same buffer or disjoint."""
+    import torch
+    rng = np.random.default_rng(1)
+    dims = synth.GDN_DIMS
+    dev = torch.device("cuda")
+    w = synth.gdn_weights(rng)
+    tw = {n: torch.from_numpy(v.view(np.int16) if v.dtype == np.uint16 else v).to(dev)
+          for n, v in w.items()}
+    layer = hip.gdn_layer(dims, tw)
+    tok = synth.gdn_tokens(rng, 2)
+    t = {n: torch.from_numpy(v.view(np.int16)).to(dev) for n, v in tok.items()}
+    conv, S = synth.gdn_state(rng, 2)
+    c = torch.from_numpy(conv.view(np.int16)).to(dev)
+    Sb = torch.zeros((3 * dims[1], 128, 128), dtype=torch.float32, device=dev)
+    y = torch.empty((2, dims[1] * dims[3]), dtype=torch.int16, device=dev)
+    with pytest.raises(RuntimeError, match="disjoint"):
+        hip.gdn_decode_into(layer, [0, 1, 2], t["qkv"], t["z"], t["a"], t["b"],
+                            c, Sb[:2 * dims[1]], c.clone(), Sb[dims[1]:], y)
