@@ -257,7 +257,8 @@ constexpr int RS = DK + 4;   // LDS row stride: 16-byte aligned rows on distinct
 constexpr int PC = 4 * DK;   // pre-conv channels of one K head: q, k, 2 x v
 
 // Ascending sum of squares of one 128-float LDS row, one rounding per mul
-// and add, with 16-byte reads kept in flight ahead of the add chain.
+// and add, with 16-byte reads kept in flight ahead of the add chain (the
+// same over a row of 128 bf16 codes below).
 __device__ __forceinline__ float row_sumsq(const float *row) {
     const float4 *x4 = reinterpret_cast<const float4 *>(row);
     float ss = 0.0f;
@@ -271,6 +272,23 @@ __device__ __forceinline__ float row_sumsq(const float *row) {
     }
     return ss;
 }
+
+__device__ __forceinline__ float row_sumsq(const uint16_t *row) {
+    typedef unsigned short u16x8 __attribute__((ext_vector_type(8)));
+    const u16x8 *x8 = reinterpret_cast<const u16x8 *>(row);
+    float ss = 0.0f;
+#pragma unroll 4
+    for (int j = 0; j < DK / 8; j++) {
+        const u16x8 v = x8[j];
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            const float x = bf2f(v[i]);
+            ss = ss + x * x;
+        }
+    }
+    return ss;
+}
+constexpr int RSC = DV + 8;  // LDS row stride in bf16 codes: 16-byte aligned rows
 
 // k_gdn_prep: per (tile of 16 tokens, K head), 256 threads. The tile's
 // pre-conv inputs of the head (q, k and its two v-heads' channels) plus
@@ -439,8 +457,10 @@ __global__ __launch_bounds__(256) void k_gdn_prep(
 
 // k_gdn_post: blocks [0, ceil(Ttot*hv/64)) apply the gated RMSNorm
 // (c/gdn.h:639-661) to 64 consecutive (token, v-head) rows of ob: 16-byte
-// loads into LDS, one lane per row for the ordered sum of squares, then
-// elementwise with 16-byte z loads and y stores. The remaining blocks
+// loads, the rows parked in LDS as codes (17 KiB a block, 8 blocks per CU
+// to hide the serial sums), one lane per row for the ordered sum of
+// squares, then elementwise from the registers with 16-byte z loads and
+// y stores. The remaining blocks
 // write each sequence's new conv state (the last three pre-conv inputs of
 // [old state | tokens]) after every reader of the old one has finished.
 __global__ __launch_bounds__(256) void k_gdn_post(
@@ -458,7 +478,7 @@ __global__ __launch_bounds__(256) void k_gdn_post(
     if ((size_t)blockIdx.x < nnorm) {
         const size_t r0 = (size_t)blockIdx.x * PR;
         const int nr = (int)min((size_t)PR, nrows - r0);
-        __shared__ __attribute__((aligned(16))) float os[PR * RS];
+        __shared__ __attribute__((aligned(16))) uint16_t os[PR * RSC];
         __shared__ float rs[PR];
         // every load of the block (the rows and their z) in flight at once
         constexpr int NPC = PR * DV / 8 / 256;
@@ -474,14 +494,11 @@ __global__ __launch_bounds__(256) void k_gdn_post(
 #pragma unroll
         for (int k = 0; k < NPC; k++) {
             const int e = tid + 256 * k, row = e / (DV / 8), c8 = (e % (DV / 8)) * 8;
-            if (row < nr) {
-#pragma unroll
-                for (int i = 0; i < 8; i++) os[row * RS + c8 + i] = bf2f(ov[k][i]);
-            }
+            if (row < nr) *reinterpret_cast<u16x8 *>(os + row * RSC + c8) = ov[k];
         }
         __syncthreads();
         if (tid < nr) {
-            rs[tid] = 1.0f / sqrtf(row_sumsq(os + tid * RS) / (float)DV + kEps);
+            rs[tid] = 1.0f / sqrtf(row_sumsq(os + tid * RSC) / (float)DV + kEps);
         }
         __syncthreads();
 #pragma unroll
@@ -494,7 +511,7 @@ __global__ __launch_bounds__(256) void k_gdn_post(
                 u16x8 out;
 #pragma unroll
                 for (int i = 0; i < 8; i++) {
-                    const float x1 = rndf(os[row * RS + c8 + i] * rs[row]);
+                    const float x1 = rndf(bf2f(ov[k][i]) * rs[row]);
                     const float x2 = rndf(x1 * bf2f(wv[i]));
                     out[i] = f2bf(x2 * silu_f[zv[i]]);     // silu(z), fp32
                 }
