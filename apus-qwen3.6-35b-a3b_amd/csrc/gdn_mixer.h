@@ -17,15 +17,24 @@ struct GdnScratch {
     float *graw;        // [Ttot][hv]: g itself (log decay), when requested
 };
 
+// Token offsets of up to kGdnCuInline sequences by value (kernel
+// arguments), so a small prefill needs no device copy of its metadata.
+constexpr int kGdnCuInline = 256;
+struct GdnCu {
+    int32_t cu[kGdnCuInline + 1];
+};
+
 int gdn_check_layer(const ApusHipGdnLayer *L);
 int gdn_check_offsets(size_t B, const int32_t *cu);
-// conv + l2norm + gates for every token (reads the old conv state)
-int gdn_prep(const ApusHipGdnLayer *L, size_t B, const int32_t *dcu,
+// conv + l2norm + gates for every token (reads the old conv state).
+// Token offsets: dcu (device) when non-null, else from the host array cu
+// by value (B <= kGdnCuInline).
+int gdn_prep(const ApusHipGdnLayer *L, size_t B, const int32_t *cu, const int32_t *dcu,
              size_t Ttot, const uint16_t *qkv, const uint16_t *a,
              const uint16_t *b, const uint16_t *conv_state, GdnScratch *w,
              bool want_graw);
 // gated RMSNorm of w->ob into y, then the new conv state
-int gdn_post(const ApusHipGdnLayer *L, size_t B, const int32_t *dcu,
+int gdn_post(const ApusHipGdnLayer *L, size_t B, const int32_t *cu, const int32_t *dcu,
              size_t Ttot, const GdnScratch *w, const uint16_t *z,
              const uint16_t *qkv, uint16_t *conv_state, uint16_t *y);
 

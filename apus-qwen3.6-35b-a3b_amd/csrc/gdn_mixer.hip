@@ -299,7 +299,7 @@ constexpr int RSC = DV + 8;  // LDS row stride in bf16 codes: 16-byte aligned ro
 // the l2norm (c/gdn.h:402-416); 32 lanes evaluate the (exp(g), beta) gates
 // of the two v-heads, optionally with the raw g.
 __global__ __launch_bounds__(256) void k_gdn_prep(
-    const int32_t *__restrict__ cu, int B, int Ttot, const uint16_t *__restrict__ qkv,
+    GdnCu ci, const int32_t *__restrict__ dcu, int B, int Ttot, const uint16_t *__restrict__ qkv,
     const uint16_t *__restrict__ a, const uint16_t *__restrict__ b,
     const uint16_t *__restrict__ conv_w, const float *__restrict__ A_log,
     const float *__restrict__ dt_bias, const uint16_t *__restrict__ conv_state,
@@ -307,6 +307,7 @@ __global__ __launch_bounds__(256) void k_gdn_prep(
     float2 *__restrict__ gate, float *__restrict__ graw, int hk, float qscale,
     const uint16_t *__restrict__ silu_bf, const uint16_t *__restrict__ sig_bf) {
     typedef unsigned short u16x8 __attribute__((ext_vector_type(8)));
+    const int32_t *cu = dcu ? dcu : ci.cu;
     const int tile = blockIdx.x / hk, kh = blockIdx.x % hk;
     const int tb = tile * PT, nt = min(PT, Ttot - tb);
     const int tid = threadIdx.x;
@@ -464,11 +465,12 @@ __global__ __launch_bounds__(256) void k_gdn_prep(
 // write each sequence's new conv state (the last three pre-conv inputs of
 // [old state | tokens]) after every reader of the old one has finished.
 __global__ __launch_bounds__(256) void k_gdn_post(
-    const int32_t *__restrict__ cu, int B, int Ttot,
+    GdnCu ci, const int32_t *__restrict__ dcu, int B, int Ttot,
     const uint16_t *__restrict__ ob, const uint16_t *__restrict__ z,
     const uint16_t *__restrict__ onorm_w, uint16_t *__restrict__ y,
     const uint16_t *__restrict__ qkv, uint16_t *__restrict__ conv_state,
     int hk, const float *__restrict__ silu_f) {
+    const int32_t *cu = dcu ? dcu : ci.cu;
     const int hv = hk * REP;
     const size_t kd = (size_t)hk * DK, vd = (size_t)hv * DV, cd = 2 * kd + vd;
     const int tid = threadIdx.x;
@@ -557,7 +559,15 @@ int gdn_check_offsets(size_t B, const int32_t *cu) {
     return kOk;
 }
 
-int gdn_prep(const ApusHipGdnLayer *L, size_t B, const int32_t *dcu,
+// the offsets by value when they fit, else the device copy
+static bool gdn_cu_arg(size_t B, const int32_t *cu, const int32_t *dcu, GdnCu *ci) {
+    if (dcu) return true;
+    if (B > (size_t)kGdnCuInline || !cu) return false;
+    memcpy(ci->cu, cu, (B + 1) * 4);
+    return true;
+}
+
+int gdn_prep(const ApusHipGdnLayer *L, size_t B, const int32_t *cu, const int32_t *dcu,
              size_t Ttot, const uint16_t *qkv, const uint16_t *a,
              const uint16_t *b, const uint16_t *conv_state, GdnScratch *w,
              bool want_graw) {
@@ -572,23 +582,27 @@ int gdn_prep(const ApusHipGdnLayer *L, size_t B, const int32_t *dcu,
     const float qscale = (float)pow((double)L->dk, -0.5);
     const ActTables *tabs = act_tables();
     if (!tabs) return kErrHip;
+    GdnCu ci;
+    if (!gdn_cu_arg(B, cu, dcu, &ci)) return set_error(kErrArgument, "no token offsets");
     APUS_TIMED("k_gdn_prep",
                k_gdn_prep<<<(unsigned)(cdiv(Ttot, PT) * L->hk), 256, 0, stream()>>>(
-        dcu, (int)B, (int)Ttot, qkv, a, b, L->conv_w, L->A_log, L->dt_bias, conv_state,
+        ci, dcu, (int)B, (int)Ttot, qkv, a, b, L->conv_w, L->A_log, L->dt_bias, conv_state,
         w->qk, w->vconv, w->gate, w->graw, (int)L->hk, qscale, tabs->silu_bf, tabs->sig_bf));
     return launch_check("k_gdn_prep");
 }
 
-int gdn_post(const ApusHipGdnLayer *L, size_t B, const int32_t *dcu,
+int gdn_post(const ApusHipGdnLayer *L, size_t B, const int32_t *cu, const int32_t *dcu,
              size_t Ttot, const GdnScratch *w, const uint16_t *z,
              const uint16_t *qkv, uint16_t *conv_state, uint16_t *y) {
     const size_t cd = 2 * L->hk * DK + L->hv * DV;
     const size_t nblk = cdiv(Ttot * L->hv, PR) + B * (cd / 256);
     const ActTables *tabs = act_tables();
     if (!tabs) return kErrHip;
+    GdnCu ci;
+    if (!gdn_cu_arg(B, cu, dcu, &ci)) return set_error(kErrArgument, "no token offsets");
     APUS_TIMED("k_gdn_post",
                k_gdn_post<<<(unsigned)nblk, 256, 0, stream()>>>(
-        dcu, (int)B, (int)Ttot, w->ob, z, L->onorm_w, y, qkv, conv_state,
+        ci, dcu, (int)B, (int)Ttot, w->ob, z, L->onorm_w, y, qkv, conv_state,
         (int)L->hk, tabs->silu_f));
     return launch_check("k_gdn_post");
 }

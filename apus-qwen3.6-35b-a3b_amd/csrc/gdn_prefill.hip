@@ -841,8 +841,9 @@ int apus_hip_gdn_prefill(const ApusHipGdnLayer *L, size_t B, const int32_t *cu,
     if (Ttot == 0) return kOk;
     if (B * L->hv * NCB > 0x7fffffffu) return set_error(kErrArgument, "batch too large");
 
-    // metadata: [cu | chunk offsets], uploaded (k_gdn_prep/post read the
-    // device copy) and, for small batches, also passed by value
+    // metadata [cu | chunk offsets]: by value for small batches (k_gdn_prep
+    // and k_gdn_post take cu for up to kGdnCuInline sequences, WY and the
+    // scan both arrays for up to kPrefillInline), else a device copy
     std::vector<int32_t> meta(2 * (B + 1));
     memcpy(meta.data(), cu, (B + 1) * 4);
     int32_t *coff = meta.data() + B + 1;
@@ -855,11 +856,14 @@ int apus_hip_gdn_prefill(const ApusHipGdnLayer *L, size_t B, const int32_t *cu,
     if (B <= (size_t)kPrefillInline) {
         memcpy(sq.cu, cu, (B + 1) * 4);
         memcpy(sq.coff, coff, (B + 1) * 4);
-        int32_t *m = (int32_t *)scratch(kScratchMeta3, meta.size() * 4);
-        if (!m) return kErrHip;
-        k_prefill_meta<<<1, 256, 0, stream()>>>(sq, m);
-        APUS_LAUNCHED("k_prefill_meta");
-        dmeta = m;
+        dmeta = nullptr;                       // prep / post take cu by value
+        if (B > (size_t)kGdnCuInline) {
+            int32_t *m = (int32_t *)scratch(kScratchMeta3, meta.size() * 4);
+            if (!m) return kErrHip;
+            k_prefill_meta<<<1, 256, 0, stream()>>>(sq, m);
+            APUS_LAUNCHED("k_prefill_meta");
+            dmeta = m;
+        }
         kmeta = nullptr;
     } else {
         dmeta = (const int32_t *)upload_small(kScratchMeta, meta.data(), meta.size() * 4);
@@ -868,7 +872,7 @@ int apus_hip_gdn_prefill(const ApusHipGdnLayer *L, size_t B, const int32_t *cu,
     }
 
     GdnScratch w;
-    if (int r = gdn_prep(L, B, dmeta, Ttot, qkv, a, b, conv_state, &w, true)) return r;
+    if (int r = gdn_prep(L, B, cu, dmeta, Ttot, qkv, a, b, conv_state, &w, true)) return r;
     const size_t units = nch * L->hv;
     float *Ub = (float *)scratch(kScratchGdnChunk, units * C * DV * 4);
     uint16_t *Wb = (uint16_t *)scratch(kScratchGdnChunk2, units * C * DK * 4);
@@ -886,7 +890,7 @@ int apus_hip_gdn_prefill(const ApusHipGdnLayer *L, size_t B, const int32_t *cu,
                k_gdn_chunk_scan<<<(unsigned)(B * L->hv * NCB), 512, 0, stream()>>>(
         sq, kmeta, Qp, Kp, Ub, Wb, Ab, Fb, S, w.ob, (int)L->hk));
     APUS_LAUNCHED("k_gdn_chunk_scan");
-    return gdn_post(L, B, dmeta, Ttot, &w, z, qkv, conv_state, y);
+    return gdn_post(L, B, cu, dmeta, Ttot, &w, z, qkv, conv_state, y);
 }
 
 }  // extern "C"

@@ -111,3 +111,14 @@ def test_prefill_then_decode(hip, orc):
     assert np.array_equal(dconv.cpu().numpy().view(np.uint16), c_o)
     assert_state_close(Su.cpu().numpy(), S_o, what="prefill+decode S")
     assert_bf16_rows(y.cpu().numpy().view(np.uint16), y_o, 128, what="prefill+decode y")
+
+
+@pytest.mark.parametrize("B", [260, 410])
+def test_prefill_many_sequences(hip, orc, B):
+    """Batches past the by-value metadata limits (256 sequences for the
+    token-parallel kernels, 400 for the chunk kernels): the offsets then
+    travel through a device copy."""
+    rng = np.random.default_rng(B)
+    lens = rng.integers(1, 5, B)
+    cu = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+    _run_prefill(hip, orc, rng, cu, tag=f"B{B}")
