@@ -36,6 +36,8 @@ EXPORTS = [
     "apus_hip_attn_gqa_decode_mt", "apus_hip_attn_outgate",
     "apus_hip_gdn_decode", "apus_hip_gdn_decode_into", "apus_hip_gdn_prefill", "apus_hip_gdn_state_pack", "apus_hip_gdn_state_unpack",
     "apus_hip_attn_cache_pack", "apus_hip_attn_cache_unpack", "apus_hip_attn_decode", "apus_hip_attn_prefill",
+    "apus_hip_bf16_gemv", "apus_hip_bf16_gemm", "apus_hip_bf16_weights_release",
+    "apus_hip_bf16_gemm_dev", "apus_hip_bf16_gemm_mfma_dev",
 ]
 
 
@@ -347,3 +349,35 @@ def attn_prefill(layer, cu, pos0, qg, k, v, kcache, vcache, max_seq, y):
     _chk(load().apus_hip_attn_prefill(C.byref(layer), _sz(B), cup, pos0.ctypes.data_as(_i32p),
                                       _dp(qg), _dp(k), _dp(v), _dp(kcache), _dp(vcache),
                                       _sz(max_seq), _dp(y)))
+
+
+# ---- projections (c/bf16.h:178-231)
+def bf16_gemv(w, x):
+    """Drop-in of the reference's bf16_gemv hook: numpy w [O,K], x [K]
+    (uint16 codes) -> y [O]. Bitwise the reference's order."""
+    O, K = w.shape
+    y = np.empty(O, np.uint16)
+    _chk(load().apus_hip_bf16_gemv(_u16(w), _u16(x), _u16(y), _sz(O), _sz(K)))
+    return y
+
+
+def bf16_gemm(w, x):
+    """Drop-in of the bf16_gemm hook: w [O,K], x [M,K] -> y [M,O]."""
+    O, K = w.shape
+    M = x.shape[0]
+    y = np.empty((M, O), np.uint16)
+    _chk(load().apus_hip_bf16_gemm(_u16(w), _u16(x), _u16(y), _sz(M), _sz(O), _sz(K)))
+    return y
+
+
+def bf16_weights_release():
+    _chk(load().apus_hip_bf16_weights_release())
+
+
+def bf16_gemm_dev(w, x, y, exact=True):
+    """Device tensors (int16 views of bf16 codes): w [O,K], x [M,K],
+    y [M,O]. exact: the reference's order (bitwise); else the MFMA GEMM."""
+    O, K = w.shape
+    M = x.shape[0]
+    f = load().apus_hip_bf16_gemm_dev if exact else load().apus_hip_bf16_gemm_mfma_dev
+    _chk(f(_dp(w), _dp(x), _dp(y), _sz(M), _sz(O), _sz(K)))

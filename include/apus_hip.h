@@ -256,6 +256,36 @@ int apus_hip_attn_decode(const ApusHipAttnLayer *L, size_t B,
                          const uint16_t *v, uint16_t *kcache,
                          uint16_t *vcache, size_t max_seq, uint16_t *y);
 
+/* ---- projections on either side of the path (c/bf16.h:178-231) --------
+ * y[m][o] = rnd(sum_k w[o][k] * x[m][k]), w [O][K], x [M][K], y [M][O],
+ * bf16 codes, fp32 accumulation. */
+
+/* Drop-ins for the reference's backend hook slots bf16_gemv / bf16_gemm
+ * (ApusBackendHooks, c/backend_metal.h:68-75, called from
+ * apus_bf16_gemv_hot / apus_bf16_gemm_hot, c/bf16.h:199-231) with their
+ * argument lists. HOST pointers. The k sum runs in the reference's order
+ * (ascending k, one rounding per multiply and per add, c/bf16.h:285-293),
+ * so y is bitwise the reference's. w must be a stable weight: its device
+ * copy is made at the first call and reused while (w, O*K) is unchanged
+ * (the Metal backend's stable-pointer rule, c/backend_metal.h:42-48);
+ * apus_hip_bf16_weights_release drops every copy. */
+int apus_hip_bf16_gemv(const uint16_t *w, const uint16_t *x, uint16_t *y,
+                       size_t O, size_t K);
+int apus_hip_bf16_gemm(const uint16_t *w, const uint16_t *x, uint16_t *y,
+                       size_t M, size_t O, size_t K);
+int apus_hip_bf16_weights_release(void);
+
+/* Device-pointer forms (no counterpart in the reference; the tier-2 calls
+ * around the device-resident mixers). _dev: the reference's order, bitwise,
+ * one lane per output (decode-sized M). _mfma_dev: the 16x16x32 bf16 MFMA,
+ * for prefill and large batches; its sums run in the MFMA's order, a
+ * tolerance class of the reference (|c - r| <= 2e-3 (|r| + sum_k |w x|)).
+ * Needs K % 8 == 0 and 16-byte aligned w, x. */
+int apus_hip_bf16_gemm_dev(const uint16_t *w, const uint16_t *x, uint16_t *y,
+                           size_t M, size_t O, size_t K);
+int apus_hip_bf16_gemm_mfma_dev(const uint16_t *w, const uint16_t *x,
+                                uint16_t *y, size_t M, size_t O, size_t K);
+
 #ifdef __cplusplus
 }
 #endif

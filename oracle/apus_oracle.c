@@ -320,6 +320,22 @@ void orc_attn_outgate(const uint16_t *o, const uint16_t *gate, uint16_t *y,
     }
 }
 
+/* ---- projections (c/bf16.h:285-300: per output an ascending fp32 sum of
+ * widened products, one rounding per multiply and per add, then RNE; the
+ * gemm is the gemv per row). Outputs are independent, so the OpenMP split
+ * over (m, o) leaves every sum's order unchanged. */
+void orc_bf16_gemm(const uint16_t *w, const uint16_t *x, uint16_t *y,
+                   size_t M, size_t O, size_t K) {
+#pragma omp parallel for schedule(static)
+    for (long u = 0; u < (long)(M * O); u++) {
+        const size_t m = (size_t)u / O, o = (size_t)u % O;
+        const uint16_t *wr = w + o * K, *xr = x + m * K;
+        float acc = 0.0f;
+        for (size_t k = 0; k < K; k++) acc += f32(wr[k]) * f32(xr[k]);
+        y[m * O + o] = rnd(acc);
+    }
+}
+
 /* ---- GDN mixer (c/layer.h:236-286 decode, 427-492 prefill) ------------
  * Phase 1 (per sequence): conv over the sequence's tokens, then per token
  * beta, decay, l2norm of the K heads. Phase 2 (per (sequence, v-head)):

@@ -104,6 +104,10 @@ void orc_attn_gqa_mt(const uint16_t *q, const uint16_t *kc,
                      size_t H, size_t Hkv, size_t D, float scale,
                      int nthreads);
 /* (d) sigmoid output gate                             (c/attn.h:524-531) */
+/* y [M][O] = rnd(w [O][K] . x [M][K]) in the reference's order
+ * (c/bf16.h:285-300) */
+void orc_bf16_gemm(const uint16_t *w, const uint16_t *x, uint16_t *y,
+                   size_t M, size_t O, size_t K);
 void orc_attn_outgate(const uint16_t *o, const uint16_t *gate, uint16_t *y,
                       size_t N);
 

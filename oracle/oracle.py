@@ -216,6 +216,14 @@ class Oracle(_Ops):
                                C.c_int(nthreads))
         return (y, trd) if trace else y
 
+    def bf16_gemm(self, w, x):
+        """w [O,K], x [M,K] (uint16 codes) -> y [M,O] (c/bf16.h:285-300)."""
+        O, K = w.shape
+        M = x.shape[0]
+        y = np.empty((M, O), np.uint16)
+        self.lib.orc_bf16_gemm(u16(w), u16(x), u16(y), _sz(M), _sz(O), _sz(K))
+        return y
+
     def attn_mixer(self, dims, w, cu, pos0, qg, k, v, kcache, vcache,
                    cache_stride, nthreads=0, capture=False):
         """dims = (nh, nkv, d, rot, theta); w = dict(qn_w, kn_w).
@@ -262,6 +270,24 @@ class Reference(_Ops):
                                   _sz(Tk), _sz(H), _sz(Hkv), _sz(D),
                                   C.c_float(scale))
         return o
+
+    def bf16_gemm(self, w, x, hot=True):
+        """The reference's gemm: hot (threaded x86 path) or the scalar
+        anchor, y [M,O]."""
+        O, K = w.shape
+        M = x.shape[0]
+        y = np.empty((M, O), np.uint16)
+        if hot:
+            self.lib.ref_bf16_gemm_hot(u16(w), u16(x), u16(y), _sz(M), _sz(O), _sz(K))
+        else:
+            self.lib.apus_bf16_gemm_scalar(u16(w), u16(x), u16(y), _sz(M), _sz(O), _sz(K))
+        return y
+
+    def bf16_gemv(self, w, x):
+        O, K = w.shape
+        y = np.empty(O, np.uint16)
+        self.lib.ref_bf16_gemv_hot(u16(w), u16(x), u16(y), _sz(O), _sz(K))
+        return y
 
     def gdn_mixer(self, dims, w, cu, qkv, z, a, b, conv_state, S):
         hk, hv, dk, dv = dims

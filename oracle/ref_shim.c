@@ -5,8 +5,9 @@
  * TEST INFRASTRUCTURE: used only to pin the oracle restatement bitwise
  * and, optionally, as bench.py's "reference" CPU baseline.
  *
- * Besides the reference's exported op symbols (apus_gdn_*, apus_attn_*),
- * this file adds two drivers that sequence those ops exactly as the
+ * Besides the reference's exported op symbols (apus_gdn_*, apus_attn_*,
+ * apus_bf16_gemv_scalar / _gemm_scalar), the projection hot paths
+ * (ref_bf16_gemv_hot / _gemm_hot) and two drivers that sequence those ops exactly as the
  * reference's layer does between its projections, for B sequences run
  * one after another (the reference engine is single-sequence):
  *   ref_gdn_mixer  -- c/layer.h:445-489 (conv over the span, then per
@@ -29,6 +30,17 @@
 #include <string.h>
 
 int ref_pool_threads(void) { return apus_pool_threads(); }
+
+/* The projection hot paths without a backend hook installed: the x86
+ * threaded gemv / gemm of the reference's CPU build (c/bf16.h:178-222). */
+void ref_bf16_gemv_hot(const uint16_t *w, const uint16_t *x, uint16_t *y,
+                       size_t O, size_t K) {
+    apus_bf16_gemv_hot_cpu(w, x, y, O, K);
+}
+void ref_bf16_gemm_hot(const uint16_t *w, const uint16_t *x, uint16_t *y,
+                       size_t M, size_t O, size_t K) {
+    apus_bf16_gemm_hot_cpu(w, x, y, M, O, K);
+}
 
 void ref_gdn_mixer(size_t hk, size_t hv, size_t dk, size_t dv,
                    const uint16_t *conv_w, const float *A_log,

@@ -124,6 +124,17 @@ def main():
                                atok["v"], kc, vc, maxs * 2 * 64)
     v["am_kc1"], v["am_vc1"] = kc, vc
 
+    # projections (c/bf16.h:285-300): the x86 hot gemm, ragged shapes and a
+    # K that is not a multiple of 8 (its own seed: the vectors above are
+    # unchanged by this addition)
+    prng = np.random.default_rng(20260901)
+    v["gemm_w"] = synth.normal_bf16(prng, (37, 120), 0.1)
+    v["gemm_x"] = synth.normal_bf16(prng, (3, 120))
+    v["gemm_y"] = ref.bf16_gemm(v["gemm_w"], v["gemm_x"])
+    v["gemm_w2"] = synth.normal_bf16(prng, (19, 45), 0.3)
+    v["gemm_x2"] = synth.normal_bf16(prng, (2, 45))
+    v["gemm_y2"] = ref.bf16_gemm(v["gemm_w2"], v["gemm_x2"])
+
     out = os.path.join(HERE, "ref_vectors.npz")
     np.savez_compressed(out, **v)
     print(out, os.path.getsize(out), "bytes,", len(v), "arrays")

@@ -98,3 +98,18 @@ def test_hip_ops_match_reference_vectors(hip, gv):
             assert_bf16_close(a, r, what=k)
         else:
             assert_state_close(a, r, what=k)
+
+
+def test_oracle_gemm_matches_reference_vectors(orc, gv):
+    for sfx in ("", "2"):
+        y = orc.bf16_gemm(gv["gemm_w" + sfx], gv["gemm_x" + sfx])
+        assert _same_bits(y, gv["gemm_y" + sfx])
+
+
+@pytest.mark.gpu
+def test_hip_gemm_matches_reference_vectors(hip, gv):
+    """The projection drop-ins are bitwise the reference's (its order)."""
+    for sfx in ("", "2"):
+        w, x = gv["gemm_w" + sfx], gv["gemm_x" + sfx]
+        assert _same_bits(hip.bf16_gemm(w, x), gv["gemm_y" + sfx])
+        assert _same_bits(hip.bf16_gemv(w, np.ascontiguousarray(x[0])), gv["gemm_y" + sfx][0])

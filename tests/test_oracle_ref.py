@@ -149,3 +149,16 @@ def test_attn_mixer_bitwise(orc, ref, rng):
     y2 = ref.attn_mixer(dims, w, cu, pos0, tok["qg"], tok["k"], tok["v"], k2, v2, stride)
     assert np.array_equal(y1, y2)
     assert np.array_equal(k1, k2) and np.array_equal(v1, v2)
+
+
+@pytest.mark.parametrize("M,O,K", [(1, 300, 2048), (4, 129, 4096), (3, 17, 37)])
+def test_bf16_gemm_bitwise(orc, ref, rng, M, O, K):
+    """The projection restatement against the reference's x86 hot path and
+    its scalar anchor (c/bf16.h:178-231, 285-300)."""
+    w = synth.normal_bf16(rng, (O, K), 0.05)
+    x = synth.normal_bf16(rng, (M, K))
+    y = orc.bf16_gemm(w, x)
+    assert np.array_equal(y, ref.bf16_gemm(w, x))
+    assert np.array_equal(y, ref.bf16_gemm(w, x, hot=False))
+    if M == 1:
+        assert np.array_equal(y[0], ref.bf16_gemv(w, np.ascontiguousarray(x[0])))

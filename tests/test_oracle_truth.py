@@ -307,3 +307,25 @@ def test_outgate_corners(orc, rng):
     assert y[0] == bf16_bits(np.array([bf16_f32(o[:1])[0] * np.float32(0.5)], np.float32))[0]
     assert y[1] == o[1]
     assert abs(bf16_f32(y[2:3])[0]) < 1e-6 * (abs(bf16_f32(o[2:3])[0]) + 1e-6)
+
+
+def test_gemm_truth_and_corners(orc, rng):
+    """Projections (c/bf16.h:285-300): against the float64 sum within the
+    fp32 accumulation bound (K 2^-24 sum|w x|) plus the final rounding; a
+    permutation matrix returns x's codes exactly (catches a transposed or
+    shifted index); K = 0 gives +0; sign symmetry is exact."""
+    M, O, K = 3, 64, 1024
+    w = synth.normal_bf16(rng, (O, K), 0.05)
+    x = synth.normal_bf16(rng, (M, K))
+    y = orc.bf16_gemm(w, x)
+    wf, xf = bf16_f32(w).astype(np.float64), bf16_f32(x).astype(np.float64)
+    gold = xf @ wf.T
+    esc = np.abs(xf) @ np.abs(wf).T
+    assert tol_ok(bf16_f32(y), gold, esc, 2.0 ** -8, K * 2.0 ** -24).all()
+    perm = rng.permutation(K)[:O]
+    P = np.zeros((O, K), np.uint16)
+    P[np.arange(O), perm] = 0x3F80                      # 1.0
+    assert np.array_equal(orc.bf16_gemm(P, x), x[:, perm])
+    assert np.array_equal(orc.bf16_gemm(w ^ np.uint16(0x8000), x), y ^ np.uint16(0x8000))
+    z = orc.bf16_gemm(np.zeros((5, 0), np.uint16), np.zeros((2, 0), np.uint16))
+    assert z.shape == (2, 5) and np.all(z == 0)
