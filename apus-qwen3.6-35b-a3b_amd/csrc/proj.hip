@@ -10,13 +10,14 @@
 //                scalar anchor c/bf16.h:285-293, which the reference's
 //                threaded and Metal paths reproduce bitwise). Bitwise
 //                against the reference. The weight row is read 16 bytes
-//                at a time, four pieces ahead of the add chain; the x row
-//                is uniform across the wavefront (scalar loads).
-//   k_gemm_mfma  the 16x16x32 bf16 MFMA with fp32 accumulation for many
-//                rows (prefill, large decode batches): one workgroup per
-//                (64 outputs, 64 rows); wavefront w owns outputs
-//                16w..16w+15 and every row block, so each weight piece is
-//                loaded once per row tile. The MFMA sums in its own order:
+//                at a time, 16 to 32 pieces ahead of the add chain; the x row
+//                is staged in LDS once per wavefront.
+//   k_gemm_mfma  the 16x16x32 bf16 MFMA with fp32 accumulation for
+//                decode batches (up to kMfmaRows rows): one workgroup per
+//                (64 outputs, 64 rows), its 4 wavefronts splitting K, so
+//                each weight piece is loaded once per row tile. Larger
+//                batches (prefill) go to rocBLAS's bf16 GEMM (fp32
+//                compute), a plain library GEMM. Both sum in their own order:
 //                the tolerance class of the attention kernels (|c - r| <=
 //                2e-3 (|r| + esc), esc = sum_k |w x|).
 // Host-pointer drop-ins keep device copies of the weights keyed by their
@@ -26,6 +27,8 @@
 #include <string.h>
 
 #include <unordered_map>
+
+#include <rocblas/rocblas.h>
 
 #include "../../include/apus_hip.h"
 #include "apus_dev.h"
@@ -51,24 +54,54 @@ __global__ __launch_bounds__(64) void k_gemm_seq(const uint16_t *__restrict__ w,
     const uint16_t *wr = w + (size_t)min(o, O - 1) * K;
     float acc = 0.0f;
     if (VEC) {
-        const u16x8 *w8 = reinterpret_cast<const u16x8 *>(wr);
-        const u16x8 *x8 = reinterpret_cast<const u16x8 *>(xr);
+        // the x row in LDS (dynamic, K codes): its reads wait on the LDS
+        // counter, so the vector-memory waits count weight loads only
+        extern __shared__ __attribute__((aligned(16))) u16x8 xs_lds[];
         const int n8 = K / 8;
-        constexpr int AHEAD = 4;
-        u16x8 wq[AHEAD];
+        for (int i = threadIdx.x; i < n8; i += 64)
+            xs_lds[i] = reinterpret_cast<const u16x8 *>(xr)[i];
+        __syncthreads();
+        const u16x8 *w8 = reinterpret_cast<const u16x8 *>(wr);
+        const u16x8 *x8 = xs_lds;
+        constexpr int R = 16;          // pieces per round; two register sets
+        // rounds alternate between the sets: while one set is summed the
+        // next round's loads are in flight into the other. Prefetch indices
+        // are clamped to the row (no branch around a load), so each wait
+        // counts only the loads issued after the set it needs.
+        u16x8 qa[R], qb[R];
 #pragma unroll
-        for (int i = 0; i < AHEAD; i++) wq[i] = i < n8 ? w8[i] : u16x8{0, 0, 0, 0, 0, 0, 0, 0};
-        for (int p = 0; p < n8; p += AHEAD) {
+        for (int i = 0; i < R; i++) qa[i] = w8[min(i, n8 - 1)];
+        asm volatile("" ::: "memory");
+        __builtin_amdgcn_sched_barrier(0);
+        int p = 0;
+        for (; p + 2 * R <= n8; p += 2 * R) {
 #pragma unroll
-            for (int i = 0; i < AHEAD; i++) {
-                if (p + i < n8) {
-                    const u16x8 wv = wq[i];
-                    if (p + i + AHEAD < n8) wq[i] = w8[p + i + AHEAD];
-                    const u16x8 xv = x8[p + i];
+            for (int i = 0; i < R; i++) qb[i] = w8[min(p + R + i, n8 - 1)];
+            // keep the prefetches here (the compiler would sink each load
+            // to its first use and wait on it there)
+            asm volatile("" ::: "memory");
+            __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-                    for (int j = 0; j < 8; j++) acc = acc + bf2f(wv[j]) * bf2f(xv[j]);
-                }
+            for (int i = 0; i < R; i++) {
+                const u16x8 xv = x8[p + i];
+#pragma unroll
+                for (int j = 0; j < 8; j++) acc = acc + bf2f(qa[i][j]) * bf2f(xv[j]);
             }
+#pragma unroll
+            for (int i = 0; i < R; i++) qa[i] = w8[min(p + 2 * R + i, n8 - 1)];
+            asm volatile("" ::: "memory");
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int i = 0; i < R; i++) {
+                const u16x8 xv = x8[p + R + i];
+#pragma unroll
+                for (int j = 0; j < 8; j++) acc = acc + bf2f(qb[i][j]) * bf2f(xv[j]);
+            }
+        }
+        for (int i = 0; p + i < n8; i++) {
+            const u16x8 wv = w8[p + i], xv = x8[p + i];
+#pragma unroll
+            for (int j = 0; j < 8; j++) acc = acc + bf2f(wv[j]) * bf2f(xv[j]);
         }
     } else {
         for (int k = 0; k < K; k++) acc = acc + bf2f(wr[k]) * bf2f(xr[k]);
@@ -83,7 +116,15 @@ __device__ __forceinline__ bf16x8 ld_op(const uint16_t *base, int r, int nrows, 
     return __builtin_bit_cast(bf16x8, v);
 }
 
-constexpr int MT = 64, OT = 64, MB = MT / 16;
+// One workgroup per (64 outputs, up to 64 rows); its 4 wavefronts split K
+// (32-wide k step st goes to wavefront st % 4), each with all 4 x 4
+// 16x16 output blocks, the next step's operands in flight, and add their
+// partial sums through LDS. Operands come through buffer loads whose rows
+// past M or O sit out of the buffer's range and read as zero, so every
+// load and MFMA is unconditional (no branch joins for the compiler to
+// drain the memory counter at). Needs K % 32 == 0.
+constexpr int MT = 64, OT = 64, MB = MT / 16, OB = OT / 16, NWV = 4;
+constexpr int kOutOfRange = 0x40000000;   // a byte offset past every operand
 
 __global__ __launch_bounds__(256) void k_gemm_mfma(const uint16_t *__restrict__ w,
                                                    const uint16_t *__restrict__ x,
@@ -91,36 +132,77 @@ __global__ __launch_bounds__(256) void k_gemm_mfma(const uint16_t *__restrict__ 
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int r16 = lane & 15, g8 = (lane >> 4) * 8, kq = (lane >> 4) * 4;
-    const int o = blockIdx.x * OT + wave * 16 + r16;     // this lane's weight row
-    const int m0 = blockIdx.y * MT;
-    f32x4 acc[MB];
+    const int o0 = blockIdx.x * OT, m0 = blockIdx.y * MT;
+    const auto wr = buf_rsrc(w, (uint32_t)((size_t)O * K * 2));
+    const auto xr = buf_rsrc(x, (uint32_t)((size_t)M * K * 2));
+    int woff[OB], xoff[MB];
 #pragma unroll
-    for (int b = 0; b < MB; b++) acc[b] = f32x4{0.f, 0.f, 0.f, 0.f};
-    // one k step ahead
-    bf16x8 bw = ld_op(w, o, O, K, g8), ax[MB];
+    for (int c = 0; c < OB; c++) {
+        const int o = o0 + c * 16 + r16;
+        woff[c] = o < O ? (o * K + g8) * 2 : kOutOfRange;
+    }
 #pragma unroll
-    for (int b = 0; b < MB; b++) ax[b] = ld_op(x, m0 + b * 16 + r16, M, K, g8);
-    for (int k = 0; k < K; k += 32) {
-        const bf16x8 bc = bw;
-        bf16x8 ac[MB];
+    for (int b = 0; b < MB; b++) {
+        const int m = m0 + b * 16 + r16;
+        xoff[b] = m < M ? (m * K + g8) * 2 : kOutOfRange;
+    }
+    f32x4 acc[MB][OB];
+#pragma unroll
+    for (int b = 0; b < MB; b++)
+#pragma unroll
+        for (int c = 0; c < OB; c++) acc[b][c] = f32x4{0.f, 0.f, 0.f, 0.f};
+    const int nsteps = K / 32;
+    bf16x8 bw[OB], ax[MB];
+    // step st's operands; steps past K are clamped to the last (loaded,
+    // not used)
+    auto load = [&](int st) {
+        const int kb = min(st, nsteps - 1) * 64;
+#pragma unroll
+        for (int c = 0; c < OB; c++)
+            bw[c] = __builtin_bit_cast(bf16x8, llvm_raw_ptr_buffer_load_v4f32(wr, woff[c] + kb, 0, 0));
+#pragma unroll
+        for (int b = 0; b < MB; b++)
+            ax[b] = __builtin_bit_cast(bf16x8, llvm_raw_ptr_buffer_load_v4f32(xr, xoff[b] + kb, 0, 0));
+    };
+    load(wave);
+    for (int st = wave; st < nsteps; st += NWV) {
+        bf16x8 bc[OB], ac[MB];
+#pragma unroll
+        for (int c = 0; c < OB; c++) bc[c] = bw[c];
 #pragma unroll
         for (int b = 0; b < MB; b++) ac[b] = ax[b];
-        bw = ld_op(w, o, O, K, k + 32 + g8);
-#pragma unroll
-        for (int b = 0; b < MB; b++) ax[b] = ld_op(x, m0 + b * 16 + r16, M, K, k + 32 + g8);
+        load(st + NWV);
+        asm volatile("" ::: "memory");
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int b = 0; b < MB; b++)
-            acc[b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ac[b], bc, acc[b], 0, 0, 0);
+#pragma unroll
+            for (int c = 0; c < OB; c++)
+                acc[b][c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ac[b], bc[c], acc[b][c], 0, 0, 0);
     }
-    // D[row kq + i][column r16] of row block b: row m0 + 16b + kq + i, output o
-    if (o < O) {
+    // the partial sums of the 4 wavefronts through LDS, added in wavefront
+    // order; wavefront v then finishes row block v
+    __shared__ f32x4 part[NWV][MB][OB][64];
 #pragma unroll
-        for (int b = 0; b < MB; b++)
+    for (int b = 0; b < MB; b++)
+#pragma unroll
+        for (int c = 0; c < OB; c++) part[wave][b][c][lane] = acc[b][c];
+    __syncthreads();
+    const int b = wave;
+#pragma unroll
+    for (int c = 0; c < OB; c++) {
+        f32x4 s = part[0][b][c][lane];
+#pragma unroll
+        for (int v = 1; v < NWV; v++) s += part[v][b][c][lane];
+        // D[row kq + i][column r16]: row m0 + 16b + kq + i, output o0 + 16c + r16
+        const int o = o0 + c * 16 + r16;
+        if (o < O) {
 #pragma unroll
             for (int i = 0; i < 4; i++) {
                 const int m = m0 + b * 16 + kq + i;
-                if (m < M) y[(size_t)m * O + o] = f2bf(acc[b][i]);
+                if (m < M) y[(size_t)m * O + o] = f2bf(s[i]);
             }
+        }
     }
 }
 
@@ -138,7 +220,9 @@ int launch_seq(const uint16_t *w, const uint16_t *x, uint16_t *y, size_t M, size
     const bool vec = K % 8 == 0 && ((uintptr_t)w | (uintptr_t)x) % 16 == 0;
     const dim3 grid(cdiv(O, 64), (unsigned)M);
     if (vec) {
-        APUS_TIMED("k_gemm_seq", k_gemm_seq<true><<<grid, 64, 0, stream()>>>(w, x, y, (int)O, (int)K));
+        if (K * 2 > 64 * 1024) return set_error(kErrUnsupported, "sequential gemm takes K up to 32768");
+        APUS_TIMED("k_gemm_seq",
+                   k_gemm_seq<true><<<grid, 64, K * 2, stream()>>>(w, x, y, (int)O, (int)K));
     } else {
         APUS_TIMED("k_gemm_seq", k_gemm_seq<false><<<grid, 64, 0, stream()>>>(w, x, y, (int)O, (int)K));
     }
@@ -190,6 +274,33 @@ int host_gemm(const uint16_t *w, const uint16_t *x, uint16_t *y, size_t M, size_
     return stage_out(y, dy, M * O * 2);
 }
 
+// rocBLAS for prefill-sized row counts: y (column-major O x M, ldc O) =
+// w^T (w is column-major K x O) . x (column-major K x M), bf16 in and
+// out, fp32 compute. One handle per device, on the library's stream.
+constexpr size_t kMfmaRows = 256;
+std::unordered_map<int, rocblas_handle> g_blas;
+
+int blas_gemm(const uint16_t *w, const uint16_t *x, uint16_t *y, size_t M, size_t O, size_t K) {
+    const int dev = current_device();
+    rocblas_handle &h = g_blas[dev];
+    if (!h && rocblas_create_handle(&h) != rocblas_status_success) {
+        h = nullptr;
+        return set_error(kErrHip, "rocblas_create_handle failed");
+    }
+    if (rocblas_set_stream(h, stream()) != rocblas_status_success)
+        return set_error(kErrHip, "rocblas_set_stream failed");
+    const float one = 1.0f, zero = 0.0f;
+    const rocblas_status st = rocblas_gemm_ex(
+        h, rocblas_operation_transpose, rocblas_operation_none, (rocblas_int)O, (rocblas_int)M,
+        (rocblas_int)K, &one, w, rocblas_datatype_bf16_r, (rocblas_int)K, x,
+        rocblas_datatype_bf16_r, (rocblas_int)K, &zero, y, rocblas_datatype_bf16_r,
+        (rocblas_int)O, y, rocblas_datatype_bf16_r, (rocblas_int)O, rocblas_datatype_f32_r,
+        rocblas_gemm_algo_standard, 0, 0);
+    if (st != rocblas_status_success)
+        return set_error(kErrHip, "rocblas_gemm_ex failed (%d)", (int)st);
+    return kOk;
+}
+
 }  // namespace
 
 extern "C" {
@@ -224,8 +335,14 @@ int apus_hip_bf16_gemm_mfma_dev(const uint16_t *w, const uint16_t *x, uint16_t *
     APUS_READY();
     if (int r = check_dims(M, O, K)) return r;
     if (M == 0 || O == 0) return kOk;
-    if (K % 8 != 0 || ((uintptr_t)w | (uintptr_t)x) % 16 != 0)
-        return set_error(kErrUnsupported, "MFMA gemm needs K %% 8 == 0 and 16-byte aligned rows");
+    // the hand kernel: decode-sized M, K % 32 == 0, 16-byte aligned rows,
+    // operands under 1 GiB; everything else (prefill) through rocBLAS
+    if (M > kMfmaRows || K % 32 != 0 || ((uintptr_t)w | (uintptr_t)x) % 16 != 0 ||
+        O * K * 2 >= (size_t)kOutOfRange || M * K * 2 >= (size_t)kOutOfRange) {
+        int r = kOk;
+        APUS_TIMED("rocblas_gemm_bf16", r = blas_gemm(w, x, y, M, O, K));
+        return r;
+    }
     const dim3 grid(cdiv(O, OT), cdiv(M, MT));
     APUS_TIMED("k_gemm_mfma",
                k_gemm_mfma<<<grid, 256, 0, stream()>>>(w, x, y, (int)M, (int)O, (int)K));

@@ -16,6 +16,9 @@ reported under "configs" with their own roofline fractions:
   c3   config 3   gated-GQA causal prefill, T=8192 (cache fill + attention)
   c4   config 4   hybrid decode block, 3 GDN + 1 GQA layers, 128 sequences
                   verifying 1..4 tokens each at log-normal cached contexts
+  p1, p64, p4096  the GDN input projection (2048 -> 12352) beside the path:
+                  1 token (reference-order kernel, bitwise), 64 tokens
+                  (MFMA GEMM), 4096 tokens (rocBLAS bf16 GEMM)
 Input buffer sets rotate so the 256 MB Infinity Cache cannot serve
 repeated reads. The CPU baseline is the reference's own scalar anchors
 (oracle/_ref, built from the reference sources) when present, else the
@@ -419,6 +422,41 @@ def bench_mixed_block(torch, B, steps, warmup, seed):
                 roofline=kernel_roofline(kt, table, wl))
 
 
+PROJ_O, PROJ_K = CD + VD + 2 * HV, 2048   # GDN in_proj: qkv | z | a | b (12352 x 2048)
+
+
+def bench_proj(torch, M, exact, steps, warmup, seed):
+    """The GDN layer's input projection (the step on the path's input
+    side): y [M, 12352] = x [M, 2048] . w^T, bf16. exact: the
+    reference-order kernel (bitwise, decode-sized M); else the MFMA GEMM.
+    Weight sets rotate so the 50 MB weight is read from HBM."""
+    import apus_hip
+    O, K = PROJ_O, PROJ_K
+    nsets = 6
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    sets = []
+    for _ in range(nsets):
+        w = (torch.randn((O, K), generator=g, device="cuda") * K ** -0.5).to(torch.bfloat16)
+        x = torch.randn((M, K), generator=g, device="cuda").to(torch.bfloat16)
+        y = torch.empty((M, O), dtype=torch.bfloat16, device="cuda")
+        sets.append((w.view(torch.int16), x.view(torch.int16), y.view(torch.int16)))
+
+    def step(i):
+        w, x, y = sets[i]
+        apus_hip.bf16_gemm_dev(w, x, y, exact=exact)
+
+    kname = "k_gemm_seq" if exact else ("k_gemm_mfma" if M <= 256 else "rocblas_gemm_bf16")
+    bytes_ = O * K * 2 + M * K * 2 + M * O * 2
+    flops = 2 * M * O * K
+    table = {kname: ("hbm", bytes_, HBM_PEAK) if M <= 256 else ("mfma", flops, BF16_PEAK)}
+    total, per, kt = time_steps(torch, step, steps, warmup, nsets, table)
+    wl = f"gdn_in_proj_m{M}"
+    return dict(workload=wl, tokens_per_step=M, ms_per_step=total / steps * 1e3,
+                step_event_ms=float(np.mean(per)) * 1e3, kernels_ms=kt, alg_bytes=bytes_,
+                alg_flops=flops, exact=exact, tok_s=M * steps / total,
+                roofline=kernel_roofline(kt, table, wl))
+
+
 def bench_copy(torch, steps, warmup):
     """Calibration workload for HBM counters: a plain 1 GiB device copy
     (reads 1 GiB, writes 1 GiB); rocprofv3 FETCH_SIZE / WRITE_SIZE of its
@@ -504,7 +542,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--only", default="c0,c0b,c1,c2,c3,c4")
+    ap.add_argument("--only", default="c0,c0b,c1,c2,c3,c4,p1,p64,p4096")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-tokens", type=int, default=8192)
     ap.add_argument("--cpu-threads", type=int, default=CPU_THREADS)
@@ -544,6 +582,10 @@ def main():
     if "c4" in want:
         res["c4"] = bench_mixed_block(torch, 128, args.steps, args.warmup, 15)
         log("c4", res["c4"])
+    for name, M, exact in (("p1", 1, True), ("p64", 64, False), ("p4096", 4096, False)):
+        if name in want:
+            res[name] = bench_proj(torch, M, exact, args.steps, args.warmup, 16)
+            log(name, res[name])
     if "copy" in want:
         res["copy"] = bench_copy(torch, args.steps, args.warmup)
         log("copy", res["copy"])

@@ -277,10 +277,11 @@ int apus_hip_bf16_weights_release(void);
 
 /* Device-pointer forms (no counterpart in the reference; the tier-2 calls
  * around the device-resident mixers). _dev: the reference's order, bitwise,
- * one lane per output (decode-sized M). _mfma_dev: the 16x16x32 bf16 MFMA,
- * for prefill and large batches; its sums run in the MFMA's order, a
- * tolerance class of the reference (|c - r| <= 2e-3 (|r| + sum_k |w x|)).
- * Needs K % 8 == 0 and 16-byte aligned w, x. */
+ * one lane per output (decode-sized M). _mfma_dev: the 16x16x32 bf16 MFMA
+ * for decode batches up to 256 rows (K % 32 == 0, 16-byte aligned w, x),
+ * rocBLAS's bf16 GEMM (fp32 compute) otherwise (prefill); both sum in their
+ * own order, a tolerance class of the reference (|c - r| <= 2e-3 (|r| +
+ * sum_k |w x|)). */
 int apus_hip_bf16_gemm_dev(const uint16_t *w, const uint16_t *x, uint16_t *y,
                            size_t M, size_t O, size_t K);
 int apus_hip_bf16_gemm_mfma_dev(const uint16_t *w, const uint16_t *x,

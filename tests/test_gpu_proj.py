@@ -63,7 +63,9 @@ def test_gemm_dev_bitwise(hip, orc, M, O, K):
     assert np.array_equal(y.cpu().numpy().view(np.uint16), orc.bf16_gemm(w, x))
 
 
-@pytest.mark.parametrize("M,O,K", [(64, 12352, 2048), (200, 1000, 4096), (5, 70, 40)])
+@pytest.mark.parametrize("M,O,K", [(64, 12352, 2048), (200, 1000, 4096), (5, 70, 40),
+                                   (300, 517, 2048),    # through rocBLAS
+                                   (7, 90, 40)])        # K % 32 != 0: rocBLAS
 def test_gemm_mfma_tolerance(hip, orc, M, O, K):
     import torch
     rng = np.random.default_rng(M * 31 + K)
