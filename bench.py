@@ -553,7 +553,7 @@ def main():
         return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path "
-              "(the hot path shards without communication; see DESIGN.md). "
+              "(the mixers shard by sequence or by head with no exchange inside the path). "
               "Run with --gpus 1.", file=sys.stderr)
         sys.exit(2)
 
