@@ -85,3 +85,16 @@ def lognormal_contexts(rng, B, mu=np.log(4096.0), sigma=1.0, lo=256, hi=65536):
     """Config 4 context lengths: LogNormal(mu, sigma) clipped to [lo, hi]."""
     c = np.exp(rng.normal(mu, sigma, B))
     return np.clip(np.round(c), lo, hi).astype(np.int64)
+
+
+def mixed_block_shape(B=128, seed=15):
+    """Config 4's ragged batch: cached contexts LogNormal(mu = ln 4096,
+    sigma = 1.0) clipped to [256, 65536] (truncated to integers), and 1..4
+    verify tokens per sequence; cached + new tokens stay within 65536.
+    Returns (ctx [B] int32, k [B] int32). seed 15 is the benchmark's draw
+    (mean context 7510, max 36066, 325 verify tokens)."""
+    rng = np.random.default_rng(seed)
+    ctx = np.clip(np.exp(rng.normal(np.log(4096.0), 1.0, B)), 256, 65536).astype(np.int64)
+    k = rng.integers(1, 5, B)
+    ctx = np.minimum(ctx, 65536 - k)
+    return ctx.astype(np.int32), k.astype(np.int32)

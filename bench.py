@@ -346,17 +346,6 @@ def bench_attn_prefill(torch, T, steps, warmup, seed):
                 layer_mfma_frac=flops / st / BF16_PEAK, roofline=kernel_roofline(kt, table, wl))
 
 
-def mixed_block_shape(B, seed):
-    """Config 4's ragged batch: cached context lengths log-normal around
-    4096 (mu = ln 4096, sigma = 1.0), clipped to [256, 65536], and 1..4
-    verify tokens per sequence, from a fixed seed."""
-    rng = np.random.default_rng(seed)
-    ctx = np.clip(np.exp(rng.normal(np.log(4096.0), 1.0, B)), 256, 65536).astype(np.int64)
-    k = rng.integers(1, 5, B)
-    ctx = np.minimum(ctx, 65536 - k)          # cached + new tokens stay within 65536
-    return ctx.astype(np.int32), k.astype(np.int32)
-
-
 def bench_mixed_block(torch, B, steps, warmup, seed):
     """Config 4: one hybrid decode block in the model's 3:1 ratio -- three
     Gated DeltaNet layers (each with its own weights, conv state and
@@ -373,7 +362,8 @@ def bench_mixed_block(torch, B, steps, warmup, seed):
         x = torch.randn(shape, generator=g, device=dev, dtype=torch.float32) * std + mean
         return x.to(torch.bfloat16).view(torch.int16)
 
-    ctx, k = mixed_block_shape(B, seed)
+    import synth
+    ctx, k = synth.mixed_block_shape(B, seed)
     cu = np.concatenate([[0], np.cumsum(k)]).astype(np.int32)
     T = int(cu[-1])
     gdn = []

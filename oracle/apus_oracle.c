@@ -410,25 +410,22 @@ void orc_gdn_mixer(const OrcGdnDims *dm, const uint16_t *conv_w,
 }
 
 /* ---- attention mixer (c/layer.h:288-331 decode, 498-564 prefill) ------ */
-void orc_attn_mixer(const OrcAttnDims *dm, const uint16_t *qn_w,
-                    const uint16_t *kn_w, size_t B, const int32_t *cu,
-                    const int32_t *pos0, const uint16_t *qg,
-                    const uint16_t *k, const uint16_t *v, uint16_t *kcache,
-                    uint16_t *vcache, size_t cache_stride, uint16_t *y,
-                    uint16_t *qf, uint16_t *kf, int nthreads) {
+/* per token: q/k (1+w) norm, rope at its own position, cache append
+ * (c/layer.h:300-316) */
+void orc_attn_prep_off(const OrcAttnDims *dm, const uint16_t *qn_w,
+                       const uint16_t *kn_w, size_t B, const int32_t *cu,
+                       const int32_t *pos0, const uint16_t *qg,
+                       const uint16_t *k, const uint16_t *v,
+                       uint16_t *kcache, uint16_t *vcache,
+                       const size_t *cache_off, uint16_t *qn, uint16_t *kf,
+                       int nthreads) {
     size_t nh = dm->nh, nkv = dm->nkv, d = dm->d, rot = dm->rot;
-    size_t Ttot = (size_t)cu[B];
-    float scale = (float)(1.0 / sqrt((double)d));
     int nt = nthr(nthreads);
-    uint16_t *qn = malloc(Ttot * nh * d * sizeof *qn);
-    uint16_t *ao = malloc(Ttot * nh * d * sizeof *ao);
     long BB = (long)B;
-
-    /* per token: q/k (1+w) norm, rope at its own position, cache append */
 #pragma omp parallel for schedule(static) num_threads(nt)
     for (long s = 0; s < BB; s++) {
-        uint16_t *kc = kcache + (size_t)s * cache_stride;
-        uint16_t *vc = vcache + (size_t)s * cache_stride;
+        uint16_t *kc = kcache + cache_off[s];
+        uint16_t *vc = vcache + cache_off[s];
         for (size_t t = (size_t)cu[s]; t < (size_t)cu[s + 1]; t++) {
             size_t pos = (size_t)pos0[s] + (t - (size_t)cu[s]);
             for (size_t h = 0; h < nh; h++) {
@@ -448,6 +445,24 @@ void orc_attn_mixer(const OrcAttnDims *dm, const uint16_t *qn_w,
             if (kf) memcpy(kf + t * nkv * d, krow, nkv * d * sizeof *krow);
         }
     }
+}
+
+void orc_attn_mixer_off(const OrcAttnDims *dm, const uint16_t *qn_w,
+                        const uint16_t *kn_w, size_t B, const int32_t *cu,
+                        const int32_t *pos0, const uint16_t *qg,
+                        const uint16_t *k, const uint16_t *v,
+                        uint16_t *kcache, uint16_t *vcache,
+                        const size_t *cache_off, uint16_t *y, uint16_t *qf,
+                        uint16_t *kf, uint16_t *attno, int nthreads) {
+    size_t nh = dm->nh, nkv = dm->nkv, d = dm->d;
+    size_t Ttot = (size_t)cu[B];
+    float scale = (float)(1.0 / sqrt((double)d));
+    int nt = nthr(nthreads);
+    uint16_t *qn = malloc(Ttot * nh * d * sizeof *qn);
+    uint16_t *ao = malloc(Ttot * nh * d * sizeof *ao);
+
+    orc_attn_prep_off(dm, qn_w, kn_w, B, cu, pos0, qg, k, v, kcache, vcache,
+                      cache_off, qn, kf, nthreads);
 
     /* (sequence, token, head) rows, each over its causal key range */
     size_t grp = nh / nkv;
@@ -461,15 +476,15 @@ void orc_attn_mixer(const OrcAttnDims *dm, const uint16_t *qn_w,
     {
         uint16_t *ab = malloc((maxk + 1) * sizeof *ab);
         float *eb = malloc((maxk + 1) * sizeof *eb);
-#pragma omp for schedule(static)
+#pragma omp for schedule(dynamic, 4)
         for (long u = 0; u < units; u++) {
             size_t t = (size_t)u / nh, h = (size_t)u % nh, hk = h / grp;
             size_t s = 0;
             while ((size_t)cu[s + 1] <= t) s++;
             size_t p = (size_t)pos0[s] + (t - (size_t)cu[s]);
             orc_attn_gqa_row(qn + (t * nh + h) * d,
-                             kcache + s * cache_stride + hk * d,
-                             vcache + s * cache_stride + hk * d,
+                             kcache + cache_off[s] + hk * d,
+                             vcache + cache_off[s] + hk * d,
                              ao + (t * nh + h) * d, nkv, d, scale, ab, eb, p);
         }
         free(ab);
@@ -487,6 +502,20 @@ void orc_attn_mixer(const OrcAttnDims *dm, const uint16_t *qn_w,
         free(gate);
     }
     if (qf) memcpy(qf, qn, Ttot * nh * d * sizeof *qn);
+    if (attno) memcpy(attno, ao, Ttot * nh * d * sizeof *ao);
     free(qn);
     free(ao);
+}
+
+void orc_attn_mixer(const OrcAttnDims *dm, const uint16_t *qn_w,
+                    const uint16_t *kn_w, size_t B, const int32_t *cu,
+                    const int32_t *pos0, const uint16_t *qg,
+                    const uint16_t *k, const uint16_t *v, uint16_t *kcache,
+                    uint16_t *vcache, size_t cache_stride, uint16_t *y,
+                    uint16_t *qf, uint16_t *kf, int nthreads) {
+    size_t *off = malloc((B + 1) * sizeof *off);
+    for (size_t s = 0; s < B; s++) off[s] = s * cache_stride;
+    orc_attn_mixer_off(dm, qn_w, kn_w, B, cu, pos0, qg, k, v, kcache, vcache,
+                       off, y, qf, kf, NULL, nthreads);
+    free(off);
 }

@@ -164,6 +164,27 @@ void orc_attn_mixer(const OrcAttnDims *dm, const uint16_t *qn_w,
                     uint16_t *vcache, size_t cache_stride, uint16_t *y,
                     uint16_t *qf, uint16_t *kf, int nthreads);
 
+/* As orc_attn_mixer with sequence s's caches at kcache/vcache +
+ * cache_off[s] (element offsets; each [>= pos0+new, nkv, d]); attno
+ * (optional) captures the attention output before the gate [Ttot,nh*d]. */
+void orc_attn_mixer_off(const OrcAttnDims *dm, const uint16_t *qn_w,
+                        const uint16_t *kn_w, size_t B, const int32_t *cu,
+                        const int32_t *pos0, const uint16_t *qg,
+                        const uint16_t *k, const uint16_t *v,
+                        uint16_t *kcache, uint16_t *vcache,
+                        const size_t *cache_off, uint16_t *y, uint16_t *qf,
+                        uint16_t *kf, uint16_t *attno, int nthreads);
+
+/* The mixer's first phase only (c/layer.h:300-316): per token q/k norm,
+ * rope and the cache append; qn [Ttot, nh*d] receives the roped q. */
+void orc_attn_prep_off(const OrcAttnDims *dm, const uint16_t *qn_w,
+                       const uint16_t *kn_w, size_t B, const int32_t *cu,
+                       const int32_t *pos0, const uint16_t *qg,
+                       const uint16_t *k, const uint16_t *v,
+                       uint16_t *kcache, uint16_t *vcache,
+                       const size_t *cache_off, uint16_t *qn, uint16_t *kf,
+                       int nthreads);
+
 /* Host-side RoPE table (c/attn.h:251-255 per pair): cs[2*R] bf16 codes,
  * cos then sin, for one position. */
 void orc_attn_rope_table(float pos, size_t rot, double theta, uint16_t *cs);

@@ -241,6 +241,45 @@ class Oracle(_Ops):
                                 u16(y), u16(qf), u16(kf), C.c_int(nthreads))
         return (y, qf, kf) if capture else y
 
+    def attn_mixer_off(self, dims, w, cu, pos0, qg, k, v, kcache, vcache,
+                       cache_off, nthreads=0, capture=False):
+        """As attn_mixer with sequence s's caches at element offset
+        cache_off[s] of the flat kcache/vcache arrays ([rows, nkv, d] from
+        there). capture adds (qf, kf, attno): roped q, roped k and the
+        attention output before the gate."""
+        nh, nkv, d, rot, theta = dims
+        B = len(cu) - 1
+        Ttot = int(cu[-1])
+        off = np.ascontiguousarray(cache_off, np.uint64)
+        y = np.empty((Ttot, nh * d), np.uint16)
+        qf = np.empty((Ttot, nh * d), np.uint16) if capture else None
+        kf = np.empty((Ttot, nkv * d), np.uint16) if capture else None
+        ao = np.empty((Ttot, nh * d), np.uint16) if capture else None
+        self.lib.orc_attn_mixer_off(
+            C.byref(_AttnDims(nh, nkv, d, rot, theta)), u16(w["qn_w"]),
+            u16(w["kn_w"]), _sz(B), i32(cu), i32(pos0), u16(qg), u16(k),
+            u16(v), u16(kcache), u16(vcache),
+            off.ctypes.data_as(C.POINTER(_sz)), u16(y), u16(qf), u16(kf),
+            u16(ao), C.c_int(nthreads))
+        return (y, qf, kf, ao) if capture else y
+
+    def attn_prep_off(self, dims, w, cu, pos0, qg, k, v, kcache, vcache,
+                      cache_off, nthreads=0):
+        """The mixer's norm / rope / append phase only; returns the roped
+        q [Ttot, nh*d] (the caches are appended in place)."""
+        nh, nkv, d, rot, theta = dims
+        B = len(cu) - 1
+        Ttot = int(cu[-1])
+        off = np.ascontiguousarray(cache_off, np.uint64)
+        qn = np.empty((Ttot, nh * d), np.uint16)
+        self.lib.orc_attn_prep_off(
+            C.byref(_AttnDims(nh, nkv, d, rot, theta)), u16(w["qn_w"]),
+            u16(w["kn_w"]), _sz(B), i32(cu), i32(pos0), u16(qg), u16(k),
+            u16(v), u16(kcache), u16(vcache),
+            off.ctypes.data_as(C.POINTER(_sz)), u16(qn), None,
+            C.c_int(nthreads))
+        return qn
+
 
 class Reference(_Ops):
     """The reference's own anchors built from /root/reference/c

@@ -151,6 +151,41 @@ def test_attn_mixer_bitwise(orc, ref, rng):
     assert np.array_equal(k1, k2) and np.array_equal(v1, v2)
 
 
+def test_attn_mixer_off_bitwise(orc, ref, rng):
+    """The offset-addressed oracle mixer (compact per-sequence caches, as
+    the full-size GPU tests use) against the reference ops wired as
+    c/layer.h over strided caches; its prep phase gives the captured roped
+    q, and outgate(attno, gate) gives y."""
+    dims = synth.ATTN_DIMS
+    nh, nkv, d = dims[:3]
+    w = synth.attn_weights(rng)
+    cu = np.array([0, 2, 6, 7], np.int32)
+    pos0 = np.array([9, 0, 30], np.int32)
+    tok = synth.attn_tokens(rng, 7)
+    maxs = 32
+    kc = synth.normal_bf16(rng, (3, maxs, nkv, d))
+    vc = synth.normal_bf16(rng, (3, maxs, nkv, d))
+    k2, v2 = kc.copy(), vc.copy()
+    y2 = ref.attn_mixer(dims, w, cu, pos0, tok["qg"], tok["k"], tok["v"], k2, v2, maxs * nkv * d)
+    rows = pos0 + np.diff(cu)
+    off = np.concatenate([[0], np.cumsum(rows * nkv * d)])
+    hk = np.concatenate([kc[s, :rows[s]].reshape(-1) for s in range(3)])
+    hv = np.concatenate([vc[s, :rows[s]].reshape(-1) for s in range(3)])
+    hk2, hv2 = hk.copy(), hv.copy()
+    y1, qf, kf, ao = orc.attn_mixer_off(dims, w, cu, pos0, tok["qg"], tok["k"], tok["v"], hk, hv,
+                                        off[:-1], nthreads=3, capture=True)
+    assert np.array_equal(y1, y2)
+    for s in range(3):
+        assert np.array_equal(hk[off[s]:off[s + 1]].reshape(-1, nkv, d), k2[s, :rows[s]])
+        assert np.array_equal(hv[off[s]:off[s + 1]].reshape(-1, nkv, d), v2[s, :rows[s]])
+    qn = orc.attn_prep_off(dims, w, cu, pos0, tok["qg"], tok["k"], tok["v"], hk2, hv2, off[:-1])
+    assert np.array_equal(qn, qf)
+    assert np.array_equal(hk2, hk) and np.array_equal(hv2, hv)
+    gate = np.ascontiguousarray(tok["qg"].reshape(7, nh, 2 * d)[:, :, d:]).reshape(-1)
+    assert np.array_equal(ref.attn_outgate(np.ascontiguousarray(ao.reshape(-1)), gate),
+                          y1.reshape(-1))
+
+
 @pytest.mark.parametrize("M,O,K", [(1, 300, 2048), (4, 129, 4096), (3, 17, 37)])
 def test_bf16_gemm_bitwise(orc, ref, rng, M, O, K):
     """The projection restatement against the reference's x86 hot path and
