@@ -38,6 +38,14 @@ EXPORTS = [
     "apus_hip_attn_cache_pack", "apus_hip_attn_cache_unpack", "apus_hip_attn_decode", "apus_hip_attn_prefill",
     "apus_hip_bf16_gemv", "apus_hip_bf16_gemm", "apus_hip_bf16_weights_release",
     "apus_hip_bf16_gemm_dev", "apus_hip_bf16_gemm_mfma_dev",
+    "apus_hip_gdn_decode_slots", "apus_hip_gdn_prefill_slots",
+    "apus_hip_attn_cache_pack_paged", "apus_hip_attn_cache_unpack_paged",
+    "apus_hip_attn_decode_paged", "apus_hip_attn_prefill_paged",
+    "apus_hip_kv_pool_create", "apus_hip_kv_pool_destroy", "apus_hip_kv_pool_cache",
+    "apus_hip_kv_seq_open", "apus_hip_kv_seq_reserve", "apus_hip_kv_seq_close",
+    "apus_hip_kv_pool_free_blocks",
+    "apus_hip_gdn_pool_create", "apus_hip_gdn_pool_destroy", "apus_hip_gdn_pool_state",
+    "apus_hip_gdn_slot_open", "apus_hip_gdn_slot_close",
 ]
 
 
@@ -52,6 +60,11 @@ class GdnLayer(C.Structure):
     _fields_ = [("hk", _sz), ("hv", _sz), ("dk", _sz), ("dv", _sz),
                 ("conv_w", _vp), ("A_log", _vp), ("dt_bias", _vp),
                 ("onorm_w", _vp)]
+
+
+class KvCache(C.Structure):
+    """ApusHipKvCache (include/apus_hip.h): a paged KV cache."""
+    _fields_ = [("k", _vp), ("v", _vp), ("block_table", _vp), ("max_blocks", _sz)]
 
 
 class AttnLayer(C.Structure):
@@ -86,6 +99,7 @@ def load(path=None):
         for name in EXPORTS:
             getattr(_lib, name).restype = C.c_int
         _lib.apus_hip_last_error.restype = _sz
+        _lib.apus_hip_kv_pool_free_blocks.restype = _sz
     return _lib
 
 
@@ -381,3 +395,116 @@ def bf16_gemm_dev(w, x, y, exact=True):
     M = x.shape[0]
     f = load().apus_hip_bf16_gemm_dev if exact else load().apus_hip_bf16_gemm_mfma_dev
     _chk(f(_dp(w), _dp(x), _dp(y), _sz(M), _sz(O), _sz(K)))
+
+
+# ---- paged KV cache and state pools
+def _i32arr(x):
+    x = np.ascontiguousarray(np.asarray(x, dtype=np.int32))
+    return x, x.ctypes.data_as(_i32p)
+
+
+def attn_decode_paged(layer, rows, cu, pos0, qg, k, v, kv, y):
+    """Decode on a paged cache: kv is a KvCache, rows the block-table row of
+    each sequence (host)."""
+    cu, cup, B = _cu_arr(cu)
+    rows, rp = _i32arr(rows)
+    pos0, pp = _i32arr(pos0)
+    _chk(load().apus_hip_attn_decode_paged(C.byref(layer), _sz(B), rp, cup, pp, _dp(qg), _dp(k),
+                                           _dp(v), C.byref(kv), _dp(y)))
+
+
+def attn_prefill_paged(layer, rows, cu, pos0, qg, k, v, kv, y):
+    cu, cup, B = _cu_arr(cu)
+    rows, rp = _i32arr(rows)
+    pos0, pp = _i32arr(pos0)
+    _chk(load().apus_hip_attn_prefill_paged(C.byref(layer), _sz(B), rp, cup, pp, _dp(qg), _dp(k),
+                                            _dp(v), C.byref(kv), _dp(y)))
+
+
+def attn_cache_pack_paged(kc_ref, vc_ref, ntok, nkv, d, kv, row):
+    _chk(load().apus_hip_attn_cache_pack_paged(_dp(kc_ref), _dp(vc_ref), _sz(ntok), _sz(nkv),
+                                               _sz(d), C.byref(kv), C.c_int32(row)))
+
+
+def attn_cache_unpack_paged(kv, row, ntok, nkv, d, kc_ref, vc_ref):
+    _chk(load().apus_hip_attn_cache_unpack_paged(C.byref(kv), C.c_int32(row), _sz(ntok), _sz(nkv),
+                                                 _sz(d), _dp(kc_ref), _dp(vc_ref)))
+
+
+def gdn_decode_slots(layer, slot_in, slot_out, cu, qkv, z, a, b, conv, S, y):
+    cu, cup, B = _cu_arr(cu)
+    si, sip = _i32arr(slot_in)
+    so, sop = _i32arr(slot_out)
+    _chk(load().apus_hip_gdn_decode_slots(C.byref(layer), _sz(B), sip, sop, cup, _dp(qkv), _dp(z),
+                                          _dp(a), _dp(b), C.c_void_p(conv), C.c_void_p(S),
+                                          _dp(y)))
+
+
+def gdn_prefill_slots(layer, slots, cu, qkv, z, a, b, conv, S, y):
+    cu, cup, B = _cu_arr(cu)
+    sl, slp = _i32arr(slots)
+    _chk(load().apus_hip_gdn_prefill_slots(C.byref(layer), _sz(B), slp, cup, _dp(qkv), _dp(z),
+                                           _dp(a), _dp(b), C.c_void_p(conv), C.c_void_p(S),
+                                           _dp(y)))
+
+
+class KvPool:
+    """apus_hip_kv_pool_*: a paged KV cache shared by nlayers layers."""
+
+    def __init__(self, nlayers, nkv, d, nblocks, max_rows, max_blocks):
+        self.h = C.c_void_p()
+        _chk(load().apus_hip_kv_pool_create(_sz(nlayers), _sz(nkv), _sz(d), _sz(nblocks),
+                                            _sz(max_rows), _sz(max_blocks), C.byref(self.h)))
+
+    def cache(self, layer):
+        kv = KvCache()
+        _chk(load().apus_hip_kv_pool_cache(self.h, _sz(layer), C.byref(kv)))
+        return kv
+
+    def open(self):
+        r = C.c_int32()
+        _chk(load().apus_hip_kv_seq_open(self.h, C.byref(r)))
+        return r.value
+
+    def reserve(self, row, ntok):
+        _chk(load().apus_hip_kv_seq_reserve(self.h, C.c_int32(row), _sz(ntok)))
+
+    def close(self, row):
+        _chk(load().apus_hip_kv_seq_close(self.h, C.c_int32(row)))
+
+    def free_blocks(self):
+        return load().apus_hip_kv_pool_free_blocks(self.h)
+
+    def destroy(self):
+        if self.h:
+            _chk(load().apus_hip_kv_pool_destroy(self.h))
+            self.h = C.c_void_p()
+
+
+class GdnPool:
+    """apus_hip_gdn_pool_*: per-sequence GDN states for nlayers layers."""
+
+    def __init__(self, nlayers, dims, nslots):
+        hk, hv, dk, dv = dims
+        self.h = C.c_void_p()
+        _chk(load().apus_hip_gdn_pool_create(_sz(nlayers), _sz(hk), _sz(hv), _sz(dk), _sz(dv),
+                                             _sz(nslots), C.byref(self.h)))
+
+    def state(self, layer):
+        """(conv, S) device base addresses of the layer's slot arrays."""
+        conv, S = C.c_void_p(), C.c_void_p()
+        _chk(load().apus_hip_gdn_pool_state(self.h, _sz(layer), C.byref(conv), C.byref(S)))
+        return conv.value, S.value
+
+    def open(self):
+        r = C.c_int32()
+        _chk(load().apus_hip_gdn_slot_open(self.h, C.byref(r)))
+        return r.value
+
+    def close(self, slot):
+        _chk(load().apus_hip_gdn_slot_close(self.h, C.c_int32(slot)))
+
+    def destroy(self):
+        if self.h:
+            _chk(load().apus_hip_gdn_pool_destroy(self.h))
+            self.h = C.c_void_p()

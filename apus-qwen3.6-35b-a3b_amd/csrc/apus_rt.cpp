@@ -7,6 +7,8 @@
 #include <stdlib.h>
 #include <string.h>
 
+#include <algorithm>
+#include <deque>
 #include <vector>
 
 #include "../../include/apus_hip.h"
@@ -25,7 +27,6 @@ struct Buf {
     size_t n = 0;
 };
 Buf g_scratch[kScratchSlots];
-Buf g_small[kScratchSlots];
 
 struct RopeTab {
     size_t rot = 0;
@@ -142,31 +143,98 @@ void *scratch(int slot, size_t bytes) {
     return b.p;
 }
 
-void *upload_small(int slot, const void *host, size_t bytes) {
-    Buf &b = g_small[slot];
-    if (b.n < bytes) {
-        if (b.p) {
-            if (hipStreamSynchronize(g_stream) != hipSuccess) return nullptr;
-            (void)hipFree(b.p);
-        }
-        size_t want = bytes < 4096 ? 4096 : bytes * 2;
-        if (hipMalloc(&b.p, want) != hipSuccess) {
-            b.p = nullptr;
-            b.n = 0;
-            set_error(kErrHip, "hipMalloc of %zu bytes failed", want);
+// ---- stream-ordered uploads through a pinned ring ------------------------
+// Host bytes are copied into a pinned staging ring and sent with an
+// asynchronous copy into the matching offset of a device ring, so the
+// caller's array is free on return and nothing waits for the GPU. A chunk
+// is reused only after an event recorded at a later upload -- i.e. after
+// every kernel enqueued before that upload, which includes the chunk's
+// consumers -- has completed.
+namespace {
+struct UploadRing {
+    char *host = nullptr, *dev = nullptr;
+    size_t cap = 0, head = 0;
+    struct Mark {
+        size_t begin, end;
+        hipEvent_t ev;
+    };
+    std::deque<Mark> live;
+};
+UploadRing g_ring;
+
+int ring_reserve(size_t cap) {
+    UploadRing &r = g_ring;
+    if (r.cap >= cap) return kOk;
+    if (r.dev) {
+        APUS_HIP_TRY(hipStreamSynchronize(g_stream));
+        for (auto &m : r.live)
+            if (m.ev) g_event_pool.push_back(m.ev);
+        r.live.clear();
+        (void)hipFree(r.dev);
+        (void)hipHostFree(r.host);
+        r.dev = r.host = nullptr;
+        r.cap = r.head = 0;
+    }
+    APUS_HIP_TRY(hipMalloc((void **)&r.dev, cap));
+    if (hipHostMalloc((void **)&r.host, cap, hipHostMallocDefault) != hipSuccess) {
+        (void)hipFree(r.dev);
+        r.dev = nullptr;
+        return set_error(kErrHip, "hipHostMalloc of %zu bytes failed", cap);
+    }
+    r.cap = cap;
+    r.head = 0;
+    return kOk;
+}
+}  // namespace
+
+// Stage `bytes` of host data in the ring and copy them to dst (nullptr:
+// the ring's own device chunk); returns the device address or nullptr.
+static void *ring_put(void *dst, const void *host, size_t bytes) {
+    UploadRing &r = g_ring;
+    const size_t n = std::max<size_t>((bytes + 255) / 256 * 256, 256);
+    if (ring_reserve(std::max<size_t>(n * 4, (size_t)4 << 20)) != kOk) return nullptr;
+    // the previous chunk's consumers are all enqueued by now
+    if (!r.live.empty() && !r.live.back().ev) {
+        hipEvent_t e = take_event();
+        if (!e || hipEventRecord(e, g_stream) != hipSuccess) {
+            set_error(kErrHip, "event record failed");
             return nullptr;
         }
-        b.n = want;
+        r.live.back().ev = e;
     }
-    // Synchronous with respect to the host buffer: the caller may reuse
-    // its array as soon as we return.
-    if (hipMemcpyAsync(b.p, host, bytes, hipMemcpyHostToDevice, g_stream) !=
-            hipSuccess ||
-        hipStreamSynchronize(g_stream) != hipSuccess) {
+    if (r.head + n > r.cap) r.head = 0;
+    const size_t b = r.head, en = b + n;
+    // wait for (and retire) every live chunk overlapping [b, en)
+    for (auto it = r.live.begin(); it != r.live.end();) {
+        if (it->begin < en && b < it->end) {
+            if (hipEventSynchronize(it->ev) != hipSuccess) {
+                set_error(kErrHip, "event wait failed");
+                return nullptr;
+            }
+            g_event_pool.push_back(it->ev);
+            it = r.live.erase(it);
+        } else {
+            ++it;
+        }
+    }
+    if (bytes) memcpy(r.host + b, host, bytes);
+    void *to = dst ? dst : r.dev + b;
+    if (bytes &&
+        hipMemcpyAsync(to, r.host + b, bytes, hipMemcpyHostToDevice, g_stream) != hipSuccess) {
         set_error(kErrHip, "upload of %zu bytes failed", bytes);
         return nullptr;
     }
-    return b.p;
+    r.live.push_back(UploadRing::Mark{b, en, nullptr});
+    r.head = en;
+    return to;
+}
+
+const void *upload_async(const void *host, size_t bytes) {
+    return ring_put(nullptr, host, bytes);
+}
+
+int copy_to_device_async(void *dst, const void *host, size_t bytes) {
+    return ring_put(dst, host, bytes) ? kOk : kErrHip;
 }
 
 const uint16_t *rope_table(size_t rot, double theta, size_t max_pos) {

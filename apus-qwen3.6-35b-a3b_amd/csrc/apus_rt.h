@@ -66,9 +66,14 @@ void *scratch(int slot, size_t bytes);
 // cover positions 0..max_pos-1.
 const uint16_t *rope_table(size_t rot, double theta, size_t max_pos);
 
-// Upload a small host array (e.g. token offsets) to device memory owned
-// by the library; stream-ordered, valid until the next call with `slot`.
-void *upload_small(int slot, const void *host, size_t bytes);
+// Stream-ordered upload of a host array through a pinned staging ring: the
+// returned device copy is valid for the work the caller enqueues before
+// its next upload; the host array may be reused on return; no wait for the
+// GPU (the ring recycles a chunk once work enqueued after it completed).
+const void *upload_async(const void *host, size_t bytes);
+// host -> device copy into caller memory, stream-ordered, without waiting
+// (staged through the ring).
+int copy_to_device_async(void *dst, const void *host, size_t bytes);
 
 // Opt-in per-kernel timing: when enabled (apus_hip_timing_enable), a pair
 // of events is recorded on the library stream around each wrapped launch;

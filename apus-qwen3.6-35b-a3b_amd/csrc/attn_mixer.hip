@@ -1,29 +1,28 @@
 // attn_mixer.hip -- batched, device-resident gated-GQA mixer for gfx950:
-// the op sequence of c/layer.h:300-322 (decode) for B sequences of 1..n
-// new tokens each (n > 1 is the MTP verify shape, c/mtp.h:36-75).
+// the op sequence of c/layer.h:300-322 (decode) for B sequences of 1..4
+// new tokens each (more than one is the MTP verify shape, c/mtp.h:36-75).
 //
-// Device KV-cache layout (tier 2). Sequence s of a batch owns
-//   K  kcache + s*nkv*max_seq*d   as [nkv][max_seq][d]
-//   V  vcache + s*nkv*d*max_seq   as [nkv][max_seq/32][d][32]
-// K rows keep d contiguous (the QK^T MFMA operand reads 8 consecutive d of
-// a key). V is stored transposed in 32-key blocks: the P.V MFMA operand
-// reads 8 consecutive keys of one d with one 16-byte load, and the 32 keys
-// x 256 d of a step are one contiguous 16 KiB block (long DRAM bursts; a
-// plain [d][max_seq] transpose made every 64-byte piece a separate DRAM
-// page). The reference's cache is [pos][nkv][d] for both
-// (c/layer.h:164-165); apus_hip_attn_cache_pack/unpack convert.
+// The KV cache is addressed in blocks of 32 positions through a block
+// table (attn_mixer.h): the flat layout of apus_hip_attn_decode is the
+// identity table, a paged cache (apus_hip_kv_pool_*) passes its own.
 //
-// Decode kernels (split-K over the context, one wavefront per (split, kv
-// head); the 8 q heads of a kv head and up to 4 new tokens form the MFMA
-// rows, so K and V are read once per group). The split sizes are chosen
-// per call so each kernel's grid is one full round of resident waves:
-//   k_attn_prep     q/k (1+w) RMSNorm, RoPE, cache append
-//   k_attn_scores   A = rnd(rnd(q.k)*scale) on MFMA 32x32x16 bf16 into a
-//                   bf16 score buffer, per-split (max, sum exp)
-//   k_attn_pv       P = rnd(exp(A-m)/s) with the global (m, s) -- the
-//                   reference's normalised bf16 probabilities
+// Decode kernels (split-K over the context; the 8 q heads of a kv head and
+// up to 4 new tokens form the MFMA rows, so K and V are read once per
+// group). The splits are balanced ("stream-K"): the (sequence, kv head)
+// pairs' key ranges, each padded to a multiple of 64, are laid end to end
+// and cut into equal runs of T keys, one per wavefront, so every wavefront
+// streams the same number of keys however ragged the contexts are; a run
+// that crosses a pair boundary is processed as two segments. Segment
+// (pair p, wavefront w) keeps its partial results in slot p + w (unique:
+// consecutive segments raise p or w or both).
+//   k_attn_prep     q/k (1+w) RMSNorm, RoPE, K append
+//   k_attn_vappend  V append
+//   k_attn_scores   A = rnd(rnd(q.k)*scale) on MFMA 16x16x32 bf16 into a
+//                   bf16 score buffer, per-segment (max, sum exp)
+//   k_attn_pv       P = rnd(exp(A-m)/s) with the pair's global (m, s) --
+//                   the reference's normalised bf16 probabilities
 //                   (c/attn.h:354-360) -- times V on MFMA, fp32 partials
-//   k_attn_combine  sum of the partials, rnd, sigmoid output gate
+//   k_attn_combine  sum of the partials in key order, rnd, sigmoid gate
 // Scores and the P.V sum accumulate in a different order than the
 // reference's sequential loops (a tolerance class); everything else
 // follows the reference op for op.
@@ -74,12 +73,12 @@ __device__ __forceinline__ int seq_of(const int32_t *off, int n, int x) {
 }
 
 // Metadata views: by value (AttnSeqs) or, for large batches, a device
-// array cu[B+1] | pos0[B] | soff[B+1] | soff2[B+1].
+// array cu[B+1] | pos0[B] | ccap[B+1] | hd[B].
 struct Meta {
-    const int32_t *cu, *pos0, *soff, *soff2;
+    const int32_t *cu, *pos0, *ccap, *hd;
 };
 __device__ __forceinline__ Meta meta_of(const AttnSeqs &sq, const int32_t *dmeta) {
-    if (!dmeta) return Meta{sq.cu, sq.pos0, sq.soff, sq.soff2};
+    if (!dmeta) return Meta{sq.cu, sq.pos0, sq.ccap, sq.hd};
     const int n = sq.n;
     return Meta{dmeta, dmeta + n + 1, dmeta + 2 * n + 1, dmeta + 3 * n + 2};
 }
@@ -99,9 +98,8 @@ constexpr int PRS = D + 8;               // LDS row pitch (bf16): rows on distin
 __global__ __launch_bounds__(256) void k_attn_prep(
     AttnSeqs sq, const int32_t *__restrict__ dmeta, const uint16_t *__restrict__ qg,
     const uint16_t *__restrict__ kin, const uint16_t *__restrict__ qn_w,
-    const uint16_t *__restrict__ kn_w, const uint16_t *__restrict__ rope,
-    uint16_t *__restrict__ kcache, size_t max_seq, uint16_t *__restrict__ qn, int nh,
-    int nkv, int nrows, int rpb) {
+    const uint16_t *__restrict__ kn_w, const uint16_t *__restrict__ rope, KvRef kv,
+    uint16_t *__restrict__ qn, int nh, int nkv, int nrows, int rpb) {
     const Meta mt = meta_of(sq, dmeta);
     const int32_t *cu = mt.cu, *pos0 = mt.pos0;
     const int nslot = nh + nkv;
@@ -207,21 +205,21 @@ __global__ __launch_bounds__(256) void k_attn_prep(
             for (int i = 0; i < 8; i++) out[i] = f2bf(n[i]);
         }
         uint16_t *dst = isq ? qn + ((size_t)tt * nh + slot) * D
-                            : kcache + (((size_t)rseq[r] * nkv + (slot - nh)) * max_seq +
-                                        rpos[r]) * D;
+                            : kv.k + ((kv_block_id(kv, mt.hd[rseq[r]], rpos[r] / KVB) * nkv +
+                                       (slot - nh)) * KVB + rpos[r] % KVB) * D;
         *reinterpret_cast<u16x8 *>(dst + p * 8) = out;
     }
 }
 
 // k_attn_vappend: the new tokens' v rows (raw, c/layer.h:315-316) into the
-// transposed V cache [seq][kv head][position / 32][d][32]. One block per
+// transposed V blocks [kv head][d][32]. One block per
 // (sequence, kv head, 32-position block the new tokens touch): the rows are
 // staged in LDS, then thread d writes its 32 keys -- one 64-byte run, so
 // the block is written as contiguous 16 KiB (a block only partly covered
 // by new tokens keeps its other keys: element stores for those).
 __global__ __launch_bounds__(256) void k_attn_vappend(
     AttnSeqs sq, const int32_t *__restrict__ dmeta, const uint16_t *__restrict__ vin,
-    uint16_t *__restrict__ vcache, size_t max_seq, int nkv, int maxnb) {
+    KvRef kv, int nkv, int maxnb) {
     const Meta mt = meta_of(sq, dmeta);
     const int s = blockIdx.x / (nkv * maxnb), rem = blockIdx.x % (nkv * maxnb);
     const int kvh = rem / maxnb, bi = rem % maxnb;
@@ -247,7 +245,7 @@ __global__ __launch_bounds__(256) void k_attn_vappend(
         if (k >= klo && k < khi) *reinterpret_cast<u16x8 *>(vt + k * PRS + pc * 8) = v4[j];
     }
     __syncthreads();
-    uint16_t *blk = vcache + (((size_t)s * nkv + kvh) * (max_seq / 32) + b) * D * 32;
+    uint16_t *blk = kv.v + (kv_block_id(kv, mt.hd[s], b) * nkv + kvh) * D * KVB;
     const int d = tid;
     if (klo == 0 && khi == 32) {
 #pragma unroll
@@ -264,33 +262,53 @@ __global__ __launch_bounds__(256) void k_attn_vappend(
 
 // Row n of the 32 MFMA rows is (token n / GRP, q head n % GRP of the kv
 // head); rows past the sequence's tokens are padding.
-struct SplitCtx {
-    int s, kvh, sp, gsplit, tq, pos0, ctx, k0, k1;
+//
+// A segment: keys [k0, k1) of the pair (sequence s, kv head kvh), its
+// partial results in slot p + w (p = s*nkv + kvh, w the wavefront's run).
+struct Seg {
+    int s, kvh, slot, tq, pos0, k0, k1, cap;
+    size_t abase;                  // the pair's scores: As + abase, [kRows][cap]
 };
 
-__device__ __forceinline__ SplitCtx split_ctx_of(const int32_t *cu, const int32_t *pos0,
-                                                 const int32_t *soff, int nseq, int nkv, int ks,
-                                                 int item) {
-    SplitCtx c;
-    c.kvh = item % nkv;
-    c.gsplit = item / nkv;
-    c.s = seq_of(soff, nseq, c.gsplit);
-    c.sp = c.gsplit - soff[c.s];
-    c.tq = cu[c.s + 1] - cu[c.s];
-    c.pos0 = pos0[c.s];
-    c.ctx = c.pos0 + c.tq;
-    c.k0 = c.sp * ks;
-    c.k1 = min(c.ctx, c.k0 + ks);
-    return c;
+// The segment of run w (keys x1 > x of the padded pair space) starting at
+// x; *xn is where the next one starts. False for a segment that holds only
+// padding keys (nothing to compute or store).
+__device__ __forceinline__ bool seg_at(const Meta &mt, int n, int nkv, int w, int x, int x1,
+                                       Seg &g, int *xn) {
+    const int s = seq_of(mt.ccap, n, x / nkv);
+    const int base = nkv * mt.ccap[s], cap = mt.ccap[s + 1] - mt.ccap[s];
+    const int local = x - base, kvh = local / cap, k0 = local % cap;
+    const int xe = min(x1, base + (kvh + 1) * cap);
+    g.s = s;
+    g.kvh = kvh;
+    g.slot = s * nkv + kvh + w;
+    g.tq = mt.cu[s + 1] - mt.cu[s];
+    g.pos0 = mt.pos0[s];
+    g.k0 = k0;
+    g.k1 = min(k0 + (xe - x), g.pos0 + g.tq);
+    g.cap = __builtin_amdgcn_readfirstlane(cap);
+    g.abase = (size_t)kRows * (size_t)__builtin_amdgcn_readfirstlane(base + kvh * cap);
+    *xn = xe;
+    return g.k0 < g.k1;
+}
+
+// The runs of T keys a pair's real keys fall in: w0 .. w1 (inclusive).
+__device__ __forceinline__ void pair_runs(const Meta &mt, int nkv, int s, int kvh, int T,
+                                          int *w0, int *w1) {
+    const int cap = mt.ccap[s + 1] - mt.ccap[s];
+    const int ps = nkv * mt.ccap[s] + kvh * cap;
+    const int ctx = mt.pos0[s] + mt.cu[s + 1] - mt.cu[s];
+    *w0 = ps / T;
+    *w1 = (ps + ctx - 1) / T;
 }
 
 
 // ---- k_attn_scores: W streaming wavefronts + 1 writer per workgroup ------
-// Each streaming wavefront owns one (split, kv head) item. MFMA 16x16x32
-// bf16 (A: lane l holds row l%16, k (l/16)*8..+8; B: col l%16, same k; D:
-// rows (l/16)*4+i, col l%16). S^T[key][row] = K Q^T: the four lanes of a key
-// row read 64 contiguous bytes of it per instruction. NRB row blocks of 16
-// (NRB = 2 when a sequence has more than 2 tokens).
+// Each streaming wavefront owns one run of T1 keys (one or more segments).
+// MFMA 16x16x32 bf16 (A: lane l holds row l%16, k (l/16)*8..+8; B: col
+// l%16, same k; D: rows (l/16)*4+i, col l%16). S^T[key][row] = K Q^T: the
+// four lanes of a key row read 64 contiguous bytes of it per instruction.
+// NRB row blocks of 16 (NRB = 2 when a sequence has more than 2 tokens).
 //
 // The streaming wavefronts issue no global stores. The vector memory
 // counter is shared by loads and stores and retires in order, and a store
@@ -298,15 +316,24 @@ __device__ __forceinline__ SplitCtx split_ctx_of(const int32_t *cu, const int32_
 // any later wait on a K load would stall behind it (measured: a 3% store mix
 // costs ~20% of the stream, whether or not the stores reach HBM). Instead
 // each 64-key group's scores go into a per-wavefront LDS ring of kScRing
-// slots, a "ready" count in LDS publishes them, and the workgroup's last
-// wavefront copies published slots to global memory and returns them with
-// a "done" count. A wavefront's DS instructions execute in issue order, so a count written after its data is never seen before that data.
+// slots with a header saying where they belong, a "ready" count in LDS
+// publishes them, and the workgroup's last wavefront copies published
+// slots to global memory and returns them with a "done" count. A
+// wavefront's DS instructions execute in issue order, so a count written
+// after its data is never seen before that data.
 constexpr int kScRing = 4;
 template <int NRB> struct ScoresShape {
     static constexpr int W = NRB == 1 ? 11 : 7;   // streaming wavefronts (+1 writer)
     static constexpr int SLOT = 2 * NRB * 64;     // uint4 per slot: 16*NRB rows x 64 keys
 };
-template <int NRB> constexpr int scores_items_per_block() { return ScoresShape<NRB>::W; }
+template <int NRB> constexpr int scores_waves_per_block() { return ScoresShape<NRB>::W; }
+
+// where a ring slot's scores go: rows [kRows][cap] at As + abase, keys
+// kq0 .. min(kq0 + 64, k1), rows of tokens < tq
+struct RingHdr {
+    uint32_t alo, ahi;
+    int cap, kq0, k1, tq;
+};
 
 // relaxed workgroup-scope atomics: no cached values, and (unlike volatile)
 // no wait on the vector memory counter
@@ -319,37 +346,29 @@ __device__ __forceinline__ void lds_count_store(int *p, int v) {
 }
 __device__ __forceinline__ void compiler_fence() { asm volatile("" ::: "memory"); }
 
-// the K-cache score rows of item (split, kv head): [row][cap], absolute keys
-struct ScItem {
-    SplitCtx c;
-    uint16_t *Ab;
-    size_t cap;
-    int ngroups;
-};
-__device__ __forceinline__ ScItem scores_item(const Meta &mt, const AttnSeqs &sq, int nkv, int item,
-                                              int nitems, uint16_t *As) {
-    ScItem it;
-    if (item >= nitems) {
-        it.ngroups = 0;
-        return it;
-    }
-    it.c = split_ctx_of(mt.cu, mt.pos0, mt.soff, sq.n, nkv, sq.ks1, item);
-    it.cap = (size_t)(mt.soff[it.c.s + 1] - mt.soff[it.c.s]) * sq.ks1;
-    it.Ab = As + (size_t)mt.soff[it.c.s] * sq.ks1 * nkv * kRows + (size_t)it.c.kvh * kRows * it.cap;
-    it.ngroups = (it.c.k1 - it.c.k0 + 63) / 64;
-    return it;
+// a wave-uniform pointer held in scalar registers
+__device__ __forceinline__ const uint16_t *uniform_ptr(const uint16_t *p) {
+    const uint64_t a = (uint64_t)p;
+    return (const uint16_t *)(((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)(a >> 32))
+                               << 32) |
+                              (uint32_t)__builtin_amdgcn_readfirstlane((int)a));
 }
 
-// The streaming wavefront of k_attn_scores for an item whose sequence has
-// NR row blocks of queries (its ring slots, SLOT uint4 each, and counters
-// given).
+// K rows of cache block b of segment g (kv head g.kvh)
+__device__ __forceinline__ const uint16_t *kblock(const KvRef &kv, const Meta &mt, const Seg &g,
+                                                  int nkv, int b) {
+    return uniform_ptr(kv.k + (kv_block_id_u(kv, mt.hd[g.s], b) * nkv + g.kvh) * KVB * D);
+}
+
+// The streaming wavefront's part for one segment whose sequence has NR
+// row blocks of queries; grp counts the wavefront's ring groups across its
+// segments.
 template <int NR, int SLOT>
-__device__ __forceinline__ void scores_stream(const Meta &mt, const SplitCtx &c,
-                                              const uint16_t *__restrict__ qn,
-                                              const uint16_t *__restrict__ kcache, size_t max_seq,
-                                              int nh, int nkv, float scale,
-                                              float2 *__restrict__ stats, uint4 *ringw,
-                                              int *readyw, int *donew) {
+__device__ __forceinline__ void scores_seg(const Meta &mt, const Seg &c,
+                                           const uint16_t *__restrict__ qn, const KvRef &kv,
+                                           int nh, int nkv, float scale,
+                                           float2 *__restrict__ stats, uint4 *ringw,
+                                           RingHdr *hdrw, int *readyw, int *donew, int &grp) {
     const int32_t *cu = mt.cu;
     const int l = threadIdx.x & 63, c16 = l & 15, q4 = l >> 4;
 
@@ -369,7 +388,6 @@ __device__ __forceinline__ void scores_stream(const Meta &mt, const SplitCtx &c,
             qf[rb][ds] = vrow[rb] ? v : bf16x8{};
         }
     }
-    const uint16_t *Kb = kcache + ((size_t)c.s * nkv + c.kvh) * max_seq * D;
     float mrun[NR], lrun[NR];
 #pragma unroll
     for (int rb = 0; rb < NR; rb++) { mrun[rb] = -INFINITY; lrun[rb] = 0.0f; }
@@ -378,12 +396,16 @@ __device__ __forceinline__ void scores_stream(const Meta &mt, const SplitCtx &c,
     // row m of block j is key g0 + (m/4)*16 + 4*j + m%4, so the lane whose
     // output rows are m = 4*q4 .. 4*q4+3 ends a group holding the 16
     // consecutive scores g0 + 16*q4 .. +15 of its row: 32 bytes per lane and
-    // 128 contiguous bytes per row. K rows past the split end are clamped to
-    // a valid row, never zeroed (touching a loaded value on issue would wait
-    // for it); their scores are never stored or counted.
-    auto load_k = [&](int g0, int j, bf16x8 (&f)[D / 32]) {
+    // 128 contiguous bytes per row. K rows past the segment end are clamped
+    // to its last row, never zeroed (touching a loaded value on issue would
+    // wait for it); their scores are never stored or counted. A group's 64
+    // keys lie in two cache blocks (g0 is a multiple of 64); their bases are
+    // looked up one group ahead (scalar loads).
+    const int blast = (c.k1 - 1) >> 5;
+    auto load_k = [&](int g0, int j, int bA, const uint16_t *pA, const uint16_t *pB,
+                      bf16x8 (&f)[D / 32]) {
         const int key = min(g0 + (c16 >> 2) * 16 + 4 * j + (c16 & 3), c.k1 - 1);
-        const uint16_t *kr = Kb + (size_t)key * D + q4 * 8;
+        const uint16_t *kr = ((key >> 5) == bA ? pA : pB) + (size_t)(key & 31) * D + q4 * 8;
 #pragma unroll
         for (int ds = 0; ds < D / 32; ds++) f[ds] = ld_bf16x8(kr + ds * 32);
         // keep the loads here: the scheduler would otherwise sink them to
@@ -398,11 +420,16 @@ __device__ __forceinline__ void scores_stream(const Meta &mt, const SplitCtx &c,
     kmask = __builtin_amdgcn_readfirstlane(min(kmask, c.pos0 + 1));
     // Double buffering: while one 16-key block is multiplied the next one's
     // 8 loads are in flight (the loads are unconditional: the prefetch past
-    // the split's end re-reads its last row), so the stream never drains
+    // the segment's end re-reads its last row), so the stream never drains
     // between groups.
+    int bA = min(c.k0 >> 5, blast);
+    const uint16_t *pA = kblock(kv, mt, c, nkv, bA), *pB = kblock(kv, mt, c, nkv, min(bA + 1, blast));
     bf16x8 kA[D / 32], kB[D / 32];
-    load_k(c.k0, 0, kA);
-    for (int g0 = c.k0, grp = 0; g0 < c.k1; g0 += 64, grp++) {
+    load_k(c.k0, 0, bA, pA, pB, kA);
+    for (int g0 = c.k0; g0 < c.k1; g0 += 64, grp++) {
+        // the next group's blocks (clamped to the segment's last one)
+        const int nA = min((g0 + 64) >> 5, blast);
+        const uint16_t *qA = kblock(kv, mt, c, nkv, nA), *qB = kblock(kv, mt, c, nkv, min(nA + 1, blast));
         // the writer must have drained this group's ring slot (read early;
         // it is normally long done)
         const int dn = lds_count_load(donew);
@@ -424,26 +451,32 @@ __device__ __forceinline__ void scores_stream(const Meta &mt, const SplitCtx &c,
                 for (int e = 0; e < 4; e += 2)
                     sc[rb][2 * j + e / 2] = pack2(acc[rb][e] * scale, acc[rb][e + 1] * scale);
         };
-        load_k(g0, 1, kB);
+        load_k(g0, 1, bA, pA, pB, kB);
         mma(0, kA);
-        load_k(g0, 2, kA);
+        load_k(g0, 2, bA, pA, pB, kA);
         mma(1, kB);
-        load_k(g0, 3, kB);
+        load_k(g0, 3, bA, pA, pB, kB);
         mma(2, kA);
-        load_k(g0 + 64, 0, kA);
+        load_k(g0 + 64, 0, nA, qA, qB, kA);
         mma(3, kB);
+        bA = nA;
+        pA = qA;
+        pB = qB;
 
         // publish the group's scores to the writer through the ring
         if (grp >= kScRing && dn <= grp - kScRing)
             while (lds_count_load(donew) <= grp - kScRing) __builtin_amdgcn_s_sleep(1);
         compiler_fence();
-        uint4 *sl = ringw + (grp % kScRing) * SLOT;
+        const int rs = grp % kScRing;
+        uint4 *sl = ringw + rs * SLOT;
 #pragma unroll
         for (int rb = 0; rb < NR; rb++) {          // row rb*16 + c16, keys 16*q4..+15
             uint4 *r = sl + (rb * 16 + c16) * 8 + 2 * q4;
             r[0] = make_uint4(sc[rb][0], sc[rb][1], sc[rb][2], sc[rb][3]);
             r[1] = make_uint4(sc[rb][4], sc[rb][5], sc[rb][6], sc[rb][7]);
         }
+        if (l == 0)
+            hdrw[rs] = RingHdr{(uint32_t)c.abase, (uint32_t)(c.abase >> 32), c.cap, g0, c.k1, c.tq};
         compiler_fence();
         if (l == 0) lds_count_store(readyw, grp + 1);
 
@@ -457,7 +490,7 @@ __device__ __forceinline__ void scores_stream(const Meta &mt, const SplitCtx &c,
                 a[2 * e] = __uint_as_float(sc[rb][e] << 16);
                 a[2 * e + 1] = __uint_as_float(sc[rb][e] & 0xffff0000u);
             }
-            if (g0 + 64 > kmask) {             // (wave-uniform) keys past a query or the split
+            if (g0 + 64 > kmask) {             // (wave-uniform) keys past a query or the segment
 #pragma unroll
                 for (int e = 0; e < 16; e++) {
                     const int kk = kq + e;
@@ -489,18 +522,18 @@ __device__ __forceinline__ void scores_stream(const Meta &mt, const SplitCtx &c,
             ls = mm > -INFINITY ? ls * exp_fast(m - mm) + lo * exp_fast(mo - mm) : 0.0f;
             m = mm;
         }
-        if (q4 == 0 && vrow[rb])
-            stats[((size_t)c.gsplit * nkv + c.kvh) * kRows + rb * 16 + c16] = make_float2(m, ls);
+        if (q4 == 0 && vrow[rb]) stats[(size_t)c.slot * kRows + rb * 16 + c16] = make_float2(m, ls);
     }
 }
 
 template <int NRB>
 __global__ __launch_bounds__(64 * (ScoresShape<NRB>::W + 1)) void k_attn_scores(
-    AttnSeqs sq, const int32_t *__restrict__ dmeta, const uint16_t *__restrict__ qn,
-    const uint16_t *__restrict__ kcache, size_t max_seq, int nh, int nkv, float scale,
-    uint16_t *__restrict__ As, float2 *__restrict__ stats, int nitems) {
+    AttnSeqs sq, const int32_t *__restrict__ dmeta, const uint16_t *__restrict__ qn, KvRef kv,
+    int nh, int nkv, float scale, uint16_t *__restrict__ As, float2 *__restrict__ stats,
+    int nruns) {
     constexpr int W = ScoresShape<NRB>::W, SLOT = ScoresShape<NRB>::SLOT;
     __shared__ uint4 ring[W][kScRing][SLOT];
+    __shared__ RingHdr hdr[W][kScRing];
     __shared__ int ready[W], done[W];
     const int wave = threadIdx.x >> 6, l = threadIdx.x & 63;
     if (threadIdx.x < W) {
@@ -509,29 +542,26 @@ __global__ __launch_bounds__(64 * (ScoresShape<NRB>::W + 1)) void k_attn_scores(
     }
     __syncthreads();
     const Meta mt = meta_of(sq, dmeta);
+    const int n = sq.n, T = sq.T1, total = nkv * mt.ccap[n];
 
     if (wave == W) {
-        // ---- writer: copy published slots of the W items to global memory.
-        // Item parameters are computed once, before any store is issued: a
-        // load after a store would wait for the store's acknowledgement.
-        int nxt[W], ng[W], k0[W], k1[W], tq[W];
-        uint16_t *Ab[W];
-        size_t cap[W];
+        // ---- writer: copy published slots of the W runs to global memory.
+        // The group counts are computed before any store is issued: a load
+        // after a store would wait for the store's acknowledgement.
+        int nxt[W], ng[W];
 #pragma unroll
         for (int w = 0; w < W; w++) {
-            const ScItem it = scores_item(mt, sq, nkv, blockIdx.x * W + w, nitems, As);
             nxt[w] = 0;
-            ng[w] = it.ngroups;
-            if (ng[w] > 0) {
-                k0[w] = it.c.k0;
-                k1[w] = it.c.k1;
-                tq[w] = it.c.tq;
-                Ab[w] = it.Ab;
-                cap[w] = it.cap;
-            } else {
-                k0[w] = k1[w] = tq[w] = 0;
-                Ab[w] = nullptr;
-                cap[w] = 0;
+            ng[w] = 0;
+            const int run = blockIdx.x * W + w;
+            if (run >= nruns) continue;
+            int x = run * T;
+            const int x1 = min(x + T, total);
+            while (x < x1) {
+                Seg g;
+                int xn;
+                if (seg_at(mt, n, nkv, run, x, x1, g, &xn)) ng[w] += (g.k1 - g.k0 + 63) / 64;
+                x = xn;
             }
         }
         for (;;) {
@@ -547,12 +577,14 @@ __global__ __launch_bounds__(64 * (ScoresShape<NRB>::W + 1)) void k_attn_scores(
                 // of row 8*i + l/8, so a row's 128 bytes are whole lines
                 for (int g = nxt[w]; g < rd; g++) {
                     const uint4 *sl = ring[w][g % kScRing];
-                    const int kq = k0[w] + 64 * g + 8 * (l & 7);
+                    const RingHdr h = hdr[w][g % kScRing];
+                    uint16_t *Ab = As + (((size_t)h.ahi << 32) | h.alo);
+                    const int kq = h.kq0 + 8 * (l & 7);
 #pragma unroll
                     for (int i = 0; i < 2 * NRB; i++) {
                         const int row = 8 * i + (l >> 3);
-                        if (row / GRP < tq[w] && kq < k1[w])
-                            *reinterpret_cast<uint4 *>(Ab[w] + (size_t)row * cap[w] + kq) = sl[i * 64 + l];
+                        if (row / GRP < h.tq && kq < h.k1)
+                            *reinterpret_cast<uint4 *>(Ab + (size_t)row * h.cap + kq) = sl[i * 64 + l];
                     }
                 }
                 compiler_fence();
@@ -566,41 +598,49 @@ __global__ __launch_bounds__(64 * (ScoresShape<NRB>::W + 1)) void k_attn_scores(
         return;
     }
 
-    // ---- streaming wavefront
-    const int item = blockIdx.x * W + wave;
-    if (item >= nitems) return;
-    const SplitCtx c = split_ctx_of(mt.cu, mt.pos0, mt.soff, sq.n, nkv, sq.ks1, item);
-    // a sequence with at most 2 tokens fills one row block
-    if (NRB == 2 && c.tq <= 2)
-        scores_stream<1, SLOT>(mt, c, qn, kcache, max_seq, nh, nkv, scale, stats, ring[wave][0],
-                               &ready[wave], &done[wave]);
-    else
-        scores_stream<NRB, SLOT>(mt, c, qn, kcache, max_seq, nh, nkv, scale, stats, ring[wave][0],
-                                 &ready[wave], &done[wave]);
+    // ---- streaming wavefront: its run's segments in order
+    const int run = blockIdx.x * W + wave;
+    if (run >= nruns) return;
+    int x = run * T, grp = 0;
+    const int x1 = min(x + T, total);
+    while (x < x1) {
+        Seg g;
+        int xn;
+        if (seg_at(mt, n, nkv, run, x, x1, g, &xn)) {
+            // a sequence with at most 2 tokens fills one row block
+            if (NRB == 2 && g.tq <= 2)
+                scores_seg<1, SLOT>(mt, g, qn, kv, nh, nkv, scale, stats, ring[wave][0],
+                                    hdr[wave], &ready[wave], &done[wave], grp);
+            else
+                scores_seg<NRB, SLOT>(mt, g, qn, kv, nh, nkv, scale, stats, ring[wave][0],
+                                      hdr[wave], &ready[wave], &done[wave], grp);
+        }
+        x = xn;
+    }
 }
 
-// ---- k_attn_pv: one wavefront per (split, kv head) ---------------------
+// ---- k_attn_pv: one run of T2 keys per item ------------------------------
 // O^T[d][row] = sum_key V^T[d][key] P^T[key][row] on MFMA 16x16x32: the
-// transposed V cache is the A operand (4 lanes read 64 contiguous bytes of
-// one d row), the probabilities the B operand.
-// DH wavefronts share an item, each owning D/DH of the d rows (DH = 2 for two
-// row blocks: 2 x 64 accumulators and the next step's V operands would not
-// fit in registers at two wavefronts per SIMD otherwise).
-// P.V over one item for a sequence with NR row blocks of queries; this
+// transposed V blocks are the A operand (4 lanes read 64 contiguous bytes
+// of one d row), the probabilities the B operand. DH = 2 wavefronts share a
+// run, each owning half of the d rows: the accumulators and the next
+// step's V operands then fit three wavefronts per SIMD for one row block
+// and two for two.
+// P.V over one segment for a sequence with NR row blocks of queries; this
 // wavefront owns d blocks hb*NB .. +NB
 template <int NR, int NB>
-__device__ __forceinline__ void pv_item(const Meta &mt, const SplitCtx &c, int hb,
-                                        const AttnSeqs &sq, const uint16_t *__restrict__ vcache,
-                                        size_t max_seq, int nkv, const uint16_t *__restrict__ As,
-                                        const float2 *__restrict__ stats, float *__restrict__ Op) {
-    const int32_t *soff = mt.soff;
+__device__ __forceinline__ void pv_seg(const Meta &mt, const Seg &c, int hb, const AttnSeqs &sq,
+                                       const KvRef &kv, int nkv, const uint16_t *__restrict__ As,
+                                       const float2 *__restrict__ stats, float *__restrict__ Op) {
     const int l = threadIdx.x, c16 = l & 15, q4 = l >> 4;
 
-    // global (max, sum) of each row over every split of this (seq, kv head)
+    // global (max, sum) of each row over the pair's score segments
+    int w0, w1;
+    pair_runs(mt, nkv, c.s, c.kvh, sq.T1, &w0, &w1);
+    const int p = c.s * nkv + c.kvh;
     float m[NR], rsum[NR];
     bool vrow[NR];
     int lim[NR];
-    const int ns = soff[c.s + 1] - soff[c.s];
 #pragma unroll
     for (int rb = 0; rb < NR; rb++) {
         const int n = rb * 16 + c16, t = n / GRP;
@@ -608,12 +648,22 @@ __device__ __forceinline__ void pv_item(const Meta &mt, const SplitCtx &c, int h
         lim[rb] = c.pos0 + t;
         float mm = -INFINITY, ss = 0.0f;
         if (vrow[rb]) {
-            for (int p = 0; p < ns; p++) {
-                const float2 st = stats[((size_t)(soff[c.s] + p) * nkv + c.kvh) * kRows + n];
-                if (st.x == -INFINITY) continue;
-                const float mn = fmaxf(mm, st.x);
-                ss = ss * exp_fast(mm - mn) + st.y * exp_fast(st.x - mn);
-                mm = mn;
+            // eight segments' statistics in flight at a time (a long pair
+            // has dozens; one dependent load each would serialise their
+            // latencies)
+            for (int w = w0; w <= w1; w += 8) {
+                float2 st[8];
+#pragma unroll
+                for (int i = 0; i < 8; i++)
+                    st[i] = w + i <= w1 ? stats[(size_t)(p + w + i) * kRows + n]
+                                        : make_float2(-INFINITY, 0.0f);
+#pragma unroll
+                for (int i = 0; i < 8; i++) {
+                    if (st[i].x == -INFINITY) continue;
+                    const float mn = fmaxf(mm, st[i].x);
+                    ss = ss * exp_fast(mm - mn) + st[i].y * exp_fast(st[i].x - mn);
+                    mm = mn;
+                }
             }
         }
         // P = rnd(e^{A - m} / s) formed as rnd(exp2(A log2(e) - K)), K =
@@ -623,9 +673,7 @@ __device__ __forceinline__ void pv_item(const Meta &mt, const SplitCtx &c, int h
         m[rb] = mm;
         rsum[rb] = mm * kL2E + __builtin_amdgcn_logf(ss);
     }
-    const uint16_t *Vb = vcache + ((size_t)c.s * nkv + c.kvh) * D * max_seq;
-    const size_t cap = (size_t)(soff[c.s + 1] - soff[c.s]) * sq.ks1;
-    const uint16_t *Ab = As + (size_t)soff[c.s] * sq.ks1 * nkv * kRows + (size_t)c.kvh * kRows * cap;
+    const uint16_t *Ab = As + c.abase;
     f32x4 acc[NR][NB];
 #pragma unroll
     for (int rb = 0; rb < NR; rb++)
@@ -634,25 +682,32 @@ __device__ __forceinline__ void pv_item(const Meta &mt, const SplitCtx &c, int h
 
     // V^T and score fragments of the next 32-key step are loaded while the
     // current step is multiplied. Loads never touch their value on issue
-    // (that would wait for them): addresses are clamped into the cache's
-    // valid 8-key groups and the out-of-range keys are masked at use.
+    // (that would wait for them): addresses are clamped into the segment's
+    // valid 8-key groups and the out-of-range keys are masked at use. A
+    // step's 32 keys are one cache block (its base a scalar lookup).
     const int kclamp = ((c.k1 - 1) / 8) * 8;   // last aligned group holding a valid key
     const int kmask = min(c.k1, c.pos0 + 1);   // the first key masked for some row
+    const int hd = mt.hd[c.s];
+    // V block of the step at kb (clamped lanes stay in kb's block: kclamp
+    // lies in [kb, kb + 24] whenever kb + 8*q4 passes it)
+    auto vblock = [&](int kb) {
+        return uniform_ptr(kv.v + (kv_block_id_u(kv, hd, min(kb, c.k1 - 1) >> 5) * nkv + c.kvh) *
+                                      D * KVB);
+    };
     u16x8 vf[NB], af[NR];
-    auto load_step = [&](int kb, u16x8 *fv, u16x8 *fa) {
+    auto load_step = [&](int kb, const uint16_t *Vb, u16x8 *fv, u16x8 *fa) {
         const int kq = min(kb + q4 * 8, kclamp);
 #pragma unroll
         for (int b = 0; b < NB; b++)
-            fv[b] = *reinterpret_cast<const u16x8 *>(
-                Vb + ((size_t)(kq / 32) * D + (hb * NB + b) * 16 + c16) * 32 + kq % 32);
+            fv[b] = *reinterpret_cast<const u16x8 *>(Vb + ((hb * NB + b) * 16 + c16) * KVB + (kq & 31));
 #pragma unroll
         for (int rb = 0; rb < NR; rb++)
-            fa[rb] = *reinterpret_cast<const u16x8 *>(Ab + (size_t)(rb * 16 + c16) * cap + kq);
+            fa[rb] = *reinterpret_cast<const u16x8 *>(Ab + (size_t)(rb * 16 + c16) * c.cap + kq);
     };
-    load_step(c.k0, vf, af);
+    load_step(c.k0, vblock(c.k0), vf, af);
     for (int kb = c.k0; kb < c.k1; kb += 32) {
         u16x8 vn[NB], an[NR];
-        if (kb + 32 < c.k1) load_step(kb + 32, vn, an);
+        if (kb + 32 < c.k1) load_step(kb + 32, vblock(kb + 32), vn, an);
         const int kq = kb + q4 * 8;            // this lane's 8 keys
         bf16x8 pf[NR];
 #pragma unroll
@@ -662,7 +717,7 @@ __device__ __forceinline__ void pv_item(const Meta &mt, const SplitCtx &c, int h
 #pragma unroll
             for (int e = 0; e < 8; e++)
                 e8[e] = __builtin_amdgcn_exp2f(fmaf(bf2f(af[rb][e]), kL2E, -rsum[rb]));
-            if (kb + 32 > kmask) {             // (wave-uniform) keys past a query or the split
+            if (kb + 32 > kmask) {             // (wave-uniform) keys past a query or the segment
 #pragma unroll
                 for (int e = 0; e < 8; e++)
                     if (!(kq + e <= lim[rb] && kq + e < c.k1)) e8[e] = 0.0f;
@@ -689,7 +744,7 @@ __device__ __forceinline__ void pv_item(const Meta &mt, const SplitCtx &c, int h
 #pragma unroll
     for (int rb = 0; rb < NR; rb++) {
         if (!vrow[rb]) continue;
-        float *orow = Op + (((size_t)c.gsplit * nkv + c.kvh) * kRows + rb * 16 + c16) * D;
+        float *orow = Op + ((size_t)c.slot * kRows + rb * 16 + c16) * D;
 #pragma unroll
         for (int b = 0; b < NB; b++)
             *reinterpret_cast<float4 *>(orow + (hb * NB + b) * 16 + q4 * 4) =
@@ -699,18 +754,26 @@ __device__ __forceinline__ void pv_item(const Meta &mt, const SplitCtx &c, int h
 
 template <int NRB, int DH>
 __global__ __launch_bounds__(64) void k_attn_pv(
-    AttnSeqs sq, const int32_t *__restrict__ dmeta, const uint16_t *__restrict__ vcache,
-    size_t max_seq, int nkv, const uint16_t *__restrict__ As,
-    const float2 *__restrict__ stats, float *__restrict__ Op) {
+    AttnSeqs sq, const int32_t *__restrict__ dmeta, KvRef kv, int nkv,
+    const uint16_t *__restrict__ As, const float2 *__restrict__ stats, float *__restrict__ Op) {
     const Meta mt = meta_of(sq, dmeta);
     constexpr int NB = D / 16 / DH;            // 16-row d blocks of this wavefront
     const int hb = DH == 1 ? 0 : (int)(blockIdx.x % DH);
-    const SplitCtx c = split_ctx_of(mt.cu, mt.pos0, mt.soff2, sq.n, nkv, sq.ks2, blockIdx.x / DH);
-    // a sequence with at most 2 tokens fills one row block
-    if (NRB == 2 && c.tq <= 2)
-        pv_item<1, NB>(mt, c, hb, sq, vcache, max_seq, nkv, As, stats, Op);
-    else
-        pv_item<NRB, NB>(mt, c, hb, sq, vcache, max_seq, nkv, As, stats, Op);
+    const int run = (int)(blockIdx.x / DH), n = sq.n, T = sq.T2;
+    int x = run * T;
+    const int x1 = min(x + T, nkv * mt.ccap[n]);
+    while (x < x1) {
+        Seg g;
+        int xn;
+        if (seg_at(mt, n, nkv, run, x, x1, g, &xn)) {
+            // a sequence with at most 2 tokens fills one row block
+            if (NRB == 2 && g.tq <= 2)
+                pv_seg<1, NB>(mt, g, hb, sq, kv, nkv, As, stats, Op);
+            else
+                pv_seg<NRB, NB>(mt, g, hb, sq, kv, nkv, As, stats, Op);
+        }
+        x = xn;
+    }
 }
 
 // ---- k_attn_combine: one block per (token, q head), d threads ----------
@@ -719,40 +782,51 @@ __global__ __launch_bounds__(D) void k_attn_combine(
     const uint16_t *__restrict__ qg, int nh, int nkv, uint16_t *__restrict__ y,
     const uint16_t *__restrict__ sig_bf) {
     const Meta mt = meta_of(sq, dmeta);
-    const int32_t *cu = mt.cu, *soff = mt.soff2;
+    const int32_t *cu = mt.cu;
     const int tt = blockIdx.x / nh, h = blockIdx.x % nh;
     const int s = seq_of(cu, sq.n, tt), t = tt - cu[s];
     const int kvh = h / GRP, n = t * GRP + h % GRP;
     const int dd = threadIdx.x;
+    int w0, w1;
+    pair_runs(mt, nkv, s, kvh, sq.T2, &w0, &w1);
+    const int p = s * nkv + kvh;
     float sum = 0.0f;
-    for (int p = soff[s]; p < soff[s + 1]; p++)
-        sum += Op[(((size_t)p * nkv + kvh) * kRows + n) * D + dd];
+    for (int w = w0; w <= w1; w += 8) {          // eight partials in flight, summed in order
+        float v[8];
+#pragma unroll
+        for (int i = 0; i < 8; i++)
+            v[i] = w + i <= w1 ? Op[((size_t)(p + w + i) * kRows + n) * D + dd] : 0.0f;
+#pragma unroll
+        for (int i = 0; i < 8; i++)
+            if (w + i <= w1) sum += v[i];
+    }
     const float o = rndf(sum);
     const float gt = bf2f(sig_bf[qg[((size_t)tt * nh + h) * 2 * D + D + dd]]);  // rnd(sigmoid)
     y[((size_t)tt * nh + h) * D + dd] = f2bf(o * gt);
 }
 
-// ---- cache layout conversion (one sequence) ----------------------------
+// ---- cache layout conversion (one sequence: block-table row h) ---------
+// reference layout [ntok][nkv][D] <-> the cache blocks of row h
 __global__ void k_cache_pack(const uint16_t *__restrict__ kref, const uint16_t *__restrict__ vref,
-                             size_t ntok, int nkv, uint16_t *__restrict__ kc,
-                             uint16_t *__restrict__ vc, size_t max_seq) {
+                             size_t ntok, int nkv, KvRef kv, int h) {
     size_t e = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (e >= ntok * nkv * D) return;
     size_t p = e / (nkv * D), r = e % (nkv * D);
     int hk = (int)(r / D), dd = (int)(r % D);
-    kc[((size_t)hk * max_seq + p) * D + dd] = kref[e];
-    vc[(size_t)hk * D * max_seq + ((p / 32) * D + dd) * 32 + p % 32] = vref[e];
+    const size_t id = kv_block_id(kv, h, (int)(p / KVB)) * nkv + hk;
+    kv.k[(id * KVB + p % KVB) * D + dd] = kref[e];
+    kv.v[(id * D + dd) * KVB + p % KVB] = vref[e];
 }
 
-__global__ void k_cache_unpack(const uint16_t *__restrict__ kc, const uint16_t *__restrict__ vc,
-                               size_t ntok, int nkv, size_t max_seq,
+__global__ void k_cache_unpack(KvRef kv, int h, size_t ntok, int nkv,
                                uint16_t *__restrict__ kref, uint16_t *__restrict__ vref) {
     size_t e = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (e >= ntok * nkv * D) return;
     size_t p = e / (nkv * D), r = e % (nkv * D);
     int hk = (int)(r / D), dd = (int)(r % D);
-    kref[e] = kc[((size_t)hk * max_seq + p) * D + dd];
-    vref[e] = vc[(size_t)hk * D * max_seq + ((p / 32) * D + dd) * 32 + p % 32];
+    const size_t id = kv_block_id(kv, h, (int)(p / KVB)) * nkv + hk;
+    kref[e] = kv.k[(id * KVB + p % KVB) * D + dd];
+    vref[e] = kv.v[(id * D + dd) * KVB + p % KVB];
 }
 
 }  // namespace
@@ -769,81 +843,68 @@ int attn_check_layer(const ApusHipAttnLayer *L) {
     return kOk;
 }
 
-// Fill the metadata (by value, or uploaded when B is large) and choose the
-// split sizes: each kernel's grid should be one round of resident waves
-// (scores: one workgroup of W streaming wavefronts per CU; P.V: occupancy x
-// 4 SIMDs x CUs) so no straggler round is left; ks1 (scores) is a multiple
-// of 64 keys, ks2 (P.V) of 32.
-static int attn_meta(size_t B, const int32_t *cu, const int32_t *pos0, size_t max_seq,
-                     size_t nkv, AttnSeqs *sq, const int32_t **dmeta, size_t *nsplit1,
-                     size_t *nsplit2, size_t *max_tok) {
+KvRef kv_flat(uint16_t *kcache, uint16_t *vcache, size_t max_seq) {
+    return KvRef{kcache, vcache, nullptr, (int32_t)(max_seq / KVB)};
+}
+
+static size_t ceil64(size_t x) { return (x + 63) / 64 * 64; }
+
+int attn_meta(size_t B, const int32_t *cu, const int32_t *pos0, const int32_t *rows,
+              size_t bstride, size_t nkv, int max_new, AttnSeqs *sq, const int32_t **dmeta,
+              size_t *max_tok) {
     if (!cu || !pos0 || cu[0] != 0) return set_error(kErrArgument, "bad offsets");
-    if (max_seq % 32 != 0) return set_error(kErrArgument, "max_seq must be a multiple of 32");
-    size_t mt = 0, keys = 0;
+    std::vector<int32_t> ccap(B + 1, 0);
+    size_t mt = 0;
     for (size_t s = 0; s < B; s++) {
         const int32_t tq = cu[s + 1] - cu[s];
-        if (tq < 1 || tq > kRows / GRP)
+        if (tq < 0) return set_error(kErrArgument, "token offsets must ascend");
+        if (max_new > 0 && (tq < 1 || tq > max_new))
             return set_error(kErrUnsupported, "decode takes 1..%d new tokens per sequence (got %d)",
-                             kRows / GRP, tq);
-        if (pos0[s] < 0 || (size_t)pos0[s] + (size_t)tq > max_seq)
+                             max_new, tq);
+        if (pos0[s] < 0 || (size_t)pos0[s] + (size_t)tq > bstride * KVB)
             return set_error(kErrArgument, "sequence %zu overflows the cache (%d+%d > %zu)", s,
-                             pos0[s], tq, max_seq);
-        keys += (size_t)pos0[s] + (size_t)tq;
+                             pos0[s], tq, bstride * KVB);
+        if (rows && rows[s] < 0) return set_error(kErrArgument, "negative block-table row");
+        const size_t cap = ceil64((size_t)pos0[s] + (size_t)tq);
+        if (nkv * ((size_t)ccap[s] + cap) > (size_t)0x7ff00000)
+            return set_error(kErrUnsupported, "too many cached keys in one call");
+        ccap[s + 1] = ccap[s] + (int32_t)cap;
         if ((size_t)tq > mt) mt = (size_t)tq;
     }
-    const size_t slots = 4 * (size_t)cu_count();
-    // scores: one workgroup per CU, W streaming wavefronts each
-    const size_t w1 = mt <= 2 ? scores_items_per_block<1>() : scores_items_per_block<2>(), occ2 = 2;
-    // the smallest split (a multiple of gran, 256..16384 keys) whose items
-    // -- each sequence's last split partial -- fit in one round of waves
-    auto pick = [&](size_t waves, size_t gran) {
-        size_t k = (keys * nkv + waves - 1) / waves;
-        k = std::min<size_t>(std::max<size_t>((k + gran - 1) / gran * gran, 256), 16384);
-        for (; k < 16384; k += gran) {
-            size_t items = 0;
-            for (size_t s = 0; s < B; s++)
-                items += ((size_t)pos0[s] + (size_t)(cu[s + 1] - cu[s]) + k - 1) / k * nkv;
-            if (items <= waves) break;
-        }
-        return k;
-    };
-    // P.V: two wavefronts per item (halves of d) when a sequence has more
-    // than 2 tokens
-    const size_t ks1 = pick(w1 * cu_count(), 64), ks2 = pick(occ2 * slots / (mt <= 2 ? 1 : 2), 32);
-    std::vector<int32_t> soff(B + 1, 0), soff2(B + 1, 0);
-    for (size_t s = 0; s < B; s++) {
-        const size_t ctx = (size_t)pos0[s] + (size_t)(cu[s + 1] - cu[s]);
-        soff[s + 1] = soff[s] + (int32_t)((ctx + ks1 - 1) / ks1);
-        soff2[s + 1] = soff2[s] + (int32_t)((ctx + ks2 - 1) / ks2);
-    }
-    *nsplit1 = (size_t)soff[B];
-    *nsplit2 = (size_t)soff2[B];
     *max_tok = mt;
     sq->n = (int32_t)B;
-    sq->ks1 = (int32_t)ks1;
-    sq->ks2 = (int32_t)ks2;
+    sq->T1 = sq->T2 = 64;
     *dmeta = nullptr;
     if (B <= (size_t)kAttnInlineSeqs) {
         memcpy(sq->cu, cu, (B + 1) * 4);
         memcpy(sq->pos0, pos0, B * 4);
-        memcpy(sq->soff, soff.data(), (B + 1) * 4);
-        memcpy(sq->soff2, soff2.data(), (B + 1) * 4);
+        memcpy(sq->ccap, ccap.data(), (B + 1) * 4);
+        for (size_t s = 0; s < B; s++) sq->hd[s] = rows ? rows[s] : (int32_t)s;
     } else {
-        std::vector<int32_t> m(4 * B + 3);
+        std::vector<int32_t> m(4 * B + 2);
         memcpy(m.data(), cu, (B + 1) * 4);
         memcpy(m.data() + B + 1, pos0, B * 4);
-        memcpy(m.data() + 2 * B + 1, soff.data(), (B + 1) * 4);
-        memcpy(m.data() + 3 * B + 2, soff2.data(), (B + 1) * 4);
-        *dmeta = (const int32_t *)upload_small(kScratchMeta2, m.data(), m.size() * 4);
+        memcpy(m.data() + 2 * B + 1, ccap.data(), (B + 1) * 4);
+        for (size_t s = 0; s < B; s++) m[3 * B + 2 + s] = rows ? rows[s] : (int32_t)s;
+        *dmeta = (const int32_t *)upload_async(m.data(), m.size() * 4);
         if (!*dmeta) return kErrHip;
     }
+    // decode: balanced runs of T keys per wavefront, each kernel's grid one
+    // round of resident wavefronts (scores: W streaming wavefronts per CU;
+    // P.V: two wavefronts per run, each owning half of d, at three
+    // wavefronts per SIMD for one row block, two for two)
+    const size_t total = nkv * (size_t)ccap[B];
+    const size_t w1 = (mt <= 2 ? scores_waves_per_block<1>() : scores_waves_per_block<2>()) *
+                      (size_t)cu_count();
+    const size_t w2 = (mt <= 2 ? 3 : 2) * 4 * (size_t)cu_count() / 2;
+    sq->T1 = (int32_t)std::max<size_t>(64, ceil64((total + w1 - 1) / w1));
+    sq->T2 = (int32_t)std::max<size_t>(64, ceil64((total + w2 - 1) / w2));
     return kOk;
 }
 
 int attn_prep(const ApusHipAttnLayer *L, const AttnSeqs &sq, const int32_t *dmeta,
               size_t Ttot, size_t max_pos, int maxnb, const uint16_t *qg, const uint16_t *k,
-              const uint16_t *v, uint16_t *kcache, uint16_t *vcache, size_t max_seq,
-              uint16_t *qn) {
+              const uint16_t *v, const KvRef &kv, uint16_t *qn) {
     const uint16_t *rope = rope_table(L->rot, L->theta, max_pos);
     if (!rope) return kErrHip;
     const size_t nrows = Ttot * (L->nh + L->nkv);
@@ -851,23 +912,90 @@ int attn_prep(const ApusHipAttnLayer *L, const AttnSeqs &sq, const int32_t *dmet
     const int rpb = nrows < (size_t)8 * PRB * cu_count() ? 8 : PRB;
     APUS_TIMED("k_attn_prep",
                k_attn_prep<<<cdiv(nrows, rpb), 256, 0, stream()>>>(
-        sq, dmeta, qg, k, L->qn_w, L->kn_w, rope, kcache, max_seq, qn, (int)L->nh,
-        (int)L->nkv, (int)nrows, rpb));
+        sq, dmeta, qg, k, L->qn_w, L->kn_w, rope, kv, qn, (int)L->nh, (int)L->nkv, (int)nrows,
+        rpb));
     if (int r = launch_check("k_attn_prep")) return r;
     APUS_TIMED("k_attn_vappend",
                k_attn_vappend<<<(unsigned)(sq.n * L->nkv * maxnb), 256, 0, stream()>>>(
-        sq, dmeta, v, vcache, max_seq, (int)L->nkv, maxnb));
+        sq, dmeta, v, kv, (int)L->nkv, maxnb));
     return launch_check("k_attn_vappend");
 }
 
-// the most 32-position V blocks one sequence's new tokens touch
+// the most 32-position cache blocks one sequence's new tokens touch
 int attn_max_vblocks(size_t B, const int32_t *cu, const int32_t *pos0) {
     int m = 1;
     for (size_t s = 0; s < B; s++) {
         const int ns = cu[s + 1] - cu[s];
-        if (ns > 0) m = std::max(m, (pos0[s] + ns - 1) / 32 - pos0[s] / 32 + 1);
+        if (ns > 0) m = std::max(m, (pos0[s] + ns - 1) / KVB - pos0[s] / KVB + 1);
     }
     return m;
+}
+
+int attn_decode_kv(const ApusHipAttnLayer *L, size_t B, const int32_t *cu, const int32_t *pos0,
+                   const int32_t *rows, const uint16_t *qg, const uint16_t *k,
+                   const uint16_t *v, const KvRef &kv, uint16_t *y) {
+    if (int r = attn_check_layer(L)) return r;
+    if (B == 0) return kOk;
+    AttnSeqs sq;
+    const int32_t *dmeta = nullptr;
+    size_t mt = 0;
+    if (int r = attn_meta(B, cu, pos0, rows, (size_t)kv.bstride, L->nkv, kRows / GRP, &sq, &dmeta,
+                          &mt))
+        return r;
+    const size_t Ttot = (size_t)cu[B], nkv = L->nkv;
+    size_t max_pos = 0, keys = 0;
+    for (size_t s = 0; s < B; s++) {
+        max_pos = std::max(max_pos, (size_t)pos0[s] + (size_t)(cu[s + 1] - cu[s]));
+        keys += ceil64((size_t)pos0[s] + (size_t)(cu[s + 1] - cu[s]));
+    }
+    const size_t total = nkv * keys;
+    const size_t nruns1 = (total + sq.T1 - 1) / sq.T1, nruns2 = (total + sq.T2 - 1) / sq.T2;
+    uint16_t *qn = (uint16_t *)scratch(kScratchAttnQ, Ttot * L->nh * D * 2);
+    uint16_t *As = (uint16_t *)scratch(kScratchAttnA, total * kRows * 2);
+    float2 *st = (float2 *)scratch(kScratchAttnStat, (nruns1 + B * nkv) * kRows * 8);
+    float *Op = (float *)scratch(kScratchAttnPart, (nruns2 + B * nkv) * kRows * D * 4);
+    if (!qn || !As || !st || !Op) return kErrHip;
+    if (int r = attn_prep(L, sq, dmeta, Ttot, max_pos, attn_max_vblocks(B, cu, pos0), qg, k, v,
+                          kv, qn))
+        return r;
+    const float scale = (float)(1.0 / sqrt((double)L->d));
+    const ActTables *tabs = act_tables();
+    if (!tabs) return kErrHip;
+    // one 16-row block covers up to 2 new tokens per sequence (8 heads each)
+    if (mt <= 2) {
+        APUS_TIMED("k_attn_scores",
+                   k_attn_scores<1><<<cdiv(nruns1, scores_waves_per_block<1>()),
+                                      64 * (scores_waves_per_block<1>() + 1), 0, stream()>>>(
+                       sq, dmeta, qn, kv, (int)L->nh, (int)nkv, scale, As, st, (int)nruns1));
+        APUS_LAUNCHED("k_attn_scores");
+        APUS_TIMED("k_attn_pv",
+                   k_attn_pv<1, 2><<<(unsigned)(2 * nruns2), 64, 0, stream()>>>(
+                       sq, dmeta, kv, (int)nkv, As, st, Op));
+        APUS_LAUNCHED("k_attn_pv");
+    } else {
+        APUS_TIMED("k_attn_scores",
+                   k_attn_scores<2><<<cdiv(nruns1, scores_waves_per_block<2>()),
+                                      64 * (scores_waves_per_block<2>() + 1), 0, stream()>>>(
+                       sq, dmeta, qn, kv, (int)L->nh, (int)nkv, scale, As, st, (int)nruns1));
+        APUS_LAUNCHED("k_attn_scores");
+        APUS_TIMED("k_attn_pv",
+                   k_attn_pv<2, 2><<<(unsigned)(2 * nruns2), 64, 0, stream()>>>(
+                       sq, dmeta, kv, (int)nkv, As, st, Op));
+        APUS_LAUNCHED("k_attn_pv");
+    }
+    APUS_TIMED("k_attn_combine",
+               k_attn_combine<<<(unsigned)(Ttot * L->nh), D, 0, stream()>>>(
+                   sq, dmeta, Op, qg, (int)L->nh, (int)nkv, y, tabs->sig_bf));
+    APUS_LAUNCHED("k_attn_combine");
+    return kOk;
+}
+
+static int kv_of(const ApusHipKvCache *c, KvRef *r) {
+    if (!c || !c->k || !c->v || !c->block_table || c->max_blocks == 0 ||
+        c->max_blocks > 0x7fffffff)
+        return set_error(kErrArgument, "bad paged KV cache descriptor");
+    *r = KvRef{c->k, c->v, c->block_table, (int32_t)c->max_blocks};
+    return kOk;
 }
 
 }  // namespace apus
@@ -879,54 +1007,35 @@ int apus_hip_attn_decode(const ApusHipAttnLayer *L, size_t B, const int32_t *cu,
                          const uint16_t *v, uint16_t *kcache, uint16_t *vcache,
                          size_t max_seq, uint16_t *y) {
     APUS_READY();
-    if (int r = attn_check_layer(L)) return r;
-    if (B == 0) return kOk;
-    AttnSeqs sq;
-    const int32_t *dmeta = nullptr;
-    size_t ns1 = 0, ns2 = 0, mt = 0;
-    if (int r = attn_meta(B, cu, pos0, max_seq, L->nkv, &sq, &dmeta, &ns1, &ns2, &mt)) return r;
-    const size_t Ttot = (size_t)cu[B];
-    size_t max_pos = 0;
-    for (size_t s = 0; s < B; s++)
-        max_pos = std::max(max_pos, (size_t)pos0[s] + (size_t)(cu[s + 1] - cu[s]));
-    uint16_t *qn = (uint16_t *)scratch(kScratchAttnQ, Ttot * L->nh * D * 2);
-    uint16_t *As = (uint16_t *)scratch(kScratchAttnA, ns1 * (size_t)sq.ks1 * L->nkv * kRows * 2);
-    float2 *st = (float2 *)scratch(kScratchAttnStat, ns1 * L->nkv * kRows * 8);
-    float *Op = (float *)scratch(kScratchAttnPart, ns2 * L->nkv * kRows * D * 4);
-    if (!qn || !As || !st || !Op) return kErrHip;
-    if (int r = attn_prep(L, sq, dmeta, Ttot, max_pos, attn_max_vblocks(B, cu, pos0), qg, k, v,
-                          kcache, vcache, max_seq, qn))
-        return r;
-    const float scale = (float)(1.0 / sqrt((double)L->d));
-    const ActTables *tabs = act_tables();
-    if (!tabs) return kErrHip;
-    const unsigned grid = (unsigned)(ns1 * L->nkv), grid2 = (unsigned)(ns2 * L->nkv);
-    // one 16-row block covers up to 2 new tokens per sequence (8 heads each)
-    if (mt <= 2) {
-        APUS_TIMED("k_attn_scores",
-                   k_attn_scores<1><<<cdiv(grid, scores_items_per_block<1>()),
-                                      64 * (scores_items_per_block<1>() + 1), 0, stream()>>>(
-                       sq, dmeta, qn, kcache, max_seq, (int)L->nh, (int)L->nkv, scale, As, st,
-                       (int)grid));
-        APUS_LAUNCHED("k_attn_scores");
-        APUS_TIMED("k_attn_pv",
-                   k_attn_pv<1, 1><<<grid2, 64, 0, stream()>>>(sq, dmeta, vcache, max_seq, (int)L->nkv, As, st, Op));
-        APUS_LAUNCHED("k_attn_pv");
+    if (max_seq % KVB != 0) return set_error(kErrArgument, "max_seq must be a multiple of %d", KVB);
+    return attn_decode_kv(L, B, cu, pos0, nullptr, qg, k, v, kv_flat(kcache, vcache, max_seq), y);
+}
+
+int apus_hip_attn_decode_paged(const ApusHipAttnLayer *L, size_t B, const int32_t *rows,
+                               const int32_t *cu, const int32_t *pos0, const uint16_t *qg,
+                               const uint16_t *k, const uint16_t *v, const ApusHipKvCache *kv,
+                               uint16_t *y) {
+    APUS_READY();
+    KvRef r;
+    if (int e = kv_of(kv, &r)) return e;
+    if (!rows) return set_error(kErrArgument, "NULL block-table rows");
+    return attn_decode_kv(L, B, cu, pos0, rows, qg, k, v, r, y);
+}
+
+static int cache_xfer(bool pack, const uint16_t *kc_ref, const uint16_t *vc_ref, uint16_t *ko,
+                      uint16_t *vo, size_t ntok, size_t nkv, size_t d, const KvRef &kv, int h) {
+    if (d != (size_t)D) return set_error(kErrUnsupported, "cache pack supports d=256");
+    if (ntok > (size_t)kv.bstride * KVB) return set_error(kErrArgument, "ntok exceeds the cache");
+    if (ntok == 0) return kOk;
+    if (pack) {
+        k_cache_pack<<<cdiv(ntok * nkv * D, 256), 256, 0, stream()>>>(kc_ref, vc_ref, ntok,
+                                                                       (int)nkv, kv, h);
+        APUS_LAUNCHED("k_cache_pack");
     } else {
-        APUS_TIMED("k_attn_scores",
-                   k_attn_scores<2><<<cdiv(grid, scores_items_per_block<2>()),
-                                      64 * (scores_items_per_block<2>() + 1), 0, stream()>>>(
-                       sq, dmeta, qn, kcache, max_seq, (int)L->nh, (int)L->nkv, scale, As, st,
-                       (int)grid));
-        APUS_LAUNCHED("k_attn_scores");
-        APUS_TIMED("k_attn_pv",
-                   k_attn_pv<2, 2><<<2 * grid2, 64, 0, stream()>>>(sq, dmeta, vcache, max_seq, (int)L->nkv, As, st, Op));
-        APUS_LAUNCHED("k_attn_pv");
+        k_cache_unpack<<<cdiv(ntok * nkv * D, 256), 256, 0, stream()>>>(kv, h, ntok, (int)nkv,
+                                                                         ko, vo);
+        APUS_LAUNCHED("k_cache_unpack");
     }
-    APUS_TIMED("k_attn_combine",
-               k_attn_combine<<<(unsigned)(Ttot * L->nh), D, 0, stream()>>>(sq, dmeta, Op, qg, (int)L->nh,
-                                                                  (int)L->nkv, y, tabs->sig_bf));
-    APUS_LAUNCHED("k_attn_combine");
     return kOk;
 }
 
@@ -934,26 +1043,37 @@ int apus_hip_attn_cache_pack(const uint16_t *kc_ref, const uint16_t *vc_ref, siz
                              size_t nkv, size_t d, uint16_t *kcache, uint16_t *vcache,
                              size_t max_seq) {
     APUS_READY();
-    if (d != (size_t)D) return set_error(kErrUnsupported, "cache pack supports d=256");
-    if (ntok > max_seq || max_seq % 32) return set_error(kErrArgument, "bad ntok/max_seq");
-    if (ntok == 0) return kOk;
-    k_cache_pack<<<cdiv(ntok * nkv * D, 256), 256, 0, stream()>>>(kc_ref, vc_ref, ntok, (int)nkv,
-                                                                   kcache, vcache, max_seq);
-    APUS_LAUNCHED("k_cache_pack");
-    return kOk;
+    if (max_seq % KVB) return set_error(kErrArgument, "max_seq must be a multiple of %d", KVB);
+    return cache_xfer(true, kc_ref, vc_ref, nullptr, nullptr, ntok, nkv, d,
+                      kv_flat(kcache, vcache, max_seq), 0);
 }
 
 int apus_hip_attn_cache_unpack(const uint16_t *kcache, const uint16_t *vcache, size_t ntok,
                                size_t nkv, size_t d, size_t max_seq, uint16_t *kc_ref,
                                uint16_t *vc_ref) {
     APUS_READY();
-    if (d != (size_t)D) return set_error(kErrUnsupported, "cache unpack supports d=256");
-    if (ntok > max_seq || max_seq % 32) return set_error(kErrArgument, "bad ntok/max_seq");
-    if (ntok == 0) return kOk;
-    k_cache_unpack<<<cdiv(ntok * nkv * D, 256), 256, 0, stream()>>>(kcache, vcache, ntok, (int)nkv,
-                                                                     max_seq, kc_ref, vc_ref);
-    APUS_LAUNCHED("k_cache_unpack");
-    return kOk;
+    if (max_seq % KVB) return set_error(kErrArgument, "max_seq must be a multiple of %d", KVB);
+    return cache_xfer(false, nullptr, nullptr, kc_ref, vc_ref, ntok, nkv, d,
+                      kv_flat(const_cast<uint16_t *>(kcache), const_cast<uint16_t *>(vcache),
+                              max_seq), 0);
+}
+
+int apus_hip_attn_cache_pack_paged(const uint16_t *kc_ref, const uint16_t *vc_ref, size_t ntok,
+                                   size_t nkv, size_t d, const ApusHipKvCache *kv, int32_t row) {
+    APUS_READY();
+    KvRef r;
+    if (int e = kv_of(kv, &r)) return e;
+    if (row < 0) return set_error(kErrArgument, "negative block-table row");
+    return cache_xfer(true, kc_ref, vc_ref, nullptr, nullptr, ntok, nkv, d, r, row);
+}
+
+int apus_hip_attn_cache_unpack_paged(const ApusHipKvCache *kv, int32_t row, size_t ntok,
+                                     size_t nkv, size_t d, uint16_t *kc_ref, uint16_t *vc_ref) {
+    APUS_READY();
+    KvRef r;
+    if (int e = kv_of(kv, &r)) return e;
+    if (row < 0) return set_error(kErrArgument, "negative block-table row");
+    return cache_xfer(false, nullptr, nullptr, kc_ref, vc_ref, ntok, nkv, d, r, row);
 }
 
 }  // extern "C"

@@ -70,7 +70,6 @@ constexpr int NW = 8;                  // wavefronts per workgroup, two per SIMD
 constexpr int TQ = 4 * NW;             // query tokens per workgroup
 constexpr int KT = 64;                 // keys per tile
 constexpr int VB = 32;                 // keys per V^T block of the cache
-constexpr int TILE_BYTES = KT * D * 2; // one K or V tile in the cache
 constexpr int KROW = D * 2 + 16;       // K row pitch in LDS (one 16-byte pad)
 constexpr int KBUF = KT * KROW;        // one K tile in LDS
 constexpr int KHALF = 32 * KROW;       // its second 32 keys
@@ -84,12 +83,13 @@ typedef int i32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x8_t __attribute__((ext_vector_type(8)));
 typedef __attribute__((address_space(3))) void lds_void;
 
-constexpr int kFaInline = 300;
+constexpr int kFaInline = 224;
 struct FaSeqs {
     int32_t n;
     int32_t cu[kFaInline + 1];
     int32_t pos0[kFaInline];
     int32_t toff[kFaInline + 1];       // query-tile offsets
+    int32_t hd[kFaInline];             // block-table rows
 };
 
 __device__ __forceinline__ int seq_of(const int32_t *off, int n, int x) {
@@ -157,33 +157,34 @@ __device__ __forceinline__ void dma16(i32x4 r, int voff, int soff, uint32_t lds)
 }
 
 // K rows of key tile kt -> the K buffer at LDS address kb (row pitch
-// KROW): wavefront w copies rows 8w..8w+7, one row (32 pieces, lanes
-// 0..31) per instruction. The resource ends at the last key, so rows past
-// it are zero (and their scores masked).
-__device__ __forceinline__ void fa_dma_k(uint32_t kb, i32x4 kr, int kt, int wave) {
+// KROW): wavefront w copies tile rows 8w..8w+7, one row (32 pieces, lanes
+// 0..31) per instruction, from cache block 2kt + w/4 (its rows
+// 8(w%4)..+7) given by the resource kr, which ends at the last key: rows
+// past it read zero (and their scores are masked).
+__device__ __forceinline__ void fa_dma_k(uint32_t kb, i32x4 kr, int wave) {
     const int lane = fa_lane();
     if (lane < 32) {
 #pragma unroll
         for (int j = 0; j < 8; j++) {
-            const int r = 8 * wave + j;
-            dma16(kr, (r * D + lane * 8) * 2, kt * TILE_BYTES, kb + r * KROW);
+            const int r = 8 * wave + j, rb = 8 * (wave & 3) + j;
+            dma16(kr, (rb * D + lane * 8) * 2, 0, kb + r * KROW);
         }
     }
 }
 
 // V^T blocks 2kt, 2kt+1 -> the LDS blocks at vb0, vb1 ([d][32 keys]):
 // wavefront w copies the 1 KiB groups 4w..4w+3 of block w / 4 (16 d-rows
-// of 4 pieces each). The resource ends at the last key's block; keys past
-// the last one inside that block are zeroed in LDS before use.
-__device__ __forceinline__ void fa_dma_v(uint32_t vb0, uint32_t vb1, i32x4 vr, int kt, int wave) {
+// of 4 pieces each) from the cache block given by vr (empty for a block
+// past the last key: it reads zero). Keys past the last one inside its
+// block are zeroed in LDS before use.
+__device__ __forceinline__ void fa_dma_v(uint32_t vb0, uint32_t vb1, i32x4 vr, int wave) {
     const int lane = fa_lane();
 #pragma unroll
     for (int j = 0; j < 4; j++) {
         const int q = 4 * wave + j, bb = q >> 4, g = q & 15;
         const int r = 16 * g + (lane >> 2);
         const int c = (lane & 3) ^ ((r >> 2) & 3);
-        dma16(vr, (bb * D * VB + r * VB + c * 8) * 2, kt * TILE_BYTES,
-              (bb ? vb1 : vb0) + g * 16 * VB * 2);
+        dma16(vr, (r * VB + c * 8) * 2, 0, (bb ? vb1 : vb0) + g * 16 * VB * 2);
     }
 }
 
@@ -215,12 +216,33 @@ __device__ __forceinline__ u16x8 lds16(const char *p) {
 __shared__ __attribute__((aligned(16))) char fa_lds[2 * KBUF + 5 * VHALF];
 
 struct FaCtx {
-    i32x4 kr, vr;                      // this (sequence, kv head)'s K rows / V^T blocks
+    KvRef kv;                          // the cache
+    int hd, kvh, nkv, nblk;            // block-table row, kv head, kv heads, cache blocks used
     int nkt, nkeys;                    // key tiles, keys
     int tid, wave, lane, l32, h;
     float c2;                          // scale * log2(e)
     uint32_t lds;                      // LDS address of fa_lds
 };
+
+// The cache block wavefront w copies for key tile kt (clamped to the last
+// block holding keys), its id (a block-table load for a paged cache), and
+// the buffer resources of its K rows and V^T block.
+__device__ __forceinline__ int fa_block(const FaCtx &c, int kt) {
+    return min(2 * kt + (c.wave >> 2), c.nblk - 1);
+}
+__device__ __forceinline__ int fa_block_id(const FaCtx &c, int b) {
+    return c.kv.btab ? c.kv.btab[(size_t)c.hd * c.kv.bstride + b] : c.hd * c.kv.bstride + b;
+}
+__device__ __forceinline__ i32x4 fa_krsrc(const FaCtx &c, int kt, int id) {
+    const int b = 2 * kt + (c.wave >> 2);
+    const int valid = max(0, min(KVB, c.nkeys - KVB * b));
+    return fa_rsrc(c.kv.k + ((size_t)id * c.nkv + c.kvh) * KVB * D, (uint32_t)valid * D * 2);
+}
+__device__ __forceinline__ i32x4 fa_vrsrc(const FaCtx &c, int kt, int id) {
+    const int b = 2 * kt + (c.wave >> 2);
+    return fa_rsrc(c.kv.v + ((size_t)id * c.nkv + c.kvh) * D * KVB,
+                   b < c.nblk ? (uint32_t)(D * KVB * 2) : 0u);
+}
 
 // running softmax state of one query row (per lane)
 struct FaRow {
@@ -428,13 +450,13 @@ __device__ __forceinline__ void fa_publish() {
 
 __global__ __launch_bounds__(64 * NW) void k_attn_fa(
     FaSeqs sq, const int32_t *__restrict__ dmeta, const uint16_t *__restrict__ qn,
-    const uint16_t *__restrict__ qg, const uint16_t *__restrict__ kcache,
-    const uint16_t *__restrict__ vcache, size_t max_seq, int nh, int nkv, float scale,
+    const uint16_t *__restrict__ qg, KvRef kv, int nh, int nkv, float scale,
     uint16_t *__restrict__ y, const uint16_t *__restrict__ sig_bf) {
     const int n = sq.n;
     const int32_t *cu = dmeta ? dmeta : sq.cu;
     const int32_t *pos0 = dmeta ? dmeta + n + 1 : sq.pos0;
     const int32_t *toff = dmeta ? dmeta + 2 * n + 1 : sq.toff;
+    const int32_t *hdv = dmeta ? dmeta + 3 * n + 2 : sq.hd;
     const int ntiles = toff[n];
     const int g = ntiles - 1 - (int)(blockIdx.x / nkv);
     const int kvh = blockIdx.x % nkv;
@@ -452,12 +474,12 @@ __global__ __launch_bounds__(64 * NW) void k_attn_fa(
     c.h = c.lane >> 5;
     c.l32 = c.lane & 31;
     c.wave = __builtin_amdgcn_readfirstlane(c.tid >> 6);
-    const uint16_t *kc = kcache + ((size_t)s * nkv + kvh) * max_seq * D;
-    const uint16_t *vc = vcache + ((size_t)s * nkv + kvh) * D * max_seq;
+    c.kv = kv;
+    c.hd = __builtin_amdgcn_readfirstlane(hdv[s]);
+    c.kvh = kvh;
+    c.nkv = nkv;
     c.nkt = (c.nkeys + KT - 1) / KT;
-    const int nblk = (c.nkeys + VB - 1) / VB;
-    c.kr = fa_rsrc(kc, (uint32_t)c.nkeys * D * 2);
-    c.vr = fa_rsrc(vc, (uint32_t)nblk * D * VB * 2);
+    c.nblk = (c.nkeys + VB - 1) / VB;
     c.lds = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(lds_void *)fa_lds);
     c.c2 = scale * 1.44269504088896341f;
     const int nkt = c.nkt;
@@ -465,8 +487,11 @@ __global__ __launch_bounds__(64 * NW) void k_attn_fa(
     auto kbuf = [&](int u) { return (u & 1) * KBUF; };
     auto vbuf = [&](int u, int half) { return 2 * KBUF + ((2 * u + half) % 5) * VHALF; };
 
-    // tile u = 0 .. 2nkt-1 of the key stream: pass u / nkt, key tile u % nkt
-    fa_dma_k(c.lds + kbuf(0), c.kr, 0, c.wave);
+    // tile u = 0 .. 2nkt-1 of the key stream: pass u / nkt, key tile u %
+    // nkt. idn: this wavefront's block id for the next tile to copy, read
+    // a tile ahead (its load completes under the tile's copies).
+    fa_dma_k(c.lds + kbuf(0), fa_krsrc(c, 0, fa_block_id(c, fa_block(c, 0))), c.wave);
+    int idn = fa_block_id(c, fa_block(c, 1 % nkt));
 
     // query row of this lane: token 4w + l32/8, head l32%8 of the kv head
     const int tk = c.wave * 4 + c.l32 / GRP, head = kvh * GRP + c.l32 % GRP;
@@ -484,9 +509,12 @@ __global__ __launch_bounds__(64 * NW) void k_attn_fa(
     auto begin_tile = [&](int u) {
         fa_publish();
         if (u + 1 < 2 * nkt) {
-            fa_dma_k(c.lds + kbuf(u + 1), c.kr, (u + 1) % nkt, c.wave);
+            const int kt1 = (u + 1) % nkt, id = __builtin_amdgcn_readfirstlane(idn);
+            fa_dma_k(c.lds + kbuf(u + 1), fa_krsrc(c, kt1, id), c.wave);
             if (u + 1 >= nkt)
-                fa_dma_v(c.lds + vbuf(u + 1, 0), c.lds + vbuf(u + 1, 1), c.vr, u + 1 - nkt, c.wave);
+                fa_dma_v(c.lds + vbuf(u + 1, 0), c.lds + vbuf(u + 1, 1), fa_vrsrc(c, kt1, id),
+                         c.wave);
+            idn = fa_block_id(c, fa_block(c, (u + 2) % nkt));
         }
         // the last tile's V keys past nkeys: zero (P is 0 there, but
         // 0 * NaN from unwritten cache memory would not be)
@@ -584,6 +612,64 @@ __global__ __launch_bounds__(64 * NW) void k_attn_fa(
 
 }  // namespace
 
+namespace apus {
+
+int attn_prefill_kv(const ApusHipAttnLayer *L, size_t B, const int32_t *cu, const int32_t *pos0,
+                    const int32_t *rows, const uint16_t *qg, const uint16_t *k,
+                    const uint16_t *v, const KvRef &kv, uint16_t *y) {
+    if (int r = attn_check_layer(L)) return r;
+    if (B == 0) return kOk;
+    // q/k norm + RoPE + cache append (shared with decode); the metadata
+    // also checks the offsets and the cache capacity
+    AttnSeqs as;
+    const int32_t *adm = nullptr;
+    size_t mt = 0;
+    if (int r = attn_meta(B, cu, pos0, rows, (size_t)kv.bstride, L->nkv, 0, &as, &adm, &mt))
+        return r;
+    const size_t Ttot = (size_t)cu[B];
+    if (Ttot == 0) return kOk;
+    size_t max_pos = 0;
+    std::vector<int32_t> meta(4 * B + 2);
+    int32_t *mcu = meta.data(), *mpos = mcu + B + 1, *mtoff = mpos + B, *mhd = mtoff + B + 1;
+    mtoff[0] = 0;
+    for (size_t s = 0; s < B; s++) {
+        const int32_t ns = cu[s + 1] - cu[s];
+        max_pos = std::max(max_pos, (size_t)pos0[s] + (size_t)ns);
+        mtoff[s + 1] = mtoff[s] + (ns + TQ - 1) / TQ;
+        mhd[s] = rows ? rows[s] : (int32_t)s;
+    }
+    memcpy(mcu, cu, (B + 1) * 4);
+    memcpy(mpos, pos0, B * 4);
+    const size_t ntiles = (size_t)mtoff[B];
+    FaSeqs fs;
+    fs.n = (int32_t)B;
+    const int32_t *fdm = nullptr;
+    if (B <= (size_t)kFaInline) {
+        memcpy(fs.cu, cu, (B + 1) * 4);
+        memcpy(fs.pos0, pos0, B * 4);
+        memcpy(fs.toff, mtoff, (B + 1) * 4);
+        memcpy(fs.hd, mhd, B * 4);
+    } else {
+        fdm = (const int32_t *)upload_async(meta.data(), meta.size() * 4);
+        if (!fdm) return kErrHip;
+    }
+    uint16_t *qn = (uint16_t *)scratch(kScratchAttnQ, Ttot * L->nh * D * 2);
+    if (!qn) return kErrHip;
+    if (int r = attn_prep(L, as, adm, Ttot, max_pos, attn_max_vblocks(B, cu, pos0), qg, k, v,
+                          kv, qn))
+        return r;
+    const float scale = (float)(1.0 / sqrt((double)L->d));
+    const ActTables *tabs = act_tables();
+    if (!tabs) return kErrHip;
+    APUS_TIMED("k_attn_fa",
+               k_attn_fa<<<(unsigned)(ntiles * L->nkv), 64 * NW, 0, stream()>>>(
+                   fs, fdm, qn, qg, kv, (int)L->nh, (int)L->nkv, scale, y, tabs->sig_bf));
+    APUS_LAUNCHED("k_attn_fa");
+    return kOk;
+}
+
+}  // namespace apus
+
 extern "C" {
 
 int apus_hip_attn_prefill(const ApusHipAttnLayer *L, size_t B, const int32_t *cu,
@@ -591,70 +677,22 @@ int apus_hip_attn_prefill(const ApusHipAttnLayer *L, size_t B, const int32_t *cu
                           const uint16_t *v, uint16_t *kcache, uint16_t *vcache,
                           size_t max_seq, uint16_t *y) {
     APUS_READY();
-    if (int r = attn_check_layer(L)) return r;
-    if (B == 0) return kOk;
-    if (!cu || !pos0 || cu[0] != 0) return set_error(kErrArgument, "bad offsets");
     if (max_seq % VB != 0) return set_error(kErrArgument, "max_seq must be a multiple of %d", VB);
-    if (L->nh != GRP * L->nkv)
-        return set_error(kErrUnsupported, "prefill supports nh = %d * nkv", GRP);
-    size_t max_pos = 0;
-    std::vector<int32_t> meta(3 * B + 2);
-    int32_t *mcu = meta.data(), *mpos = mcu + B + 1, *mtoff = mpos + B;
-    mtoff[0] = 0;
-    for (size_t s = 0; s < B; s++) {
-        const int32_t ns = cu[s + 1] - cu[s];
-        if (ns < 0) return set_error(kErrArgument, "token offsets must ascend");
-        if (pos0[s] < 0 || (size_t)pos0[s] + (size_t)ns > max_seq)
-            return set_error(kErrArgument, "sequence %zu overflows the cache (%d+%d > %zu)", s,
-                             pos0[s], ns, max_seq);
-        max_pos = std::max(max_pos, (size_t)pos0[s] + (size_t)ns);
-        mtoff[s + 1] = mtoff[s] + (ns + TQ - 1) / TQ;
-    }
-    memcpy(mcu, cu, (B + 1) * 4);
-    memcpy(mpos, pos0, B * 4);
-    const size_t Ttot = (size_t)cu[B];
-    if (Ttot == 0) return kOk;
-    const size_t ntiles = (size_t)mtoff[B];
+    return attn_prefill_kv(L, B, cu, pos0, nullptr, qg, k, v, kv_flat(kcache, vcache, max_seq),
+                           y);
+}
 
-    // q/k norm + RoPE + cache append (shared with decode)
-    AttnSeqs as;
-    as.n = (int32_t)B;
-    as.ks1 = as.ks2 = 0;
-    const int32_t *adm = nullptr;
-    FaSeqs fs;
-    fs.n = (int32_t)B;
-    const int32_t *fdm = nullptr;
-    if (B <= (size_t)kAttnInlineSeqs) {
-        memcpy(as.cu, cu, (B + 1) * 4);
-        memcpy(as.pos0, pos0, B * 4);
-    }
-    if (B <= (size_t)kFaInline) {
-        memcpy(fs.cu, cu, (B + 1) * 4);
-        memcpy(fs.pos0, pos0, B * 4);
-        memcpy(fs.toff, mtoff, (B + 1) * 4);
-    }
-    if (B > (size_t)kAttnInlineSeqs || B > (size_t)kFaInline) {
-        // [cu | pos0 | toff] serves both (attn_prep reads cu and pos0 at the
-        // same offsets)
-        fdm = (const int32_t *)upload_small(kScratchMeta2, meta.data(), meta.size() * 4);
-        if (!fdm) return kErrHip;
-        if (B > (size_t)kAttnInlineSeqs) adm = fdm;
-        if (B <= (size_t)kFaInline) fdm = nullptr;
-    }
-    uint16_t *qn = (uint16_t *)scratch(kScratchAttnQ, Ttot * L->nh * D * 2);
-    if (!qn) return kErrHip;
-    if (int r = attn_prep(L, as, adm, Ttot, max_pos, attn_max_vblocks(B, cu, pos0), qg, k, v,
-                          kcache, vcache, max_seq, qn))
-        return r;
-    const float scale = (float)(1.0 / sqrt((double)L->d));
-    const ActTables *tabs = act_tables();
-    if (!tabs) return kErrHip;
-    APUS_TIMED("k_attn_fa",
-               k_attn_fa<<<(unsigned)(ntiles * L->nkv), 64 * NW, 0, stream()>>>(
-                   fs, fdm, qn, qg, kcache, vcache, max_seq, (int)L->nh, (int)L->nkv, scale, y,
-                   tabs->sig_bf));
-    APUS_LAUNCHED("k_attn_fa");
-    return kOk;
+int apus_hip_attn_prefill_paged(const ApusHipAttnLayer *L, size_t B, const int32_t *rows,
+                                const int32_t *cu, const int32_t *pos0, const uint16_t *qg,
+                                const uint16_t *k, const uint16_t *v, const ApusHipKvCache *kv,
+                                uint16_t *y) {
+    APUS_READY();
+    if (!kv || !kv->k || !kv->v || !kv->block_table || kv->max_blocks == 0 ||
+        kv->max_blocks > 0x7fffffff)
+        return set_error(kErrArgument, "bad paged KV cache descriptor");
+    if (!rows) return set_error(kErrArgument, "NULL block-table rows");
+    return attn_prefill_kv(L, B, cu, pos0, rows, qg, k, v,
+                           KvRef{kv->k, kv->v, kv->block_table, (int32_t)kv->max_blocks}, y);
 }
 
 }  // extern "C"

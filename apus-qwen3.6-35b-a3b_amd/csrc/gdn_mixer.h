@@ -28,14 +28,15 @@ int gdn_check_layer(const ApusHipGdnLayer *L);
 int gdn_check_offsets(size_t B, const int32_t *cu);
 // conv + l2norm + gates for every token (reads the old conv state).
 // Token offsets: dcu (device) when non-null, else from the host array cu
-// by value (B <= kGdnCuInline).
+// by value (B <= kGdnCuInline). slots (device, nullable): the conv-state
+// slot of each sequence (identity when null).
 int gdn_prep(const ApusHipGdnLayer *L, size_t B, const int32_t *cu, const int32_t *dcu,
              size_t Ttot, const uint16_t *qkv, const uint16_t *a,
              const uint16_t *b, const uint16_t *conv_state, GdnScratch *w,
-             bool want_graw);
+             bool want_graw, const int32_t *slots);
 // gated RMSNorm of w->ob into y, then the new conv state
 int gdn_post(const ApusHipGdnLayer *L, size_t B, const int32_t *cu, const int32_t *dcu,
              size_t Ttot, const GdnScratch *w, const uint16_t *z,
-             const uint16_t *qkv, uint16_t *conv_state, uint16_t *y);
+             const uint16_t *qkv, uint16_t *conv_state, uint16_t *y, const int32_t *slots);
 
 }  // namespace apus

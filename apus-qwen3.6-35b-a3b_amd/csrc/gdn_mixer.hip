@@ -26,6 +26,9 @@
 #include <stdint.h>
 #include <string.h>
 
+#include <algorithm>
+#include <vector>
+
 #include "../../include/apus_hip.h"
 #include "apus_dev.h"
 #include "apus_host.h"
@@ -106,7 +109,7 @@ void k_gdn_decode(
     const uint16_t *a, const uint16_t *b, const uint16_t *conv_w,
     const float *A_log, const float *dt_bias, const uint16_t *onorm_w,
     const uint16_t *conv_state, const float *S, uint16_t *conv_out, float *S_out,
-    uint16_t *y, int hk, float qscale) {
+    uint16_t *y, int hk, float qscale, const int32_t *slot_in, const int32_t *slot_out) {
     // (no __restrict__ on the small operands: it would let the compiler sink
     // their loads past the ordering barrier below the state loads)
     const int s = blockIdx.x / hk, kh = blockIdx.x % hk;
@@ -120,6 +123,10 @@ void k_gdn_decode(
     const int t0 = dcu ? dcu[s] : ca.cu[s];
     const int t1 = dcu ? dcu[s + 1] : ca.cu[s + 1];
     if (t0 == t1) return;
+    // the state slots this sequence reads and writes (identity without a
+    // slot map)
+    const int si = slot_in ? __builtin_amdgcn_readfirstlane(slot_in[s]) : s;
+    const int so = slot_out ? __builtin_amdgcn_readfirstlane(slot_out[s]) : s;
 
     __shared__ __attribute__((aligned(16))) float raw[2 * DK];   // conv q, k
     __shared__ __attribute__((aligned(16))) float qkn[2 * DK];   // normed q, k
@@ -129,8 +136,8 @@ void k_gdn_decode(
 
     const size_t cqk = tid < DK ? (size_t)kh * DK + tid : kd + (size_t)kh * DK + (tid - DK);
     const size_t cv = 2 * kd + (size_t)h * DV + j;
-    const uint16_t *stq = conv_state + (size_t)s * cd * 3 + cqk * 3;
-    const uint16_t *stv = conv_state + (size_t)s * cd * 3 + cv * 3;
+    const uint16_t *stq = conv_state + (size_t)si * cd * 3 + cqk * 3;
+    const uint16_t *stv = conv_state + (size_t)si * cd * 3 + cv * 3;
     // Small per-token operands, loaded as raw bits before the state tile.
     uint32_t cwq_lo, cwq_hi, cwv_lo, cwv_hi;          // 4 bf16 conv taps each
     {
@@ -155,7 +162,7 @@ void k_gdn_decode(
     asm volatile("" ::: "memory");
     __builtin_amdgcn_sched_barrier(0);
     // this wave's 128x64 state tile: 32 x 16-byte loads per lane
-    const auto Sr = buf_rsrc(const_cast<float *>(S) + ((size_t)s * hv + h) * DK * DV, DK * DV * 4);
+    const auto Sr = buf_rsrc(const_cast<float *>(S) + ((size_t)si * hv + h) * DK * DV, DK * DV * 4);
     const int voff = (half * 32 * 64 + lane) * 16;
     float sr[DK];
 #pragma unroll
@@ -239,13 +246,13 @@ void k_gdn_decode(
         const float x2 = rndf(x1 * wo);
         y[(size_t)t * vd + (size_t)h * DV + j] = f2bf(x2 * zg);
     }
-    const auto Sw = buf_rsrc(S_out + ((size_t)s * hv + h) * DK * DV, DK * DV * 4);
+    const auto Sw = buf_rsrc(S_out + ((size_t)so * hv + h) * DK * DV, DK * DV * 4);
 #pragma unroll
     for (int q = 0; q < DK / 4; q++)
         buf_st4(Sw, voff, q * 1024,
                 f32x4_t{sr[4 * q + 0], sr[4 * q + 1], sr[4 * q + 2], sr[4 * q + 3]});
-    uint16_t *otq = conv_out + (size_t)s * cd * 3 + cqk * 3;
-    uint16_t *otv = conv_out + (size_t)s * cd * 3 + cv * 3;
+    uint16_t *otq = conv_out + (size_t)so * cd * 3 + cqk * 3;
+    uint16_t *otv = conv_out + (size_t)so * cd * 3 + cv * 3;
     otq[0] = q0; otq[1] = q1; otq[2] = q2;
     otv[0] = v0; otv[1] = v1; otv[2] = v2;
 }
@@ -305,7 +312,8 @@ __global__ __launch_bounds__(256) void k_gdn_prep(
     const float *__restrict__ dt_bias, const uint16_t *__restrict__ conv_state,
     float *__restrict__ qk, uint16_t *__restrict__ vconv,
     float2 *__restrict__ gate, float *__restrict__ graw, int hk, float qscale,
-    const uint16_t *__restrict__ silu_bf, const uint16_t *__restrict__ sig_bf) {
+    const uint16_t *__restrict__ silu_bf, const uint16_t *__restrict__ sig_bf,
+    const int32_t *__restrict__ slots) {
     typedef unsigned short u16x8 __attribute__((ext_vector_type(8)));
     const int32_t *cu = dcu ? dcu : ci.cu;
     const int tile = blockIdx.x / hk, kh = blockIdx.x % hk;
@@ -387,7 +395,7 @@ __global__ __launch_bounds__(256) void k_gdn_prep(
         if (i < nt) {
             const int2 ts = tseq[i];
             const int t = tb + i, t0 = ts.y;
-            const uint16_t *cst = conv_state + (size_t)ts.x * cd * 3;
+            const uint16_t *cst = conv_state + (size_t)(slots ? slots[ts.x] : ts.x) * cd * 3;
             float xq[4], xv[4];
 #pragma unroll
             for (int u = 0; u < 4; u++) {
@@ -469,7 +477,7 @@ __global__ __launch_bounds__(256) void k_gdn_post(
     const uint16_t *__restrict__ ob, const uint16_t *__restrict__ z,
     const uint16_t *__restrict__ onorm_w, uint16_t *__restrict__ y,
     const uint16_t *__restrict__ qkv, uint16_t *__restrict__ conv_state,
-    int hk, const float *__restrict__ silu_f) {
+    int hk, const float *__restrict__ silu_f, const int32_t *__restrict__ slots) {
     const int32_t *cu = dcu ? dcu : ci.cu;
     const int hv = hk * REP;
     const size_t kd = (size_t)hk * DK, vd = (size_t)hv * DV, cd = 2 * kd + vd;
@@ -527,7 +535,7 @@ __global__ __launch_bounds__(256) void k_gdn_post(
     const size_t s = bb / per, c = (bb % per) * 256 + tid;
     const int t0 = cu[s], n = cu[s + 1] - t0;
     if (n == 0) return;
-    uint16_t *st = conv_state + s * cd * 3 + c * 3;
+    uint16_t *st = conv_state + (size_t)(slots ? slots[s] : (int32_t)s) * cd * 3 + c * 3;
     uint16_t w3[3];
     for (int jj = 0; jj < 3; jj++) {
         int idx = n - 3 + jj;          // position in the token span
@@ -570,7 +578,7 @@ static bool gdn_cu_arg(size_t B, const int32_t *cu, const int32_t *dcu, GdnCu *c
 int gdn_prep(const ApusHipGdnLayer *L, size_t B, const int32_t *cu, const int32_t *dcu,
              size_t Ttot, const uint16_t *qkv, const uint16_t *a,
              const uint16_t *b, const uint16_t *conv_state, GdnScratch *w,
-             bool want_graw) {
+             bool want_graw, const int32_t *slots) {
     const size_t kd = L->hk * DK, vd = L->hv * DV;
     w->qk = (float *)scratch(kScratchGdnQK, Ttot * 2 * kd * 4);
     w->vconv = (uint16_t *)scratch(kScratchGdnV, Ttot * vd * 2);
@@ -587,13 +595,14 @@ int gdn_prep(const ApusHipGdnLayer *L, size_t B, const int32_t *cu, const int32_
     APUS_TIMED("k_gdn_prep",
                k_gdn_prep<<<(unsigned)(cdiv(Ttot, PT) * L->hk), 256, 0, stream()>>>(
         ci, dcu, (int)B, (int)Ttot, qkv, a, b, L->conv_w, L->A_log, L->dt_bias, conv_state,
-        w->qk, w->vconv, w->gate, w->graw, (int)L->hk, qscale, tabs->silu_bf, tabs->sig_bf));
+        w->qk, w->vconv, w->gate, w->graw, (int)L->hk, qscale, tabs->silu_bf, tabs->sig_bf,
+        slots));
     return launch_check("k_gdn_prep");
 }
 
 int gdn_post(const ApusHipGdnLayer *L, size_t B, const int32_t *cu, const int32_t *dcu,
              size_t Ttot, const GdnScratch *w, const uint16_t *z,
-             const uint16_t *qkv, uint16_t *conv_state, uint16_t *y) {
+             const uint16_t *qkv, uint16_t *conv_state, uint16_t *y, const int32_t *slots) {
     const size_t cd = 2 * L->hk * DK + L->hv * DV;
     const size_t nblk = cdiv(Ttot * L->hv, PR) + B * (cd / 256);
     const ActTables *tabs = act_tables();
@@ -603,8 +612,85 @@ int gdn_post(const ApusHipGdnLayer *L, size_t B, const int32_t *cu, const int32_
     APUS_TIMED("k_gdn_post",
                k_gdn_post<<<(unsigned)nblk, 256, 0, stream()>>>(
         ci, dcu, (int)B, (int)Ttot, w->ob, z, L->onorm_w, y, qkv, conv_state,
-        (int)L->hk, tabs->silu_f));
+        (int)L->hk, tabs->silu_f, slots));
     return launch_check("k_gdn_post");
+}
+
+}  // namespace apus
+
+extern "C" {
+
+}  // extern "C"
+
+namespace apus {
+
+// Decode / verify with optional state slot maps (host arrays; nullptr:
+// sequence s uses slot s).
+static int gdn_decode_run(const ApusHipGdnLayer *L, size_t B, const int32_t *cu,
+                          const uint16_t *qkv, const uint16_t *z, const uint16_t *a,
+                          const uint16_t *b, const uint16_t *conv_in, const float *S_in,
+                          uint16_t *conv_out, float *S_out, uint16_t *y, const int32_t *sin_h,
+                          const int32_t *sout_h) {
+    if (int r = gdn_check_layer(L)) return r;
+    if (B == 0) return kOk;
+    if (int r = gdn_check_offsets(B, cu)) return r;
+    if (cu[B] == 0) return kOk;
+    CuArgs ca;
+    const int32_t *dcu = nullptr;
+    if (B <= (size_t)kInlineSeqs) {
+        memcpy(ca.cu, cu, (B + 1) * sizeof(int32_t));
+    } else {
+        dcu = (const int32_t *)upload_async(cu, (B + 1) * 4);
+        if (!dcu) return kErrHip;
+    }
+    const int32_t *dsin = nullptr, *dsout = nullptr;
+    if (sin_h) {
+        std::vector<int32_t> m(2 * B);
+        memcpy(m.data(), sin_h, B * 4);
+        memcpy(m.data() + B, sout_h, B * 4);
+        dsin = (const int32_t *)upload_async(m.data(), m.size() * 4);
+        if (!dsin) return kErrHip;
+        dsout = dsin + B;
+    }
+    const float qscale = (float)pow((double)L->dk, -0.5);
+    const bool multi = (size_t)cu[B] != B;     // some sequence has != 1 token
+    auto kern = multi ? k_gdn_decode<true> : k_gdn_decode<false>;
+    APUS_TIMED("k_gdn_decode",
+               kern<<<(unsigned)(B * L->hk), 256, 0, stream()>>>(
+        ca, dcu, qkv, z, a, b, L->conv_w, L->A_log, L->dt_bias, L->onorm_w,
+        conv_in, S_in, conv_out, S_out, y, (int)L->hk, qscale, dsin, dsout));
+    APUS_LAUNCHED("k_gdn_decode");
+    return kOk;
+}
+
+// Slot maps must not let one sequence's writes land in another's reads or
+// writes: the output slots of the sequences with tokens are distinct, and
+// none is another sequence's input slot.
+static int check_slot_maps(size_t B, const int32_t *cu, const int32_t *sin, const int32_t *sout,
+                           size_t nslots) {
+    std::vector<std::pair<int32_t, int32_t>> outs, ins;
+    for (size_t s = 0; s < B; s++) {
+        if (sin[s] < 0 || sout[s] < 0 || (nslots && ((size_t)sin[s] >= nslots ||
+                                                      (size_t)sout[s] >= nslots)))
+            return set_error(kErrArgument, "state slot of sequence %zu out of range", s);
+        if (cu[s + 1] == cu[s]) continue;
+        outs.emplace_back(sout[s], (int32_t)s);
+        ins.emplace_back(sin[s], (int32_t)s);
+    }
+    std::sort(outs.begin(), outs.end());
+    std::sort(ins.begin(), ins.end());
+    for (size_t i = 1; i < outs.size(); i++)
+        if (outs[i].first == outs[i - 1].first)
+            return set_error(kErrArgument, "two sequences write state slot %d", outs[i].first);
+    for (auto &o : outs) {
+        auto it = std::lower_bound(ins.begin(), ins.end(), std::make_pair(o.first, INT32_MIN));
+        for (; it != ins.end() && it->first == o.first; ++it)
+            if (it->second != o.second)
+                return set_error(kErrArgument,
+                                 "state slot %d is written by sequence %d and read by %d",
+                                 o.first, o.second, it->second);
+    }
+    return kOk;
 }
 
 }  // namespace apus
@@ -617,10 +703,7 @@ int apus_hip_gdn_decode_into(const ApusHipGdnLayer *L, size_t B, const int32_t *
                              const uint16_t *conv_in, const float *S_in,
                              uint16_t *conv_out, float *S_out, uint16_t *y) {
     APUS_READY();
-    if (int r = gdn_check_layer(L)) return r;
-    if (B == 0) return kOk;
-    if (int r = gdn_check_offsets(B, cu)) return r;
-    if (cu[B] == 0) return kOk;
+    if (!L) return set_error(kErrArgument, "NULL layer");
     // in place, or two disjoint state sets: a partial overlap would let one
     // workgroup's writes land in another's inputs
     const size_t nS = B * L->hv * DK * DV * 4, nC = B * (2 * L->hk * DK + L->hv * DV) * 3 * 2;
@@ -630,23 +713,8 @@ int apus_hip_gdn_decode_into(const ApusHipGdnLayer *L, size_t B, const int32_t *
     };
     if (overlap(S_in, S_out, nS) || overlap(conv_in, conv_out, nC))
         return set_error(kErrArgument, "state in/out must be the same buffer or disjoint");
-    CuArgs ca;
-    const int32_t *dcu = nullptr;
-    if (B <= (size_t)kInlineSeqs) {
-        memcpy(ca.cu, cu, (B + 1) * sizeof(int32_t));
-    } else {
-        dcu = (const int32_t *)upload_small(kScratchMeta, cu, (B + 1) * 4);
-        if (!dcu) return kErrHip;
-    }
-    const float qscale = (float)pow((double)L->dk, -0.5);
-    const bool multi = (size_t)cu[B] != B;     // some sequence has != 1 token
-    auto kern = multi ? k_gdn_decode<true> : k_gdn_decode<false>;
-    APUS_TIMED("k_gdn_decode",
-               kern<<<(unsigned)(B * L->hk), 256, 0, stream()>>>(
-        ca, dcu, qkv, z, a, b, L->conv_w, L->A_log, L->dt_bias, L->onorm_w,
-        conv_in, S_in, conv_out, S_out, y, (int)L->hk, qscale));
-    APUS_LAUNCHED("k_gdn_decode");
-    return kOk;
+    return gdn_decode_run(L, B, cu, qkv, z, a, b, conv_in, S_in, conv_out, S_out, y, nullptr,
+                          nullptr);
 }
 
 int apus_hip_gdn_decode(const ApusHipGdnLayer *L, size_t B, const int32_t *cu,
@@ -655,6 +723,18 @@ int apus_hip_gdn_decode(const ApusHipGdnLayer *L, size_t B, const int32_t *cu,
                         uint16_t *conv_state, float *S, uint16_t *y) {
     return apus_hip_gdn_decode_into(L, B, cu, qkv, z, a, b, conv_state, S,
                                     conv_state, S, y);
+}
+
+int apus_hip_gdn_decode_slots(const ApusHipGdnLayer *L, size_t B, const int32_t *slot_in,
+                              const int32_t *slot_out, const int32_t *cu, const uint16_t *qkv,
+                              const uint16_t *z, const uint16_t *a, const uint16_t *b,
+                              uint16_t *conv, float *S, uint16_t *y) {
+    APUS_READY();
+    if (B == 0) return kOk;
+    if (!slot_in || !slot_out) return set_error(kErrArgument, "NULL slot map");
+    if (int r = gdn_check_offsets(B, cu)) return r;
+    if (int r = check_slot_maps(B, cu, slot_in, slot_out, 0)) return r;
+    return gdn_decode_run(L, B, cu, qkv, z, a, b, conv, S, conv, S, y, slot_in, slot_out);
 }
 
 int apus_hip_gdn_state_pack(const float *S_ref, float *S_dev, size_t nmat) {

@@ -40,6 +40,7 @@
 #include <stdint.h>
 #include <string.h>
 
+#include <algorithm>
 #include <vector>
 
 #include "../../include/apus_hip.h"
@@ -661,7 +662,8 @@ __global__ __launch_bounds__(512) void k_gdn_chunk_scan(
     ChunkSeqs sq, const int32_t *__restrict__ dmeta, const uint16_t *__restrict__ Qp,
     const uint16_t *__restrict__ Kp, const float *__restrict__ Ub,
     const uint16_t *__restrict__ Wb, const uint16_t *__restrict__ Ab,
-    const float *__restrict__ Fb, float *__restrict__ S, uint16_t *__restrict__ ob, int hk) {
+    const float *__restrict__ Fb, float *__restrict__ S, uint16_t *__restrict__ ob, int hk,
+    const int32_t *__restrict__ slots) {
     const int hv = hk * REP;
     const size_t vd = (size_t)hv * DV;
     const int nsh = sq.n * hv;
@@ -688,7 +690,7 @@ __global__ __launch_bounds__(512) void k_gdn_chunk_scan(
     __shared__ __attribute__((aligned(16))) uint16_t Ost[4][16 * CB];   // output role: rnd(o) tiles
 
     // state slice in: packed layout ((j/64*32 + i/4)*64 + j%64)*4 + i%4
-    float *Sm = S + (size_t)sh * DK * DV;
+    float *Sm = S + ((size_t)(slots ? slots[s] : s) * hv + h) * DK * DV;
     const int jb = (cb * CB) / 64 * 32, jl = (cb * CB) % 64;
     for (int e = tid; e < CB * DK; e += 512) {
         const int q = e / 64, rem = e % 64, jj = rem / 4, r = rem % 4;
@@ -828,12 +830,14 @@ __global__ __launch_bounds__(512) void k_gdn_chunk_scan(
 
 }  // namespace
 
-extern "C" {
+namespace apus {
 
-int apus_hip_gdn_prefill(const ApusHipGdnLayer *L, size_t B, const int32_t *cu,
-                         const uint16_t *qkv, const uint16_t *z, const uint16_t *a,
-                         const uint16_t *b, uint16_t *conv_state, float *S, uint16_t *y) {
-    APUS_READY();
+// Chunked prefill; slots_h (host, nullable): the state slot of each
+// sequence in conv_state / S (identity when null).
+static int gdn_prefill_run(const ApusHipGdnLayer *L, size_t B, const int32_t *cu,
+                           const uint16_t *qkv, const uint16_t *z, const uint16_t *a,
+                           const uint16_t *b, uint16_t *conv_state, float *S, uint16_t *y,
+                           const int32_t *slots_h) {
     if (int r = gdn_check_layer(L)) return r;
     if (B == 0) return kOk;
     if (int r = gdn_check_offsets(B, cu)) return r;
@@ -866,13 +870,18 @@ int apus_hip_gdn_prefill(const ApusHipGdnLayer *L, size_t B, const int32_t *cu,
         }
         kmeta = nullptr;
     } else {
-        dmeta = (const int32_t *)upload_small(kScratchMeta, meta.data(), meta.size() * 4);
+        dmeta = (const int32_t *)upload_async(meta.data(), meta.size() * 4);
         if (!dmeta) return kErrHip;
         kmeta = dmeta;
     }
 
+    const int32_t *slots = nullptr;
+    if (slots_h) {
+        slots = (const int32_t *)upload_async(slots_h, B * 4);
+        if (!slots) return kErrHip;
+    }
     GdnScratch w;
-    if (int r = gdn_prep(L, B, cu, dmeta, Ttot, qkv, a, b, conv_state, &w, true)) return r;
+    if (int r = gdn_prep(L, B, cu, dmeta, Ttot, qkv, a, b, conv_state, &w, true, slots)) return r;
     const size_t units = nch * L->hv;
     float *Ub = (float *)scratch(kScratchGdnChunk, units * C * DV * 4);
     uint16_t *Wb = (uint16_t *)scratch(kScratchGdnChunk2, units * C * DK * 4);
@@ -888,9 +897,40 @@ int apus_hip_gdn_prefill(const ApusHipGdnLayer *L, size_t B, const int32_t *cu,
     APUS_LAUNCHED("k_gdn_chunk_wy");
     APUS_TIMED("k_gdn_chunk_scan",
                k_gdn_chunk_scan<<<(unsigned)(B * L->hv * NCB), 512, 0, stream()>>>(
-        sq, kmeta, Qp, Kp, Ub, Wb, Ab, Fb, S, w.ob, (int)L->hk));
+        sq, kmeta, Qp, Kp, Ub, Wb, Ab, Fb, S, w.ob, (int)L->hk, slots));
     APUS_LAUNCHED("k_gdn_chunk_scan");
-    return gdn_post(L, B, cu, dmeta, Ttot, &w, z, qkv, conv_state, y);
+    return gdn_post(L, B, cu, dmeta, Ttot, &w, z, qkv, conv_state, y, slots);
+}
+
+}  // namespace apus
+
+extern "C" {
+
+int apus_hip_gdn_prefill(const ApusHipGdnLayer *L, size_t B, const int32_t *cu,
+                         const uint16_t *qkv, const uint16_t *z, const uint16_t *a,
+                         const uint16_t *b, uint16_t *conv_state, float *S, uint16_t *y) {
+    APUS_READY();
+    return gdn_prefill_run(L, B, cu, qkv, z, a, b, conv_state, S, y, nullptr);
+}
+
+int apus_hip_gdn_prefill_slots(const ApusHipGdnLayer *L, size_t B, const int32_t *slots,
+                               const int32_t *cu, const uint16_t *qkv, const uint16_t *z,
+                               const uint16_t *a, const uint16_t *b, uint16_t *conv,
+                               float *S, uint16_t *y) {
+    APUS_READY();
+    if (B == 0) return kOk;
+    if (!slots) return set_error(kErrArgument, "NULL slot map");
+    if (int r = gdn_check_offsets(B, cu)) return r;
+    std::vector<int32_t> sorted;
+    for (size_t s = 0; s < B; s++) {
+        if (slots[s] < 0) return set_error(kErrArgument, "negative state slot");
+        if (cu[s + 1] > cu[s]) sorted.push_back(slots[s]);
+    }
+    std::sort(sorted.begin(), sorted.end());
+    for (size_t i = 1; i < sorted.size(); i++)
+        if (sorted[i] == sorted[i - 1])
+            return set_error(kErrArgument, "two sequences use state slot %d", sorted[i]);
+    return gdn_prefill_run(L, B, cu, qkv, z, a, b, conv, S, y, slots);
 }
 
 }  // extern "C"

@@ -191,6 +191,22 @@ int apus_hip_gdn_decode_into(const ApusHipGdnLayer *L, size_t B,
                              const float *S_in, uint16_t *conv_out,
                              float *S_out, uint16_t *y);
 
+/* GDN decode / verify on a state pool (no counterpart in the reference,
+ * whose layer state is one sequence's, c/layer.h:159-167): conv and S are
+ * the base of a layer's slot arrays -- slot i at conv + i*conv_dim*3 and
+ * S + i*hv*dk*dv (device layout) -- and sequence s reads its state from
+ * slot_in[s] and writes it to slot_out[s] (HOST arrays). slot_out[s] ==
+ * slot_in[s] decodes in place; a different output slot keeps the input as
+ * an MTP snapshot (the rollback of c/mtp.h:70-75 is then a re-feed from the
+ * kept slot). The output slots of sequences with tokens must be distinct
+ * and none may be another sequence's input slot. */
+int apus_hip_gdn_decode_slots(const ApusHipGdnLayer *L, size_t B,
+                              const int32_t *slot_in, const int32_t *slot_out,
+                              const int32_t *cu, const uint16_t *qkv,
+                              const uint16_t *z, const uint16_t *a,
+                              const uint16_t *b, uint16_t *conv, float *S,
+                              uint16_t *y);
+
 /* Chunked GDN prefill: the same layer and arguments as apus_hip_gdn_decode
  * for sequences of any length (c/layer.h:427-492, the prompt path; the
  * reference steps the recurrence token by token, c/gdn.h:627-635). The
@@ -206,6 +222,15 @@ int apus_hip_gdn_prefill(const ApusHipGdnLayer *L, size_t B,
                          const uint16_t *b, uint16_t *conv_state, float *S,
                          uint16_t *y);
 
+/* apus_hip_gdn_prefill on a state pool: sequence s's state is slot
+ * slots[s] (HOST array, distinct for sequences with tokens) of the slot
+ * arrays conv / S (layout as apus_hip_gdn_decode_slots). */
+int apus_hip_gdn_prefill_slots(const ApusHipGdnLayer *L, size_t B,
+                               const int32_t *slots, const int32_t *cu,
+                               const uint16_t *qkv, const uint16_t *z,
+                               const uint16_t *a, const uint16_t *b,
+                               uint16_t *conv, float *S, uint16_t *y);
+
 /* Full-attention layer weights + dims (hot fields of ApusLayerCfg/W,
  * c/layer.h:113-157). Device pointers. */
 typedef struct {
@@ -214,19 +239,42 @@ typedef struct {
     const uint16_t *qn_w, *kn_w;    /* [d] bf16, (1+w) storage */
 } ApusHipAttnLayer;
 
-/* Device KV-cache layout. Sequence s of a batch owns
- *   K: kcache + s*nkv*max_seq*d, laid out [nkv][max_seq][d];
- *   V: vcache + s*nkv*d*max_seq, laid out [nkv][max_seq/32][d][32]
- *      (transposed in blocks of 32 positions),
- * bf16, max_seq a multiple of 32. The reference keeps both as
- * [max_seq][nkv][d] (c/layer.h:164-165); pack/unpack convert the first
- * ntok positions of one sequence (device pointers). */
+/* Device KV-cache layout: blocks of 32 positions. Block b (positions
+ * 32b .. 32b+31) of a sequence is a K block [nkv][32][d] (d contiguous) and
+ * a V block [nkv][d][32] (transposed), bf16, at block id `id`:
+ *   K: kcache + id * nkv*32*d,   V: vcache + id * nkv*d*32.
+ * Flat caches (apus_hip_attn_decode / _prefill): sequence s of the batch
+ * owns ids s*(max_seq/32) .. s*(max_seq/32) + max_seq/32 - 1 in order,
+ * i.e. max_seq*nkv*d elements of each array, max_seq a multiple of 32.
+ * Paged caches (ApusHipKvCache below): ids come from a block table. The
+ * reference keeps both as [max_seq][nkv][d] (c/layer.h:164-165); pack /
+ * unpack convert the first ntok positions of one sequence (device
+ * pointers). */
 int apus_hip_attn_cache_pack(const uint16_t *kc_ref, const uint16_t *vc_ref,
                              size_t ntok, size_t nkv, size_t d,
                              uint16_t *kcache, uint16_t *vcache, size_t max_seq);
 int apus_hip_attn_cache_unpack(const uint16_t *kcache, const uint16_t *vcache,
                                size_t ntok, size_t nkv, size_t d, size_t max_seq,
                                uint16_t *kc_ref, uint16_t *vc_ref);
+
+/* Paged KV cache (no counterpart in the reference, whose cache is one
+ * flat [max_seq][nkv][d] array per sequence, c/model.h:615-616): block
+ * arrays k and v (device) and a device block table [rows][max_blocks] whose
+ * entry [h][b] is the id of block b of the sequence at table row h. The
+ * *_paged calls take, per sequence of the batch, its table row (HOST array
+ * rows[B]); a sequence may use blocks 0 .. ceil((pos0+new)/32) - 1 of its
+ * row. apus_hip_kv_pool_* below manage such a cache. */
+typedef struct {
+    uint16_t *k, *v;
+    const int32_t *block_table;
+    size_t max_blocks;
+} ApusHipKvCache;
+int apus_hip_attn_cache_pack_paged(const uint16_t *kc_ref, const uint16_t *vc_ref,
+                                   size_t ntok, size_t nkv, size_t d,
+                                   const ApusHipKvCache *kv, int32_t row);
+int apus_hip_attn_cache_unpack_paged(const ApusHipKvCache *kv, int32_t row,
+                                     size_t ntok, size_t nkv, size_t d,
+                                     uint16_t *kc_ref, uint16_t *vc_ref);
 
 /* Full-attention causal prefill for B sequences of any length (c/layer.h:
  * 498-564: per token q/k (1+w) RMSNorm, partial RoPE, cache append, then
@@ -255,6 +303,56 @@ int apus_hip_attn_decode(const ApusHipAttnLayer *L, size_t B,
                          const uint16_t *qg, const uint16_t *k,
                          const uint16_t *v, uint16_t *kcache,
                          uint16_t *vcache, size_t max_seq, uint16_t *y);
+
+/* apus_hip_attn_prefill / _decode on a paged cache: sequence s of the
+ * batch lives at block-table row rows[s] (HOST array). */
+int apus_hip_attn_prefill_paged(const ApusHipAttnLayer *L, size_t B,
+                                const int32_t *rows, const int32_t *cu,
+                                const int32_t *pos0, const uint16_t *qg,
+                                const uint16_t *k, const uint16_t *v,
+                                const ApusHipKvCache *kv, uint16_t *y);
+int apus_hip_attn_decode_paged(const ApusHipAttnLayer *L, size_t B,
+                               const int32_t *rows, const int32_t *cu,
+                               const int32_t *pos0, const uint16_t *qg,
+                               const uint16_t *k, const uint16_t *v,
+                               const ApusHipKvCache *kv, uint16_t *y);
+
+/* ---- state managers (no counterpart in the reference; its engine keeps
+ * one sequence's state per layer, c/model.h:615-616) ----------------------
+ * KV pool: nlayers full-attention layers' block arrays of nblocks blocks
+ * each (32 positions x nkv x d, K and V) sharing one block table of
+ * max_rows rows x max_blocks entries. A sequence opens a row, reserves
+ * positions as it grows (blocks are taken from a free list; the table
+ * update is stream-ordered on the library stream) and closes the row when
+ * it ends; a rollback is a position rewind (pos0 of the next call), with
+ * no table change. apus_hip_kv_pool_cache gives layer l's ApusHipKvCache
+ * for the *_paged calls. Close a row only after the work that reads it has
+ * been enqueued before the next reserve of its blocks by another row (the
+ * library stream orders them). */
+typedef struct ApusHipKvPool ApusHipKvPool;
+int apus_hip_kv_pool_create(size_t nlayers, size_t nkv, size_t d, size_t nblocks,
+                            size_t max_rows, size_t max_blocks, ApusHipKvPool **out);
+int apus_hip_kv_pool_destroy(ApusHipKvPool *pool);
+int apus_hip_kv_pool_cache(const ApusHipKvPool *pool, size_t layer,
+                           ApusHipKvCache *out);
+int apus_hip_kv_seq_open(ApusHipKvPool *pool, int32_t *row);
+int apus_hip_kv_seq_reserve(ApusHipKvPool *pool, int32_t row, size_t ntok);
+int apus_hip_kv_seq_close(ApusHipKvPool *pool, int32_t row);
+size_t apus_hip_kv_pool_free_blocks(const ApusHipKvPool *pool);
+
+/* GDN state pool: nlayers GDN layers' slot arrays of nslots sequence
+ * states each (conv state + recurrent state); apus_hip_gdn_pool_state
+ * gives layer l's bases for the *_slots calls. A slot opened for a new
+ * sequence starts from zero state in every layer (c/layer.h:219-227,
+ * stream-ordered). */
+typedef struct ApusHipGdnPool ApusHipGdnPool;
+int apus_hip_gdn_pool_create(size_t nlayers, size_t hk, size_t hv, size_t dk,
+                             size_t dv, size_t nslots, ApusHipGdnPool **out);
+int apus_hip_gdn_pool_destroy(ApusHipGdnPool *pool);
+int apus_hip_gdn_pool_state(const ApusHipGdnPool *pool, size_t layer,
+                            uint16_t **conv, float **S);
+int apus_hip_gdn_slot_open(ApusHipGdnPool *pool, int32_t *slot);
+int apus_hip_gdn_slot_close(ApusHipGdnPool *pool, int32_t slot);
 
 /* ---- projections on either side of the path (c/bf16.h:178-231) --------
  * y[m][o] = rnd(sum_k w[o][k] * x[m][k]), w [O][K], x [M][K], y [M][O],

@@ -75,18 +75,20 @@ def _fill_caches(hip, torch, g, B, ctx, rows, max_seq):
     return dk, dv, off, hk, hv
 
 
-def _check_appended(dk, dv, hk, hv, off, pos0, k):
+def _check_appended(dk, dv, hk, hv, off, pos0, k, max_seq=None, hip=None):
     """The rows the mixer appended (positions pos0[s] .. pos0[s]+k[s]-1)
-    equal the oracle's, bit for bit."""
+    equal the oracle's, bit for bit (read back through the cache unpack)."""
+    import torch
     for s in range(len(pos0)):
         p0, p1 = int(pos0[s]), int(pos0[s]) + int(k[s])
-        Kd = _h(dk[s, :, p0:p1]).transpose(1, 0, 2)                 # [n, nkv, d]
-        blk = dv[s, :, p0 // 32:(p1 - 1) // 32 + 1]                   # [nkv, nb, d, 32]
-        Vd = _h(blk.permute(1, 3, 0, 2).reshape(-1, NKV, D))[p0 % 32:p0 % 32 + (p1 - p0)]
+        rk = torch.empty((p1, NKV, D), dtype=torch.int16, device="cuda")
+        rv = torch.empty_like(rk)
+        hip.attn_cache_unpack(dk[s], dv[s], p1, NKV, D, max_seq, rk, rv)
+        torch.cuda.synchronize()
         Ko = hk[off[s]:off[s + 1]].reshape(-1, NKV, D)[p0:p1]
         Vo = hv[off[s]:off[s + 1]].reshape(-1, NKV, D)[p0:p1]
-        assert np.array_equal(Kd, Ko), f"k cache rows of sequence {s}"
-        assert np.array_equal(Vd, Vo), f"v cache rows of sequence {s}"
+        assert np.array_equal(_h(rk[p0:p1]), Ko), f"k cache rows of sequence {s}"
+        assert np.array_equal(_h(rv[p0:p1]), Vo), f"v cache rows of sequence {s}"
 
 
 def _attn_decode_case(hip, orc, seed, ctx, k, tag):
@@ -114,7 +116,7 @@ def _attn_decode_case(hip, orc, seed, ctx, k, tag):
     y_o, qf, _, _ = orc.attn_mixer_off(synth.ATTN_DIMS, w, cu, pos0, tok["qg"], tok["k"],
                                        tok["v"], hk, hv, off[:-1], nthreads=NTHREADS,
                                        capture=True)
-    _check_appended(dk, dv, hk, hv, off, pos0, k)
+    _check_appended(dk, dv, hk, hv, off, pos0, k, max_seq, hip)
     esc = np.concatenate([
         attn_esc_rows(qf[cu[s]:cu[s + 1]], hk[off[s]:off[s + 1]].reshape(-1, NKV, D),
                       hv[off[s]:off[s + 1]].reshape(-1, NKV, D),
@@ -164,7 +166,7 @@ def test_attn_prefill_b260(hip, orc):
     y_o, qf, _, _ = orc.attn_mixer_off(synth.ATTN_DIMS, w, cu, ctx, tok["qg"], tok["k"],
                                        tok["v"], hk, hv, off[:-1], nthreads=NTHREADS,
                                        capture=True)
-    _check_appended(dk, dv, hk, hv, off, ctx, k)
+    _check_appended(dk, dv, hk, hv, off, ctx, k, max_seq, hip)
     esc = np.concatenate([
         attn_esc_rows(qf[cu[s]:cu[s + 1]], hk[off[s]:off[s + 1]].reshape(-1, NKV, D),
                       hv[off[s]:off[s + 1]].reshape(-1, NKV, D),
@@ -200,7 +202,7 @@ def test_config3_full_sampled(hip, orc):
     pos0 = np.zeros(1, np.int32)
     qn = orc.attn_prep_off(synth.ATTN_DIMS, w, cu, pos0, tok["qg"], tok["k"], tok["v"], kc, vc,
                            np.zeros(1, np.int64), nthreads=NTHREADS)
-    _check_appended(dk, dv, kc, vc, np.array([0, kc.size]), pos0, [T])
+    _check_appended(dk, dv, kc, vc, np.array([0, kc.size]), pos0, [T], T, hip)
     K = kc.reshape(T, NKV, D)
     V = vc.reshape(T, NKV, D)
     scale = np.float32(1.0 / 16.0)
@@ -276,7 +278,7 @@ def test_config4_full(hip, orc):
     y_o, qf, _, _ = orc.attn_mixer_off(synth.ATTN_DIMS, aw, cu, ctx, atok["qg"], atok["k"],
                                        atok["v"], hk, hv, off[:-1], nthreads=NTHREADS,
                                        capture=True)
-    _check_appended(dk, dv, hk, hv, off, ctx, k)
+    _check_appended(dk, dv, hk, hv, off, ctx, k, max_seq, hip)
     esc = np.concatenate([
         attn_esc_rows(qf[cu[s]:cu[s + 1]], hk[off[s]:off[s + 1]].reshape(-1, NKV, D),
                       hv[off[s]:off[s + 1]].reshape(-1, NKV, D),
