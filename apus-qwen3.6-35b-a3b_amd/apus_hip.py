@@ -45,7 +45,8 @@ EXPORTS = [
     "apus_hip_kv_seq_open", "apus_hip_kv_seq_reserve", "apus_hip_kv_seq_close",
     "apus_hip_kv_pool_free_blocks",
     "apus_hip_gdn_pool_create", "apus_hip_gdn_pool_destroy", "apus_hip_gdn_pool_state",
-    "apus_hip_gdn_slot_open", "apus_hip_gdn_slot_close",
+    "apus_hip_gdn_slot_open", "apus_hip_gdn_slot_close", "apus_hip_gdn_slot_load",
+    "apus_hip_gdn_slot_store",
 ]
 
 
@@ -503,6 +504,14 @@ class GdnPool:
 
     def close(self, slot):
         _chk(load().apus_hip_gdn_slot_close(self.h, C.c_int32(slot)))
+
+    def load_state(self, layer, slot, conv, S):
+        """Import one sequence's state (device tensors, reference layout:
+        conv [conv_dim*3] codes, S [hv, dk, dv] f32) into a slot."""
+        _chk(load().apus_hip_gdn_slot_load(self.h, _sz(layer), C.c_int32(slot), _dp(conv), _dp(S)))
+
+    def store_state(self, layer, slot, conv, S):
+        _chk(load().apus_hip_gdn_slot_store(self.h, _sz(layer), C.c_int32(slot), _dp(conv), _dp(S)))
 
     def destroy(self):
         if self.h:

@@ -422,17 +422,21 @@ __device__ __forceinline__ void scores_seg(const Meta &mt, const Seg &c,
     // 8 loads are in flight (the loads are unconditional: the prefetch past
     // the segment's end re-reads its last row), so the stream never drains
     // between groups.
+    // block bases of groups g0 (pA, pB), g0 + 64 (qA, qB); the lookups for
+    // g0 + 128 are issued after the group's LDS count read, so their
+    // scalar-load latency is never part of an LDS wait
     int bA = min(c.k0 >> 5, blast);
     const uint16_t *pA = kblock(kv, mt, c, nkv, bA), *pB = kblock(kv, mt, c, nkv, min(bA + 1, blast));
+    int nA = min((c.k0 + 64) >> 5, blast);
+    const uint16_t *qA = kblock(kv, mt, c, nkv, nA), *qB = kblock(kv, mt, c, nkv, min(nA + 1, blast));
     bf16x8 kA[D / 32], kB[D / 32];
     load_k(c.k0, 0, bA, pA, pB, kA);
     for (int g0 = c.k0; g0 < c.k1; g0 += 64, grp++) {
-        // the next group's blocks (clamped to the segment's last one)
-        const int nA = min((g0 + 64) >> 5, blast);
-        const uint16_t *qA = kblock(kv, mt, c, nkv, nA), *qB = kblock(kv, mt, c, nkv, min(nA + 1, blast));
         // the writer must have drained this group's ring slot (read early;
         // it is normally long done)
         const int dn = lds_count_load(donew);
+        const int mA = min((g0 + 128) >> 5, blast);
+        const uint16_t *rA = kblock(kv, mt, c, nkv, mA), *rB = kblock(kv, mt, c, nkv, min(mA + 1, blast));
         uint32_t sc[NR][8];                  // bf16 score codes, two per word
         auto mma = [&](int j, const bf16x8 *kf) {
             f32x4 acc[NR];
@@ -462,6 +466,9 @@ __device__ __forceinline__ void scores_seg(const Meta &mt, const Seg &c,
         bA = nA;
         pA = qA;
         pB = qB;
+        nA = mA;
+        qA = rA;
+        qB = rB;
 
         // publish the group's scores to the writer through the ring
         if (grp >= kScRing && dn <= grp - kScRing)

@@ -213,28 +213,55 @@ void k_gdn_decode(
         __syncthreads();
         qkn[tid] = tid < DK ? (raw[tid] * rsq[0]) * qscale : raw[tid] * rsq[1];
         __syncthreads();
-        // c/gdn.h:482-503 on column j, with k and q broadcast by readlane
-        const float k0 = qkn[DK + lane], k1 = qkn[DK + 64 + lane];
-        const float qa = qkn[lane], qb = qkn[64 + lane];
+        // c/gdn.h:482-503 on column j. k and q reach every lane as LDS
+        // broadcast reads, four values per 16-byte read, so the VALU only
+        // does the seven operations per state element the reference's
+        // rounding order needs (a readlane per broadcast value would add
+        // three VALU operations per element).
+        const float4 *K4 = reinterpret_cast<const float4 *>(qkn + DK);
+        const float4 *Q4 = reinterpret_cast<const float4 *>(qkn);
         const float2 gb = gt[r];
+        // The reads run two groups of four ahead; a scheduling barrier per
+        // group keeps the compiler from hoisting all of them (the state
+        // slice already holds 128 registers).
         float kv = 0.0f;
+        float4 kn0 = K4[0], kn1 = K4[1];
 #pragma unroll
-        for (int i = 0; i < DK; i++) {
-            const float ki = lane_bcast(i < 64 ? k0 : k1, i & 63);
-            sr[i] = sr[i] * gb.x;
-            kv = kv + ki * sr[i];
+        for (int i4 = 0; i4 < DK / 4; i4++) {
+            const float4 kk = kn0;
+            kn0 = kn1;
+            if (i4 + 2 < DK / 4) kn1 = K4[i4 + 2];
+            const float ke[4] = {kk.x, kk.y, kk.z, kk.w};
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const int i = 4 * i4 + e;
+                sr[i] = sr[i] * gb.x;
+                kv = kv + ke[e] * sr[i];
+            }
+            __builtin_amdgcn_sched_barrier(0);
         }
         const float delta = (bf2f(cvv) - kv) * gb.y;
-        // opaque copy: keeps the first pass's 128 broadcasts from staying live
-        float k0b = k0, k1b = k1;
-        asm volatile("" : "+v"(k0b), "+v"(k1b));
         float acc = 0.0f;
+        kn0 = K4[0];
+        kn1 = K4[1];
+        float4 qn0 = Q4[0], qn1 = Q4[1];
 #pragma unroll
-        for (int i = 0; i < DK; i++) {
-            const float ki = lane_bcast(i < 64 ? k0b : k1b, i & 63);
-            const float qi = lane_bcast(i < 64 ? qa : qb, i & 63);
-            sr[i] = sr[i] + ki * delta;
-            acc = acc + qi * sr[i];
+        for (int i4 = 0; i4 < DK / 4; i4++) {
+            const float4 kk = kn0, qq = qn0;
+            kn0 = kn1;
+            qn0 = qn1;
+            if (i4 + 2 < DK / 4) {
+                kn1 = K4[i4 + 2];
+                qn1 = Q4[i4 + 2];
+            }
+            const float ke[4] = {kk.x, kk.y, kk.z, kk.w}, qe[4] = {qq.x, qq.y, qq.z, qq.w};
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const int i = 4 * i4 + e;
+                sr[i] = sr[i] + ke[e] * delta;
+                acc = acc + qe[e] * sr[i];
+            }
+            __builtin_amdgcn_sched_barrier(0);
         }
         const float o = rndf(acc);
         ob[r][j] = o;

@@ -243,6 +243,37 @@ int apus_hip_gdn_slot_open(ApusHipGdnPool *p, int32_t *slot) {
     return kOk;
 }
 
+// Copy one sequence's state between a slot of one layer and caller arrays
+// in the reference layout (conv [conv_dim*3] bf16, S [hv][dk][dv] f32;
+// device pointers), stream-ordered.
+static int slot_xfer(ApusHipGdnPool *p, size_t layer, int32_t slot, bool load, uint16_t *conv,
+                     float *S) {
+    if (!p || layer >= p->nlayers || slot < 0 || (size_t)slot >= p->nslots || !p->used[slot])
+        return set_error(kErrArgument, "bad layer or slot %d is not open", slot);
+    if (!conv || !S) return set_error(kErrArgument, "NULL state array");
+    uint16_t *pc = p->conv[layer] + (size_t)slot * p->cd * 3;
+    float *pS = p->S[layer] + (size_t)slot * p->hv * p->dk * p->dv;
+    const size_t cb = p->cd * 3 * 2;
+    if (load) {
+        APUS_HIP_TRY(hipMemcpyAsync(pc, conv, cb, hipMemcpyDeviceToDevice, stream()));
+        return apus_hip_gdn_state_pack(S, pS, p->hv);
+    }
+    APUS_HIP_TRY(hipMemcpyAsync(conv, pc, cb, hipMemcpyDeviceToDevice, stream()));
+    return apus_hip_gdn_state_unpack(pS, S, p->hv);
+}
+
+int apus_hip_gdn_slot_load(ApusHipGdnPool *p, size_t layer, int32_t slot,
+                           const uint16_t *conv, const float *S) {
+    APUS_READY();
+    return slot_xfer(p, layer, slot, true, const_cast<uint16_t *>(conv), const_cast<float *>(S));
+}
+
+int apus_hip_gdn_slot_store(ApusHipGdnPool *p, size_t layer, int32_t slot, uint16_t *conv,
+                            float *S) {
+    APUS_READY();
+    return slot_xfer(p, layer, slot, false, conv, S);
+}
+
 int apus_hip_gdn_slot_close(ApusHipGdnPool *p, int32_t slot) {
     if (!p || slot < 0 || (size_t)slot >= p->nslots || !p->used[slot])
         return set_error(kErrArgument, "slot %d is not open", slot);

@@ -541,42 +541,66 @@ def bench_mixed_block(torch, B, steps, warmup, seed, leg=None):
     recurrent state per sequence) and one gated-GQA layer (a bf16 KV cache
     per sequence) -- over B sequences that each verify 1..4 tokens at a
     log-normal cached context. value = verified tokens per second through
-    the block. The recurrent states (3 x 256 MB) and caches (GBs) exceed
-    the Infinity Cache, so one input set is used."""
+    the block. The states live as a serving engine keeps them: the GDN
+    states in a slot pool (apus_hip_gdn_pool_*, slots in shuffled order)
+    and the KV cache in 32-position blocks of a paged pool sized to the
+    contexts (apus_hip_kv_pool_*; blocks handed out interleaved across
+    sequences, no per-sequence maximum reserved). The recurrent states
+    (3 x 256 MB) and caches (GBs) exceed the Infinity Cache, so one input
+    set is used."""
     import apus_hip
     import synth
     g, bf = _bf_gen(torch, seed)
+    rng = np.random.default_rng(seed)
     ctx, k = synth.mixed_block_shape(B, seed)
     cu = np.concatenate([[0], np.cumsum(k)]).astype(np.int32)
     T = int(cu[-1])
+    gpool = apus_hip.GdnPool(3, GDN, B + 8)
+    opened = [gpool.open() for _ in range(B + 8)]
+    slots = [opened[i] for i in rng.permutation(B + 8)[:B]]
     gdn = []
-    for _ in range(3):
+    for li in range(3):
         w = dict(conv_w=bf((CD, 4), 0.1), A_log=torch.rand(HV, generator=g, device="cuda") * 2.7,
                  dt_bias=torch.ones(HV, device="cuda"), onorm_w=bf((DV,), 0.1, 1.0))
+        conv, S = gpool.state(li)
         gdn.append(dict(layer=apus_hip.gdn_layer(GDN, w), w=w, qkv=bf((T, CD)), z=bf((T, VD)),
-                        a=bf((T, HV)), b=bf((T, HV)), conv=bf((B, CD * 3)),
-                        S=torch.randn((B, HV, DK, DV), generator=g, device="cuda") * 0.02,
+                        a=bf((T, HV)), b=bf((T, HV)), conv=conv, S=S,
                         y=torch.empty((T, VD), dtype=torch.int16, device="cuda")))
+        for sl in slots:                    # prior state: conv ~ N(0,1), S ~ N(0, 0.02)
+            gpool.load_state(li, sl, bf((CD * 3,)),
+                             torch.randn((HV, DK, DV), generator=g, device="cuda") * 0.02)
     aw = dict(qn_w=bf((AD,), 0.1), kn_w=bf((AD,), 0.1))
     alayer = apus_hip.attn_layer(ATTN, aw)
-    max_seq = int(-(-int((ctx + k).max()) // 32) * 32)
+    nblk = -(-(ctx + k) // 32)
+    kpool = apus_hip.KvPool(1, NKV, AD, int(nblk.sum()), B, int(nblk.max()))
+    rows = [kpool.open() for _ in range(B)]
+    have = np.zeros(B, np.int64)
+    while (have < nblk).any():                  # blocks interleaved across sequences
+        for s in rng.permutation(B):
+            if have[s] < nblk[s]:
+                have[s] += 1
+                kpool.reserve(rows[s], int(have[s]) * 32)
+    kv = kpool.cache(0)
+
     # caches filled with finite random bf16 codes, |x| in [2^-8, 2) with
-    # random signs, without an fp32 temporary of the caches' size
+    # random signs
     def codes(shape):
         x = torch.randint(0x3B80, 0x4000, shape, dtype=torch.int16, device="cuda", generator=g)
         sign = torch.randint(0, 2, shape, dtype=torch.int16, device="cuda", generator=g) << 15
         return x.bitwise_or_(sign)
-    kc = codes((B, NKV, max_seq, AD))
-    vc = codes((B, NKV, max_seq // 32, AD, 32))
+    for s in range(B):
+        apus_hip.attn_cache_pack_paged(codes((int(ctx[s]), NKV, AD)), codes((int(ctx[s]), NKV, AD)),
+                                       int(ctx[s]), NKV, AD, kv, rows[s])
     att = dict(qg=bf((T, NH, 2 * AD)), k=bf((T, NKV, AD)), v=bf((T, NKV, AD)),
                y=torch.empty((T, NH * AD), dtype=torch.int16, device="cuda"))
+    torch.cuda.synchronize()
 
     def step(i):
         for L in gdn:
-            apus_hip.gdn_decode(L["layer"], cu, L["qkv"], L["z"], L["a"], L["b"], L["conv"],
-                                L["S"], L["y"])
-        apus_hip.attn_decode(alayer, cu, ctx, att["qg"], att["k"], att["v"], kc, vc, max_seq,
-                             att["y"])
+            apus_hip.gdn_decode_slots(L["layer"], slots, slots, cu, L["qkv"], L["z"], L["a"],
+                                      L["b"], L["conv"], L["S"], L["y"])
+        apus_hip.attn_decode_paged(alayer, rows, cu, ctx, att["qg"], att["k"], att["v"], kv,
+                                   att["y"])
 
     gdn_bytes = sum(gdn_seq_bytes(int(x)) for x in k) + GDN_WEIGHT_BYTES
     attn_bytes = sum(attn_decode_bytes(int(c) + int(x), int(x)) for c, x in zip(ctx, k)) + 2 * AD * 2
@@ -595,22 +619,46 @@ def bench_mixed_block(torch, B, steps, warmup, seed, leg=None):
              ctx_mean=float(ctx.mean()), ctx_max=int(ctx.max()), verify_tokens=T,
              shape="ctx ~ LogNormal(ln 4096, 1.0) clipped to [256, 65536], 1..4 verify tokens, "
                    f"seed {seed}",
+             state="GDN slot pool (shuffled slots), paged KV pool of "
+                   f"{int(nblk.sum())} 32-position blocks (interleaved)",
              tok_s=T * steps / total, layer_hbm_gbs=bytes_ / st / 1e9,
              layer_hbm_frac=bytes_ / st / HBM_PEAK,
              roofline=kernel_roofline(kt, table, wl))
     if leg:
-        pre = [(_h16(L["conv"]), _gdn_state_host(torch, L["S"])) for L in gdn]
+        def slot_states(li):
+            conv = torch.empty((B, CD * 3), dtype=torch.int16, device="cuda")
+            S = torch.empty((B, HV, DK, DV), dtype=torch.float32, device="cuda")
+            for i, sl in enumerate(slots):
+                gpool.store_state(li, sl, conv[i], S[i])
+            return conv, S
+        pre = []
+        for li in range(3):
+            c0, S0 = slot_states(li)
+            torch.cuda.synchronize()
+            pre.append((_h16(c0), S0.cpu().numpy()))
         step(0)
         par = {}
         for i, L in enumerate(gdn):
+            c1, S1r = slot_states(i)
+            S1 = torch.empty_like(S1r)
+            apus_hip.gdn_state_pack(S1r, S1)        # the checker unpacks the device layout
             par[f"gdn{i}"] = leg.gdn(torch, L["w"], cu, {n: L[n] for n in ("qkv", "z", "a", "b")},
-                                     pre[i][0], pre[i][1], L["y"], L["conv"], L["S"])
-        caches = _host_caches(torch, kc, vc, max_seq, ctx + k)
+                                     pre[i][0], pre[i][1], L["y"], c1, S1)
+        caches = []
+        for s in range(B):
+            n = int(ctx[s] + k[s])
+            rk = torch.empty((n, NKV, AD), dtype=torch.int16, device="cuda")
+            rv = torch.empty_like(rk)
+            apus_hip.attn_cache_unpack_paged(kv, rows[s], n, NKV, AD, rk, rv)
+            torch.cuda.synchronize()
+            caches.append((_h16(rk), _h16(rv)))
         par["attn"] = leg.attn(torch, aw, cu, ctx, {n: att[n] for n in ("qg", "k", "v")}, caches,
                                att["y"])
         par["pass"] = all(v["pass"] for v in par.values())
         par["sample"] = "the whole block step (all 128 sequences, every layer)"
         r["parity"] = par
+    kpool.destroy()
+    gpool.destroy()
     return r
 
 

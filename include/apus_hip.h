@@ -353,6 +353,14 @@ int apus_hip_gdn_pool_state(const ApusHipGdnPool *pool, size_t layer,
                             uint16_t **conv, float **S);
 int apus_hip_gdn_slot_open(ApusHipGdnPool *pool, int32_t *slot);
 int apus_hip_gdn_slot_close(ApusHipGdnPool *pool, int32_t slot);
+/* Copy one sequence's state of one layer between an open slot and arrays
+ * in the reference layout (conv [conv_dim*3] bf16, S [hv][dk][dv] f32,
+ * c/layer.h:159-162; DEVICE pointers): load imports a state (a snapshot,
+ * or one computed elsewhere), store exports it. Stream-ordered. */
+int apus_hip_gdn_slot_load(ApusHipGdnPool *pool, size_t layer, int32_t slot,
+                           const uint16_t *conv, const float *S);
+int apus_hip_gdn_slot_store(ApusHipGdnPool *pool, size_t layer, int32_t slot,
+                            uint16_t *conv, float *S);
 
 /* ---- projections on either side of the path (c/bf16.h:178-231) --------
  * y[m][o] = rnd(sum_k w[o][k] * x[m][k]), w [O][K], x [M][K], y [M][O],
