@@ -47,6 +47,9 @@ EXPORTS = [
     "apus_hip_gdn_pool_create", "apus_hip_gdn_pool_destroy", "apus_hip_gdn_pool_state",
     "apus_hip_gdn_slot_open", "apus_hip_gdn_slot_close", "apus_hip_gdn_slot_load",
     "apus_hip_gdn_slot_store",
+    "apus_hip_st_open", "apus_hip_st_close", "apus_hip_st_ntensors", "apus_hip_st_find",
+    "apus_hip_st_read", "apus_hip_gdn_layer_load", "apus_hip_attn_layer_load",
+    "apus_hip_gdn_layer_free", "apus_hip_attn_layer_free", "apus_hip_trace_set",
 ]
 
 
@@ -101,6 +104,7 @@ def load(path=None):
             getattr(_lib, name).restype = C.c_int
         _lib.apus_hip_last_error.restype = _sz
         _lib.apus_hip_kv_pool_free_blocks.restype = _sz
+        _lib.apus_hip_st_ntensors.restype = _sz
     return _lib
 
 
@@ -517,3 +521,94 @@ class GdnPool:
         if self.h:
             _chk(load().apus_hip_gdn_pool_destroy(self.h))
             self.h = C.c_void_p()
+
+
+# ---- weight container reader
+ST_DTYPES = {0: "I8", 1: "U8", 2: "F8_E8M0", 3: "F8_E4M3", 4: "BF16", 5: "F16", 6: "F32",
+             7: "I32", 8: "I64", 9: "OTHER"}
+
+
+class StTensor(C.Structure):
+    """ApusHipStTensor (include/apus_hip.h)."""
+    _fields_ = [("name", C.c_char * 160), ("dtype", C.c_int), ("ndim", C.c_int),
+                ("shape", C.c_int64 * 8), ("nbytes", _sz)]
+
+
+class Container:
+    """apus_hip_st_*: a safetensors shard or a directory with
+    model.safetensors.index.json (host-side; no device needed)."""
+
+    def __init__(self, path):
+        self.h = C.c_void_p()
+        _chk(load().apus_hip_st_open(os.fsencode(path), C.byref(self.h)))
+
+    def __len__(self):
+        return load().apus_hip_st_ntensors(self.h)
+
+    def find(self, name):
+        t = StTensor()
+        _chk(load().apus_hip_st_find(self.h, name.encode(), C.byref(t)))
+        return dict(name=t.name.decode(), dtype=ST_DTYPES[t.dtype],
+                    shape=tuple(t.shape[i] for i in range(t.ndim)), nbytes=t.nbytes)
+
+    def read(self, name):
+        """The payload as raw bytes (numpy uint8)."""
+        info = self.find(name)
+        buf = np.empty(info["nbytes"], np.uint8)
+        _chk(load().apus_hip_st_read(self.h, name.encode(), buf.ctypes.data_as(_vp),
+                                     _sz(buf.size)))
+        return buf
+
+    def gdn_layer(self, layer, dims):
+        """GdnLayer with device copies of layer `layer`'s weights (free with
+        free_gdn_layer)."""
+        hk, hv, dk, dv = dims
+        L = GdnLayer()
+        _chk(load().apus_hip_gdn_layer_load(self.h, C.c_int(layer), _sz(hk), _sz(hv), _sz(dk),
+                                            _sz(dv), C.byref(L)))
+        return L
+
+    def attn_layer(self, layer, dims):
+        nh, nkv, d, rot, theta = dims
+        L = AttnLayer()
+        _chk(load().apus_hip_attn_layer_load(self.h, C.c_int(layer), _sz(nh), _sz(nkv), _sz(d),
+                                             _sz(rot), C.c_double(theta), C.byref(L)))
+        return L
+
+    def close(self):
+        if self.h:
+            _chk(load().apus_hip_st_close(self.h))
+            self.h = C.c_void_p()
+
+
+def free_gdn_layer(L):
+    _chk(load().apus_hip_gdn_layer_free(C.byref(L)))
+
+
+def free_attn_layer(L):
+    _chk(load().apus_hip_attn_layer_free(C.byref(L)))
+
+
+# ---- named-intermediate capture
+class GdnTrace(C.Structure):
+    """ApusHipGdnTrace (include/apus_hip.h)."""
+    _fields_ = [("qkv_conv", _vp), ("beta", _vp), ("gdecay", _vp), ("rec_o", _vp),
+                ("onorm", _vp)]
+
+
+class AttnTrace(C.Structure):
+    """ApusHipAttnTrace (include/apus_hip.h)."""
+    _fields_ = [("qf", _vp), ("kf", _vp), ("attno", _vp), ("mgate", _vp)]
+
+
+def trace_set(gdn=None, attn=None):
+    """gdn / attn: dicts of device tensors by field name (missing fields are
+    not captured), or None to stop tracing that mixer."""
+    def mk(cls, d):
+        if d is None:
+            return None
+        return cls(*[_dp(d.get(f)) for f, _ in cls._fields_])
+    g, a = mk(GdnTrace, gdn), mk(AttnTrace, attn)
+    trace_set._keep = (gdn, attn)      # the tensors must outlive the trace
+    _chk(load().apus_hip_trace_set(C.byref(g) if g is not None else None,
+                                   C.byref(a) if a is not None else None))

@@ -280,6 +280,15 @@ const uint16_t *rope_table(size_t rot, double theta, size_t max_pos) {
     return g_rope.dev;
 }
 
+namespace {
+ApusHipGdnTrace g_gdn_trace;
+ApusHipAttnTrace g_attn_trace;
+bool g_gdn_traced = false, g_attn_traced = false;
+}  // namespace
+
+const ApusHipGdnTrace *gdn_trace() { return g_gdn_traced ? &g_gdn_trace : nullptr; }
+const ApusHipAttnTrace *attn_trace() { return g_attn_traced ? &g_attn_trace : nullptr; }
+
 int timing_begin(const char *name) {
     if (!g_timing) return -1;
     size_t i = 0;
@@ -383,6 +392,14 @@ int apus_hip_timing_get(const char *name, double *total_ms, size_t *count) {
         }
         *count = k.ev.size();
     }
+    return kOk;
+}
+
+int apus_hip_trace_set(const ApusHipGdnTrace *gdn, const ApusHipAttnTrace *attn) {
+    g_gdn_traced = gdn != nullptr;
+    g_attn_traced = attn != nullptr;
+    if (gdn) g_gdn_trace = *gdn;
+    if (attn) g_attn_trace = *attn;
     return kOk;
 }
 

@@ -11,6 +11,8 @@
 #include <stddef.h>
 #include <stdint.h>
 
+#include "../../include/apus_hip.h"
+
 namespace apus {
 
 enum Status : int {
@@ -74,6 +76,10 @@ const void *upload_async(const void *host, size_t bytes);
 // host -> device copy into caller memory, stream-ordered, without waiting
 // (staged through the ring).
 int copy_to_device_async(void *dst, const void *host, size_t bytes);
+
+// The trace sinks set by apus_hip_trace_set (nullptr when tracing is off).
+const ApusHipGdnTrace *gdn_trace();
+const ApusHipAttnTrace *attn_trace();
 
 // Opt-in per-kernel timing: when enabled (apus_hip_timing_enable), a pair
 // of events is recorded on the library stream around each wrapped launch;

@@ -99,7 +99,7 @@ __global__ __launch_bounds__(256) void k_attn_prep(
     AttnSeqs sq, const int32_t *__restrict__ dmeta, const uint16_t *__restrict__ qg,
     const uint16_t *__restrict__ kin, const uint16_t *__restrict__ qn_w,
     const uint16_t *__restrict__ kn_w, const uint16_t *__restrict__ rope, KvRef kv,
-    uint16_t *__restrict__ qn, int nh, int nkv, int nrows, int rpb) {
+    uint16_t *__restrict__ qn, int nh, int nkv, int nrows, int rpb, uint16_t *__restrict__ tr_kf) {
     const Meta mt = meta_of(sq, dmeta);
     const int32_t *cu = mt.cu, *pos0 = mt.pos0;
     const int nslot = nh + nkv;
@@ -208,6 +208,8 @@ __global__ __launch_bounds__(256) void k_attn_prep(
                             : kv.k + ((kv_block_id(kv, mt.hd[rseq[r]], rpos[r] / KVB) * nkv +
                                        (slot - nh)) * KVB + rpos[r] % KVB) * D;
         *reinterpret_cast<u16x8 *>(dst + p * 8) = out;
+        if (!isq && tr_kf)                    // (trace) the appended k row
+            *reinterpret_cast<u16x8 *>(tr_kf + ((size_t)tt * nkv + (slot - nh)) * D + p * 8) = out;
     }
 }
 
@@ -787,7 +789,7 @@ __global__ __launch_bounds__(64) void k_attn_pv(
 __global__ __launch_bounds__(D) void k_attn_combine(
     AttnSeqs sq, const int32_t *__restrict__ dmeta, const float *__restrict__ Op,
     const uint16_t *__restrict__ qg, int nh, int nkv, uint16_t *__restrict__ y,
-    const uint16_t *__restrict__ sig_bf) {
+    const uint16_t *__restrict__ sig_bf, uint16_t *__restrict__ tr_attno) {
     const Meta mt = meta_of(sq, dmeta);
     const int32_t *cu = mt.cu;
     const int tt = blockIdx.x / nh, h = blockIdx.x % nh;
@@ -810,6 +812,17 @@ __global__ __launch_bounds__(D) void k_attn_combine(
     const float o = rndf(sum);
     const float gt = bf2f(sig_bf[qg[((size_t)tt * nh + h) * 2 * D + D + dd]]);  // rnd(sigmoid)
     y[((size_t)tt * nh + h) * D + dd] = f2bf(o * gt);
+    if (tr_attno) tr_attno[((size_t)tt * nh + h) * D + dd] = f2bf(o);      // (trace)
+}
+
+// (trace) mgate = rnd(sigmoid(gate)) for every (token, head, d)
+__global__ void k_trace_mgate(const uint16_t *__restrict__ qg, size_t n, int nh,
+                              const uint16_t *__restrict__ sig_bf, uint16_t *__restrict__ mg) {
+    const size_t e = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (e >= n) return;
+    const size_t row = e / D, dd = e % D;     // row = token * nh + head
+    mg[e] = sig_bf[qg[row * 2 * D + D + dd]];
+    (void)nh;
 }
 
 // ---- cache layout conversion (one sequence: block-table row h) ---------
@@ -920,8 +933,21 @@ int attn_prep(const ApusHipAttnLayer *L, const AttnSeqs &sq, const int32_t *dmet
     APUS_TIMED("k_attn_prep",
                k_attn_prep<<<cdiv(nrows, rpb), 256, 0, stream()>>>(
         sq, dmeta, qg, k, L->qn_w, L->kn_w, rope, kv, qn, (int)L->nh, (int)L->nkv, (int)nrows,
-        rpb));
+        rpb, attn_trace() ? attn_trace()->kf : nullptr));
     if (int r = launch_check("k_attn_prep")) return r;
+    if (const ApusHipAttnTrace *tr = attn_trace()) {
+        if (tr->qf)
+            APUS_HIP_TRY(hipMemcpyAsync(tr->qf, qn, Ttot * L->nh * D * 2, hipMemcpyDeviceToDevice,
+                                        stream()));
+        if (tr->mgate) {
+            const ActTables *tabs = act_tables();
+            if (!tabs) return kErrHip;
+            const size_t n = Ttot * L->nh * D;
+            k_trace_mgate<<<cdiv(n, 256), 256, 0, stream()>>>(qg, n, (int)L->nh, tabs->sig_bf,
+                                                               tr->mgate);
+            if (int r = launch_check("k_trace_mgate")) return r;
+        }
+    }
     APUS_TIMED("k_attn_vappend",
                k_attn_vappend<<<(unsigned)(sq.n * L->nkv * maxnb), 256, 0, stream()>>>(
         sq, dmeta, v, kv, (int)L->nkv, maxnb));
@@ -992,7 +1018,8 @@ int attn_decode_kv(const ApusHipAttnLayer *L, size_t B, const int32_t *cu, const
     }
     APUS_TIMED("k_attn_combine",
                k_attn_combine<<<(unsigned)(Ttot * L->nh), D, 0, stream()>>>(
-                   sq, dmeta, Op, qg, (int)L->nh, (int)nkv, y, tabs->sig_bf));
+                   sq, dmeta, Op, qg, (int)L->nh, (int)nkv, y, tabs->sig_bf,
+                   attn_trace() ? attn_trace()->attno : nullptr));
     APUS_LAUNCHED("k_attn_combine");
     return kOk;
 }

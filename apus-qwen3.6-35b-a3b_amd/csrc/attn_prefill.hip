@@ -451,7 +451,7 @@ __device__ __forceinline__ void fa_publish() {
 __global__ __launch_bounds__(64 * NW) void k_attn_fa(
     FaSeqs sq, const int32_t *__restrict__ dmeta, const uint16_t *__restrict__ qn,
     const uint16_t *__restrict__ qg, KvRef kv, int nh, int nkv, float scale,
-    uint16_t *__restrict__ y, const uint16_t *__restrict__ sig_bf) {
+    uint16_t *__restrict__ y, const uint16_t *__restrict__ sig_bf, uint16_t *__restrict__ tr_attno) {
     const int n = sq.n;
     const int32_t *cu = dmeta ? dmeta : sq.cu;
     const int32_t *pos0 = dmeta ? dmeta + n + 1 : sq.pos0;
@@ -597,14 +597,16 @@ __global__ __launch_bounds__(64 * NW) void k_attn_fa(
             for (int q4 = 0; q4 < 4; q4++) {
                 const int d0 = mt * 32 + 8 * q4 + 4 * c.h;
                 const u16x4 gv = *reinterpret_cast<const u16x4 *>(gr + d0);
-                u16x4 out;
+                u16x4 out, oc;
 #pragma unroll
                 for (int i = 0; i < 4; i++) {
                     const float ov = rndf(o[mt][4 * q4 + i]);
                     const float gs = bf2f(sig_bf[gv[i]]);     // rnd(sigmoid(gate))
                     out[i] = f2bf(ov * gs);
+                    oc[i] = f2bf(ov);
                 }
                 *reinterpret_cast<u16x4 *>(yr + d0) = out;
+                if (tr_attno) *reinterpret_cast<u16x4 *>(tr_attno + row * D + d0) = oc;   // (trace)
             }
         }
     }
@@ -663,7 +665,8 @@ int attn_prefill_kv(const ApusHipAttnLayer *L, size_t B, const int32_t *cu, cons
     if (!tabs) return kErrHip;
     APUS_TIMED("k_attn_fa",
                k_attn_fa<<<(unsigned)(ntiles * L->nkv), 64 * NW, 0, stream()>>>(
-                   fs, fdm, qn, qg, kv, (int)L->nh, (int)L->nkv, scale, y, tabs->sig_bf));
+                   fs, fdm, qn, qg, kv, (int)L->nh, (int)L->nkv, scale, y, tabs->sig_bf,
+                   attn_trace() ? attn_trace()->attno : nullptr));
     APUS_LAUNCHED("k_attn_fa");
     return kOk;
 }

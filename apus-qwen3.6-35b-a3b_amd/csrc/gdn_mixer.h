@@ -33,7 +33,7 @@ int gdn_check_offsets(size_t B, const int32_t *cu);
 int gdn_prep(const ApusHipGdnLayer *L, size_t B, const int32_t *cu, const int32_t *dcu,
              size_t Ttot, const uint16_t *qkv, const uint16_t *a,
              const uint16_t *b, const uint16_t *conv_state, GdnScratch *w,
-             bool want_graw, const int32_t *slots);
+             bool want_graw, const int32_t *slots, const ApusHipGdnTrace *tr = nullptr);
 // gated RMSNorm of w->ob into y, then the new conv state
 int gdn_post(const ApusHipGdnLayer *L, size_t B, const int32_t *cu, const int32_t *dcu,
              size_t Ttot, const GdnScratch *w, const uint16_t *z,

@@ -109,7 +109,8 @@ void k_gdn_decode(
     const uint16_t *a, const uint16_t *b, const uint16_t *conv_w,
     const float *A_log, const float *dt_bias, const uint16_t *onorm_w,
     const uint16_t *conv_state, const float *S, uint16_t *conv_out, float *S_out,
-    uint16_t *y, int hk, float qscale, const int32_t *slot_in, const int32_t *slot_out) {
+    uint16_t *y, int hk, float qscale, const int32_t *slot_in, const int32_t *slot_out,
+    uint16_t *tr_ob) {
     // (no __restrict__ on the small operands: it would let the compiler sink
     // their loads past the ordering barrier below the state loads)
     const int s = blockIdx.x / hk, kh = blockIdx.x % hk;
@@ -265,6 +266,7 @@ void k_gdn_decode(
         }
         const float o = rndf(acc);
         ob[r][j] = o;
+        if (tr_ob) tr_ob[(size_t)t * vd + (size_t)h * DV + j] = f2bf(o);   // (trace) rec_o
         __syncthreads();
         if (tid == 0 || tid == DK)
             rso[tid / DK] = 1.0f / sqrtf(seq_sumsq(ob[tid / DK], DV) / (float)DV + kEps);
@@ -340,7 +342,8 @@ __global__ __launch_bounds__(256) void k_gdn_prep(
     float *__restrict__ qk, uint16_t *__restrict__ vconv,
     float2 *__restrict__ gate, float *__restrict__ graw, int hk, float qscale,
     const uint16_t *__restrict__ silu_bf, const uint16_t *__restrict__ sig_bf,
-    const int32_t *__restrict__ slots) {
+    const int32_t *__restrict__ slots, uint16_t *__restrict__ tr_conv,
+    uint16_t *__restrict__ tr_beta) {
     typedef unsigned short u16x8 __attribute__((ext_vector_type(8)));
     const int32_t *cu = dcu ? dcu : ci.cu;
     const int tile = blockIdx.x / hk, kh = blockIdx.x % hk;
@@ -465,6 +468,10 @@ __global__ __launch_bounds__(256) void k_gdn_prep(
         if (i < nt) {
             rrow[i * RS] = bf2f(sq[i]);
             vconv[(size_t)(tb + i) * vd + (size_t)h * DV + j] = sv[i];
+            if (tr_conv) {                    // (trace) conv+SiLU codes, c/layer.h:178
+                tr_conv[(size_t)(tb + i) * cd + cqk] = sq[i];
+                tr_conv[(size_t)(tb + i) * cd + cv] = sv[i];
+            }
         }
     }
     __syncthreads();
@@ -478,9 +485,11 @@ __global__ __launch_bounds__(256) void k_gdn_prep(
         if (r < nt) {
             const size_t t = (size_t)(tb + r);
             const float g = decay_of(a[t * hv + hh], A_log[hh], dt_bias[hh]);
-            const float bt = bf2f(sig_bf[b[t * hv + hh]]);
+            const uint16_t btc = sig_bf[b[t * hv + hh]];
+            const float bt = bf2f(btc);
             gate[t * hv + hh] = make_float2(exp_cr(g), bt);
             if (graw) graw[t * hv + hh] = g;
+            if (tr_beta) tr_beta[t * hv + hh] = btc;
         }
     }
     __syncthreads();
@@ -605,7 +614,7 @@ static bool gdn_cu_arg(size_t B, const int32_t *cu, const int32_t *dcu, GdnCu *c
 int gdn_prep(const ApusHipGdnLayer *L, size_t B, const int32_t *cu, const int32_t *dcu,
              size_t Ttot, const uint16_t *qkv, const uint16_t *a,
              const uint16_t *b, const uint16_t *conv_state, GdnScratch *w,
-             bool want_graw, const int32_t *slots) {
+             bool want_graw, const int32_t *slots, const ApusHipGdnTrace *tr) {
     const size_t kd = L->hk * DK, vd = L->hv * DV;
     w->qk = (float *)scratch(kScratchGdnQK, Ttot * 2 * kd * 4);
     w->vconv = (uint16_t *)scratch(kScratchGdnV, Ttot * vd * 2);
@@ -614,6 +623,9 @@ int gdn_prep(const ApusHipGdnLayer *L, size_t B, const int32_t *cu, const int32_
     w->graw = want_graw ? (float *)scratch(kScratchGdnChunk3, Ttot * L->hv * 4) : nullptr;
     if (!w->qk || !w->vconv || !w->gate || !w->ob || (want_graw && !w->graw))
         return kErrHip;
+    // a traced call without the raw gates for WY writes them straight to
+    // the trace
+    float *graw = w->graw ? w->graw : (tr ? tr->gdecay : nullptr);
     const float qscale = (float)pow((double)L->dk, -0.5);
     const ActTables *tabs = act_tables();
     if (!tabs) return kErrHip;
@@ -622,8 +634,8 @@ int gdn_prep(const ApusHipGdnLayer *L, size_t B, const int32_t *cu, const int32_
     APUS_TIMED("k_gdn_prep",
                k_gdn_prep<<<(unsigned)(cdiv(Ttot, PT) * L->hk), 256, 0, stream()>>>(
         ci, dcu, (int)B, (int)Ttot, qkv, a, b, L->conv_w, L->A_log, L->dt_bias, conv_state,
-        w->qk, w->vconv, w->gate, w->graw, (int)L->hk, qscale, tabs->silu_bf, tabs->sig_bf,
-        slots));
+        w->qk, w->vconv, w->gate, graw, (int)L->hk, qscale, tabs->silu_bf, tabs->sig_bf,
+        slots, tr ? tr->qkv_conv : nullptr, tr ? tr->beta : nullptr));
     return launch_check("k_gdn_prep");
 }
 
@@ -679,14 +691,31 @@ static int gdn_decode_run(const ApusHipGdnLayer *L, size_t B, const int32_t *cu,
         if (!dsin) return kErrHip;
         dsout = dsin + B;
     }
+    const ApusHipGdnTrace *tr = gdn_trace();
+    if (tr && (tr->qkv_conv || tr->beta || tr->gdecay)) {
+        // the token-parallel intermediates from the same inputs and the
+        // old conv state, before the decode rewrites it
+        const int32_t *pcu = dcu;
+        if (!pcu && B > (size_t)kGdnCuInline) {
+            pcu = (const int32_t *)upload_async(cu, (B + 1) * 4);
+            if (!pcu) return kErrHip;
+        }
+        GdnScratch w;
+        if (int r = gdn_prep(L, B, cu, pcu, (size_t)cu[B], qkv, a, b, conv_in, &w, false, dsin, tr))
+            return r;
+    }
     const float qscale = (float)pow((double)L->dk, -0.5);
     const bool multi = (size_t)cu[B] != B;     // some sequence has != 1 token
     auto kern = multi ? k_gdn_decode<true> : k_gdn_decode<false>;
     APUS_TIMED("k_gdn_decode",
                kern<<<(unsigned)(B * L->hk), 256, 0, stream()>>>(
         ca, dcu, qkv, z, a, b, L->conv_w, L->A_log, L->dt_bias, L->onorm_w,
-        conv_in, S_in, conv_out, S_out, y, (int)L->hk, qscale, dsin, dsout));
+        conv_in, S_in, conv_out, S_out, y, (int)L->hk, qscale, dsin, dsout,
+        tr ? tr->rec_o : nullptr));
     APUS_LAUNCHED("k_gdn_decode");
+    if (tr && tr->onorm)                       // the gated norm's output is y
+        APUS_HIP_TRY(hipMemcpyAsync(tr->onorm, y, (size_t)cu[B] * L->hv * DV * 2,
+                                    hipMemcpyDeviceToDevice, stream()));
     return kOk;
 }
 

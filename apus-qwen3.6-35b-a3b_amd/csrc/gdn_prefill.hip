@@ -881,7 +881,12 @@ static int gdn_prefill_run(const ApusHipGdnLayer *L, size_t B, const int32_t *cu
         if (!slots) return kErrHip;
     }
     GdnScratch w;
-    if (int r = gdn_prep(L, B, cu, dmeta, Ttot, qkv, a, b, conv_state, &w, true, slots)) return r;
+    const ApusHipGdnTrace *tr = gdn_trace();
+    if (int r = gdn_prep(L, B, cu, dmeta, Ttot, qkv, a, b, conv_state, &w, true, slots, tr))
+        return r;
+    if (tr && tr->gdecay)
+        APUS_HIP_TRY(hipMemcpyAsync(tr->gdecay, w.graw, Ttot * L->hv * 4,
+                                    hipMemcpyDeviceToDevice, stream()));
     const size_t units = nch * L->hv;
     float *Ub = (float *)scratch(kScratchGdnChunk, units * C * DV * 4);
     uint16_t *Wb = (uint16_t *)scratch(kScratchGdnChunk2, units * C * DK * 4);
@@ -899,7 +904,14 @@ static int gdn_prefill_run(const ApusHipGdnLayer *L, size_t B, const int32_t *cu
                k_gdn_chunk_scan<<<(unsigned)(B * L->hv * NCB), 512, 0, stream()>>>(
         sq, kmeta, Qp, Kp, Ub, Wb, Ab, Fb, S, w.ob, (int)L->hk, slots));
     APUS_LAUNCHED("k_gdn_chunk_scan");
-    return gdn_post(L, B, cu, dmeta, Ttot, &w, z, qkv, conv_state, y, slots);
+    if (tr && tr->rec_o)                       // rnd(o) of every token, as the scan left it
+        APUS_HIP_TRY(hipMemcpyAsync(tr->rec_o, w.ob, Ttot * L->hv * DV * 2,
+                                    hipMemcpyDeviceToDevice, stream()));
+    if (int r = gdn_post(L, B, cu, dmeta, Ttot, &w, z, qkv, conv_state, y, slots)) return r;
+    if (tr && tr->onorm)
+        APUS_HIP_TRY(hipMemcpyAsync(tr->onorm, y, Ttot * L->hv * DV * 2, hipMemcpyDeviceToDevice,
+                                    stream()));
+    return kOk;
 }
 
 }  // namespace apus

@@ -66,6 +66,35 @@ int    apus_hip_memset(void *dst, int value, size_t bytes);
 int    apus_hip_timing_enable(int on);
 int    apus_hip_timing_get(const char *kernel, double *total_ms, size_t *count);
 
+/* Named-intermediate capture, the hot-path fields of the reference's
+ * ApusLayerTrace (c/layer.h:172-189; filled per token at c/layer.h:275-285
+ * and 324-330). While a trace is set, every tier-2 GDN mixer call
+ * (apus_hip_gdn_decode, _decode_into, _decode_slots, _prefill,
+ * _prefill_slots) writes, for each of its packed tokens t:
+ *   qkv_conv [t][conv_dim] bf16  conv1d+SiLU output (q|k|v)
+ *   beta     [t][hv]       bf16  sigmoid(b)
+ *   gdecay   [t][hv]       f32   the decay g
+ *   rec_o    [t][hv*dv]    bf16  rnd(o) of the recurrence
+ *   onorm    [t][hv*dv]    bf16  the gated RMSNorm output (= the mixer's y)
+ * and every tier-2 attention call (decode, prefill, paged or flat):
+ *   qf       [t][nh*d]     bf16  q after (1+w) RMSNorm and RoPE
+ *   kf       [t][nkv*d]    bf16  k after norm and RoPE (the appended row)
+ *   attno    [t][nh*d]     bf16  the attention output before the gate
+ *   mgate    [t][nh*d]     bf16  rnd(sigmoid(gate))
+ * DEVICE pointers; any member may be NULL; NULL structs stop tracing. The
+ * values are those the kernels compute (the chunked prefill's rec_o is its
+ * tolerance class). Tracing adds work and is meant for checking, as the
+ * reference uses its trace for the stage gates (tests/m4c). */
+typedef struct {
+    uint16_t *qkv_conv, *beta;
+    float    *gdecay;
+    uint16_t *rec_o, *onorm;
+} ApusHipGdnTrace;
+typedef struct {
+    uint16_t *qf, *kf, *attno, *mgate;
+} ApusHipAttnTrace;
+int apus_hip_trace_set(const ApusHipGdnTrace *gdn, const ApusHipAttnTrace *attn);
+
 /* ---- Tier 1: GDN ops (c/gdn.h) -------------------------------------- */
 /* replaces apus_gdn_conv1d      (c/gdn.h:107-108, impl 314-318) */
 int apus_hip_gdn_conv1d(const uint16_t *x, const uint16_t *w, uint16_t *out,
@@ -361,6 +390,53 @@ int apus_hip_gdn_slot_load(ApusHipGdnPool *pool, size_t layer, int32_t slot,
                            const uint16_t *conv, const float *S);
 int apus_hip_gdn_slot_store(ApusHipGdnPool *pool, size_t layer, int32_t slot,
                             uint16_t *conv, float *S);
+
+/* ---- weight container reader (replaces c/st.h:64-89: apus_st_open /
+ * apus_st_find / apus_st_set_open / apus_st_set_get) -----------------------
+ * A path is one .safetensors shard or a directory holding
+ * model.safetensors.index.json and its shards. Shards are opened header-
+ * only; apus_hip_st_read copies one tensor's payload (pread) into caller
+ * memory. Host-side only: these calls need no device and ignore
+ * APUS_HIP_DISABLE. Codes of ApusHipStTensor.dtype follow the reference's
+ * ApusStDtype order (c/st.h:44-48). */
+#define APUS_HIP_ST_I8 0
+#define APUS_HIP_ST_U8 1
+#define APUS_HIP_ST_F8_E8M0 2
+#define APUS_HIP_ST_F8_E4M3 3
+#define APUS_HIP_ST_BF16 4
+#define APUS_HIP_ST_F16 5
+#define APUS_HIP_ST_F32 6
+#define APUS_HIP_ST_I32 7
+#define APUS_HIP_ST_I64 8
+#define APUS_HIP_ST_OTHER 9
+#define APUS_HIP_ST_MAX_NDIM 8
+typedef struct {
+    char    name[160];
+    int     dtype;
+    int     ndim;
+    int64_t shape[APUS_HIP_ST_MAX_NDIM];
+    size_t  nbytes;
+} ApusHipStTensor;
+typedef struct ApusHipSt ApusHipSt;
+int    apus_hip_st_open(const char *path, ApusHipSt **out);
+int    apus_hip_st_close(ApusHipSt *st);
+size_t apus_hip_st_ntensors(const ApusHipSt *st);
+int    apus_hip_st_find(ApusHipSt *st, const char *name, ApusHipStTensor *info);
+int    apus_hip_st_read(ApusHipSt *st, const char *name, void *dst, size_t cap);
+
+/* One layer's hot-path weights from a container onto the device, under the
+ * reference's tensor names (c/model.h:440-490): GDN layer L reads
+ * model.language_model.layers.L.linear_attn.{conv1d.weight, norm.weight}
+ * (BF16) and .{A_log, dt_bias} (F32, or BF16 widened as c/model.h:249-275
+ * does); a full-attention layer reads .self_attn.{q_norm,k_norm}.weight
+ * (BF16). The device copies belong to the layer struct until *_free. */
+int apus_hip_gdn_layer_load(ApusHipSt *st, int layer, size_t hk, size_t hv,
+                            size_t dk, size_t dv, ApusHipGdnLayer *out);
+int apus_hip_attn_layer_load(ApusHipSt *st, int layer, size_t nh, size_t nkv,
+                             size_t d, size_t rot, double theta,
+                             ApusHipAttnLayer *out);
+int apus_hip_gdn_layer_free(ApusHipGdnLayer *layer);
+int apus_hip_attn_layer_free(ApusHipAttnLayer *layer);
 
 /* ---- projections on either side of the path (c/bf16.h:178-231) --------
  * y[m][o] = rnd(sum_k w[o][k] * x[m][k]), w [O][K], x [M][K], y [M][O],
