@@ -50,6 +50,7 @@ EXPORTS = [
     "apus_hip_st_open", "apus_hip_st_close", "apus_hip_st_ntensors", "apus_hip_st_find",
     "apus_hip_st_read", "apus_hip_gdn_layer_load", "apus_hip_attn_layer_load",
     "apus_hip_gdn_layer_free", "apus_hip_attn_layer_free", "apus_hip_trace_set",
+    "apus_hip_gdn_prefill_noalloc",
 ]
 
 
@@ -319,6 +320,14 @@ def gdn_prefill(layer, cu, qkv, z, a, b, conv_state, S, y):
     _chk(load().apus_hip_gdn_prefill(C.byref(layer), _sz(B), cup, _dp(qkv),
                                      _dp(z), _dp(a), _dp(b), _dp(conv_state),
                                      _dp(S), _dp(y)))
+
+
+def gdn_prefill_noalloc(layer, cu, qkv, z, a, b, conv_state, S, y):
+    """apus_hip_gdn_prefill_noalloc: the chunked prefill in the library's
+    fixed per-device scratch (allocates nothing)."""
+    cu, cup, B = _cu_arr(cu)
+    _chk(load().apus_hip_gdn_prefill_noalloc(C.byref(layer), _sz(B), cup, _dp(qkv), _dp(z),
+                                             _dp(a), _dp(b), _dp(conv_state), _dp(S), _dp(y)))
 
 
 def gdn_state_pack(S_ref, S_dev):

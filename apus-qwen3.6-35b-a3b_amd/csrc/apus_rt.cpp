@@ -113,6 +113,16 @@ int ensure_ready() {
                          g_device, prop.gcnArchName);
     g_cus = prop.multiProcessorCount > 0 ? prop.multiProcessorCount : 256;
     g_ready = 1;
+    // device set-up the allocation-free entry relies on: its scratch's
+    // address and the activation tables (allocated here, never in it)
+    if (int r = noalloc_setup(g_device)) {
+        g_ready = 0;
+        return r;
+    }
+    if (!act_tables()) {
+        g_ready = 0;
+        return kErrHip;
+    }
     return kOk;
 }
 

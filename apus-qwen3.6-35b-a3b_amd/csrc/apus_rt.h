@@ -77,6 +77,13 @@ const void *upload_async(const void *host, size_t bytes);
 // (staged through the ring).
 int copy_to_device_async(void *dst, const void *host, size_t bytes);
 
+// The allocation-free entry point's per-device scratch (noalloc.hip): its
+// size, the set-up taking its device address (once per device, device
+// current), and that address for the current device (nullptr before set-up).
+constexpr size_t kNoAllocScratchBytes = (size_t)96 << 20;
+int noalloc_setup(int dev);
+void *noalloc_scratch();
+
 // The trace sinks set by apus_hip_trace_set (nullptr when tracing is off).
 const ApusHipGdnTrace *gdn_trace();
 const ApusHipAttnTrace *attn_trace();

@@ -10,11 +10,11 @@ namespace apus {
 
 // Per-call device intermediates (library scratch).
 struct GdnScratch {
-    float *qk;          // [Ttot][2][hk*128]: l2-normed q (scaled), k
-    uint16_t *vconv;    // [Ttot][hv*128]: conv+SiLU of the v channels
-    float2 *gate;       // [Ttot][hv]: (exp(g), beta)
-    uint16_t *ob;       // [Ttot][hv*128]: rnd(recurrence output)
-    float *graw;        // [Ttot][hv]: g itself (log decay), when requested
+    float *qk = nullptr;          // [Ttot][2][hk*128]: l2-normed q (scaled), k
+    uint16_t *vconv = nullptr;    // [Ttot][hv*128]: conv+SiLU of the v channels
+    float2 *gate = nullptr;       // [Ttot][hv]: (exp(g), beta)
+    uint16_t *ob = nullptr;       // [Ttot][hv*128]: rnd(recurrence output)
+    float *graw = nullptr;        // [Ttot][hv]: g itself (log decay), when requested
 };
 
 // Token offsets of up to kGdnCuInline sequences by value (kernel
@@ -26,7 +26,9 @@ struct GdnCu {
 
 int gdn_check_layer(const ApusHipGdnLayer *L);
 int gdn_check_offsets(size_t B, const int32_t *cu);
-// conv + l2norm + gates for every token (reads the old conv state).
+// conv + l2norm + gates for every token (reads the old conv state). The
+// intermediates go to w's buffers when w->qk is set (a caller workspace),
+// else to library scratch.
 // Token offsets: dcu (device) when non-null, else from the host array cu
 // by value (B <= kGdnCuInline). slots (device, nullable): the conv-state
 // slot of each sequence (identity when null).

@@ -616,11 +616,13 @@ int gdn_prep(const ApusHipGdnLayer *L, size_t B, const int32_t *cu, const int32_
              const uint16_t *b, const uint16_t *conv_state, GdnScratch *w,
              bool want_graw, const int32_t *slots, const ApusHipGdnTrace *tr) {
     const size_t kd = L->hk * DK, vd = L->hv * DV;
-    w->qk = (float *)scratch(kScratchGdnQK, Ttot * 2 * kd * 4);
-    w->vconv = (uint16_t *)scratch(kScratchGdnV, Ttot * vd * 2);
-    w->gate = (float2 *)scratch(kScratchGdnGate, Ttot * L->hv * 8);
-    w->ob = (uint16_t *)scratch(kScratchGdnOB, Ttot * vd * 2);
-    w->graw = want_graw ? (float *)scratch(kScratchGdnChunk3, Ttot * L->hv * 4) : nullptr;
+    if (!w->qk) {                              // else the caller's workspace
+        w->qk = (float *)scratch(kScratchGdnQK, Ttot * 2 * kd * 4);
+        w->vconv = (uint16_t *)scratch(kScratchGdnV, Ttot * vd * 2);
+        w->gate = (float2 *)scratch(kScratchGdnGate, Ttot * L->hv * 8);
+        w->ob = (uint16_t *)scratch(kScratchGdnOB, Ttot * vd * 2);
+        w->graw = want_graw ? (float *)scratch(kScratchGdnChunk3, Ttot * L->hv * 4) : nullptr;
+    }
     if (!w->qk || !w->vconv || !w->gate || !w->ob || (want_graw && !w->graw))
         return kErrHip;
     // a traced call without the raw gates for WY writes them straight to
@@ -700,7 +702,7 @@ static int gdn_decode_run(const ApusHipGdnLayer *L, size_t B, const int32_t *cu,
             pcu = (const int32_t *)upload_async(cu, (B + 1) * 4);
             if (!pcu) return kErrHip;
         }
-        GdnScratch w;
+        GdnScratch w{};
         if (int r = gdn_prep(L, B, cu, pcu, (size_t)cu[B], qkv, a, b, conv_in, &w, false, dsin, tr))
             return r;
     }

@@ -834,10 +834,49 @@ namespace apus {
 
 // Chunked prefill; slots_h (host, nullable): the state slot of each
 // sequence in conv_state / S (identity when null).
+// The buffers of one prefill call carved from a workspace (256-byte
+// aligned pieces): the token-parallel intermediates, the per (chunk,
+// v-head) WY operands and the device metadata. bytes: the total.
+struct PrefillWs {
+    GdnScratch w;
+    float *Ub = nullptr, *Fb = nullptr;
+    uint16_t *Wb = nullptr, *Ab = nullptr, *Qp = nullptr, *Kp = nullptr;
+    int32_t *meta = nullptr;
+    size_t bytes = 0;
+};
+static PrefillWs prefill_ws_carve(char *base, size_t Ttot, size_t nch, size_t B, size_t hk,
+                                  size_t hv) {
+    PrefillWs p;
+    size_t off = 0;
+    auto take = [&](size_t n) {
+        char *q = base ? base + off : nullptr;
+        off += (n + 255) / 256 * 256;
+        return q;
+    };
+    const size_t kd = hk * DK, vd = hv * DV, units = nch * hv;
+    p.w.qk = (float *)take(Ttot * 2 * kd * 4);
+    p.w.vconv = (uint16_t *)take(Ttot * vd * 2);
+    p.w.gate = (float2 *)take(Ttot * hv * 8);
+    p.w.ob = (uint16_t *)take(Ttot * vd * 2);
+    p.w.graw = (float *)take(Ttot * hv * 4);
+    p.Ub = (float *)take(units * C * DV * 4);
+    p.Wb = (uint16_t *)take(units * C * DK * 4);
+    p.Ab = (uint16_t *)take(units * C * C * 4);
+    p.Fb = (float *)take(units * 2 * C * 4);
+    p.Qp = (uint16_t *)take(nch * hk * C * DK * 4);
+    p.Kp = (uint16_t *)take(nch * hk * C * DK * 4);
+    p.meta = (int32_t *)take(2 * (B + 1) * 4);
+    p.bytes = off;
+    return p;
+}
+
+// ws: a workspace of ws_bytes bytes the whole call works in (nothing is
+// allocated; then B <= kPrefillInline and no slot map), or nullptr for
+// library scratch.
 static int gdn_prefill_run(const ApusHipGdnLayer *L, size_t B, const int32_t *cu,
                            const uint16_t *qkv, const uint16_t *z, const uint16_t *a,
                            const uint16_t *b, uint16_t *conv_state, float *S, uint16_t *y,
-                           const int32_t *slots_h) {
+                           const int32_t *slots_h, char *ws = nullptr, size_t ws_bytes = 0) {
     if (int r = gdn_check_layer(L)) return r;
     if (B == 0) return kOk;
     if (int r = gdn_check_offsets(B, cu)) return r;
@@ -848,12 +887,32 @@ static int gdn_prefill_run(const ApusHipGdnLayer *L, size_t B, const int32_t *cu
     // metadata [cu | chunk offsets]: by value for small batches (k_gdn_prep
     // and k_gdn_post take cu for up to kGdnCuInline sequences, WY and the
     // scan both arrays for up to kPrefillInline), else a device copy
-    std::vector<int32_t> meta(2 * (B + 1));
-    memcpy(meta.data(), cu, (B + 1) * 4);
-    int32_t *coff = meta.data() + B + 1;
+    // (a stack array for the batches whose metadata travels by value: the
+    // allocation-free entry allocates nothing, host memory included)
+    int32_t meta_small[2 * (kPrefillInline + 1)];
+    std::vector<int32_t> meta_big;
+    if (B > (size_t)kPrefillInline) meta_big.resize(2 * (B + 1));
+    int32_t *meta = B > (size_t)kPrefillInline ? meta_big.data() : meta_small;
+    const size_t nmeta = 2 * (B + 1);
+    memcpy(meta, cu, (B + 1) * 4);
+    int32_t *coff = meta + B + 1;
     coff[0] = 0;
     for (size_t s = 0; s < B; s++) coff[s + 1] = coff[s] + (cu[s + 1] - cu[s] + C - 1) / C;
     const size_t nch = (size_t)coff[B];
+    PrefillWs pw;
+    if (ws) {
+        if (B > (size_t)kPrefillInline || slots_h)
+            return set_error(kErrUnsupported,
+                             "the allocation-free prefill takes up to %d sequences, no slot map",
+                             kPrefillInline);
+        pw = prefill_ws_carve(nullptr, Ttot, nch, B, L->hk, L->hv);
+        if (pw.bytes > ws_bytes)
+            return set_error(kErrUnsupported,
+                             "prefill of %zu tokens in %zu chunks needs %zu bytes of scratch; the "
+                             "allocation-free entry has %zu",
+                             Ttot, nch, pw.bytes, ws_bytes);
+        pw = prefill_ws_carve(ws, Ttot, nch, B, L->hk, L->hv);
+    }
     ChunkSeqs sq;
     sq.n = (int32_t)B;
     const int32_t *dmeta, *kmeta;
@@ -862,7 +921,7 @@ static int gdn_prefill_run(const ApusHipGdnLayer *L, size_t B, const int32_t *cu
         memcpy(sq.coff, coff, (B + 1) * 4);
         dmeta = nullptr;                       // prep / post take cu by value
         if (B > (size_t)kGdnCuInline) {
-            int32_t *m = (int32_t *)scratch(kScratchMeta3, meta.size() * 4);
+            int32_t *m = ws ? pw.meta : (int32_t *)scratch(kScratchMeta3, nmeta * 4);
             if (!m) return kErrHip;
             k_prefill_meta<<<1, 256, 0, stream()>>>(sq, m);
             APUS_LAUNCHED("k_prefill_meta");
@@ -870,7 +929,7 @@ static int gdn_prefill_run(const ApusHipGdnLayer *L, size_t B, const int32_t *cu
         }
         kmeta = nullptr;
     } else {
-        dmeta = (const int32_t *)upload_async(meta.data(), meta.size() * 4);
+        dmeta = (const int32_t *)upload_async(meta, nmeta * 4);
         if (!dmeta) return kErrHip;
         kmeta = dmeta;
     }
@@ -880,7 +939,7 @@ static int gdn_prefill_run(const ApusHipGdnLayer *L, size_t B, const int32_t *cu
         slots = (const int32_t *)upload_async(slots_h, B * 4);
         if (!slots) return kErrHip;
     }
-    GdnScratch w;
+    GdnScratch w = pw.w;                       // workspace buffers, or null: scratch
     const ApusHipGdnTrace *tr = gdn_trace();
     if (int r = gdn_prep(L, B, cu, dmeta, Ttot, qkv, a, b, conv_state, &w, true, slots, tr))
         return r;
@@ -888,12 +947,12 @@ static int gdn_prefill_run(const ApusHipGdnLayer *L, size_t B, const int32_t *cu
         APUS_HIP_TRY(hipMemcpyAsync(tr->gdecay, w.graw, Ttot * L->hv * 4,
                                     hipMemcpyDeviceToDevice, stream()));
     const size_t units = nch * L->hv;
-    float *Ub = (float *)scratch(kScratchGdnChunk, units * C * DV * 4);
-    uint16_t *Wb = (uint16_t *)scratch(kScratchGdnChunk2, units * C * DK * 4);
-    uint16_t *Ab = (uint16_t *)scratch(kScratchGdnChunk4, units * C * C * 4);
-    float *Fb = (float *)scratch(kScratchGdnChunk5, units * 2 * C * 4);
-    uint16_t *Qp = (uint16_t *)scratch(kScratchGdnChunk6, nch * L->hk * C * DK * 4);
-    uint16_t *Kp = (uint16_t *)scratch(kScratchGdnChunk7, nch * L->hk * C * DK * 4);
+    float *Ub = ws ? pw.Ub : (float *)scratch(kScratchGdnChunk, units * C * DV * 4);
+    uint16_t *Wb = ws ? pw.Wb : (uint16_t *)scratch(kScratchGdnChunk2, units * C * DK * 4);
+    uint16_t *Ab = ws ? pw.Ab : (uint16_t *)scratch(kScratchGdnChunk4, units * C * C * 4);
+    float *Fb = ws ? pw.Fb : (float *)scratch(kScratchGdnChunk5, units * 2 * C * 4);
+    uint16_t *Qp = ws ? pw.Qp : (uint16_t *)scratch(kScratchGdnChunk6, nch * L->hk * C * DK * 4);
+    uint16_t *Kp = ws ? pw.Kp : (uint16_t *)scratch(kScratchGdnChunk7, nch * L->hk * C * DK * 4);
     if (!Ub || !Wb || !Ab || !Fb || !Qp || !Kp) return kErrHip;
     APUS_TIMED("k_gdn_chunk_wy",
                k_gdn_chunk_wy<<<(unsigned)units, 256, 0, stream()>>>(
@@ -923,6 +982,16 @@ int apus_hip_gdn_prefill(const ApusHipGdnLayer *L, size_t B, const int32_t *cu,
                          const uint16_t *b, uint16_t *conv_state, float *S, uint16_t *y) {
     APUS_READY();
     return gdn_prefill_run(L, B, cu, qkv, z, a, b, conv_state, S, y, nullptr);
+}
+
+int apus_hip_gdn_prefill_noalloc(const ApusHipGdnLayer *L, size_t B, const int32_t *cu,
+                                 const uint16_t *qkv, const uint16_t *z, const uint16_t *a,
+                                 const uint16_t *b, uint16_t *conv_state, float *S, uint16_t *y) {
+    APUS_READY();
+    char *ws = (char *)noalloc_scratch();
+    if (!ws) return set_error(kErrHip, "the allocation-free scratch of this device is not set up");
+    return gdn_prefill_run(L, B, cu, qkv, z, a, b, conv_state, S, y, nullptr, ws,
+                           kNoAllocScratchBytes);
 }
 
 int apus_hip_gdn_prefill_slots(const ApusHipGdnLayer *L, size_t B, const int32_t *slots,

@@ -251,6 +251,24 @@ int apus_hip_gdn_prefill(const ApusHipGdnLayer *L, size_t B,
                          const uint16_t *b, uint16_t *conv_state, float *S,
                          uint16_t *y);
 
+/* apus_hip_gdn_prefill that allocates nothing (no counterpart in the
+ * reference; for callers that cannot allocate device memory: code under
+ * HIP graph capture, tight serving loops, hosts that forbid hipMalloc).
+ * Same arguments, results bit-identical to apus_hip_gdn_prefill. The
+ * intermediates live in one fixed per-device scratch array of 96 MiB,
+ * reserved when the library initialises a device and held until the
+ * process ends: a call needs about 33 KiB per token plus 3.6 MiB per
+ * (sequence, chunk of 64 tokens), so one sequence of up to ~1000 tokens
+ * (longer prompts are prefilled in successive calls: the state carries
+ * over); at most 400 sequences and no slot map. A larger call returns
+ * APUS_HIP_ERR_UNSUPPORTED with the size it needs. Calls on one GPU share
+ * that GPU's scratch: calls that overlap (two streams) race. */
+int apus_hip_gdn_prefill_noalloc(const ApusHipGdnLayer *L, size_t B,
+                                 const int32_t *cu, const uint16_t *qkv,
+                                 const uint16_t *z, const uint16_t *a,
+                                 const uint16_t *b, uint16_t *conv_state,
+                                 float *S, uint16_t *y);
+
 /* apus_hip_gdn_prefill on a state pool: sequence s's state is slot
  * slots[s] (HOST array, distinct for sequences with tokens) of the slot
  * arrays conv / S (layout as apus_hip_gdn_decode_slots). */
