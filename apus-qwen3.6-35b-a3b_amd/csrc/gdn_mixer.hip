@@ -96,10 +96,14 @@ __global__ void k_gdn_unpack(const float *__restrict__ src, float *__restrict__ 
 // the l2norm. The small per-token operands are loaded before the 32
 // state loads of each lane, so waiting on them never waits on the state;
 // the gates and silu(z) are evaluated while the state is in flight.
-// Token offsets arrive by value for up to kInlineSeqs sequences.
+// Token offsets arrive by value for up to kInlineSeqs sequences, and with
+// them the state slot maps when all 3B+1 words fit (B <= 320): then a
+// slotted step uploads nothing. cu[0..B] are the offsets, cu[B+1..2B] the
+// input slots and cu[2B+1..3B] the output slots.
 constexpr int kInlineSeqs = 480;
+constexpr int kInlineWords = 2 * kInlineSeqs + 1;
 struct CuArgs {
-    int32_t cu[kInlineSeqs + 1];
+    int32_t cu[kInlineWords];
 };
 
 template <bool MULTI>
@@ -110,7 +114,7 @@ void k_gdn_decode(
     const float *A_log, const float *dt_bias, const uint16_t *onorm_w,
     const uint16_t *conv_state, const float *S, uint16_t *conv_out, float *S_out,
     uint16_t *y, int hk, float qscale, const int32_t *slot_in, const int32_t *slot_out,
-    uint16_t *tr_ob) {
+    int slots_inline, uint16_t *tr_ob) {
     // (no __restrict__ on the small operands: it would let the compiler sink
     // their loads past the ordering barrier below the state loads)
     const int s = blockIdx.x / hk, kh = blockIdx.x % hk;
@@ -126,8 +130,11 @@ void k_gdn_decode(
     if (t0 == t1) return;
     // the state slots this sequence reads and writes (identity without a
     // slot map)
-    const int si = slot_in ? __builtin_amdgcn_readfirstlane(slot_in[s]) : s;
-    const int so = slot_out ? __builtin_amdgcn_readfirstlane(slot_out[s]) : s;
+    const int nseq = gridDim.x / hk;
+    const int si = slots_inline ? ca.cu[nseq + 1 + s]
+                 : slot_in ? __builtin_amdgcn_readfirstlane(slot_in[s]) : s;
+    const int so = slots_inline ? ca.cu[2 * nseq + 1 + s]
+                 : slot_out ? __builtin_amdgcn_readfirstlane(slot_out[s]) : s;
 
     __shared__ __attribute__((aligned(16))) float raw[2 * DK];   // conv q, k
     __shared__ __attribute__((aligned(16))) float qkn[2 * DK];   // normed q, k
@@ -684,8 +691,15 @@ static int gdn_decode_run(const ApusHipGdnLayer *L, size_t B, const int32_t *cu,
         dcu = (const int32_t *)upload_async(cu, (B + 1) * 4);
         if (!dcu) return kErrHip;
     }
+    const ApusHipGdnTrace *tr = gdn_trace();
+    const bool traced = tr && (tr->qkv_conv || tr->beta || tr->gdecay);
     const int32_t *dsin = nullptr, *dsout = nullptr;
-    if (sin_h) {
+    const bool slots_inline = sin_h && !dcu && 3 * B + 1 <= (size_t)kInlineWords;
+    if (slots_inline) {
+        memcpy(ca.cu + B + 1, sin_h, B * 4);
+        memcpy(ca.cu + 2 * B + 1, sout_h, B * 4);
+    }
+    if (sin_h && (!slots_inline || traced)) {     // the trace's prep pass reads them on device
         std::vector<int32_t> m(2 * B);
         memcpy(m.data(), sin_h, B * 4);
         memcpy(m.data() + B, sout_h, B * 4);
@@ -693,8 +707,7 @@ static int gdn_decode_run(const ApusHipGdnLayer *L, size_t B, const int32_t *cu,
         if (!dsin) return kErrHip;
         dsout = dsin + B;
     }
-    const ApusHipGdnTrace *tr = gdn_trace();
-    if (tr && (tr->qkv_conv || tr->beta || tr->gdecay)) {
+    if (traced) {
         // the token-parallel intermediates from the same inputs and the
         // old conv state, before the decode rewrites it
         const int32_t *pcu = dcu;
@@ -712,7 +725,7 @@ static int gdn_decode_run(const ApusHipGdnLayer *L, size_t B, const int32_t *cu,
     APUS_TIMED("k_gdn_decode",
                kern<<<(unsigned)(B * L->hk), 256, 0, stream()>>>(
         ca, dcu, qkv, z, a, b, L->conv_w, L->A_log, L->dt_bias, L->onorm_w,
-        conv_in, S_in, conv_out, S_out, y, (int)L->hk, qscale, dsin, dsout,
+        conv_in, S_in, conv_out, S_out, y, (int)L->hk, qscale, dsin, dsout, (int)slots_inline,
         tr ? tr->rec_o : nullptr));
     APUS_LAUNCHED("k_gdn_decode");
     if (tr && tr->onorm)                       // the gated norm's output is y

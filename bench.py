@@ -120,26 +120,40 @@ def time_steps(torch, fn, steps, warmup, nsets, kernels=()):
     times in s, {kernel: average launch ms}). Each step uses buffer set
     i % nsets. The wall-clock pass runs without kernel timing; a second
     pass of the same steps records HIP events around each launch of the
-    named kernels on the library's stream (apus_hip_timing_*)."""
+    named kernels on the library's stream (apus_hip_timing_*). The
+    collector runs before and stays off during each pass: a generation-2
+    collection over the process's objects takes 15-40 ms, enough to drain
+    the launch queue in the middle of a timed pass."""
+    import gc
     import apus_hip
     for i in range(warmup):
         fn(i % nsets)
     torch.cuda.synchronize()
     ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
           for _ in range(steps)]
-    t0 = time.perf_counter()
-    for i in range(steps):
-        ev[i][0].record()
-        fn(i % nsets)
-        ev[i][1].record()
-    torch.cuda.synchronize()
-    total = time.perf_counter() - t0
+    gc.collect()
+    gc.disable()
+    try:
+        t0 = time.perf_counter()
+        for i in range(steps):
+            ev[i][0].record()
+            fn(i % nsets)
+            ev[i][1].record()
+        torch.cuda.synchronize()
+        total = time.perf_counter() - t0
+    finally:
+        gc.enable()
     per = [a.elapsed_time(b) * 1e-3 for a, b in ev]
     kt = {}
     if kernels:
+        gc.collect()
+        gc.disable()
         apus_hip.timing_enable(True)
-        for i in range(steps):
-            fn(i % nsets)
+        try:
+            for i in range(steps):
+                fn(i % nsets)
+        finally:
+            gc.enable()
         for k in kernels:
             ms, n = apus_hip.timing_get(k)
             if n:
