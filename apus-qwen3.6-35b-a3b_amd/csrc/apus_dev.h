@@ -103,6 +103,33 @@ __device__ __forceinline__ void buf_st4(__amdgpu_buffer_rsrc_t r, int voff, int 
     llvm_raw_ptr_buffer_store_v4f32(v, r, voff, soff, kCpolNT);
 }
 
+// ---- global -> LDS DMA ----------------------------------------------------
+// buffer_load ... lds: each lane's 16 bytes land at the LDS byte address in
+// M0 + 16 * lane, without passing through VGPRs. Issued from inline asm, so
+// the compiler does not count these loads: the caller waits for them with
+// an explicit s_waitcnt vmcnt before reading the LDS they fill, and waits
+// for its own reads of that LDS (lgkmcnt) before refilling it.
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) void lds_void;
+
+// Buffer resource (SGPRs) over `bytes` bytes at base; offsets past the
+// end read as zero.
+__device__ __forceinline__ i32x4 dma_rsrc(const void *base, uint32_t bytes) {
+    const uint64_t a = (uint64_t)base;
+    return i32x4{__builtin_amdgcn_readfirstlane((int)(uint32_t)a),
+                 __builtin_amdgcn_readfirstlane((int)(uint32_t)(a >> 32) & 0xffff),
+                 __builtin_amdgcn_readfirstlane((int)bytes), 0x00020000};
+}
+
+// one 16-byte copy per lane from byte offset voff (per lane) + soff
+// (uniform) to LDS byte address lds (uniform) + 16 * lane
+__device__ __forceinline__ void dma16(i32x4 r, int voff, int soff, uint32_t lds) {
+    soff = __builtin_amdgcn_readfirstlane(soff);
+    lds = __builtin_amdgcn_readfirstlane(lds);
+    asm volatile("s_mov_b32 m0, %3\n\tbuffer_load_dwordx4 %0, %1, %2 offen lds"
+                 :: "v"(voff), "s"(r), "s"(soff), "s"(lds) : "memory", "m0");
+}
+
 // Exact IEEE single ops that the compiler may not fuse or reorder. The
 // kernels that promise reference-order results are compiled with FP
 // contraction off as well; these make the intent explicit at call sites.

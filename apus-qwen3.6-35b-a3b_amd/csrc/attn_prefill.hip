@@ -79,9 +79,7 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef unsigned short u16x8 __attribute__((ext_vector_type(8)));
 typedef unsigned short u16x4 __attribute__((ext_vector_type(4)));
-typedef int i32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x8_t __attribute__((ext_vector_type(8)));
-typedef __attribute__((address_space(3))) void lds_void;
 
 constexpr int kFaInline = 224;
 struct FaSeqs {
@@ -135,25 +133,6 @@ __device__ __forceinline__ int fa_lane() {
     int l = __lane_id();
     asm volatile("" : "+v"(l));
     return l;
-}
-
-// Buffer resource (SGPRs) over `bytes` bytes at base; offsets past the
-// end read as zero.
-__device__ __forceinline__ i32x4 fa_rsrc(const void *base, uint32_t bytes) {
-    const uint64_t a = (uint64_t)base;
-    return i32x4{__builtin_amdgcn_readfirstlane((int)(uint32_t)a),
-                 __builtin_amdgcn_readfirstlane((int)(uint32_t)(a >> 32) & 0xffff),
-                 __builtin_amdgcn_readfirstlane((int)bytes), 0x00020000};
-}
-
-// one 16-byte global -> LDS copy per lane: byte offset voff (per lane) +
-// soff (uniform); LDS byte address lds (uniform) + 16 * lane. Counted by
-// vmcnt; the caller waits before the barrier that publishes the tile.
-__device__ __forceinline__ void dma16(i32x4 r, int voff, int soff, uint32_t lds) {
-    soff = __builtin_amdgcn_readfirstlane(soff);
-    lds = __builtin_amdgcn_readfirstlane(lds);
-    asm volatile("s_mov_b32 m0, %3\n\tbuffer_load_dwordx4 %0, %1, %2 offen lds"
-                 :: "v"(voff), "s"(r), "s"(soff), "s"(lds) : "memory", "m0");
 }
 
 // K rows of key tile kt -> the K buffer at LDS address kb (row pitch
@@ -236,11 +215,11 @@ __device__ __forceinline__ int fa_block_id(const FaCtx &c, int b) {
 __device__ __forceinline__ i32x4 fa_krsrc(const FaCtx &c, int kt, int id) {
     const int b = 2 * kt + (c.wave >> 2);
     const int valid = max(0, min(KVB, c.nkeys - KVB * b));
-    return fa_rsrc(c.kv.k + ((size_t)id * c.nkv + c.kvh) * KVB * D, (uint32_t)valid * D * 2);
+    return dma_rsrc(c.kv.k + ((size_t)id * c.nkv + c.kvh) * KVB * D, (uint32_t)valid * D * 2);
 }
 __device__ __forceinline__ i32x4 fa_vrsrc(const FaCtx &c, int kt, int id) {
     const int b = 2 * kt + (c.wave >> 2);
-    return fa_rsrc(c.kv.v + ((size_t)id * c.nkv + c.kvh) * D * KVB,
+    return dma_rsrc(c.kv.v + ((size_t)id * c.nkv + c.kvh) * D * KVB,
                    b < c.nblk ? (uint32_t)(D * KVB * 2) : 0u);
 }
 

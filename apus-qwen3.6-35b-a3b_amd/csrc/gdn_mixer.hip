@@ -90,12 +90,29 @@ __global__ void k_gdn_unpack(const float *__restrict__ src, float *__restrict__ 
 }
 
 // ---- fused decode -------------------------------------------------------
-// One workgroup per (sequence, K head), 4 wavefronts. Wave w serves v-head
-// 2*kh + (w >> 1), value columns (w & 1)*64 + lane; thread t also owns q
-// channel t (t < 128) or k channel t-128 of the K head for the conv and
-// the l2norm. The small per-token operands are loaded before the 32
-// state loads of each lane, so waiting on them never waits on the state;
-// the gates and silu(z) are evaluated while the state is in flight.
+// One workgroup per item (sequence, K head), 4 wavefronts, two workgroups
+// per CU (the state tile lives in registers: 128 per lane). Item (s, kh)
+// serves v-heads 2kh and 2kh+1; wave w serves v-head r = w >> 1, value
+// columns (w & 1)*64 + lane of it; thread t also owns q channel t
+// (t < 128) or k channel t-128 of the K head, and the t-th of the item's
+// 256 v channels.
+//
+// The reference evaluates c/layer.h:250-273 + c/gdn.h:471-504 token by
+// token; every op and operand order of that is kept, but scheduled so that
+// no serial single-lane chain runs once per token. Per chunk of up to KT
+// tokens:
+//   A  conv of q, k, v and silu(z) for all the chunk's tokens (thread-
+//      parallel); then the 2n l2-norm sums and the 2n gate pairs, one lane
+//      each, in parallel (waves 0 and 1); normalised q, k to LDS.
+//   B  the recurrence, each wave on its own columns with no barrier.
+//   C  the 2n output-norm sums in parallel lanes, then y.
+// With one token the state tile is loaded before phase A (the gate math
+// runs under the loads); with several, after it (the tile's 128 registers
+// are then not live through phase A). The other workgroup on the CU runs
+// while this one waits for memory or sits in a serial phase.
+//
+// MODE 0: one token per sequence; 1: up to KT; 2: any number, in chunks of
+// KT (the host picks the mode from the largest token count).
 // Token offsets arrive by value for up to kInlineSeqs sequences, and with
 // them the state slot maps when all 3B+1 words fit (B <= 320): then a
 // slotted step uploads nothing. cu[0..B] are the offsets, cu[B+1..2B] the
@@ -106,191 +123,289 @@ struct CuArgs {
     int32_t cu[kInlineWords];
 };
 
-template <bool MULTI>
+constexpr int KT = 4;                          // tokens per chunk
+
+// Ascending sum of squares of 128 LDS floats (one rounding per mul and
+// add). Unrolled by four 16-byte reads: enough reads in flight to cover
+// most of their latency, few enough registers to run beside a live state
+// tile.
+__device__ __forceinline__ float sumsq128(const float *x) {
+    const float4 *x4 = reinterpret_cast<const float4 *>(x);
+    float ss = 0.0f;
+#pragma unroll 4
+    for (int i = 0; i < 32; i++) {
+        const float4 v = x4[i];
+        ss = ss + v.x * v.x;
+        ss = ss + v.y * v.y;
+        ss = ss + v.z * v.z;
+        ss = ss + v.w * v.w;
+    }
+    return ss;
+}
+
+// ---- phase B: the recurrence of one chunk on one wave's columns ---------
+// c/gdn.h:482-503 on column j for the chunk's n tokens: per token a decay +
+// k.S pass and an update + q.S pass. k and q reach every lane as LDS
+// broadcast reads, four values per 16-byte read, so the VALU only does the
+// seven operations per state element that the reference's rounding order
+// needs. Reads run two groups of four rows ahead; a memory clobber and a
+// scheduling barrier per group keep the compiler from hoisting them all
+// (the state slice holds 128 registers). o_k = rnd(q_k . S_k) goes to
+// ob[k] and, when tracing, to tr[k * tr_stride].
+__device__ __forceinline__ void recur_chunk(float (&sr)[DK], const float (*raw)[2 * DK],
+                                            const float2 (*gt)[REP], const float (*cvs)[256],
+                                            float (*ob)[REP][DV], int n, int r, int j, int tid,
+                                            uint16_t *tr, size_t tr_stride) {
+#pragma unroll 1
+    for (int k = 0; k < n; k++) {
+        const float4 *K4 = reinterpret_cast<const float4 *>(&raw[k][DK]);
+        const float4 *Q4 = reinterpret_cast<const float4 *>(&raw[k][0]);
+        float kv = 0.0f;
+        {   // decay and k.S
+            const float g = gt[k][r].x;
+            float4 kn0 = K4[0], kn1 = K4[1];
+#pragma unroll
+            for (int i4 = 0; i4 < DK / 4; i4++) {
+                const float4 kk = kn0;
+                kn0 = kn1;
+                if (i4 + 2 < DK / 4) kn1 = K4[i4 + 2];
+                const float ke[4] = {kk.x, kk.y, kk.z, kk.w};
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    const int i = 4 * i4 + e;
+                    sr[i] = sr[i] * g;
+                    kv = kv + ke[e] * sr[i];
+                }
+                asm volatile("" ::: "memory");
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        }
+        {   // update and q.S
+            const float delta = (cvs[k][tid] - kv) * gt[k][r].y;
+            float acc = 0.0f;
+            float4 kn0 = K4[0], kn1 = K4[1];
+            float4 qn0 = Q4[0], qn1 = Q4[1];
+#pragma unroll
+            for (int i4 = 0; i4 < DK / 4; i4++) {
+                const float4 kk = kn0, qq = qn0;
+                kn0 = kn1;
+                qn0 = qn1;
+                if (i4 + 2 < DK / 4) {
+                    kn1 = K4[i4 + 2];
+                    qn1 = Q4[i4 + 2];
+                }
+                const float ke[4] = {kk.x, kk.y, kk.z, kk.w};
+                const float qe[4] = {qq.x, qq.y, qq.z, qq.w};
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    const int i = 4 * i4 + e;
+                    sr[i] = sr[i] + ke[e] * delta;
+                    acc = acc + qe[e] * sr[i];
+                }
+                asm volatile("" ::: "memory");
+                __builtin_amdgcn_sched_barrier(0);
+            }
+            const float o = rndf(acc);
+            ob[k][r][j] = o;
+            if (tr) tr[(size_t)k * tr_stride] = f2bf(o);      // (trace) rec_o
+        }
+    }
+}
+
+template <int MODE>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
 void k_gdn_decode(
-    CuArgs ca, const int32_t *dcu, const uint16_t *qkv, const uint16_t *z,
-    const uint16_t *a, const uint16_t *b, const uint16_t *conv_w,
+    CuArgs ca, const int32_t *__restrict__ dcu, int nseq, const uint16_t *qkv,
+    const uint16_t *z, const uint16_t *a, const uint16_t *b, const uint16_t *conv_w,
     const float *A_log, const float *dt_bias, const uint16_t *onorm_w,
     const uint16_t *conv_state, const float *S, uint16_t *conv_out, float *S_out,
-    uint16_t *y, int hk, float qscale, const int32_t *slot_in, const int32_t *slot_out,
-    int slots_inline, uint16_t *tr_ob) {
-    // (no __restrict__ on the small operands: it would let the compiler sink
-    // their loads past the ordering barrier below the state loads)
-    const int s = blockIdx.x / hk, kh = blockIdx.x % hk;
-    // the wave index is uniform per wavefront; saying so keeps the state
-    // tile's buffer descriptor in SGPRs (no per-lane waterfall loop)
+    uint16_t *y, int hk, float qscale, const int32_t *__restrict__ slot_in,
+    const int32_t *__restrict__ slot_out, int slots_inline, uint16_t *tr_ob) {
+    constexpr int KTT = MODE == 0 ? 1 : KT;
+    __shared__ __attribute__((aligned(16))) float raw[KTT][2 * DK];  // conv q, k; then normed
+    __shared__ __attribute__((aligned(16))) float ob[KTT][REP][DV];  // rnd(o)
+    __shared__ float cvs[KTT][256], zgs[KTT][256];   // thread t's conv(v), silu(z)
+    __shared__ float rsq[KTT][2], rso[KTT][REP];
+    __shared__ float2 gt[KTT][REP];                                   // exp(g), beta
+
     const int tid = threadIdx.x, lane = tid & 63;
     const int wv_ = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int r = wv_ >> 1, half = wv_ & 1, j = half * 64 + lane;
-    const int hv = hk * REP, h = kh * REP + r;
-    const size_t kd = (size_t)hk * DK, vd = (size_t)hv * DV, cd = 2 * kd + vd;
-    const int t0 = dcu ? dcu[s] : ca.cu[s];
-    const int t1 = dcu ? dcu[s + 1] : ca.cu[s + 1];
+    const int hv = hk * REP;
+    const int kd = hk * DK, vd = hv * DV, cd = 2 * kd + vd;
+    const int s = blockIdx.x / hk, kh = blockIdx.x % hk;
+    const bool inl = dcu == nullptr;
+    const int a0 = inl ? ca.cu[s] : 0, a1 = inl ? ca.cu[s + 1] : 0;
+    int d0 = 0, d1 = 0;
+    if (!inl) {
+        d0 = dcu[s];
+        d1 = dcu[s + 1];
+    }
+    const int t0 = __builtin_amdgcn_readfirstlane(inl ? a0 : d0);
+    const int t1 = __builtin_amdgcn_readfirstlane(inl ? a1 : d1);
     if (t0 == t1) return;
+    const int nt = t1 - t0;
     // the state slots this sequence reads and writes (identity without a
     // slot map)
-    const int nseq = gridDim.x / hk;
-    const int si = slots_inline ? ca.cu[nseq + 1 + s]
-                 : slot_in ? __builtin_amdgcn_readfirstlane(slot_in[s]) : s;
-    const int so = slots_inline ? ca.cu[2 * nseq + 1 + s]
-                 : slot_out ? __builtin_amdgcn_readfirstlane(slot_out[s]) : s;
+    const int ia = slots_inline ? ca.cu[nseq + 1 + s] : 0;
+    const int oa = slots_inline ? ca.cu[2 * nseq + 1 + s] : 0;
+    int id = s, od = s;
+    if (!slots_inline && slot_in) id = slot_in[s];
+    if (!slots_inline && slot_out) od = slot_out[s];
+    const int si = __builtin_amdgcn_readfirstlane(slots_inline ? ia : id);
+    const int so = __builtin_amdgcn_readfirstlane(slots_inline ? oa : od);
+    const int h = kh * REP + r;
+    const int cqk = tid < DK ? kh * DK + tid : kd + kh * DK + (tid - DK);
+    const int cvg = 2 * kd + kh * REP * DV + tid;   // this thread's v channel
+    // gate lanes: wave 1, lane 2k + rr serves token k, v-head 2kh + rr
+    const int gk = lane >> 1, grr = lane & 1, gh = kh * REP + grr;
 
-    __shared__ __attribute__((aligned(16))) float raw[2 * DK];   // conv q, k
-    __shared__ __attribute__((aligned(16))) float qkn[2 * DK];   // normed q, k
-    __shared__ __attribute__((aligned(16))) float ob[REP][DV];   // rnd(o)
-    __shared__ float rsq[2], rso[REP];
-    __shared__ float2 gt[REP];                                    // exp(g), beta
-
-    const size_t cqk = tid < DK ? (size_t)kh * DK + tid : kd + (size_t)kh * DK + (tid - DK);
-    const size_t cv = 2 * kd + (size_t)h * DV + j;
-    const uint16_t *stq = conv_state + (size_t)si * cd * 3 + cqk * 3;
-    const uint16_t *stv = conv_state + (size_t)si * cd * 3 + cv * 3;
-    // Small per-token operands, loaded as raw bits before the state tile.
-    uint32_t cwq_lo, cwq_hi, cwv_lo, cwv_hi;          // 4 bf16 conv taps each
-    {
-        const uint2 wq2 = *reinterpret_cast<const uint2 *>(conv_w + cqk * 4);
-        const uint2 wv2 = *reinterpret_cast<const uint2 *>(conv_w + cv * 4);
-        cwq_lo = wq2.x; cwq_hi = wq2.y; cwv_lo = wv2.x; cwv_hi = wv2.y;
-    }
-    uint32_t q0 = stq[0], q1 = stq[1], q2 = stq[2];
-    uint32_t v0 = stv[0], v1 = stv[1], v2 = stv[2];
+    // Small operands (raw bits).
+    const uint2 cwq = *reinterpret_cast<const uint2 *>(conv_w + (size_t)cqk * 4);
+    const uint2 cwv = *reinterpret_cast<const uint2 *>(conv_w + (size_t)cvg * 4);
+    const uint16_t *stq = conv_state + (size_t)si * cd * 3 + (size_t)cqk * 3;
+    const uint16_t *stv = conv_state + (size_t)si * cd * 3 + (size_t)cvg * 3;
+    uint32_t w0 = stq[0], w1 = stq[1], w2 = stq[2];
+    uint32_t u0 = stv[0], u1 = stv[1], u2 = stv[2];
     uint32_t wo_b = onorm_w[j];
-    const int gh = kh * REP + (tid >> 7);            // gate head of lanes 0 of waves 1, 3
     uint32_t alog_b = __float_as_uint(A_log[gh]), dtb_b = __float_as_uint(dt_bias[gh]);
-    uint32_t xq = qkv[(size_t)t0 * cd + cqk], xv = qkv[(size_t)t0 * cd + cv];
-    uint32_t zc = z[(size_t)t0 * vd + (size_t)h * DV + j];
-    uint32_t ac = a[(size_t)t0 * hv + gh], bc = b[(size_t)t0 * hv + gh];
-
-    // Keep the small loads above in front of the state loads: the memory
-    // counter retires in order, so a small load issued after the state
-    // loads would make the gate math wait for the whole state tile. The
-    // memory clobber stops IR passes sinking them, the sched_barrier stops
-    // the machine scheduler.
-    asm volatile("" ::: "memory");
-    __builtin_amdgcn_sched_barrier(0);
-    // this wave's 128x64 state tile: 32 x 16-byte loads per lane
-    const auto Sr = buf_rsrc(const_cast<float *>(S) + ((size_t)si * hv + h) * DK * DV, DK * DV * 4);
+    uint32_t xq[KTT], xv[KTT], zc[KTT], ag = 0, bg = 0;
+    const int n0 = MODE == 0 ? 1 : min(nt, KTT);
+#pragma unroll
+    for (int k = 0; k < KTT; k++) {
+        if (k < n0) {
+            const size_t t = (size_t)(t0 + k);
+            xq[k] = qkv[t * cd + cqk];
+            xv[k] = qkv[t * cd + cvg];
+            zc[k] = z[t * vd + kh * REP * DV + tid];
+        }
+    }
+    if (gk < n0) {
+        ag = a[(size_t)(t0 + gk) * hv + gh];
+        bg = b[(size_t)(t0 + gk) * hv + gh];
+    }
+    uint32_t c0x = cwq.x, c0y = cwq.y, c1x = cwv.x, c1y = cwv.y;
     const int voff = (half * 32 * 64 + lane) * 16;
     float sr[DK];
+    // This wave's 128x64 state tile (32 x 16-byte loads per lane). With one
+    // token it is loaded before phase A, whose gate math then runs under
+    // the loads; with several it is loaded after phase A, so that its 128
+    // registers are not live through phase A's per-token gate and silu
+    // code. (The descriptor is made where si and h are known uniform.)
+    constexpr bool kEarlyTile = MODE == 0;
+    auto load_tile = [&]() {
+        const int tix = __builtin_amdgcn_readfirstlane(si * hv + h);
+        const auto Sr = buf_rsrc(S + (size_t)tix * DK * DV, DK * DV * 4);
 #pragma unroll
-    for (int q = 0; q < DK / 4; q++) {
-        const f32x4_t v = buf_ld4(Sr, voff, q * 1024);
-        sr[4 * q + 0] = v[0];
-        sr[4 * q + 1] = v[1];
-        sr[4 * q + 2] = v[2];
-        sr[4 * q + 3] = v[3];
+        for (int q = 0; q < DK / 4; q++) {
+            const f32x4_t v = buf_ld4(Sr, voff, q * 1024);
+            sr[4 * q + 0] = v[0];
+            sr[4 * q + 1] = v[1];
+            sr[4 * q + 2] = v[2];
+            sr[4 * q + 3] = v[3];
+        }
+    };
+    if (kEarlyTile) {
+        // small loads stay in front of the tile loads: the memory counter
+        // retires in order, so a small load behind the tile would make the
+        // phase-A math wait for the whole tile
+        asm volatile("" ::: "memory");
+        __builtin_amdgcn_sched_barrier(0);
+        load_tile();
+        asm volatile("" : "+v"(c0x), "+v"(c0y), "+v"(c1x), "+v"(c1y), "+v"(w0), "+v"(w1),
+                     "+v"(w2), "+v"(u0), "+v"(u1), "+v"(u2), "+v"(wo_b), "+v"(alog_b),
+                     "+v"(dtb_b), "+v"(ag), "+v"(bg));
+        asm volatile("" : "+v"(xq[0]), "+v"(xv[0]), "+v"(zc[0]));
     }
-    // Pin every small operand after the state loads, so no math on them is
-    // hoisted in front of the state loads (each use then waits only for
-    // its own small load).
-    asm volatile("" : "+v"(cwq_lo), "+v"(cwq_hi), "+v"(cwv_lo), "+v"(cwv_hi),
-                 "+v"(q0), "+v"(q1), "+v"(q2), "+v"(v0), "+v"(v1), "+v"(v2),
-                 "+v"(wo_b), "+v"(alog_b), "+v"(dtb_b), "+v"(xq), "+v"(xv),
-                 "+v"(zc), "+v"(ac), "+v"(bc));
-    const float wq[4] = {__uint_as_float(cwq_lo << 16), __uint_as_float(cwq_lo & 0xffff0000u),
-                         __uint_as_float(cwq_hi << 16), __uint_as_float(cwq_hi & 0xffff0000u)};
-    const float wvv[4] = {__uint_as_float(cwv_lo << 16), __uint_as_float(cwv_lo & 0xffff0000u),
-                          __uint_as_float(cwv_hi << 16), __uint_as_float(cwv_hi & 0xffff0000u)};
+    const float wq[4] = {__uint_as_float(c0x << 16), __uint_as_float(c0x & 0xffff0000u),
+                         __uint_as_float(c0y << 16), __uint_as_float(c0y & 0xffff0000u)};
+    const float wvv[4] = {__uint_as_float(c1x << 16), __uint_as_float(c1x & 0xffff0000u),
+                          __uint_as_float(c1y << 16), __uint_as_float(c1y & 0xffff0000u)};
     const float wo = bf2f((uint16_t)wo_b);
-    const float Alog = __uint_as_float(alog_b), dtb = __uint_as_float(dtb_b);
 
-    const int tend = MULTI ? t1 : t0 + 1;   // one token: straight-line code
-    for (int t = t0; t < tend; t++) {
-        const uint16_t cq = conv_tap4(wq, bf2f(q0), bf2f(q1), bf2f(q2), bf2f(xq));
-        const uint16_t cvv = conv_tap4(wvv, bf2f(v0), bf2f(v1), bf2f(v2), bf2f(xv));
-        q0 = q1; q1 = q2; q2 = xq;
-        v0 = v1; v1 = v2; v2 = xv;   // (16-bit codes held in 32-bit registers)
-        raw[tid] = bf2f(cq);
-        if (lane == 0 && (wv_ == 1 || wv_ == 3)) {
-            const float g = decay_of(ac, Alog, dtb);
-            gt[tid >> 7] = make_float2(exp_cr(g), rndf(sigmoid_cr(bf2f(bc))));
-        }
-        const float zf = bf2f(zc);
-        const float zg = zf * sigmoid_cr(zf);          // silu(z), fp32
-        __syncthreads();
-        if (tid == 0 || tid == DK)
-            rsq[tid / DK] = 1.0f / sqrtf(seq_sumsq(raw + tid, DK) + kEps);
-        if (MULTI && t + 1 < t1) {                     // next token operands
-            xq = qkv[(size_t)(t + 1) * cd + cqk];
-            xv = qkv[(size_t)(t + 1) * cd + cv];
-            zc = z[(size_t)(t + 1) * vd + (size_t)h * DV + j];
-            ac = a[(size_t)(t + 1) * hv + gh];
-            bc = b[(size_t)(t + 1) * hv + gh];
-        }
-        __syncthreads();
-        qkn[tid] = tid < DK ? (raw[tid] * rsq[0]) * qscale : raw[tid] * rsq[1];
-        __syncthreads();
-        // c/gdn.h:482-503 on column j. k and q reach every lane as LDS
-        // broadcast reads, four values per 16-byte read, so the VALU only
-        // does the seven operations per state element the reference's
-        // rounding order needs (a readlane per broadcast value would add
-        // three VALU operations per element).
-        const float4 *K4 = reinterpret_cast<const float4 *>(qkn + DK);
-        const float4 *Q4 = reinterpret_cast<const float4 *>(qkn);
-        const float2 gb = gt[r];
-        // The reads run two groups of four ahead; a scheduling barrier per
-        // group keeps the compiler from hoisting all of them (the state
-        // slice already holds 128 registers).
-        float kv = 0.0f;
-        float4 kn0 = K4[0], kn1 = K4[1];
+    // modes 0 and 1 hold one chunk (the host checked the token counts)
+    const int cend = MODE == 2 ? nt : 1;
+    for (int c0 = 0; c0 < cend; c0 += KTT) {
+        const int n = MODE == 0 ? 1 : min(KTT, nt - c0);
+        if (MODE == 2 && c0 > 0) {                 // a later chunk's inputs
 #pragma unroll
-        for (int i4 = 0; i4 < DK / 4; i4++) {
-            const float4 kk = kn0;
-            kn0 = kn1;
-            if (i4 + 2 < DK / 4) kn1 = K4[i4 + 2];
-            const float ke[4] = {kk.x, kk.y, kk.z, kk.w};
-#pragma unroll
-            for (int e = 0; e < 4; e++) {
-                const int i = 4 * i4 + e;
-                sr[i] = sr[i] * gb.x;
-                kv = kv + ke[e] * sr[i];
+            for (int k = 0; k < KTT; k++) {
+                if (k < n) {
+                    const size_t t = (size_t)(t0 + c0 + k);
+                    xq[k] = qkv[t * cd + cqk];
+                    xv[k] = qkv[t * cd + cvg];
+                    zc[k] = z[t * vd + kh * REP * DV + tid];
+                }
             }
-            __builtin_amdgcn_sched_barrier(0);
-        }
-        const float delta = (bf2f(cvv) - kv) * gb.y;
-        float acc = 0.0f;
-        kn0 = K4[0];
-        kn1 = K4[1];
-        float4 qn0 = Q4[0], qn1 = Q4[1];
-#pragma unroll
-        for (int i4 = 0; i4 < DK / 4; i4++) {
-            const float4 kk = kn0, qq = qn0;
-            kn0 = kn1;
-            qn0 = qn1;
-            if (i4 + 2 < DK / 4) {
-                kn1 = K4[i4 + 2];
-                qn1 = Q4[i4 + 2];
+            if (gk < n) {
+                ag = a[(size_t)(t0 + c0 + gk) * hv + gh];
+                bg = b[(size_t)(t0 + c0 + gk) * hv + gh];
             }
-            const float ke[4] = {kk.x, kk.y, kk.z, kk.w}, qe[4] = {qq.x, qq.y, qq.z, qq.w};
-#pragma unroll
-            for (int e = 0; e < 4; e++) {
-                const int i = 4 * i4 + e;
-                sr[i] = sr[i] + ke[e] * delta;
-                acc = acc + qe[e] * sr[i];
-            }
-            __builtin_amdgcn_sched_barrier(0);
         }
-        const float o = rndf(acc);
-        ob[r][j] = o;
-        if (tr_ob) tr_ob[(size_t)t * vd + (size_t)h * DV + j] = f2bf(o);   // (trace) rec_o
+        // ---- A: token-parallel pieces
+        #pragma unroll
+        for (int k = 0; k < KTT; k++) {
+            if (k < n) {
+                const uint16_t cq = conv_tap4(wq, bf2f(w0), bf2f(w1), bf2f(w2), bf2f(xq[k]));
+                const uint16_t cvv = conv_tap4(wvv, bf2f(u0), bf2f(u1), bf2f(u2), bf2f(xv[k]));
+                w0 = w1; w1 = w2; w2 = xq[k];
+                u0 = u1; u1 = u2; u2 = xv[k];   // (16-bit codes held in 32-bit registers)
+                raw[k][tid] = bf2f(cq);
+                cvs[k][tid] = bf2f(cvv);
+                const float zf = bf2f(zc[k]);
+                zgs[k][tid] = zf * sigmoid_cr(zf);     // silu(z), fp32
+            }
+        }
         __syncthreads();
-        if (tid == 0 || tid == DK)
-            rso[tid / DK] = 1.0f / sqrtf(seq_sumsq(ob[tid / DK], DV) / (float)DV + kEps);
+        if (wv_ == 0 && lane < 2 * n) {                // l2-norm sums, one per lane
+            const int k = lane >> 1, qk = lane & 1;
+            rsq[k][qk] = 1.0f / sqrtf(sumsq128(&raw[k][qk * DK]) + kEps);
+        } else if (wv_ == 1 && lane < 2 * n) {         // gates, one pair per lane
+            const float g = decay_of((uint16_t)ag, __uint_as_float(alog_b), __uint_as_float(dtb_b));
+            gt[gk][grr] = make_float2(exp_cr(g), rndf(sigmoid_cr(bf2f((uint16_t)bg))));
+        }
         __syncthreads();
-        const float x1 = rndf(o * rso[r]);
-        const float x2 = rndf(x1 * wo);
-        y[(size_t)t * vd + (size_t)h * DV + j] = f2bf(x2 * zg);
+#pragma unroll
+        for (int k = 0; k < KTT; k++)
+            if (k < n)
+                raw[k][tid] = tid < DK ? (raw[k][tid] * rsq[k][0]) * qscale
+                                       : raw[k][tid] * rsq[k][1];
+        __syncthreads();
+        if (!kEarlyTile && c0 == 0) load_tile();
+        // ---- B: the recurrence on this wave's columns
+        recur_chunk(sr, raw, gt, cvs, ob, n, r, j, tid,
+                    tr_ob ? tr_ob + (size_t)(t0 + c0) * vd + h * DV + j : nullptr, vd);
+        if (c0 + KTT >= cend) {
+            // the last chunk: the tile is final; storing it here frees its
+            // registers for phase C
+            const int tox = __builtin_amdgcn_readfirstlane(so * hv + h);
+            const auto Sw = buf_rsrc(S_out + (size_t)tox * DK * DV, DK * DV * 4);
+#pragma unroll
+            for (int q = 0; q < DK / 4; q++)
+                buf_st4(Sw, voff, q * 1024,
+                        f32x4_t{sr[4 * q + 0], sr[4 * q + 1], sr[4 * q + 2], sr[4 * q + 3]});
+        }
+
+        // ---- C: output norms, then y
+        __syncthreads();
+        if (wv_ == 2 && lane < 2 * n) {
+            const int k = lane >> 1, rr = lane & 1;
+            rso[k][rr] = 1.0f / sqrtf(sumsq128(&ob[k][rr][0]) / (float)DV + kEps);
+        }
+        __syncthreads();
+#pragma unroll
+        for (int k = 0; k < KTT; k++) {
+            if (k < n) {
+                const float x1 = rndf(ob[k][r][j] * rso[k][r]);
+                const float x2 = rndf(x1 * wo);
+                y[(size_t)(t0 + c0 + k) * vd + h * DV + j] = f2bf(x2 * zgs[k][tid]);
+            }
+        }
     }
-    const auto Sw = buf_rsrc(S_out + ((size_t)so * hv + h) * DK * DV, DK * DV * 4);
-#pragma unroll
-    for (int q = 0; q < DK / 4; q++)
-        buf_st4(Sw, voff, q * 1024,
-                f32x4_t{sr[4 * q + 0], sr[4 * q + 1], sr[4 * q + 2], sr[4 * q + 3]});
-    uint16_t *otq = conv_out + (size_t)so * cd * 3 + cqk * 3;
-    uint16_t *otv = conv_out + (size_t)so * cd * 3 + cv * 3;
-    otq[0] = q0; otq[1] = q1; otq[2] = q2;
-    otv[0] = v0; otv[1] = v1; otv[2] = v2;
+    uint16_t *otq = conv_out + (size_t)so * cd * 3 + (size_t)cqk * 3;
+    uint16_t *otv = conv_out + (size_t)so * cd * 3 + (size_t)cvg * 3;
+    otq[0] = w0; otq[1] = w1; otq[2] = w2;
+    otv[0] = u0; otv[1] = u1; otv[2] = u2;
 }
 
 // ---- token-parallel pieces for the chunked prefill ------------------------
@@ -720,11 +835,12 @@ static int gdn_decode_run(const ApusHipGdnLayer *L, size_t B, const int32_t *cu,
             return r;
     }
     const float qscale = (float)pow((double)L->dk, -0.5);
-    const bool multi = (size_t)cu[B] != B;     // some sequence has != 1 token
-    auto kern = multi ? k_gdn_decode<true> : k_gdn_decode<false>;
+    int max_tok = 0;                           // the most tokens of one sequence
+    for (size_t s = 0; s < B; s++) max_tok = std::max(max_tok, cu[s + 1] - cu[s]);
+    auto kern = max_tok <= 1 ? k_gdn_decode<0> : max_tok <= KT ? k_gdn_decode<1> : k_gdn_decode<2>;
     APUS_TIMED("k_gdn_decode",
                kern<<<(unsigned)(B * L->hk), 256, 0, stream()>>>(
-        ca, dcu, qkv, z, a, b, L->conv_w, L->A_log, L->dt_bias, L->onorm_w,
+        ca, dcu, (int)B, qkv, z, a, b, L->conv_w, L->A_log, L->dt_bias, L->onorm_w,
         conv_in, S_in, conv_out, S_out, y, (int)L->hk, qscale, dsin, dsout, (int)slots_inline,
         tr ? tr->rec_o : nullptr));
     APUS_LAUNCHED("k_gdn_decode");

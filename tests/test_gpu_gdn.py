@@ -181,6 +181,19 @@ def test_gdn_decode_ragged_verify(hip, orc):
     _run_decode(hip, orc, rng, cu)
 
 
+@pytest.mark.parametrize("kmax", [1, 4, 9])
+def test_gdn_decode_many_items(hip, orc, kmax):
+    """More (sequence, K head) items than compute units, so each persistent
+    workgroup carries its pipeline across many items: 200 sequences of
+    0..kmax tokens (empty ones included). kmax 1, 4 and 9 take the
+    one-token, the up-to-four-token and the general token loop."""
+    rng = np.random.default_rng(100 + kmax)
+    k = rng.integers(0, kmax + 1, 200)
+    k[rng.integers(0, 200)] = kmax
+    cu = np.concatenate([[0], np.cumsum(k)]).astype(np.int32)
+    _run_decode(hip, orc, rng, cu)
+
+
 def test_gdn_decode_zero_state_long(hip, orc):
     """A 32-token single sequence from zero state: decode stepping through
     a prefill-length span keeps matching the sequential recurrence."""
