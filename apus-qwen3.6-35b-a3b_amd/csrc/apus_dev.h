@@ -121,6 +121,18 @@ __device__ __forceinline__ i32x4 dma_rsrc(const void *base, uint32_t bytes) {
                  __builtin_amdgcn_readfirstlane((int)bytes), 0x00020000};
 }
 
+// A wave-uniform 4-byte read through the scalar cache (s_buffer_load):
+// the value lands in an SGPR and is counted by lgkmcnt, never by the
+// vector-memory counter, so reading it cannot make a wave wait for its
+// streaming loads (a vector load inside a branch also makes the compiler
+// drain that counter at the join). bytes bounds the resource; reads past
+// it return 0.
+__device__ int llvm_s_buffer_load_i32(i32x4 rsrc, int off, int aux)
+    __asm("llvm.amdgcn.s.buffer.load.i32");
+__device__ __forceinline__ int sload_i32(const int32_t *base, uint32_t bytes, int index) {
+    return llvm_s_buffer_load_i32(dma_rsrc(base, bytes), index * 4, 0);
+}
+
 // one 16-byte copy per lane from byte offset voff (per lane) + soff
 // (uniform) to LDS byte address lds (uniform) + 16 * lane
 __device__ __forceinline__ void dma16(i32x4 r, int voff, int soff, uint32_t lds) {

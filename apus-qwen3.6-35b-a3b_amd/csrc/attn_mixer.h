@@ -5,6 +5,7 @@
 
 #include "../../include/apus_hip.h"
 #include "apus_rt.h"
+#include "apus_dev.h"
 
 namespace apus {
 
@@ -31,12 +32,13 @@ struct KvRef {
 __device__ __forceinline__ size_t kv_block_id(const KvRef &r, int h, int b) {
     return r.btab ? (size_t)r.btab[(size_t)h * r.bstride + b] : (size_t)h * r.bstride + b;
 }
-// the same for a wave-uniform (h, b): the id kept in a scalar register, so
-// addresses built on it stay scalar bases
+// the same for a wave-uniform (h, b): a scalar load into a scalar register,
+// so addresses built on it stay scalar bases and the lookup never waits on
+// (or makes the compiler drain) the vector-memory counter
 __device__ __forceinline__ size_t kv_block_id_u(const KvRef &r, int h, int b) {
-    return r.btab ? (size_t)(uint32_t)__builtin_amdgcn_readfirstlane(
-                        r.btab[(size_t)h * r.bstride + b])
-                  : (size_t)h * r.bstride + b;
+    if (!r.btab) return (size_t)h * r.bstride + b;
+    const int hu = __builtin_amdgcn_readfirstlane(h), bu = __builtin_amdgcn_readfirstlane(b);
+    return (size_t)(uint32_t)sload_i32(r.btab + (size_t)hu * r.bstride, (uint32_t)r.bstride * 4, bu);
 }
 
 // ---- per-call sequence metadata ------------------------------------------

@@ -138,32 +138,32 @@ __device__ __forceinline__ int fa_lane() {
 // K rows of key tile kt -> the K buffer at LDS address kb (row pitch
 // KROW): wavefront w copies tile rows 8w..8w+7, one row (32 pieces, lanes
 // 0..31) per instruction, from cache block 2kt + w/4 (its rows
-// 8(w%4)..+7) given by the resource kr, which ends at the last key: rows
-// past it read zero (and their scores are masked).
-__device__ __forceinline__ void fa_dma_k(uint32_t kb, i32x4 kr, int wave) {
+// 8(w%4)..+7) at byte offset soff of the resource kr, which ends at the
+// last key: rows past it read zero (and their scores are masked).
+__device__ __forceinline__ void fa_dma_k(uint32_t kb, i32x4 kr, int soff, int wave) {
     const int lane = fa_lane();
     if (lane < 32) {
 #pragma unroll
         for (int j = 0; j < 8; j++) {
             const int r = 8 * wave + j, rb = 8 * (wave & 3) + j;
-            dma16(kr, (rb * D + lane * 8) * 2, 0, kb + r * KROW);
+            dma16(kr, (rb * D + lane * 8) * 2, soff, kb + r * KROW);
         }
     }
 }
 
 // V^T blocks 2kt, 2kt+1 -> the LDS blocks at vb0, vb1 ([d][32 keys]):
 // wavefront w copies the 1 KiB groups 4w..4w+3 of block w / 4 (16 d-rows
-// of 4 pieces each) from the cache block given by vr (empty for a block
-// past the last key: it reads zero). Keys past the last one inside its
+// of 4 pieces each) from the cache block at byte offset soff of vr (a
+// block past the last key lies past the resource's end: it reads zero). Keys past the last one inside its
 // block are zeroed in LDS before use.
-__device__ __forceinline__ void fa_dma_v(uint32_t vb0, uint32_t vb1, i32x4 vr, int wave) {
+__device__ __forceinline__ void fa_dma_v(uint32_t vb0, uint32_t vb1, i32x4 vr, int soff, int wave) {
     const int lane = fa_lane();
 #pragma unroll
     for (int j = 0; j < 4; j++) {
         const int q = 4 * wave + j, bb = q >> 4, g = q & 15;
         const int r = 16 * g + (lane >> 2);
         const int c = (lane & 3) ^ ((r >> 2) & 3);
-        dma16(vr, (r * VB + c * 8) * 2, 0, (bb ? vb1 : vb0) + g * 16 * VB * 2);
+        dma16(vr, (r * VB + c * 8) * 2, soff, (bb ? vb1 : vb0) + g * 16 * VB * 2);
     }
 }
 
@@ -210,7 +210,7 @@ __device__ __forceinline__ int fa_block(const FaCtx &c, int kt) {
     return min(2 * kt + (c.wave >> 2), c.nblk - 1);
 }
 __device__ __forceinline__ int fa_block_id(const FaCtx &c, int b) {
-    return c.kv.btab ? c.kv.btab[(size_t)c.hd * c.kv.bstride + b] : c.hd * c.kv.bstride + b;
+    return (int)kv_block_id_u(c.kv, c.hd, b);
 }
 __device__ __forceinline__ i32x4 fa_krsrc(const FaCtx &c, int kt, int id) {
     const int b = 2 * kt + (c.wave >> 2);
@@ -469,8 +469,27 @@ __global__ __launch_bounds__(64 * NW) void k_attn_fa(
     // tile u = 0 .. 2nkt-1 of the key stream: pass u / nkt, key tile u %
     // nkt. idn: this wavefront's block id for the next tile to copy, read
     // a tile ahead (its load completes under the tile's copies).
-    fa_dma_k(c.lds + kbuf(0), fa_krsrc(c, 0, fa_block_id(c, fa_block(c, 0))), c.wave);
-    int idn = fa_block_id(c, fa_block(c, 1 % nkt));
+    // An identity (flat) table puts the sequence's blocks of this kv head
+    // at a fixed stride: one resource per cache covers them all and a tile
+    // only moves a scalar offset. A paged table builds each wavefront's
+    // resources from the block id, read a tile ahead.
+    const bool flat = kv.btab == nullptr;
+    const int blk_bytes = nkv * KVB * D * 2;
+    i32x4 kflat = {0, 0, 0, 0}, vflat = {0, 0, 0, 0};
+    if (flat) {
+        const size_t b0 = (size_t)c.hd * kv.bstride * nkv + kvh;   // block 0 of this kv head
+        kflat = dma_rsrc(kv.k + b0 * KVB * D,
+                         (uint32_t)((c.nblk - 1) * blk_bytes + (c.nkeys - KVB * (c.nblk - 1)) * D * 2));
+        vflat = dma_rsrc(kv.v + b0 * D * KVB, (uint32_t)((c.nblk - 1) * blk_bytes + D * KVB * 2));
+    }
+    auto wblock = [&](int kt) { return 2 * kt + (c.wave >> 2); };   // this wave's (unclamped) block
+    int idn = 0;
+    if (flat) {
+        fa_dma_k(c.lds + kbuf(0), kflat, wblock(0) * blk_bytes, c.wave);
+    } else {
+        fa_dma_k(c.lds + kbuf(0), fa_krsrc(c, 0, fa_block_id(c, fa_block(c, 0))), 0, c.wave);
+        idn = fa_block_id(c, fa_block(c, 1 % nkt));
+    }
 
     // query row of this lane: token 4w + l32/8, head l32%8 of the kv head
     const int tk = c.wave * 4 + c.l32 / GRP, head = kvh * GRP + c.l32 % GRP;
@@ -488,12 +507,20 @@ __global__ __launch_bounds__(64 * NW) void k_attn_fa(
     auto begin_tile = [&](int u) {
         fa_publish();
         if (u + 1 < 2 * nkt) {
-            const int kt1 = (u + 1) % nkt, id = __builtin_amdgcn_readfirstlane(idn);
-            fa_dma_k(c.lds + kbuf(u + 1), fa_krsrc(c, kt1, id), c.wave);
-            if (u + 1 >= nkt)
-                fa_dma_v(c.lds + vbuf(u + 1, 0), c.lds + vbuf(u + 1, 1), fa_vrsrc(c, kt1, id),
-                         c.wave);
-            idn = fa_block_id(c, fa_block(c, (u + 2) % nkt));
+            const int kt1 = (u + 1) % nkt;
+            if (flat) {
+                const int off = wblock(kt1) * blk_bytes;
+                fa_dma_k(c.lds + kbuf(u + 1), kflat, off, c.wave);
+                if (u + 1 >= nkt)
+                    fa_dma_v(c.lds + vbuf(u + 1, 0), c.lds + vbuf(u + 1, 1), vflat, off, c.wave);
+            } else {
+                const int id = __builtin_amdgcn_readfirstlane(idn);
+                fa_dma_k(c.lds + kbuf(u + 1), fa_krsrc(c, kt1, id), 0, c.wave);
+                if (u + 1 >= nkt)
+                    fa_dma_v(c.lds + vbuf(u + 1, 0), c.lds + vbuf(u + 1, 1), fa_vrsrc(c, kt1, id),
+                             0, c.wave);
+                idn = fa_block_id(c, fa_block(c, (u + 2) % nkt));
+            }
         }
         // the last tile's V keys past nkeys: zero (P is 0 there, but
         // 0 * NaN from unwritten cache memory would not be)
@@ -576,16 +603,30 @@ __global__ __launch_bounds__(64 * NW) void k_attn_fa(
             for (int q4 = 0; q4 < 4; q4++) {
                 const int d0 = mt * 32 + 8 * q4 + 4 * c.h;
                 const u16x4 gv = *reinterpret_cast<const u16x4 *>(gr + d0);
-                u16x4 out, oc;
+                u16x4 out;
 #pragma unroll
                 for (int i = 0; i < 4; i++) {
                     const float ov = rndf(o[mt][4 * q4 + i]);
                     const float gs = bf2f(sig_bf[gv[i]]);     // rnd(sigmoid(gate))
                     out[i] = f2bf(ov * gs);
-                    oc[i] = f2bf(ov);
                 }
                 *reinterpret_cast<u16x4 *>(yr + d0) = out;
-                if (tr_attno) *reinterpret_cast<u16x4 *>(tr_attno + row * D + d0) = oc;   // (trace)
+            }
+        }
+        // (trace) rnd(o) before the gate, in a loop of its own: a
+        // conditional store inside the loop above would make the compiler
+        // drain the memory counter at every join
+        if (tr_attno) {
+#pragma unroll
+            for (int mt = 0; mt < D / 32; mt++) {
+#pragma unroll
+                for (int q4 = 0; q4 < 4; q4++) {
+                    const int d0 = mt * 32 + 8 * q4 + 4 * c.h;
+                    u16x4 oc;
+#pragma unroll
+                    for (int i = 0; i < 4; i++) oc[i] = f2bf(rndf(o[mt][4 * q4 + i]));
+                    *reinterpret_cast<u16x4 *>(tr_attno + row * D + d0) = oc;
+                }
             }
         }
     }
