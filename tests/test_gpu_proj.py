@@ -64,7 +64,8 @@ def test_gemm_dev_bitwise(hip, orc, M, O, K):
 
 
 @pytest.mark.parametrize("M,O,K", [(64, 12352, 2048), (200, 1000, 4096), (5, 70, 40),
-                                   (300, 517, 2048),    # through rocBLAS
+                                   (300, 517, 2048),    # M > 256: rocBLAS
+                                   (1000, 1000, 512),   # rocBLAS, ragged edges
                                    (7, 90, 40)])        # K % 32 != 0: rocBLAS
 def test_gemm_mfma_tolerance(hip, orc, M, O, K):
     import torch
