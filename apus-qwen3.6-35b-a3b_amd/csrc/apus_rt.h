@@ -52,7 +52,7 @@ enum ScratchSlot { kScratchIn = 0, kScratchIn2, kScratchIn3, kScratchIn4,
                    kScratchWork, kScratchWork2, kScratchWork3, kScratchMeta,
                    kScratchMeta2, kScratchMeta3,
                    // batched GDN mixer intermediates
-                   kScratchGdnQK, kScratchGdnV, kScratchGdnGate, kScratchGdnOB,
+                   kScratchGdnQK, kScratchGdnQKR, kScratchGdnV, kScratchGdnGate, kScratchGdnOB,
                    kScratchGdnChunk, kScratchGdnChunk2, kScratchGdnChunk3,
                    kScratchGdnChunk4, kScratchGdnChunk5,
                    kScratchGdnChunk6, kScratchGdnChunk7,

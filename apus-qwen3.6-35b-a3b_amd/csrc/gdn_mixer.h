@@ -10,7 +10,8 @@ namespace apus {
 
 // Per-call device intermediates (library scratch).
 struct GdnScratch {
-    float *qk = nullptr;          // [Ttot][2][hk*128]: l2-normed q (scaled), k
+    uint16_t *qk = nullptr;       // [Ttot][2][hk*128]: conv+SiLU codes of q, k
+    float *qkr = nullptr;         // [Ttot][2][hk]: their l2norm factors (q, then k)
     uint16_t *vconv = nullptr;    // [Ttot][hv*128]: conv+SiLU of the v channels
     float2 *gate = nullptr;       // [Ttot][hv]: (exp(g), beta)
     uint16_t *ob = nullptr;       // [Ttot][hv*128]: rnd(recurrence output)

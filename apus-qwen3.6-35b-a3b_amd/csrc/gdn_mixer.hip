@@ -453,16 +453,18 @@ constexpr int RSC = DV + 8;  // LDS row stride in bf16 codes: 16-byte aligned ro
 // three halo tokens are staged in LDS with 16-byte loads; thread c then
 // owns one q/k channel and one v channel and walks the tokens (a
 // sequence's first three tokens take their window from the old conv
-// state). One lane per (token, q|k) takes the ordered sum of squares for
-// the l2norm (c/gdn.h:402-416); 32 lanes evaluate the (exp(g), beta) gates
-// of the two v-heads, optionally with the raw g.
+// state). The q/k codes go out as they are, and one lane per (token, q|k)
+// takes the ordered sum of squares for the l2norm (c/gdn.h:402-416) and
+// writes the row's factor 1/sqrt(ss + eps) (the normalised row is code x
+// factor, rounded once, as the chunk kernels form it); 32 lanes evaluate
+// the (exp(g), beta) gates of the two v-heads, optionally with the raw g.
 __global__ __launch_bounds__(256) void k_gdn_prep(
     GdnCu ci, const int32_t *__restrict__ dcu, int B, int Ttot, const uint16_t *__restrict__ qkv,
     const uint16_t *__restrict__ a, const uint16_t *__restrict__ b,
     const uint16_t *__restrict__ conv_w, const float *__restrict__ A_log,
     const float *__restrict__ dt_bias, const uint16_t *__restrict__ conv_state,
-    float *__restrict__ qk, uint16_t *__restrict__ vconv,
-    float2 *__restrict__ gate, float *__restrict__ graw, int hk, float qscale,
+    uint16_t *__restrict__ qk, float *__restrict__ qkr, uint16_t *__restrict__ vconv,
+    float2 *__restrict__ gate, float *__restrict__ graw, int hk,
     const uint16_t *__restrict__ silu_bf, const uint16_t *__restrict__ sig_bf,
     const int32_t *__restrict__ slots, uint16_t *__restrict__ tr_conv,
     uint16_t *__restrict__ tr_beta) {
@@ -480,7 +482,6 @@ __global__ __launch_bounds__(256) void k_gdn_prep(
     __shared__ __attribute__((aligned(16))) char prep_lds[XIN_B > RAW_B ? XIN_B : RAW_B];
     uint16_t *xin = reinterpret_cast<uint16_t *>(prep_lds);
     float *raw = reinterpret_cast<float *>(prep_lds);
-    __shared__ float rs[2][PT];
     __shared__ int2 tseq[PT];                 // (sequence, its first token) per tile token
 
     // stage rows tb-3 .. tb+nt-1 (those that exist); LDS channel order
@@ -589,6 +590,7 @@ __global__ __launch_bounds__(256) void k_gdn_prep(
     for (int i = 0; i < PT; i++) {
         if (i < nt) {
             rrow[i * RS] = bf2f(sq[i]);
+            qk[(size_t)(tb + i) * 2 * kd + cqk] = sq[i];
             vconv[(size_t)(tb + i) * vd + (size_t)h * DV + j] = sv[i];
             if (tr_conv) {                    // (trace) conv+SiLU codes, c/layer.h:178
                 tr_conv[(size_t)(tb + i) * cd + cqk] = sq[i];
@@ -599,9 +601,9 @@ __global__ __launch_bounds__(256) void k_gdn_prep(
     __syncthreads();
     if (tid < 2 * PT) {                      // ordered sums, one lane per row
         const int r = tid & (PT - 1), w = tid / PT;
-        if (r < nt) {
-            rs[w][r] = 1.0f / sqrtf(row_sumsq(raw + w * PT * RS + r * RS) + kEps);
-        }
+        if (r < nt)
+            qkr[(size_t)(tb + r) * 2 * hk + w * hk + kh] =
+                1.0f / sqrtf(row_sumsq(raw + w * PT * RS + r * RS) + kEps);
     } else if (tid >= 64 && tid < 64 + REP * PT) {   // gates of the two v-heads
         const int r = (tid - 64) & (PT - 1), hh = kh * REP + (tid - 64) / PT;
         if (r < nt) {
@@ -613,12 +615,6 @@ __global__ __launch_bounds__(256) void k_gdn_prep(
             if (graw) graw[t * hv + hh] = g;
             if (tr_beta) tr_beta[t * hv + hh] = btc;
         }
-    }
-    __syncthreads();
-    const int w = tid < DK ? 0 : 1;
-    for (int i = 0; i < nt; i++) {
-        const float x = rrow[i * RS] * rs[w][i];
-        qk[(size_t)(tb + i) * 2 * kd + cqk] = w == 0 ? x * qscale : x;
     }
 }
 
@@ -739,18 +735,18 @@ int gdn_prep(const ApusHipGdnLayer *L, size_t B, const int32_t *cu, const int32_
              bool want_graw, const int32_t *slots, const ApusHipGdnTrace *tr) {
     const size_t kd = L->hk * DK, vd = L->hv * DV;
     if (!w->qk) {                              // else the caller's workspace
-        w->qk = (float *)scratch(kScratchGdnQK, Ttot * 2 * kd * 4);
+        w->qk = (uint16_t *)scratch(kScratchGdnQK, Ttot * 2 * kd * 2);
+        w->qkr = (float *)scratch(kScratchGdnQKR, Ttot * 2 * L->hk * 4);
         w->vconv = (uint16_t *)scratch(kScratchGdnV, Ttot * vd * 2);
         w->gate = (float2 *)scratch(kScratchGdnGate, Ttot * L->hv * 8);
         w->ob = (uint16_t *)scratch(kScratchGdnOB, Ttot * vd * 2);
         w->graw = want_graw ? (float *)scratch(kScratchGdnChunk3, Ttot * L->hv * 4) : nullptr;
     }
-    if (!w->qk || !w->vconv || !w->gate || !w->ob || (want_graw && !w->graw))
+    if (!w->qk || !w->qkr || !w->vconv || !w->gate || !w->ob || (want_graw && !w->graw))
         return kErrHip;
     // a traced call without the raw gates for WY writes them straight to
     // the trace
     float *graw = w->graw ? w->graw : (tr ? tr->gdecay : nullptr);
-    const float qscale = (float)pow((double)L->dk, -0.5);
     const ActTables *tabs = act_tables();
     if (!tabs) return kErrHip;
     GdnCu ci;
@@ -758,7 +754,7 @@ int gdn_prep(const ApusHipGdnLayer *L, size_t B, const int32_t *cu, const int32_
     APUS_TIMED("k_gdn_prep",
                k_gdn_prep<<<(unsigned)(cdiv(Ttot, PT) * L->hk), 256, 0, stream()>>>(
         ci, dcu, (int)B, (int)Ttot, qkv, a, b, L->conv_w, L->A_log, L->dt_bias, conv_state,
-        w->qk, w->vconv, w->gate, graw, (int)L->hk, qscale, tabs->silu_bf, tabs->sig_bf,
+        w->qk, w->qkr, w->vconv, w->gate, graw, (int)L->hk, tabs->silu_bf, tabs->sig_bf,
         slots, tr ? tr->qkv_conv : nullptr, tr ? tr->beta : nullptr));
     return launch_check("k_gdn_prep");
 }

@@ -129,12 +129,15 @@ __device__ __forceinline__ ChunkPos chunk_pos(const int32_t *cu, const int32_t *
 //   U  fp32 [8 column slices][4 row blocks][64][4]: element (t, j) at lane
 //      (j%16) + 16*((t%16)/4) of (j/16, t/16), slot t%4 -- the
 //      accumulator layout of the scan's D tile;
-//   F  fp32 [2][C]: F[0][t] = G_t, F[1][s] = exp(gamma_C - gamma_s).
+//   F  fp32 [3][C]: F[0][t] = G_t rq_t qscale (the scale of row t of
+//      Q S0, Q as codes), F[1][s] = exp(gamma_C - gamma_s) rk_s (the scale
+//      of key s in the state update, K as codes), F[2][0] = G_C.
 // Per (chunk, K head), written by the v-head of even index (both v-heads
-// of a K head hold the same q and k):
-//   Q  in W's layout (the A operand of G_t (Q S0));
-//   K  [8 state-row blocks][2 column blocks][64][16] as a B operand: lane
-//      g*16 + i%16 holds key rows s = 8g..8g+7 of state row i.
+// of a K head hold the same q and k), the conv codes themselves (exact in
+// bf16, so one MFMA per product against a split operand's two parts):
+//   Q  the codes in W's lane order (the A operand of Q S0);
+//   K  the codes as a B operand: lane g*16 + i%16 holds key rows
+//      s = 8g..8g+7 of state row i.
 __device__ __forceinline__ size_t bx_a_index(int t, int c, int nkb) {
     return ((size_t)((t >> 4) * nkb + (c >> 5)) * 64 + ((c & 31) >> 3) * 16 + (t & 15)) * 16 + (c & 7);
 }
@@ -143,6 +146,17 @@ __device__ __forceinline__ size_t bx_b_index(int s, int i) {
 }
 __device__ __forceinline__ size_t wy_u_index(int t, int j) {
     return ((size_t)((j >> 4) * 4 + (t >> 4)) * 64 + ((t & 15) >> 2) * 16 + (j & 15)) * 4 + (t & 3);
+}
+
+// q and k travel to the scan as code planes (exact bf16, no lo part) in
+// the same lane order, 1 KiB blocks of 64 lanes x 8 codes:
+//   Q  [4 row blocks][4 column blocks][64][8];
+//   K  [8 state-row blocks][2 key blocks][64][8].
+__device__ __forceinline__ size_t bx1_a_index(int t, int c, int nkb) {
+    return ((size_t)((t >> 4) * nkb + (c >> 5)) * 64 + ((c & 31) >> 3) * 16 + (t & 15)) * 8 + (c & 7);
+}
+__device__ __forceinline__ size_t bx1_b_index(int s, int i) {
+    return ((size_t)((i >> 4) * 2 + (s >> 5)) * 64 + ((s & 31) >> 3) * 16 + (i & 15)) * 8 + (s & 7);
 }
 
 // hi = rnd(x), lo = rnd(x - hi), as bf16 codes (hardware round to nearest
@@ -181,6 +195,17 @@ __device__ __forceinline__ f32x4 mfma_x3(u16x8 ah, u16x8 al, u16x8 bh, u16x8 bl,
     c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf(ah), as_bf(bl), c, 0, 0, 0);
     c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf(ah), as_bf(bh), c, 0, 0, 0);
     return c;
+}
+
+// acc += c.x with c exact bf16 codes and x = xh + xl split: c.xl then
+// c.xh. code_is_b: the codes are the B operand (x the A operand).
+__device__ __forceinline__ f32x4 mfma_x2a(u16x8 c, u16x8 xh, u16x8 xl, f32x4 acc, bool code_is_b) {
+    if (code_is_b) {
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf(xl), as_bf(c), acc, 0, 0, 0);
+        return __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf(xh), as_bf(c), acc, 0, 0, 0);
+    }
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf(c), as_bf(xl), acc, 0, 0, 0);
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf(c), as_bf(xh), acc, 0, 0, 0);
 }
 
 __device__ __forceinline__ float4 lds4_(const float *p) {
@@ -232,14 +257,18 @@ __device__ __forceinline__ f32x4 mfma_x6(u16x8 ah, u16x8 am, u16x8 al, u16x8 bh,
     return c;
 }
 
-// k_gdn_chunk_wy: one workgroup per (chunk, v-head), two per CU (Q's LDS
-// copy is reused for L once Q K^T is done).
-__global__ __launch_bounds__(256, 2) void k_gdn_chunk_wy(
-    ChunkSeqs sq, const int32_t *__restrict__ dmeta, const float *__restrict__ qk,
-    const uint16_t *__restrict__ vconv, const float2 *__restrict__ gate,
-    const float *__restrict__ graw, float *__restrict__ Ub, uint16_t *__restrict__ Wb,
-    uint16_t *__restrict__ Ab, float *__restrict__ Fb, uint16_t *__restrict__ Qp,
-    uint16_t *__restrict__ Kp, int hk, int pair_map) {
+// k_gdn_chunk_wy: one workgroup per (chunk, v-head), up to three per CU.
+// q and k arrive as their conv+SiLU bf16 codes with one l2norm factor per
+// row (the normalised rows are q_t = rq_t qscale cq_t, k_s = rk_s ck_s), so
+// q.k and k.k are the factors times the exact dot products of the codes:
+// one bf16 MFMA per product, fp32 accumulation, no operand splitting.
+constexpr int CKP = DK + 8;            // bf16 row stride of the code copies
+__global__ __launch_bounds__(256) void k_gdn_chunk_wy(
+    ChunkSeqs sq, const int32_t *__restrict__ dmeta, const uint16_t *__restrict__ qkc,
+    const float *__restrict__ qkr, const uint16_t *__restrict__ vconv,
+    const float2 *__restrict__ gate, const float *__restrict__ graw, float *__restrict__ Ub,
+    uint16_t *__restrict__ Wb, uint16_t *__restrict__ Ab, float *__restrict__ Fb,
+    uint16_t *__restrict__ Qp, uint16_t *__restrict__ Kp, int hk, int pair_map, float qscale) {
     const int hv = hk * REP;
     const size_t kd = (size_t)hk * DK, vd = (size_t)hv * DV;
     // unit = ci * hv + h. With pair_map the two v-heads of one K head (units
@@ -252,79 +281,82 @@ __global__ __launch_bounds__(256, 2) void k_gdn_chunk_wy(
     }
     const int ci = unit / hv, h = unit % hv, kh = h / REP;
     const bool wqk = h % REP == 0;              // this v-head writes Qp / Kp
-    uint16_t *Qpu = Qp + ((size_t)ci * hk + kh) * C * DK * 2;
-    uint16_t *Kpu = Kp + ((size_t)ci * hk + kh) * C * DK * 2;
+    uint16_t *Qpu = Qp + ((size_t)ci * hk + kh) * C * DK;
+    uint16_t *Kpu = Kp + ((size_t)ci * hk + kh) * C * DK;
     const int32_t *cu = dmeta ? dmeta : sq.cu;
     const int32_t *coff = dmeta ? dmeta + sq.n + 1 : sq.coff;
     const ChunkPos P = chunk_pos(cu, coff, sq.n, ci);
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
 
-    __shared__ __attribute__((aligned(16))) float Ks[C * KP];
-    __shared__ __attribute__((aligned(16))) float QL[C * KP];   // Q, then L [C][CP]
-    __shared__ float graw_s[C], gam[C], bet[C], Gs[C];
+    // LDS: q codes (later L, then W's staging together with the k codes),
+    // k codes, the V rows, per-token factors
+    constexpr int QC_B = C * CKP * 2, L_B = C * CP * 4;
+    static_assert(QC_B >= L_B, "L does not fit over the q codes");
+    static_assert(2 * QC_B >= C * KP * 4, "W's staging does not fit over the code copies");
+    __shared__ __attribute__((aligned(16))) char wy_lds[2 * QC_B + C * DV * 2];
+    uint16_t *Qc = reinterpret_cast<uint16_t *>(wy_lds);
+    float *Ls = reinterpret_cast<float *>(wy_lds);
+    uint16_t *Kc = reinterpret_cast<uint16_t *>(wy_lds + QC_B);
+    uint16_t *Vs = reinterpret_cast<uint16_t *>(wy_lds + 2 * QC_B);
+    __shared__ float graw_s[C], gam[C], bet[C], Gs[C], rq[C], rk[C];
 
-    // The chunk's V rows (the right-hand sides b V of the forward
-    // substitution) in 16-byte pieces, loaded first: loaded after this
-    // kernel's stores, their wait would also wait for every store's
-    // acknowledgement. They go to LDS once Q's copy is free.
-    typedef unsigned short u16x8_t __attribute__((ext_vector_type(8)));
-    constexpr int NV = C * DV / 8 / 256;
-    u16x8_t vreg[NV];
-#pragma unroll
-    for (int k = 0; k < NV; k++) {
-        const int t = tid / (DV / 8) + k * (256 / (DV / 8)), c8 = (tid % (DV / 8)) * 8;
-        vreg[k] = u16x8_t{0, 0, 0, 0, 0, 0, 0, 0};
-        if (t < P.nt)
-            vreg[k] = *reinterpret_cast<const u16x8_t *>(vconv + (size_t)(P.t0 + t) * vd +
-                                                         (size_t)h * DV + c8);
-    }
-    // rows t >= nt are padding: q = k = 0, g = 0, beta = 0
+    // rows t >= nt are padding: codes 0, factors 0, g = 0, beta = 0
     // (every load issued before the first LDS store)
-    constexpr int NQ = C * DK / 4 / 256;
-    float4 qv[NQ], kv[NQ];
+    typedef unsigned short u16x8_t __attribute__((ext_vector_type(8)));
+    constexpr int NL = C * DK / 8 / 256;       // 16-byte pieces per thread per matrix
+    u16x8_t qv[NL], kv[NL], vv[NL];
 #pragma unroll
-    for (int u = 0; u < NQ; u++) {
-        const int e = tid + 256 * u, t = e / (DK / 4), q4 = (e % (DK / 4)) * 4;
-        qv[u] = kv[u] = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int u = 0; u < NL; u++) {
+        const int e = tid + 256 * u, t = e / (DK / 8), c8 = (e % (DK / 8)) * 8;
+        qv[u] = kv[u] = vv[u] = u16x8_t{0, 0, 0, 0, 0, 0, 0, 0};
         if (t < P.nt) {
-            const float *row = qk + (size_t)(P.t0 + t) * 2 * kd + (size_t)kh * DK + q4;
-            qv[u] = ld4(row);
-            kv[u] = ld4(row + kd);
+            const uint16_t *row = qkc + (size_t)(P.t0 + t) * 2 * kd + (size_t)kh * DK + c8;
+            qv[u] = *reinterpret_cast<const u16x8_t *>(row);
+            kv[u] = *reinterpret_cast<const u16x8_t *>(row + kd);
+            vv[u] = *reinterpret_cast<const u16x8_t *>(vconv + (size_t)(P.t0 + t) * vd +
+                                                       (size_t)h * DV + c8);
+        }
+    }
+    float fr = 0.0f, gr = 0.0f, br = 0.0f;
+    if (tid < 2 * C) {
+        const int t = tid & (C - 1);
+        if (t < P.nt) fr = qkr[(size_t)(P.t0 + t) * 2 * hk + (tid >= C ? hk : 0) + kh];
+    } else if (tid < 3 * C) {
+        const int t = tid - 2 * C;
+        if (t < P.nt) {
+            gr = graw[(size_t)(P.t0 + t) * hv + h];
+            br = gate[(size_t)(P.t0 + t) * hv + h].y;
         }
     }
 #pragma unroll
-    for (int u = 0; u < NQ; u++) {
-        const int e = tid + 256 * u, t = e / (DK / 4), q4 = (e % (DK / 4)) * 4;
-        *reinterpret_cast<float4 *>(QL + t * KP + q4) = qv[u];
-        *reinterpret_cast<float4 *>(Ks + t * KP + q4) = kv[u];
+    for (int u = 0; u < NL; u++) {
+        const int e = tid + 256 * u, t = e / (DK / 8), c8 = (e % (DK / 8)) * 8;
+        *reinterpret_cast<u16x8_t *>(Qc + t * CKP + c8) = qv[u];
+        *reinterpret_cast<u16x8_t *>(Kc + t * CKP + c8) = kv[u];
+        *reinterpret_cast<u16x8_t *>(Vs + t * DV + c8) = vv[u];
     }
-    if (tid < C) {
-        const bool ok = tid < P.nt;
-        graw_s[tid] = ok ? graw[(size_t)(P.t0 + tid) * hv + h] : 0.0f;
-        bet[tid] = ok ? gate[(size_t)(P.t0 + tid) * hv + h].y : 0.0f;
-    }
+    if (tid < C) rq[tid] = fr * qscale;
+    else if (tid < 2 * C) rk[tid - C] = fr;
+    else if (tid < 3 * C) { graw_s[tid - 2 * C] = gr; bet[tid - 2 * C] = br; }
     __syncthreads();
     if (wqk) {
-        // the scan's packed Q (rows t, 8 consecutive dims a unit) and K
-        // (dim i, 8 consecutive keys a unit) from the LDS copies
+        // the scan's Q (rows t, 8 consecutive dims a piece) and K (dim i,
+        // 8 consecutive keys a piece) as code planes
 #pragma unroll
         for (int u = 0; u < C * DK / 8 / 256; u++) {
             const int e = tid + 256 * u;
             {
                 const int t = e / (DK / 8), c0 = (e % (DK / 8)) * 8;
-                float x[8];
-                const float4 a0 = lds4(QL + t * KP + c0), a1 = lds4(QL + t * KP + c0 + 4);
-                x[0] = a0.x; x[1] = a0.y; x[2] = a0.z; x[3] = a0.w;
-                x[4] = a1.x; x[5] = a1.y; x[6] = a1.z; x[7] = a1.w;
-                put_split8(Qpu + bx_a_index(t, c0, DK / 32), x);
+                *reinterpret_cast<u16x8_t *>(Qpu + bx1_a_index(t, c0, DK / 32)) =
+                    *reinterpret_cast<const u16x8_t *>(Qc + t * CKP + c0);
             }
             {
                 const int i = e % DK, s0 = (e / DK) * 8;
-                float x[8];
+                u16x8_t x;
 #pragma unroll
-                for (int j = 0; j < 8; j++) x[j] = Ks[(s0 + j) * KP + i];
-                put_split8(Kpu + bx_b_index(s0, i), x);
+                for (int j = 0; j < 8; j++) x[j] = Kc[(s0 + j) * CKP + i];
+                *reinterpret_cast<u16x8_t *>(Kpu + bx1_b_index(s0, i)) = x;
             }
         }
     }
@@ -334,15 +366,18 @@ __global__ __launch_bounds__(256, 2) void k_gdn_chunk_wy(
         gam[tid] = acc;
     }
     __syncthreads();
-    float *F = Fb + (size_t)unit * 2 * C;
+    // F: the output scale G_t rq_t, the state-update scale
+    // exp(gamma_C - gamma_s) rk_s, and G_C
+    float *F = Fb + (size_t)unit * 3 * C;
     if (tid < C) {
         Gs[tid] = exp_fast(gam[tid]);
-        F[tid] = Gs[tid];
-        F[C + tid] = exp_fast(gam[C - 1] - gam[tid]);
+        F[tid] = Gs[tid] * rq[tid];
+        F[C + tid] = exp_fast(gam[C - 1] - gam[tid]) * rk[tid];
+        F[2 * C + tid] = tid == 0 ? exp_fast(gam[C - 1]) : 0.0f;
     }
 
-    // products on the split-precision MFMA 16x16x32 (lane: row / column
-    // r16, reduction indices g8 .. g8+7; result rows kq .. kq+3)
+    // products on the bf16 MFMA 16x16x32 (lane: row / column r16,
+    // reduction indices g8 .. g8+7; result rows kq .. kq+3)
     const int r16 = lane & 15, kq = (lane >> 4) * 4, g8 = (lane >> 4) * 8;
     // Q K^T, row block 3-w: A = decayed lower triangle, to global. The
     // product is formed transposed (K Q^T) so each lane holds 4 consecutive
@@ -369,26 +404,21 @@ __global__ __launch_bounds__(256, 2) void k_gdn_chunk_wy(
             const float z[4] = {0.f, 0.f, 0.f, 0.f};
             put4((rb + 1) * 16 + kq, z);
         }
-        // q.k cancels and A feeds the outputs directly, so this product
-        // takes the three-way split (24 bits, fp32's error class): the
-        // two-way split's error, relative to sum |q_i k_i|, shows as
-        // several output ulps. Q rows of this block as B operands, once.
-        u16x8 qh[DK / 32], qm[DK / 32], ql[DK / 32];
+        u16x8 qf[DK / 32];
 #pragma unroll
-        for (int ks = 0; ks < DK / 32; ks++) lds_split8x3(QL + (rb * 16 + r16) * KP + ks * 32 + g8, qh[ks], qm[ks], ql[ks]);
+        for (int ks = 0; ks < DK / 32; ks++) qf[ks] = ld8(Qc + t * CKP + ks * 32 + g8);
+        const float qt = rq[t];
         for (int cb = 0; cb <= rb; cb++) {
             f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-            for (int ks = 0; ks < DK / 32; ks++) {
-                u16x8 kh, km, kl;
-                lds_split8x3(Ks + (cb * 16 + r16) * KP + ks * 32 + g8, kh, km, kl);
-                acc = mfma_x6(kh, km, kl, qh[ks], qm[ks], ql[ks], acc);
-            }
+            for (int ks = 0; ks < DK / 32; ks++)
+                acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                    as_bf(ld8(Kc + (cb * 16 + r16) * CKP + ks * 32 + g8)), as_bf(qf[ks]), acc, 0, 0, 0);
             float v[4];
 #pragma unroll
             for (int i = 0; i < 4; i++) {
                 const int s = cb * 16 + kq + i;
-                v[i] = s <= t ? exp_fast(gam[t] - gam[s]) * acc[i] : 0.0f;
+                v[i] = s <= t ? exp_fast(gam[t] - gam[s]) * ((qt * rk[s]) * acc[i]) : 0.0f;
             }
             put4(cb * 16 + kq, v);
         }
@@ -396,32 +426,21 @@ __global__ __launch_bounds__(256, 2) void k_gdn_chunk_wy(
     // K K^T, row block w, kept in registers until Q's LDS copy is free
     f32x4 g[4];
     {
-        u16x8 wh[DK / 32], wl[DK / 32];
+        u16x8 kw[DK / 32];
 #pragma unroll
-        for (int ks = 0; ks < DK / 32; ks++) lds_split8(Ks + (wave * 16 + r16) * KP + ks * 32 + g8, wh[ks], wl[ks]);
+        for (int ks = 0; ks < DK / 32; ks++) kw[ks] = ld8(Kc + (wave * 16 + r16) * CKP + ks * 32 + g8);
 #pragma unroll
         for (int cb = 0; cb < 4; cb++) {
             g[cb] = f32x4{0.f, 0.f, 0.f, 0.f};
             if (cb <= wave) {
 #pragma unroll
-                for (int ks = 0; ks < DK / 32; ks++) {
-                    u16x8 kh, kl;
-                    lds_split8(Ks + (cb * 16 + r16) * KP + ks * 32 + g8, kh, kl);
-                    g[cb] = mfma_x3(wh[ks], wl[ks], kh, kl, g[cb]);
-                }
+                for (int ks = 0; ks < DK / 32; ks++)
+                    g[cb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                        as_bf(kw[ks]), as_bf(ld8(Kc + (cb * 16 + r16) * CKP + ks * 32 + g8)), g[cb], 0, 0, 0);
             }
         }
     }
-    __syncthreads();                   // every reader of Q is done
-    float *Ls = QL;
-    // V rows [C][DV] bf16 in the 16 KiB of Q's copy that L ([C][CP]) leaves
-    uint16_t *Vs = reinterpret_cast<uint16_t *>(QL + C * CP);
-    static_assert(C * CP * 4 + C * DV * 2 <= C * KP * 4, "V does not fit beside L");
-#pragma unroll
-    for (int k = 0; k < NV; k++) {
-        const int t = tid / (DV / 8) + k * (256 / (DV / 8)), c8 = (tid % (DV / 8)) * 8;
-        *reinterpret_cast<u16x8_t *>(Vs + t * DV + c8) = vreg[k];
-    }
+    __syncthreads();                   // every reader of the q codes is done
 #pragma unroll
     for (int cb = 0; cb < 4; cb++) {
         if (cb <= wave) {
@@ -429,7 +448,7 @@ __global__ __launch_bounds__(256, 2) void k_gdn_chunk_wy(
 #pragma unroll
             for (int i = 0; i < 4; i++) {
                 const int t = wave * 16 + kq + i;
-                Ls[t * CP + s] = s < t ? bet[t] * (exp_fast(gam[t] - gam[s]) * g[cb][i]) : 0.0f;
+                Ls[t * CP + s] = s < t ? bet[t] * (exp_fast(gam[t] - gam[s]) * ((rk[t] * rk[s]) * g[cb][i])) : 0.0f;
             }
         }
     }
@@ -535,7 +554,8 @@ __global__ __launch_bounds__(256, 2) void k_gdn_chunk_wy(
 #pragma unroll
             for (int j = 0; j < 8; j++) {
                 const int t = k0 + j;
-                v[j] = isv ? bet[t] * bf2f(Vs[t * DV + n]) : (bet[t] * Gs[t]) * Ks[t * KP + (n - DV)];
+                v[j] = isv ? bet[t] * bf2f(Vs[t * DV + n])
+                           : (bet[t] * Gs[t]) * (bf2f(Kc[t * CKP + (n - DV)]) * rk[t]);
             }
             split8(v, bh[ct], bl[ct]);
         }
@@ -556,8 +576,8 @@ __global__ __launch_bounds__(256, 2) void k_gdn_chunk_wy(
     }
     // W through LDS (L is no longer read): column tid - DV of every row in,
     // then 32-byte units of 8 consecutive columns of one row out
-    __syncthreads();                   // every reader of T and V is done
-    float *Wl = QL;
+    __syncthreads();                   // every reader of T, V and the k codes is done
+    float *Wl = reinterpret_cast<float *>(wy_lds);
     if (!isv) {
 #pragma unroll
         for (int rt = 0; rt < 4; rt++)
@@ -628,24 +648,18 @@ __device__ __forceinline__ void scan_load_wu(ScanOps &nx, const uint16_t *__rest
 
 __device__ __forceinline__ void scan_load_k(ScanOps2 &nx, const uint16_t *__restrict__ Kp,
                                             size_t uk, int wave, int lane) {
-    const uint16_t *K = Kp + uk * C * DK * 2 + ((size_t)wave * 2 * (C / 32) * 64 + lane) * 16;
+    const uint16_t *K = Kp + uk * C * DK + ((size_t)wave * 2 * (C / 32) * 64 + lane) * 8;
 #pragma unroll
     for (int r = 0; r < 2; r++)
 #pragma unroll
-        for (int kb = 0; kb < C / 32; kb++) {
-            nx.b[4 * r + 2 * kb] = ld8(K + (r * (C / 32) + kb) * 64 * 16);
-            nx.b[4 * r + 2 * kb + 1] = ld8(K + (r * (C / 32) + kb) * 64 * 16 + 8);
-        }
+        for (int kb = 0; kb < C / 32; kb++) nx.b[2 * r + kb] = ld8(K + (r * (C / 32) + kb) * 64 * 8);
 }
 
 __device__ __forceinline__ void scan_load_q(ScanOps &nx, const uint16_t *__restrict__ Qp,
                                             size_t uk, int ow, int lane) {
-    const uint16_t *Q = Qp + uk * C * DK * 2 + ((size_t)ow * (DK / 32) * 64 + lane) * 16;
+    const uint16_t *Q = Qp + uk * C * DK + ((size_t)ow * (DK / 32) * 64 + lane) * 8;
 #pragma unroll
-    for (int kb = 0; kb < DK / 32; kb++) {
-        nx.b[2 * kb] = ld8(Q + kb * 64 * 16);
-        nx.b[2 * kb + 1] = ld8(Q + kb * 64 * 16 + 8);
-    }
+    for (int kb = 0; kb < DK / 32; kb++) nx.b[kb] = ld8(Q + kb * 64 * 8);
 }
 
 __device__ __forceinline__ void scan_load_a(ScanOps2 &nx, const uint16_t *__restrict__ Ab,
@@ -686,7 +700,7 @@ __global__ __launch_bounds__(512) void k_gdn_chunk_scan(
     __shared__ __attribute__((aligned(16))) uint16_t Dl[CB * DB];
     __shared__ __attribute__((aligned(16))) uint16_t Dph[CB * DB];     // decayed D
     __shared__ __attribute__((aligned(16))) uint16_t Dpl[CB * DB];
-    __shared__ float Fs[2 * C];
+    __shared__ float Fs[3 * C];
     __shared__ __attribute__((aligned(16))) uint16_t Ost[4][16 * CB];   // output role: rnd(o) tiles
 
     // state slice in: packed layout ((j/64*32 + i/4)*64 + j%64)*4 + i%4
@@ -712,16 +726,16 @@ __global__ __launch_bounds__(512) void k_gdn_chunk_scan(
         ScanOps2 kf;
         auto load_wu = [&](ScanOps &nx, int ci) {
             const size_t u = cl(ci) * hv + h;
-            if (tid < 2 * C) nx.f = Fb[u * 2 * C + tid];
+            if (tid < 3 * C) nx.f = Fb[u * 3 * C + tid];
             scan_load_wu(nx, Wb, Ub, u, wr, lane, cb);
         };
         load_wu(ring0, c0);
-        if (tid < 2 * C) Fs[tid] = ring0.f;
+        if (tid < 3 * C) Fs[tid] = ring0.f;
         scan_load_k(kf, Kp, cl(c0) * hk + kh, wr, lane);
         load_wu(ring1, c0 + 1);
         auto step = [&](ScanOps &cur, const ScanOps &oth, int ci) {
             const bool more = ci + 1 < c1;
-            if (tid < 2 * C) cur.f = Fb[(cl(ci + 2) * hv + h) * 2 * C + tid];
+            if (tid < 3 * C) cur.f = Fb[(cl(ci + 2) * hv + h) * 3 * C + tid];
             __syncthreads();           // the state slice and Fs of this chunk are in place
             f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -740,7 +754,7 @@ __global__ __launch_bounds__(512) void k_gdn_chunk_scan(
             scan_load_wu(cur, Wb, Ub, cl(ci + 2) * hv + h, wr, lane, cb);
             __syncthreads();           // D complete
             f32x4 sn[2];
-            const float gc = Fs[C - 1];
+            const float gc = Fs[2 * C];
 #pragma unroll
             for (int r = 0; r < 2; r++) {
                 const int i0 = wr * 32 + r * 16;
@@ -748,9 +762,8 @@ __global__ __launch_bounds__(512) void k_gdn_chunk_scan(
                 for (int i = 0; i < 4; i++) sn[r][i] = gc * S0T[(kq + i) * KP + i0 + r16];
 #pragma unroll
                 for (int kb = 0; kb < C / 32; kb++)
-                    sn[r] = mfma_x3(ld8(Dph + r16 * DB + kb * 32 + g4 * 8),
-                                    ld8(Dpl + r16 * DB + kb * 32 + g4 * 8),
-                                    kf.b[4 * r + 2 * kb], kf.b[4 * r + 2 * kb + 1], sn[r]);
+                    sn[r] = mfma_x2a(kf.b[2 * r + kb], ld8(Dph + r16 * DB + kb * 32 + g4 * 8),
+                                     ld8(Dpl + r16 * DB + kb * 32 + g4 * 8), sn[r], true);
             }
             scan_load_k(kf, Kp, cl(ci + 1) * hk + kh, wr, lane);
             __syncthreads();           // every reader of the state slice and Fs is done
@@ -764,7 +777,7 @@ __global__ __launch_bounds__(512) void k_gdn_chunk_scan(
                     split_bf(sn[r][i], S0h[n * SB + col], S0l[n * SB + col]);
                 }
             }
-            if (more && tid < 2 * C) Fs[tid] = oth.f;
+            if (more && tid < 3 * C) Fs[tid] = oth.f;
         };
         for (int ci = c0; ci < c1; ci += 2) {
             step(ring0, ring1, ci);
@@ -786,9 +799,8 @@ __global__ __launch_bounds__(512) void k_gdn_chunk_scan(
             f32x4 o = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int kb = 0; kb < DK / 32; kb++)
-                o = mfma_x3(cur.b[2 * kb], cur.b[2 * kb + 1],
-                            ld8(S0h + r16 * SB + kb * 32 + g4 * 8),
-                            ld8(S0l + r16 * SB + kb * 32 + g4 * 8), o);
+                o = mfma_x2a(cur.b[kb], ld8(S0h + r16 * SB + kb * 32 + g4 * 8),
+                             ld8(S0l + r16 * SB + kb * 32 + g4 * 8), o, false);
 #pragma unroll
             for (int i = 0; i < 4; i++) o[i] = Fs[rw + kq + i] * o[i];
             scan_load_q(cur, Qp, cl(ci + 2) * hk + kh, wr, lane);
@@ -854,7 +866,8 @@ static PrefillWs prefill_ws_carve(char *base, size_t Ttot, size_t nch, size_t B,
         return q;
     };
     const size_t kd = hk * DK, vd = hv * DV, units = nch * hv;
-    p.w.qk = (float *)take(Ttot * 2 * kd * 4);
+    p.w.qk = (uint16_t *)take(Ttot * 2 * kd * 2);
+    p.w.qkr = (float *)take(Ttot * 2 * hk * 4);
     p.w.vconv = (uint16_t *)take(Ttot * vd * 2);
     p.w.gate = (float2 *)take(Ttot * hv * 8);
     p.w.ob = (uint16_t *)take(Ttot * vd * 2);
@@ -862,9 +875,9 @@ static PrefillWs prefill_ws_carve(char *base, size_t Ttot, size_t nch, size_t B,
     p.Ub = (float *)take(units * C * DV * 4);
     p.Wb = (uint16_t *)take(units * C * DK * 4);
     p.Ab = (uint16_t *)take(units * C * C * 4);
-    p.Fb = (float *)take(units * 2 * C * 4);
-    p.Qp = (uint16_t *)take(nch * hk * C * DK * 4);
-    p.Kp = (uint16_t *)take(nch * hk * C * DK * 4);
+    p.Fb = (float *)take(units * 3 * C * 4);
+    p.Qp = (uint16_t *)take(nch * hk * C * DK * 2);
+    p.Kp = (uint16_t *)take(nch * hk * C * DK * 2);
     p.meta = (int32_t *)take(2 * (B + 1) * 4);
     p.bytes = off;
     return p;
@@ -950,14 +963,14 @@ static int gdn_prefill_run(const ApusHipGdnLayer *L, size_t B, const int32_t *cu
     float *Ub = ws ? pw.Ub : (float *)scratch(kScratchGdnChunk, units * C * DV * 4);
     uint16_t *Wb = ws ? pw.Wb : (uint16_t *)scratch(kScratchGdnChunk2, units * C * DK * 4);
     uint16_t *Ab = ws ? pw.Ab : (uint16_t *)scratch(kScratchGdnChunk4, units * C * C * 4);
-    float *Fb = ws ? pw.Fb : (float *)scratch(kScratchGdnChunk5, units * 2 * C * 4);
-    uint16_t *Qp = ws ? pw.Qp : (uint16_t *)scratch(kScratchGdnChunk6, nch * L->hk * C * DK * 4);
-    uint16_t *Kp = ws ? pw.Kp : (uint16_t *)scratch(kScratchGdnChunk7, nch * L->hk * C * DK * 4);
+    float *Fb = ws ? pw.Fb : (float *)scratch(kScratchGdnChunk5, units * 3 * C * 4);
+    uint16_t *Qp = ws ? pw.Qp : (uint16_t *)scratch(kScratchGdnChunk6, nch * L->hk * C * DK * 2);
+    uint16_t *Kp = ws ? pw.Kp : (uint16_t *)scratch(kScratchGdnChunk7, nch * L->hk * C * DK * 2);
     if (!Ub || !Wb || !Ab || !Fb || !Qp || !Kp) return kErrHip;
     APUS_TIMED("k_gdn_chunk_wy",
                k_gdn_chunk_wy<<<(unsigned)units, 256, 0, stream()>>>(
-        sq, kmeta, w.qk, w.vconv, w.gate, w.graw, Ub, Wb, Ab, Fb, Qp, Kp, (int)L->hk,
-        units % 16 == 0 ? 1 : 0));
+        sq, kmeta, w.qk, w.qkr, w.vconv, w.gate, w.graw, Ub, Wb, Ab, Fb, Qp, Kp, (int)L->hk,
+        units % 16 == 0 ? 1 : 0, (float)pow((double)L->dk, -0.5)));
     APUS_LAUNCHED("k_gdn_chunk_wy");
     APUS_TIMED("k_gdn_chunk_scan",
                k_gdn_chunk_scan<<<(unsigned)(B * L->hv * NCB), 512, 0, stream()>>>(
