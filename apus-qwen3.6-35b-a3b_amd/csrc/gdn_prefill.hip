@@ -263,7 +263,7 @@ __device__ __forceinline__ f32x4 mfma_x6(u16x8 ah, u16x8 am, u16x8 al, u16x8 bh,
 // q.k and k.k are the factors times the exact dot products of the codes:
 // one bf16 MFMA per product, fp32 accumulation, no operand splitting.
 constexpr int CKP = DK + 8;            // bf16 row stride of the code copies
-__global__ __launch_bounds__(256) void k_gdn_chunk_wy(
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void k_gdn_chunk_wy(
     ChunkSeqs sq, const int32_t *__restrict__ dmeta, const uint16_t *__restrict__ qkc,
     const float *__restrict__ qkr, const uint16_t *__restrict__ vconv,
     const float2 *__restrict__ gate, const float *__restrict__ graw, float *__restrict__ Ub,
@@ -290,15 +290,18 @@ __global__ __launch_bounds__(256) void k_gdn_chunk_wy(
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
 
     // LDS: q codes (later L, then W's staging together with the k codes),
-    // k codes, the V rows, per-token factors
+    // k codes, the V codes transposed ([column][token]: the B operand of
+    // T R; the 16-byte pieces of row n XOR-swizzled by n % 8, so the MFMA
+    // operand reads spread over the banks), per-token factors (three
+    // workgroups per CU)
     constexpr int QC_B = C * CKP * 2, L_B = C * CP * 4;
     static_assert(QC_B >= L_B, "L does not fit over the q codes");
     static_assert(2 * QC_B >= C * KP * 4, "W's staging does not fit over the code copies");
-    __shared__ __attribute__((aligned(16))) char wy_lds[2 * QC_B + C * DV * 2];
+    __shared__ __attribute__((aligned(16))) char wy_lds[2 * QC_B + DV * C * 2];
     uint16_t *Qc = reinterpret_cast<uint16_t *>(wy_lds);
     float *Ls = reinterpret_cast<float *>(wy_lds);
     uint16_t *Kc = reinterpret_cast<uint16_t *>(wy_lds + QC_B);
-    uint16_t *Vs = reinterpret_cast<uint16_t *>(wy_lds + 2 * QC_B);
+    uint16_t *Vt = reinterpret_cast<uint16_t *>(wy_lds + 2 * QC_B);
     __shared__ float graw_s[C], gam[C], bet[C], Gs[C], rq[C], rk[C];
 
     // rows t >= nt are padding: codes 0, factors 0, g = 0, beta = 0
@@ -334,7 +337,8 @@ __global__ __launch_bounds__(256) void k_gdn_chunk_wy(
         const int e = tid + 256 * u, t = e / (DK / 8), c8 = (e % (DK / 8)) * 8;
         *reinterpret_cast<u16x8_t *>(Qc + t * CKP + c8) = qv[u];
         *reinterpret_cast<u16x8_t *>(Kc + t * CKP + c8) = kv[u];
-        *reinterpret_cast<u16x8_t *>(Vs + t * DV + c8) = vv[u];
+#pragma unroll
+        for (int j = 0; j < 8; j++) Vt[(c8 + j) * C + ((((t >> 3) ^ (j & 7)) << 3) | (t & 7))] = vv[u][j];
     }
     if (tid < C) rq[tid] = fr * qscale;
     else if (tid < 2 * C) rk[tid - C] = fr;
@@ -536,34 +540,42 @@ __global__ __launch_bounds__(256) void k_gdn_chunk_wy(
     for (int rt = 0; rt < 4; rt++)
 #pragma unroll
         for (int ct = 0; ct < 4; ct++) xacc[rt][ct] = f32x4{0.f, 0.f, 0.f, 0.f};
+    // R = [diag(b) V | diag(b G rk) Kc] with V and Kc exact codes: a
+    // wavefront's 64 columns are of one kind, so its T operand carries that
+    // kind's row factors (T diag(f), split hi/lo) and the codes are the B
+    // operand as they are: two MFMAs per product
 #pragma unroll
     for (int ks = 0; ks < C / 32; ks++) {
         const int k0 = ks * 32 + g8;             // this lane's 8 reduction indices
-        u16x8 ah[4], al[4], bh[4], bl[4];
+        float f[8];
+#pragma unroll
+        for (int j = 0; j < 8; j++) f[j] = isv ? bet[k0 + j] : (bet[k0 + j] * Gs[k0 + j]) * rk[k0 + j];
+        u16x8 ah[4], al[4], bc[4];
 #pragma unroll
         for (int rt = 2 * ks; rt < 4; rt++) {    // T rows 16 rt + r16
             const float4 a0 = lds4(Ls + (rt * 16 + r16) * CP + k0);
             const float4 a1 = lds4(Ls + (rt * 16 + r16) * CP + k0 + 4);
-            const float v[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+            const float v[8] = {a0.x * f[0], a0.y * f[1], a0.z * f[2], a0.w * f[3],
+                                a1.x * f[4], a1.y * f[5], a1.z * f[6], a1.w * f[7]};
             split8(v, ah[rt], al[rt]);
         }
 #pragma unroll
         for (int ct = 0; ct < 4; ct++) {         // R column n, rows k0 .. k0 + 7
             const int n = cbase + ct * 16 + r16;
-            float v[8];
+            if (isv) {
+                bc[ct] = ld8(Vt + n * C + (((k0 >> 3) ^ (n & 7)) << 3));
+            } else {
 #pragma unroll
-            for (int j = 0; j < 8; j++) {
-                const int t = k0 + j;
-                v[j] = isv ? bet[t] * bf2f(Vs[t * DV + n])
-                           : (bet[t] * Gs[t]) * (bf2f(Kc[t * CKP + (n - DV)]) * rk[t]);
+                for (int j = 0; j < 8; j++) bc[ct][j] = Kc[(k0 + j) * CKP + (n - DV)];
             }
-            split8(v, bh[ct], bl[ct]);
         }
 #pragma unroll
         for (int rt = 2 * ks; rt < 4; rt++)
 #pragma unroll
-            for (int ct = 0; ct < 4; ct++)
-                xacc[rt][ct] = mfma_x3(ah[rt], al[rt], bh[ct], bl[ct], xacc[rt][ct]);
+            for (int ct = 0; ct < 4; ct++) {
+                xacc[rt][ct] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf(al[rt]), as_bf(bc[ct]), xacc[rt][ct], 0, 0, 0);
+                xacc[rt][ct] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf(ah[rt]), as_bf(bc[ct]), xacc[rt][ct], 0, 0, 0);
+            }
     }
     const size_t ub = (size_t)unit * C * DV;
     if (isv) {                         // U: the accumulator order is U's layout
