@@ -69,4 +69,25 @@ __device__ __forceinline__ float decay_of(uint16_t a, float A_log,
     return -exp_cr(A_log) * softplus_cr(t);
 }
 
+// Ascending sum of squares of a row of 128 bf16 codes (16-byte aligned),
+// one rounding per mul and add (the l2norm's ordered sum, c/gdn.h:402-416).
+__device__ __forceinline__ float row_sumsq(const uint16_t *row) {
+    typedef unsigned short u16x8_t __attribute__((ext_vector_type(8)));
+    const u16x8_t *x8 = reinterpret_cast<const u16x8_t *>(row);
+    float ss = 0.0f;
+#pragma unroll 4
+    for (int j = 0; j < 128 / 8; j++) {
+        const u16x8_t v = x8[j];
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            const float x = bf2f(v[i]);
+            ss = ss + x * x;
+        }
+    }
+    return ss;
+}
+
+// eps of the q/k l2norm, 1/sqrt(sum x^2 + eps) (c/gdn.h:402-416)
+constexpr float kL2Eps = 1e-6f;
+
 }  // namespace apus

@@ -415,8 +415,8 @@ constexpr int RS = DK + 4;   // LDS row stride: 16-byte aligned rows on distinct
 constexpr int PC = 4 * DK;   // pre-conv channels of one K head: q, k, 2 x v
 
 // Ascending sum of squares of one 128-float LDS row, one rounding per mul
-// and add, with 16-byte reads kept in flight ahead of the add chain (the
-// same over a row of 128 bf16 codes below).
+// and add, with 16-byte reads kept in flight ahead of the add chain (over a
+// row of 128 bf16 codes: gdn_dev.h).
 __device__ __forceinline__ float row_sumsq(const float *row) {
     const float4 *x4 = reinterpret_cast<const float4 *>(row);
     float ss = 0.0f;
@@ -431,21 +431,6 @@ __device__ __forceinline__ float row_sumsq(const float *row) {
     return ss;
 }
 
-__device__ __forceinline__ float row_sumsq(const uint16_t *row) {
-    typedef unsigned short u16x8 __attribute__((ext_vector_type(8)));
-    const u16x8 *x8 = reinterpret_cast<const u16x8 *>(row);
-    float ss = 0.0f;
-#pragma unroll 4
-    for (int j = 0; j < DK / 8; j++) {
-        const u16x8 v = x8[j];
-#pragma unroll
-        for (int i = 0; i < 8; i++) {
-            const float x = bf2f(v[i]);
-            ss = ss + x * x;
-        }
-    }
-    return ss;
-}
 constexpr int RSC = DV + 8;  // LDS row stride in bf16 codes: 16-byte aligned rows
 
 // k_gdn_prep: per (tile of 16 tokens, K head), 256 threads. The tile's
@@ -662,7 +647,7 @@ __global__ __launch_bounds__(256) void k_gdn_post(
         }
         __syncthreads();
         if (tid < nr) {
-            rs[tid] = 1.0f / sqrtf(row_sumsq(os + tid * RSC) / (float)DV + kEps);
+            rs[tid] = 1.0f / sqrtf(apus::row_sumsq(os + tid * RSC) / (float)DV + kEps);
         }
         __syncthreads();
 #pragma unroll

@@ -46,6 +46,7 @@
 #include "../../include/apus_hip.h"
 #include "apus_dev.h"
 #include "apus_host.h"
+#include "gdn_dev.h"
 #include "gdn_mixer.h"
 
 using namespace apus;
@@ -258,15 +259,19 @@ __device__ __forceinline__ f32x4 mfma_x6(u16x8 ah, u16x8 am, u16x8 al, u16x8 bh,
 }
 
 // k_gdn_chunk_wy: one workgroup per (chunk, v-head), up to three per CU.
-// q and k arrive as their conv+SiLU bf16 codes with one l2norm factor per
-// row (the normalised rows are q_t = rq_t qscale cq_t, k_s = rk_s ck_s), so
-// q.k and k.k are the factors times the exact dot products of the codes:
-// one bf16 MFMA per product, fp32 accumulation, no operand splitting.
+// It forms the chunk's q, k, v conv+SiLU codes, l2norm factors and gates
+// from the layer inputs itself. The normalised rows are q_t = rq_t qscale
+// cq_t and k_s = rk_s ck_s with cq, ck the codes, so q.k and k.k are the
+// factors times the exact dot products of the codes: one bf16 MFMA per
+// product, fp32 accumulation, no operand splitting.
 constexpr int CKP = DK + 8;            // bf16 row stride of the code copies
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void k_gdn_chunk_wy(
-    ChunkSeqs sq, const int32_t *__restrict__ dmeta, const uint16_t *__restrict__ qkc,
-    const float *__restrict__ qkr, const uint16_t *__restrict__ vconv,
-    const float2 *__restrict__ gate, const float *__restrict__ graw, float *__restrict__ Ub,
+    ChunkSeqs sq, const int32_t *__restrict__ dmeta, const uint16_t *__restrict__ qkv,
+    const uint16_t *__restrict__ a, const uint16_t *__restrict__ b,
+    const uint16_t *__restrict__ conv_w, const float *__restrict__ A_log,
+    const float *__restrict__ dt_bias, const uint16_t *__restrict__ conv_state,
+    const int32_t *__restrict__ slots, const uint16_t *__restrict__ silu_bf,
+    const uint16_t *__restrict__ sig_bf, float *__restrict__ Ub,
     uint16_t *__restrict__ Wb, uint16_t *__restrict__ Ab, float *__restrict__ Fb,
     uint16_t *__restrict__ Qp, uint16_t *__restrict__ Kp, int hk, int pair_map, float qscale) {
     const int hv = hk * REP;
@@ -304,45 +309,108 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void k
     uint16_t *Vt = reinterpret_cast<uint16_t *>(wy_lds + 2 * QC_B);
     __shared__ float graw_s[C], gam[C], bet[C], Gs[C], rq[C], rk[C];
 
-    // rows t >= nt are padding: codes 0, factors 0, g = 0, beta = 0
-    // (every load issued before the first LDS store)
-    typedef unsigned short u16x8_t __attribute__((ext_vector_type(8)));
-    constexpr int NL = C * DK / 8 / 256;       // 16-byte pieces per thread per matrix
-    u16x8_t qv[NL], kv[NL], vv[NL];
+    // ---- the token-parallel front (c/layer.h:427-492 up to the
+    // recurrence) for this chunk: causal conv1d k=4 + SiLU of the q, k
+    // channels of K head kh and the v channels of head h (c/gdn.h:19-33,
+    // 220-228), the l2norm factors (c/gdn.h:402-416) and the gates
+    // (c/gdn.h:34-40). Work items are (two adjacent channels of the 384,
+    // 16 tokens), three per thread; an item reads its 16 tokens' inputs and
+    // the 3 before them (from the sequence's old conv state in its first
+    // chunk). Loads are unconditional (rows clamped into the chunk); codes
+    // of padding rows (t >= nt) are 0, as are their gates.
+    const size_t cd = 2 * kd + vd;
+    const bool first = ci == coff[P.s];
+    const uint16_t *cst = conv_state + (size_t)(slots ? slots[P.s] : P.s) * cd * 3;
+    if (tid < C) {                              // the gates of token tid
+        float g = 0.0f, bt = 0.0f;
+        if (tid < P.nt) {
+            const size_t i = (size_t)(P.t0 + tid) * hv + h;
+            g = decay_of(a[i], A_log[h], dt_bias[h]);
+            bt = bf2f(sig_bf[b[i]]);
+        }
+        graw_s[tid] = g;
+        bet[tid] = bt;
+    }
+    constexpr int TG = 16;                      // tokens per work item
+    for (int it = tid; it < (3 * DK / 2) * (C / TG); it += 256) {
+        const int lc = 2 * (it % (3 * DK / 2)), tg = (it / (3 * DK / 2)) * TG;
+        const size_t gcol = lc < DK ? (size_t)kh * DK + lc
+                          : lc < 2 * DK ? kd + (size_t)kh * DK + (lc - DK)
+                                        : 2 * kd + (size_t)h * DV + (lc - 2 * DK);
+        // inputs of rows t0 + tg - 3 .. t0 + tg + 15, two channels a word
+        uint32_t x[TG + 3];
 #pragma unroll
-    for (int u = 0; u < NL; u++) {
-        const int e = tid + 256 * u, t = e / (DK / 8), c8 = (e % (DK / 8)) * 8;
-        qv[u] = kv[u] = vv[u] = u16x8_t{0, 0, 0, 0, 0, 0, 0, 0};
-        if (t < P.nt) {
-            const uint16_t *row = qkc + (size_t)(P.t0 + t) * 2 * kd + (size_t)kh * DK + c8;
-            qv[u] = *reinterpret_cast<const u16x8_t *>(row);
-            kv[u] = *reinterpret_cast<const u16x8_t *>(row + kd);
-            vv[u] = *reinterpret_cast<const u16x8_t *>(vconv + (size_t)(P.t0 + t) * vd +
-                                                       (size_t)h * DV + c8);
+        for (int r = 0; r < TG + 3; r++) {
+            const int t = tg - 3 + r;           // chunk-relative token
+            const uint32_t vq = *reinterpret_cast<const uint32_t *>(
+                qkv + (size_t)(P.t0 + max(min(t, P.nt - 1), first ? 0 : -3)) * cd + gcol);
+            if (r < 3 && tg == 0) {
+                const uint32_t vs = (uint32_t)cst[gcol * 3 + r] | ((uint32_t)cst[(gcol + 1) * 3 + r] << 16);
+                x[r] = first ? vs : vq;
+            } else {
+                x[r] = vq;
+            }
+        }
+        float w0[4], w1[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            w0[i] = bf2f(conv_w[gcol * 4 + i]);
+            w1[i] = bf2f(conv_w[(gcol + 1) * 4 + i]);
+        }
+        auto lo = [](uint32_t v) { return bf2f((uint16_t)v); };
+        auto hi = [](uint32_t v) { return bf2f((uint16_t)(v >> 16)); };
+        // conv sums, then SiLU through the fp32 fast path; the few results it
+        // cannot vouch for come from the bf16-code table, all gathered after
+        uint16_t c0[TG], c1[TG];
+        uint32_t redo = 0;
+#pragma unroll
+        for (int j = 0; j < TG; j++) {
+            c0[j] = conv_sum4_code(w0, lo(x[j]), lo(x[j + 1]), lo(x[j + 2]), lo(x[j + 3]));
+            c1[j] = conv_sum4_code(w1, hi(x[j]), hi(x[j + 1]), hi(x[j + 2]), hi(x[j + 3]));
+            bool ok0, ok1;
+            const uint16_t r0 = silu_fast(bf2f(c0[j]), ok0), r1 = silu_fast(bf2f(c1[j]), ok1);
+            redo |= (ok0 ? 0u : 1u << j) | (ok1 ? 0u : 1u << (TG + j));
+            if (ok0) c0[j] = r0;
+            if (ok1) c1[j] = r1;
+        }
+        if (redo) {
+#pragma unroll
+            for (int j = 0; j < TG; j++) {
+                if (redo >> j & 1u) c0[j] = silu_bf[c0[j]];
+                if (redo >> (TG + j) & 1u) c1[j] = silu_bf[c1[j]];
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < TG; j++)
+            if (tg + j >= P.nt) c0[j] = c1[j] = 0;
+        if (lc < 2 * DK) {                      // q or k: rows of Qc / Kc
+            uint16_t *dst = (lc < DK ? Qc : Kc) + (lc & (DK - 1));
+#pragma unroll
+            for (int j = 0; j < TG; j++)
+                *reinterpret_cast<uint32_t *>(dst + (tg + j) * CKP) = (uint32_t)c0[j] | ((uint32_t)c1[j] << 16);
+        } else {                                // v: rows n0, n0 + 1 of Vt
+            const int n0 = lc - 2 * DK;
+#pragma unroll
+            for (int h8 = 0; h8 < TG / 8; h8++) {
+                u16x8 a0, a1;
+#pragma unroll
+                for (int j = 0; j < 8; j++) {
+                    a0[j] = c0[h8 * 8 + j];
+                    a1[j] = c1[h8 * 8 + j];
+                }
+                const int t8 = tg / 8 + h8;
+                *reinterpret_cast<u16x8 *>(Vt + n0 * C + ((t8 ^ (n0 & 7)) << 3)) = a0;
+                *reinterpret_cast<u16x8 *>(Vt + (n0 + 1) * C + ((t8 ^ ((n0 + 1) & 7)) << 3)) = a1;
+            }
         }
     }
-    float fr = 0.0f, gr = 0.0f, br = 0.0f;
-    if (tid < 2 * C) {
+    __syncthreads();
+    if (tid < 2 * C) {                          // l2norm factors, one lane per row
         const int t = tid & (C - 1);
-        if (t < P.nt) fr = qkr[(size_t)(P.t0 + t) * 2 * hk + (tid >= C ? hk : 0) + kh];
-    } else if (tid < 3 * C) {
-        const int t = tid - 2 * C;
-        if (t < P.nt) {
-            gr = graw[(size_t)(P.t0 + t) * hv + h];
-            br = gate[(size_t)(P.t0 + t) * hv + h].y;
-        }
+        const float f = t < P.nt ? 1.0f / sqrtf(row_sumsq((tid < C ? Qc : Kc) + t * CKP) + kL2Eps) : 0.0f;
+        if (tid < C) rq[t] = f * qscale;
+        else rk[t] = f;
     }
-#pragma unroll
-    for (int u = 0; u < NL; u++) {
-        const int e = tid + 256 * u, t = e / (DK / 8), c8 = (e % (DK / 8)) * 8;
-        *reinterpret_cast<u16x8_t *>(Qc + t * CKP + c8) = qv[u];
-        *reinterpret_cast<u16x8_t *>(Kc + t * CKP + c8) = kv[u];
-#pragma unroll
-        for (int j = 0; j < 8; j++) Vt[(c8 + j) * C + ((((t >> 3) ^ (j & 7)) << 3) | (t & 7))] = vv[u][j];
-    }
-    if (tid < C) rq[tid] = fr * qscale;
-    else if (tid < 2 * C) rk[tid - C] = fr;
-    else if (tid < 3 * C) { graw_s[tid - 2 * C] = gr; bet[tid - 2 * C] = br; }
     __syncthreads();
     if (wqk) {
         // the scan's Q (rows t, 8 consecutive dims a piece) and K (dim i,
@@ -352,15 +420,15 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void k
             const int e = tid + 256 * u;
             {
                 const int t = e / (DK / 8), c0 = (e % (DK / 8)) * 8;
-                *reinterpret_cast<u16x8_t *>(Qpu + bx1_a_index(t, c0, DK / 32)) =
-                    *reinterpret_cast<const u16x8_t *>(Qc + t * CKP + c0);
+                *reinterpret_cast<u16x8 *>(Qpu + bx1_a_index(t, c0, DK / 32)) =
+                    *reinterpret_cast<const u16x8 *>(Qc + t * CKP + c0);
             }
             {
                 const int i = e % DK, s0 = (e / DK) * 8;
-                u16x8_t x;
+                u16x8 x;
 #pragma unroll
                 for (int j = 0; j < 8; j++) x[j] = Kc[(s0 + j) * CKP + i];
-                *reinterpret_cast<u16x8_t *>(Kpu + bx1_b_index(s0, i)) = x;
+                *reinterpret_cast<u16x8 *>(Kpu + bx1_b_index(s0, i)) = x;
             }
         }
     }
@@ -878,12 +946,7 @@ static PrefillWs prefill_ws_carve(char *base, size_t Ttot, size_t nch, size_t B,
         return q;
     };
     const size_t kd = hk * DK, vd = hv * DV, units = nch * hv;
-    p.w.qk = (uint16_t *)take(Ttot * 2 * kd * 2);
-    p.w.qkr = (float *)take(Ttot * 2 * hk * 4);
-    p.w.vconv = (uint16_t *)take(Ttot * vd * 2);
-    p.w.gate = (float2 *)take(Ttot * hv * 8);
     p.w.ob = (uint16_t *)take(Ttot * vd * 2);
-    p.w.graw = (float *)take(Ttot * hv * 4);
     p.Ub = (float *)take(units * C * DV * 4);
     p.Wb = (uint16_t *)take(units * C * DK * 4);
     p.Ab = (uint16_t *)take(units * C * C * 4);
@@ -965,12 +1028,18 @@ static int gdn_prefill_run(const ApusHipGdnLayer *L, size_t B, const int32_t *cu
         if (!slots) return kErrHip;
     }
     GdnScratch w = pw.w;                       // workspace buffers, or null: scratch
+    if (!ws) w.ob = (uint16_t *)scratch(kScratchGdnOB, Ttot * L->hv * DV * 2);
+    if (!w.ob) return kErrHip;
     const ApusHipGdnTrace *tr = gdn_trace();
-    if (int r = gdn_prep(L, B, cu, dmeta, Ttot, qkv, a, b, conv_state, &w, true, slots, tr))
-        return r;
-    if (tr && tr->gdecay)
-        APUS_HIP_TRY(hipMemcpyAsync(tr->gdecay, w.graw, Ttot * L->hv * 4,
-                                    hipMemcpyDeviceToDevice, stream()));
+    if (tr && (tr->qkv_conv || tr->beta || tr->gdecay)) {
+        // the trace's token-parallel intermediates (the chunk kernel forms
+        // its own copies of them)
+        GdnScratch tw{};
+        if (int r = gdn_prep(L, B, cu, dmeta, Ttot, qkv, a, b, conv_state, &tw, false, slots, tr))
+            return r;
+    }
+    const ActTables *tabs = act_tables();
+    if (!tabs) return kErrHip;
     const size_t units = nch * L->hv;
     float *Ub = ws ? pw.Ub : (float *)scratch(kScratchGdnChunk, units * C * DV * 4);
     uint16_t *Wb = ws ? pw.Wb : (uint16_t *)scratch(kScratchGdnChunk2, units * C * DK * 4);
@@ -981,7 +1050,8 @@ static int gdn_prefill_run(const ApusHipGdnLayer *L, size_t B, const int32_t *cu
     if (!Ub || !Wb || !Ab || !Fb || !Qp || !Kp) return kErrHip;
     APUS_TIMED("k_gdn_chunk_wy",
                k_gdn_chunk_wy<<<(unsigned)units, 256, 0, stream()>>>(
-        sq, kmeta, w.qk, w.qkr, w.vconv, w.gate, w.graw, Ub, Wb, Ab, Fb, Qp, Kp, (int)L->hk,
+        sq, kmeta, qkv, a, b, L->conv_w, L->A_log, L->dt_bias, conv_state, slots,
+        tabs->silu_bf, tabs->sig_bf, Ub, Wb, Ab, Fb, Qp, Kp, (int)L->hk,
         units % 16 == 0 ? 1 : 0, (float)pow((double)L->dk, -0.5)));
     APUS_LAUNCHED("k_gdn_chunk_wy");
     APUS_TIMED("k_gdn_chunk_scan",

@@ -369,15 +369,17 @@ def bench_gdn_prefill(torch, T, steps, warmup, seed, leg=None):
     bytes_ = gdn_seq_bytes(T) + GDN_WEIGHT_BYTES
     flops = gdn_prefill_flops(T)
     nu = (T // 64) * HV                       # (chunk, v-head) units
-    # WY and the scan multiply fp32 operands on the bf16 MFMA in split
-    # precision (hi*hi + hi*lo + lo*hi: three bf16 MFMAs per fp32 product);
-    # frac is against the published bf16 peak, split_roof_frac against the
-    # third of it that the split form can reach for the fp32 algorithm
+    # WY and the scan multiply on the bf16 MFMA; fp32 operands are split
+    # (hi + lo, a product against another split operand is three MFMAs,
+    # against exact bf16 codes two). frac is against the published bf16
+    # peak, split_roof_frac against the share of it the executed MFMA work
+    # leaves for the algorithm's flops (SCAN/WY_EXEC_PER_UNIT below)
     table = {"k_gdn_chunk_scan": ("mfma", nu * SCAN_FLOPS_PER_UNIT, BF16_PEAK,
-                                  {"split_roof_tflops": BF16_PEAK / 3 / 1e12}),
+                                  {"split_roof_tflops": BF16_PEAK * SCAN_FLOPS_PER_UNIT
+                                   / SCAN_EXEC_PER_UNIT / 1e12}),
              "k_gdn_chunk_wy": ("mfma", nu * WY_FLOPS_PER_UNIT, BF16_PEAK,
-                                {"split_roof_tflops": BF16_PEAK / 3 / 1e12}),
-             "k_gdn_prep": ("hbm", gdn_prep_bytes(T), HBM_PEAK),
+                                {"split_roof_tflops": BF16_PEAK * WY_FLOPS_PER_UNIT
+                                 / WY_EXEC_PER_UNIT / 1e12}),
              "k_gdn_post": ("hbm", gdn_post_bytes(T), HBM_PEAK)}
     total, per, kt = time_steps(torch, step, steps, warmup, nsets, table)
     st = float(np.mean(per))
@@ -405,12 +407,12 @@ def bench_gdn_prefill(torch, T, steps, warmup, seed, leg=None):
 # triangular applications giving U and W, plus the triangular solve.
 SCAN_FLOPS_PER_UNIT = 3 * 2 * 64 * 128 * 128 + 2 * 64 * 64 * 128
 WY_FLOPS_PER_UNIT = 4 * 2 * 64 * 64 * 128 + (2 * 64 ** 3) // 3
-
-
-def gdn_prep_bytes(T):
-    """k_gdn_prep interface bytes: qkv, a, b in; fp32 l2-normed q and k,
-    conv+SiLU v (bf16), (exp g, beta) and g out; old conv state in."""
-    return T * (CD * 2 + HV * 2 * 2 + 2 * HK * DK * 4 + VD * 2 + HV * 8 + HV * 4) + CD * 3 * 2
+# MFMA flops the kernels execute for them: the scan's W S0 and A D take
+# three MFMAs per product (both operands split), Q S0 and K^T D two (q, k
+# as exact codes); WY's K K^T and Q K^T one (codes), T R two, and the
+# 32x32 off-diagonal block of T two split products
+SCAN_EXEC_PER_UNIT = 3 * 2 * 64 * 128 * 128 + 2 * 2 * 2 * 64 * 128 * 128 + 3 * 2 * 64 * 64 * 128
+WY_EXEC_PER_UNIT = 2 * 2 * 64 * 64 * 128 + 2 * 2 * 2 * 64 * 64 * 128 + 3 * 2 * 2 * 32 ** 3
 
 
 def gdn_post_bytes(T):
