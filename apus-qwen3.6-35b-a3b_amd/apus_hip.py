@@ -304,6 +304,30 @@ def gdn_decode(layer, cu, qkv, z, a, b, conv_state, S, y):
                                     _dp(S), _dp(y)))
 
 
+class BoundCall:
+    """One library call with its arguments converted once. Calling it
+    repeats the call on the same buffers and host arrays (kept alive here):
+    for a loop that re-runs one step, it leaves only the foreign-function
+    call itself on the host path."""
+    __slots__ = ("_f", "_args", "_keep")
+
+    def __init__(self, f, args, keep):
+        self._f, self._args, self._keep = f, args, keep
+
+    def __call__(self):
+        rc = self._f(*self._args)
+        if rc != 0:
+            raise ApusHipError(rc, last_error())
+
+
+def gdn_decode_bound(layer, cu, qkv, z, a, b, conv_state, S, y):
+    """gdn_decode as a BoundCall."""
+    cu, cup, B = _cu_arr(cu)
+    args = (C.byref(layer), _sz(B), cup, _dp(qkv), _dp(z), _dp(a), _dp(b), _dp(conv_state),
+            _dp(S), _dp(y))
+    return BoundCall(load().apus_hip_gdn_decode, args, (layer, cu, qkv, z, a, b, conv_state, S, y))
+
+
 def gdn_decode_into(layer, cu, qkv, z, a, b, conv_in, S_in, conv_out, S_out, y):
     """Out-of-place decode/verify: states read from (conv_in, S_in), written
     to (conv_out, S_out); sequences with no tokens are left untouched."""

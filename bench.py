@@ -118,12 +118,14 @@ class Dev:
 def time_steps(torch, fn, steps, warmup, nsets, kernels=()):
     """Run warmup then `steps` timed steps; return (total_s, per-step event
     times in s, {kernel: average launch ms}). Each step uses buffer set
-    i % nsets. The wall-clock pass runs without kernel timing; a second
-    pass of the same steps records HIP events around each launch of the
-    named kernels on the library's stream (apus_hip_timing_*). The
-    collector runs before and stays off during each pass: a generation-2
-    collection over the process's objects takes 15-40 ms, enough to drain
-    the launch queue in the middle of a timed pass."""
+    i % nsets. The wall-clock pass runs the steps back to back with nothing
+    else enqueued (an event record between steps adds its own gap on the
+    GPU, a visible share of a short step). A second pass records HIP events
+    around each step, a third around each launch of the named kernels on
+    the library's stream (apus_hip_timing_*). The collector runs before and
+    stays off during each pass: a generation-2 collection over the
+    process's objects takes 15-40 ms, enough to drain the launch queue in
+    the middle of a timed pass."""
     import gc
     import apus_hip
     for i in range(warmup):
@@ -134,13 +136,17 @@ def time_steps(torch, fn, steps, warmup, nsets, kernels=()):
     gc.collect()
     gc.disable()
     try:
+        torch.cuda.synchronize()
         t0 = time.perf_counter()
+        for i in range(steps):
+            fn(i % nsets)
+        torch.cuda.synchronize()
+        total = time.perf_counter() - t0
         for i in range(steps):
             ev[i][0].record()
             fn(i % nsets)
             ev[i][1].record()
         torch.cuda.synchronize()
-        total = time.perf_counter() - t0
     finally:
         gc.enable()
     per = [a.elapsed_time(b) * 1e-3 for a, b in ev]
@@ -332,9 +338,14 @@ def bench_gdn_decode(torch, B, steps, warmup, seed, leg=None):
     nsets = 4 if B > 1 else 8
     d = Dev(torch, B, 1, nsets, seed, zero_state=False)
 
+    # each set's call prepared once (apus_hip.BoundCall): a decode step is
+    # one launch, so per-call argument conversion would be a visible share
+    # of the wall time
+    calls = [apus_hip.gdn_decode_bound(d.layer, d.cu, s["qkv"], s["z"], s["a"], s["b"], s["conv"],
+                                       s["S"], s["y"]) for s in d.sets]
+
     def step(i):
-        s = d.sets[i]
-        apus_hip.gdn_decode(d.layer, d.cu, s["qkv"], s["z"], s["a"], s["b"], s["conv"], s["S"], s["y"])
+        calls[i]()
 
     bytes_ = B * gdn_seq_bytes(1) + GDN_WEIGHT_BYTES
     table = {"k_gdn_decode": ("hbm", bytes_, HBM_PEAK)}
