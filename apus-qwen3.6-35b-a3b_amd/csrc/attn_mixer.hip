@@ -59,8 +59,15 @@ __device__ __forceinline__ uint32_t pack2(float lo, float hi) {
 }
 typedef unsigned short u16x8 __attribute__((ext_vector_type(8)));
 
+// 16-byte loads from global memory through pointers whose address space
+// the compiler cannot infer (built from scalar registers, or selected
+// between kernel-argument and device copies): as flat loads they would
+// also count on the LDS counter, so every LDS wait of the stream would
+// wait for the loads in flight
+typedef const __attribute__((address_space(1))) u16x8 *gu16x8p;
+__device__ __forceinline__ u16x8 gld16(const uint16_t *p) { return *(gu16x8p)p; }
 __device__ __forceinline__ bf16x8 ld_bf16x8(const uint16_t *p) {
-    return __builtin_bit_cast(bf16x8, *reinterpret_cast<const u16x8 *>(p));
+    return __builtin_bit_cast(bf16x8, gld16(p));
 }
 
 __device__ __forceinline__ int seq_of(const int32_t *off, int n, int x) {
@@ -356,10 +363,12 @@ __device__ __forceinline__ const uint16_t *uniform_ptr(const uint16_t *p) {
                               (uint32_t)__builtin_amdgcn_readfirstlane((int)a));
 }
 
-// K rows of cache block b of segment g (kv head g.kvh)
-__device__ __forceinline__ const uint16_t *kblock(const KvRef &kv, const Meta &mt, const Seg &g,
-                                                  int nkv, int b) {
-    return uniform_ptr(kv.k + (kv_block_id_u(kv, mt.hd[g.s], b) * nkv + g.kvh) * KVB * D);
+// K rows of cache block b of segment g (kv head g.kvh); hd its sequence's
+// block-table row (read once per segment: a per-group read of it would be
+// a vector load whose wait drains the K stream)
+__device__ __forceinline__ const uint16_t *kblock(const KvRef &kv, int hd, const Seg &g, int nkv,
+                                                  int b) {
+    return uniform_ptr(kv.k + (kv_block_id_u(kv, hd, b) * nkv + g.kvh) * KVB * D);
 }
 
 // The streaming wavefront's part for one segment whose sequence has NR
@@ -427,10 +436,11 @@ __device__ __forceinline__ void scores_seg(const Meta &mt, const Seg &c,
     // block bases of groups g0 (pA, pB), g0 + 64 (qA, qB); the lookups for
     // g0 + 128 are issued after the group's LDS count read, so their
     // scalar-load latency is never part of an LDS wait
+    const int hd = __builtin_amdgcn_readfirstlane(mt.hd[c.s]);
     int bA = min(c.k0 >> 5, blast);
-    const uint16_t *pA = kblock(kv, mt, c, nkv, bA), *pB = kblock(kv, mt, c, nkv, min(bA + 1, blast));
+    const uint16_t *pA = kblock(kv, hd, c, nkv, bA), *pB = kblock(kv, hd, c, nkv, min(bA + 1, blast));
     int nA = min((c.k0 + 64) >> 5, blast);
-    const uint16_t *qA = kblock(kv, mt, c, nkv, nA), *qB = kblock(kv, mt, c, nkv, min(nA + 1, blast));
+    const uint16_t *qA = kblock(kv, hd, c, nkv, nA), *qB = kblock(kv, hd, c, nkv, min(nA + 1, blast));
     bf16x8 kA[D / 32], kB[D / 32];
     load_k(c.k0, 0, bA, pA, pB, kA);
     for (int g0 = c.k0; g0 < c.k1; g0 += 64, grp++) {
@@ -438,7 +448,7 @@ __device__ __forceinline__ void scores_seg(const Meta &mt, const Seg &c,
         // it is normally long done)
         const int dn = lds_count_load(donew);
         const int mA = min((g0 + 128) >> 5, blast);
-        const uint16_t *rA = kblock(kv, mt, c, nkv, mA), *rB = kblock(kv, mt, c, nkv, min(mA + 1, blast));
+        const uint16_t *rA = kblock(kv, hd, c, nkv, mA), *rB = kblock(kv, hd, c, nkv, min(mA + 1, blast));
         uint32_t sc[NR][8];                  // bf16 score codes, two per word
         auto mma = [&](int j, const bf16x8 *kf) {
             f32x4 acc[NR];
@@ -708,10 +718,10 @@ __device__ __forceinline__ void pv_seg(const Meta &mt, const Seg &c, int hb, con
         const int kq = min(kb + q4 * 8, kclamp);
 #pragma unroll
         for (int b = 0; b < NB; b++)
-            fv[b] = *reinterpret_cast<const u16x8 *>(Vb + ((hb * NB + b) * 16 + c16) * KVB + (kq & 31));
+            fv[b] = gld16(Vb + ((hb * NB + b) * 16 + c16) * KVB + (kq & 31));
 #pragma unroll
         for (int rb = 0; rb < NR; rb++)
-            fa[rb] = *reinterpret_cast<const u16x8 *>(Ab + (size_t)(rb * 16 + c16) * c.cap + kq);
+            fa[rb] = gld16(Ab + (size_t)(rb * 16 + c16) * c.cap + kq);
     };
     load_step(c.k0, vblock(c.k0), vf, af);
     for (int kb = c.k0; kb < c.k1; kb += 32) {
