@@ -100,7 +100,7 @@ __device__ __forceinline__ Meta meta_of(const AttnSeqs &sq, const int32_t *dmeta
 // (c/attn.h:244-266, the partner dims +-32 read from the staged row), and
 // a 16-byte store of q to qn or of k to the K cache. V is appended by
 // k_attn_vappend.
-constexpr int PRB = 64;                  // rows per k_attn_prep block
+constexpr int PRB = 32;                  // rows per k_attn_prep block
 constexpr int PRS = D + 8;               // LDS row pitch (bf16): rows on distinct banks
 __global__ __launch_bounds__(256) void k_attn_prep(
     AttnSeqs sq, const int32_t *__restrict__ dmeta, const uint16_t *__restrict__ qg,
@@ -115,37 +115,41 @@ __global__ __launch_bounds__(256) void k_attn_prep(
     __shared__ __attribute__((aligned(16))) uint16_t xs[PRB * PRS];
     __shared__ __attribute__((aligned(16))) uint16_t rcs[PRB * ROT];   // cos / sin codes
     __shared__ float rs[PRB];
-    __shared__ int rseq[PRB], rpos[PRB];
-    // every load of the block in flight at once: 8 row pieces and 2 code
-    // pieces per thread
-    auto row_pos = [&](int r, int &s) {
-        const int tt = (r0 + r) / nslot;
-        s = seq_of(cu, sq.n, tt);
-        return pos0[s] + (tt - cu[s]);
-    };
+    __shared__ size_t rdst[PRB];             // k rows: element offset of the cache row
+    constexpr int PTK = PRB / 2 + 2;         // tokens a block's rows can span (nslot >= 2)
+    __shared__ int tpos[PTK], thd[PTK];      // their positions and block-table rows
+    // The block's tokens' metadata first (a lookup chain of a few dependent
+    // loads, with nothing else in flight yet), then every row and cos/sin
+    // load of the block unconditionally (rows clamped into the block), so
+    // no wait drains the stream.
+    const int tt0 = r0 / nslot, ntk = (r0 + nr - 1) / nslot - tt0 + 1;
+    if (tid < ntk) {
+        const int tt = tt0 + tid, s = seq_of(cu, sq.n, tt);
+        tpos[tid] = pos0[s] + (tt - cu[s]);
+        thd[tid] = mt.hd[s];
+    }
     u16x8 xv8[PRB * (D / 8) / 256], cv2[PRB * (ROT / 8) / 256];
 #pragma unroll
     for (int k = 0; k < PRB * (D / 8) / 256; k++) {
-        const int e = tid + 256 * k, r = e / (D / 8), pc = e % (D / 8);
-        if (r < nr) {
-            const int row = r0 + r, tt = row / nslot, slot = row % nslot;
-            const uint16_t *x = slot < nh ? qg + ((size_t)tt * nh + slot) * 2 * D
-                                          : kin + ((size_t)tt * nkv + (slot - nh)) * D;
-            xv8[k] = *reinterpret_cast<const u16x8 *>(x + pc * 8);
-        }
+        const int e = tid + 256 * k, r = min(e / (D / 8), nr - 1), pc = e % (D / 8);
+        const int row = r0 + r, tt = row / nslot, slot = row % nslot;
+        const uint16_t *x = slot < nh ? qg + ((size_t)tt * nh + slot) * 2 * D
+                                      : kin + ((size_t)tt * nkv + (slot - nh)) * D;
+        xv8[k] = *reinterpret_cast<const u16x8 *>(x + pc * 8);
     }
+    __syncthreads();                          // the tokens' metadata
 #pragma unroll
     for (int k = 0; k < PRB * (ROT / 8) / 256; k++) {
-        const int e = tid + 256 * k, r = e / (ROT / 8), pc = e % (ROT / 8);
-        if (r < nr) {
-            int s;
-            cv2[k] = *reinterpret_cast<const u16x8 *>(rope + (size_t)row_pos(r, s) * ROT + pc * 8);
-        }
+        const int e = tid + 256 * k, r = min(e / (ROT / 8), nr - 1), pc = e % (ROT / 8);
+        cv2[k] = *reinterpret_cast<const u16x8 *>(rope + (size_t)tpos[(r0 + r) / nslot - tt0] * ROT + pc * 8);
     }
-    if (tid < nr) {                           // row metadata, one lane per row
-        int s;
-        rpos[tid] = row_pos(tid, s);
-        rseq[tid] = s;
+    if (tid < nr) {                           // k rows' cache offsets, one lane per row
+        const int slot = (r0 + tid) % nslot, ti = (r0 + tid) / nslot - tt0;
+        if (slot >= nh) {
+            const int pos = tpos[ti];
+            rdst[tid] = ((kv_block_id(kv, thd[ti], pos / KVB) * nkv + (slot - nh)) * KVB +
+                         pos % KVB) * D;
+        }
     }
 #pragma unroll
     for (int k = 0; k < PRB * (D / 8) / 256; k++) {
@@ -211,9 +215,9 @@ __global__ __launch_bounds__(256) void k_attn_prep(
 #pragma unroll
             for (int i = 0; i < 8; i++) out[i] = f2bf(n[i]);
         }
-        uint16_t *dst = isq ? qn + ((size_t)tt * nh + slot) * D
-                            : kv.k + ((kv_block_id(kv, mt.hd[rseq[r]], rpos[r] / KVB) * nkv +
-                                       (slot - nh)) * KVB + rpos[r] % KVB) * D;
+        // (no loads in this loop: a load's wait would also wait for the
+        // stores of the iterations before it)
+        uint16_t *dst = isq ? qn + ((size_t)tt * nh + slot) * D : kv.k + rdst[r];
         *reinterpret_cast<u16x8 *>(dst + p * 8) = out;
         if (!isq && tr_kf)                    // (trace) the appended k row
             *reinterpret_cast<u16x8 *>(tr_kf + ((size_t)tt * nkv + (slot - nh)) * D + p * 8) = out;
