@@ -265,6 +265,29 @@ __device__ __forceinline__ f32x4 mfma_x6(u16x8 ah, u16x8 am, u16x8 al, u16x8 bh,
 // factors times the exact dot products of the codes: one bf16 MFMA per
 // product, fp32 accumulation, no operand splitting.
 constexpr int CKP = DK + 8;            // bf16 row stride of the code copies
+
+// Two channels' 4-tap conv sums (tap order, one rounding per mul and add,
+// c/gdn.h:19-33), rounded to bf16 codes by one hardware round-to-nearest-
+// even conversion (v_cvt_pk_bf16_f32): the codes conv_sum4_code gives for
+// finite sums.
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint32_t conv_sum4_pair(const float (&w0)[4], const float (&w1)[4],
+                                                   uint32_t x0, uint32_t x1, uint32_t x2,
+                                                   uint32_t x3) {
+    auto lo = [](uint32_t v) { return __uint_as_float(v << 16); };
+    auto hi = [](uint32_t v) { return __uint_as_float(v & 0xffff0000u); };
+    float a = 0.0f, c = 0.0f;
+    a = a + w0[0] * lo(x0);
+    c = c + w1[0] * hi(x0);
+    a = a + w0[1] * lo(x1);
+    c = c + w1[1] * hi(x1);
+    a = a + w0[2] * lo(x2);
+    c = c + w1[2] * hi(x2);
+    a = a + w0[3] * lo(x3);
+    c = c + w1[3] * hi(x3);
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_t{a, c}, bf16x2_t));
+}
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void k_gdn_chunk_wy(
     ChunkSeqs sq, const int32_t *__restrict__ dmeta, const uint16_t *__restrict__ qkv,
     const uint16_t *__restrict__ a, const uint16_t *__restrict__ b,
@@ -357,16 +380,15 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void k
             w0[i] = bf2f(conv_w[gcol * 4 + i]);
             w1[i] = bf2f(conv_w[(gcol + 1) * 4 + i]);
         }
-        auto lo = [](uint32_t v) { return bf2f((uint16_t)v); };
-        auto hi = [](uint32_t v) { return bf2f((uint16_t)(v >> 16)); };
         // conv sums, then SiLU through the fp32 fast path; the few results it
         // cannot vouch for come from the bf16-code table, all gathered after
         uint16_t c0[TG], c1[TG];
         uint32_t redo = 0;
 #pragma unroll
         for (int j = 0; j < TG; j++) {
-            c0[j] = conv_sum4_code(w0, lo(x[j]), lo(x[j + 1]), lo(x[j + 2]), lo(x[j + 3]));
-            c1[j] = conv_sum4_code(w1, hi(x[j]), hi(x[j + 1]), hi(x[j + 2]), hi(x[j + 3]));
+            const uint32_t cc = conv_sum4_pair(w0, w1, x[j], x[j + 1], x[j + 2], x[j + 3]);
+            c0[j] = (uint16_t)cc;
+            c1[j] = (uint16_t)(cc >> 16);
             bool ok0, ok1;
             const uint16_t r0 = silu_fast(bf2f(c0[j]), ok0), r1 = silu_fast(bf2f(c1[j]), ok1);
             redo |= (ok0 ? 0u : 1u << j) | (ok1 ? 0u : 1u << (TG + j));
