@@ -334,7 +334,7 @@ __device__ __forceinline__ void pair_runs(const Meta &mt, int nkv, int s, int kv
 // slots to global memory and returns them with a "done" count. A
 // wavefront's DS instructions execute in issue order, so a count written
 // after its data is never seen before that data.
-constexpr int kScRing = 4;
+constexpr int kScRing = 3;
 template <int NRB> struct ScoresShape {
     static constexpr int W = NRB == 1 ? 11 : 7;   // streaming wavefronts (+1 writer)
     static constexpr int SLOT = 2 * NRB * 64;     // uint4 per slot: 16*NRB rows x 64 keys
@@ -383,7 +383,8 @@ __device__ __forceinline__ void scores_seg(const Meta &mt, const Seg &c,
                                            const uint16_t *__restrict__ qn, const KvRef &kv,
                                            int nh, int nkv, float scale,
                                            float2 *__restrict__ stats, uint4 *ringw,
-                                           RingHdr *hdrw, int *readyw, int *donew, int &grp) {
+                                           RingHdr *hdrw, int *readyw, int *donew, int &grp,
+                                           uint4 *stg) {
     const int32_t *cu = mt.cu;
     const int l = threadIdx.x & 63, c16 = l & 15, q4 = l >> 4;
 
@@ -416,16 +417,36 @@ __device__ __forceinline__ void scores_seg(const Meta &mt, const Seg &c,
     // wait for it); their scores are never stored or counted. A group's 64
     // keys lie in two cache blocks (g0 is a multiple of 64); their bases are
     // looked up one group ahead (scalar loads).
+    // K rows are read whole: load instruction i reads MFMA rows 2i and
+    // 2i+1 of the block (512 contiguous bytes each, lanes 0-31 and 32-63)
+    // with the streaming (non-temporal) policy, and the rows pass through
+    // this wavefront's LDS tile (row pitch 528 bytes) into the operand
+    // layout (lane (q4, c16): row c16, bytes 64 ds + 16 q4). Operand-shaped
+    // loads (64 bytes of each of 16 rows per instruction) held the stream
+    // at the vector L1's miss rate, and the streaming policy with them
+    // lost each line's second half.
     const int blast = (c.k1 - 1) >> 5;
     auto load_k = [&](int g0, int j, int bA, const uint16_t *pA, const uint16_t *pB,
-                      bf16x8 (&f)[D / 32]) {
-        const int key = min(g0 + (c16 >> 2) * 16 + 4 * j + (c16 & 3), c.k1 - 1);
-        const uint16_t *kr = ((key >> 5) == bA ? pA : pB) + (size_t)(key & 31) * D + q4 * 8;
+                      u16x8 (&f)[D / 32]) {
 #pragma unroll
-        for (int ds = 0; ds < D / 32; ds++) f[ds] = ld_bf16x8(kr + ds * 32);
+        for (int i = 0; i < D / 32; i++) {
+            const int rr = 2 * i + (l >> 5);
+            const int key = min(g0 + (rr >> 2) * 16 + 4 * j + (rr & 3), c.k1 - 1);
+            const uint16_t *kr = ((key >> 5) == bA ? pA : pB) + (size_t)(key & 31) * D + (l & 31) * 8;
+            f[i] = __builtin_nontemporal_load((gu16x8p)kr);
+        }
         // keep the loads here: the scheduler would otherwise sink them to
         // their first use and leave nothing in flight
         __builtin_amdgcn_sched_barrier(0);
+    };
+    auto stage = [&](const u16x8 (&f)[D / 32]) {
+#pragma unroll
+        for (int i = 0; i < D / 32; i++)
+            stg[(2 * i + (l >> 5)) * 33 + (l & 31)] = __builtin_bit_cast(uint4, f[i]);
+    };
+    auto unstage = [&](bf16x8 (&k)[D / 32]) {
+#pragma unroll
+        for (int ds = 0; ds < D / 32; ds++) k[ds] = __builtin_bit_cast(bf16x8, stg[c16 * 33 + ds * 4 + q4]);
     };
     // the first key past which some row's scores are masked
     int kmask = c.k1;
@@ -445,8 +466,9 @@ __device__ __forceinline__ void scores_seg(const Meta &mt, const Seg &c,
     const uint16_t *pA = kblock(kv, hd, c, nkv, bA), *pB = kblock(kv, hd, c, nkv, min(bA + 1, blast));
     int nA = min((c.k0 + 64) >> 5, blast);
     const uint16_t *qA = kblock(kv, hd, c, nkv, nA), *qB = kblock(kv, hd, c, nkv, min(nA + 1, blast));
-    bf16x8 kA[D / 32], kB[D / 32];
-    load_k(c.k0, 0, bA, pA, pB, kA);
+    u16x8 kL[D / 32];                       // the next block's rows, as loaded
+    bf16x8 kM[D / 32];                      // the current block's operands
+    load_k(c.k0, 0, bA, pA, pB, kL);
     for (int g0 = c.k0; g0 < c.k1; g0 += 64, grp++) {
         // the writer must have drained this group's ring slot (read early;
         // it is normally long done)
@@ -471,14 +493,22 @@ __device__ __forceinline__ void scores_seg(const Meta &mt, const Seg &c,
                 for (int e = 0; e < 4; e += 2)
                     sc[rb][2 * j + e / 2] = pack2(acc[rb][e] * scale, acc[rb][e + 1] * scale);
         };
-        load_k(g0, 1, bA, pA, pB, kB);
-        mma(0, kA);
-        load_k(g0, 2, bA, pA, pB, kA);
-        mma(1, kB);
-        load_k(g0, 3, bA, pA, pB, kB);
-        mma(2, kA);
-        load_k(g0 + 64, 0, nA, qA, qB, kA);
-        mma(3, kB);
+        stage(kL);
+        load_k(g0, 1, bA, pA, pB, kL);
+        unstage(kM);
+        mma(0, kM);
+        stage(kL);
+        load_k(g0, 2, bA, pA, pB, kL);
+        unstage(kM);
+        mma(1, kM);
+        stage(kL);
+        load_k(g0, 3, bA, pA, pB, kL);
+        unstage(kM);
+        mma(2, kM);
+        stage(kL);
+        load_k(g0 + 64, 0, nA, qA, qB, kL);
+        unstage(kM);
+        mma(3, kM);
         bA = nA;
         pA = qA;
         pB = qB;
@@ -556,6 +586,7 @@ __global__ __launch_bounds__(64 * (ScoresShape<NRB>::W + 1)) void k_attn_scores(
     int nruns) {
     constexpr int W = ScoresShape<NRB>::W, SLOT = ScoresShape<NRB>::SLOT;
     __shared__ uint4 ring[W][kScRing][SLOT];
+    __shared__ uint4 kstage[W][16 * 33];            // per wavefront: one 16-key K block
     __shared__ RingHdr hdr[W][kScRing];
     __shared__ int ready[W], done[W];
     const int wave = threadIdx.x >> 6, l = threadIdx.x & 63;
@@ -633,10 +664,10 @@ __global__ __launch_bounds__(64 * (ScoresShape<NRB>::W + 1)) void k_attn_scores(
             // a sequence with at most 2 tokens fills one row block
             if (NRB == 2 && g.tq <= 2)
                 scores_seg<1, SLOT>(mt, g, qn, kv, nh, nkv, scale, stats, ring[wave][0],
-                                    hdr[wave], &ready[wave], &done[wave], grp);
+                                    hdr[wave], &ready[wave], &done[wave], grp, kstage[wave]);
             else
                 scores_seg<NRB, SLOT>(mt, g, qn, kv, nh, nkv, scale, stats, ring[wave][0],
-                                      hdr[wave], &ready[wave], &done[wave], grp);
+                                      hdr[wave], &ready[wave], &done[wave], grp, kstage[wave]);
         }
         x = xn;
     }
@@ -722,7 +753,7 @@ __device__ __forceinline__ void pv_seg(const Meta &mt, const Seg &c, int hb, con
         const int kq = min(kb + q4 * 8, kclamp);
 #pragma unroll
         for (int b = 0; b < NB; b++)
-            fv[b] = gld16(Vb + ((hb * NB + b) * 16 + c16) * KVB + (kq & 31));
+            fv[b] = __builtin_nontemporal_load((gu16x8p)(Vb + ((hb * NB + b) * 16 + c16) * KVB + (kq & 31)));
 #pragma unroll
         for (int rb = 0; rb < NR; rb++)
             fa[rb] = gld16(Ab + (size_t)(rb * 16 + c16) * c.cap + kq);
