@@ -741,7 +741,7 @@ __device__ __forceinline__ void pv_seg(const Meta &mt, const Seg &c, int hb, con
     // step's 32 keys are one cache block (its base a scalar lookup).
     const int kclamp = ((c.k1 - 1) / 8) * 8;   // last aligned group holding a valid key
     const int kmask = min(c.k1, c.pos0 + 1);   // the first key masked for some row
-    const int hd = mt.hd[c.s];
+    const int hd = __builtin_amdgcn_readfirstlane(mt.hd[c.s]);   // (read once, into a scalar)
     // V block of the step at kb (clamped lanes stay in kb's block: kclamp
     // lies in [kb, kb + 24] whenever kb + 8*q4 passes it)
     auto vblock = [&](int kb) {
@@ -760,8 +760,11 @@ __device__ __forceinline__ void pv_seg(const Meta &mt, const Seg &c, int hb, con
     };
     load_step(c.k0, vblock(c.k0), vf, af);
     for (int kb = c.k0; kb < c.k1; kb += 32) {
+        // the next step's operands, unconditionally (past the segment's end
+        // the clamped addresses re-read its last step): a branch around
+        // the loads would make the compiler wait for them at its join
         u16x8 vn[NB], an[NR];
-        if (kb + 32 < c.k1) load_step(kb + 32, vblock(kb + 32), vn, an);
+        load_step(kb + 32, vblock(kb + 32), vn, an);
         const int kq = kb + q4 * 8;            // this lane's 8 keys
         bf16x8 pf[NR];
 #pragma unroll
