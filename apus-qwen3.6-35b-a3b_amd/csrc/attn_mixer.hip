@@ -280,8 +280,15 @@ __global__ __launch_bounds__(256) void k_attn_vappend(
 // partial results in slot p + w (p = s*nkv + kvh, w the wavefront's run).
 struct Seg {
     int s, kvh, slot, tq, pos0, k0, k1, cap;
-    size_t abase;                  // the pair's scores: As + abase, [kRows][cap]
+    size_t abase;                  // the pair's scores: As + abase (a_index)
 };
+
+// A pair's bf16 scores (kRows rows x cap keys) in 1 KiB pieces of 16 rows
+// x 32 keys, [row block][32-key chunk][row][key], so that the P.V operand
+// loads (16 rows x 32 keys per instruction) read whole lines
+__device__ __forceinline__ size_t a_index(int row, int key, int cap) {
+    return ((size_t)((row >> 4) * (cap >> 5) + (key >> 5)) * 16 + (row & 15)) * 32 + (key & 31);
+}
 
 // The segment of run w (keys x1 > x of the padded pair space) starting at
 // x; *xn is where the next one starts. False for a segment that holds only
@@ -341,7 +348,7 @@ template <int NRB> struct ScoresShape {
 };
 template <int NRB> constexpr int scores_waves_per_block() { return ScoresShape<NRB>::W; }
 
-// where a ring slot's scores go: rows [kRows][cap] at As + abase, keys
+// where a ring slot's scores go: the pair's rows at As + abase (a_index), keys
 // kq0 .. min(kq0 + 64, k1), rows of tokens < tq
 struct RingHdr {
     uint32_t alo, ahi;
@@ -628,7 +635,7 @@ __global__ __launch_bounds__(64 * (ScoresShape<NRB>::W + 1)) void k_attn_scores(
                 if (rd <= nxt[w]) continue;
                 compiler_fence();
                 // slot layout [row][64 keys]: lane l stores 16 bytes (8 keys)
-                // of row 8*i + l/8, so a row's 128 bytes are whole lines
+                // of row 8*i + l/8, two 64-byte runs a row
                 for (int g = nxt[w]; g < rd; g++) {
                     const uint4 *sl = ring[w][g % kScRing];
                     const RingHdr h = hdr[w][g % kScRing];
@@ -638,7 +645,7 @@ __global__ __launch_bounds__(64 * (ScoresShape<NRB>::W + 1)) void k_attn_scores(
                     for (int i = 0; i < 2 * NRB; i++) {
                         const int row = 8 * i + (l >> 3);
                         if (row / GRP < h.tq && kq < h.k1)
-                            *reinterpret_cast<uint4 *>(Ab + (size_t)row * h.cap + kq) = sl[i * 64 + l];
+                            *reinterpret_cast<uint4 *>(Ab + a_index(row, kq, h.cap)) = sl[i * 64 + l];
                     }
                 }
                 compiler_fence();
@@ -756,7 +763,7 @@ __device__ __forceinline__ void pv_seg(const Meta &mt, const Seg &c, int hb, con
             fv[b] = __builtin_nontemporal_load((gu16x8p)(Vb + ((hb * NB + b) * 16 + c16) * KVB + (kq & 31)));
 #pragma unroll
         for (int rb = 0; rb < NR; rb++)
-            fa[rb] = gld16(Ab + (size_t)(rb * 16 + c16) * c.cap + kq);
+            fa[rb] = gld16(Ab + a_index(rb * 16 + c16, kq, c.cap));
     };
     load_step(c.k0, vblock(c.k0), vf, af);
     for (int kb = c.k0; kb < c.k1; kb += 32) {
