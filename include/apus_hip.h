@@ -257,8 +257,8 @@ int apus_hip_gdn_prefill(const ApusHipGdnLayer *L, size_t B,
  * Same arguments, results bit-identical to apus_hip_gdn_prefill. The
  * intermediates live in one fixed per-device scratch array of 96 MiB,
  * reserved when the library initialises a device and held until the
- * process ends: a call needs about 33 KiB per token plus 3.6 MiB per
- * (sequence, chunk of 64 tokens), so one sequence of up to ~1000 tokens
+ * process ends: a call needs about 8 KiB per token plus 3.0 MiB per
+ * (sequence, chunk of 64 tokens), so one sequence of up to ~1700 tokens
  * (longer prompts are prefilled in successive calls: the state carries
  * over); at most 400 sequences and no slot map. A larger call returns
  * APUS_HIP_ERR_UNSUPPORTED with the size it needs. Calls on one GPU share
