@@ -15,8 +15,8 @@
 // that crosses a pair boundary is processed as two segments. Segment
 // (pair p, wavefront w) keeps its partial results in slot p + w (unique:
 // consecutive segments raise p or w or both).
-//   k_attn_prep     q/k (1+w) RMSNorm, RoPE, K append
-//   k_attn_vappend  V append
+//   k_attn_prep     q/k (1+w) RMSNorm, RoPE, K append; V append (other
+//                   blocks of the same launch)
 //   k_attn_scores   A = rnd(rnd(q.k)*scale) on MFMA 16x16x32 bf16 into a
 //                   bf16 score buffer, per-segment (max, sum exp)
 //   k_attn_pv       P = rnd(exp(A-m)/s) with the pair's global (m, s) --
@@ -90,7 +90,7 @@ __device__ __forceinline__ Meta meta_of(const AttnSeqs &sq, const int32_t *dmeta
     return Meta{dmeta, dmeta + n + 1, dmeta + 2 * n + 1, dmeta + 3 * n + 2};
 }
 
-// k_attn_prep: one block of 256 threads per rpb <= 64 rows, a row being one
+// The prep blocks of k_attn_prep: one block of 256 threads per rpb <= 64 rows, a row being one
 // (token, slot) with slots 0..nh-1 the q heads and nh..nh+nkv-1 the kv
 // heads. Rows are staged in LDS as bf16 with 16-byte loads; lane r of the
 // first wavefront takes row r's ascending sum of squares (c/attn.h:177-182,
@@ -99,25 +99,34 @@ __device__ __forceinline__ Meta meta_of(const AttnSeqs &sq, const int32_t *dmeta
 // rounding, the partial NeoX RoPE with the host-made cos/sin codes
 // (c/attn.h:244-266, the partner dims +-32 read from the staged row), and
 // a 16-byte store of q to qn or of k to the K cache. V is appended by
-// k_attn_vappend.
+// the launch's other blocks (vappend_block).
 constexpr int PRB = 32;                  // rows per k_attn_prep block
 constexpr int PRS = D + 8;               // LDS row pitch (bf16): rows on distinct banks
-__global__ __launch_bounds__(256) void k_attn_prep(
-    AttnSeqs sq, const int32_t *__restrict__ dmeta, const uint16_t *__restrict__ qg,
+constexpr int PTK = PRB / 2 + 2;             // tokens a prep block's rows can span (nslot >= 2)
+// the prep block's LDS: rows, cos / sin codes, rs, cache offsets, tokens
+struct PrepLds {
+    uint16_t xs[PRB * PRS];
+    uint16_t rcs[PRB * ROT];                 // cos / sin codes
+    float rs[PRB];
+    size_t rdst[PRB];                        // k rows: element offset of the cache row
+    int tpos[PTK], thd[PTK];                 // the tokens' positions and block-table rows
+};
+constexpr int kVappLds = 32 * PRS * 2;       // the V append block's staged rows
+constexpr int kPrepKernLds = sizeof(PrepLds) > kVappLds ? sizeof(PrepLds) : kVappLds;
+
+__device__ __forceinline__ void prep_block(
+    int bid, PrepLds &L, const Meta &mt, const AttnSeqs &sq, const uint16_t *__restrict__ qg,
     const uint16_t *__restrict__ kin, const uint16_t *__restrict__ qn_w,
-    const uint16_t *__restrict__ kn_w, const uint16_t *__restrict__ rope, KvRef kv,
+    const uint16_t *__restrict__ kn_w, const uint16_t *__restrict__ rope, const KvRef &kv,
     uint16_t *__restrict__ qn, int nh, int nkv, int nrows, int rpb, uint16_t *__restrict__ tr_kf) {
-    const Meta mt = meta_of(sq, dmeta);
     const int32_t *cu = mt.cu, *pos0 = mt.pos0;
     const int nslot = nh + nkv;
-    const int r0 = blockIdx.x * rpb, nr = min(rpb, nrows - r0);
+    const int r0 = bid * rpb, nr = min(rpb, nrows - r0);
     const int tid = threadIdx.x;
-    __shared__ __attribute__((aligned(16))) uint16_t xs[PRB * PRS];
-    __shared__ __attribute__((aligned(16))) uint16_t rcs[PRB * ROT];   // cos / sin codes
-    __shared__ float rs[PRB];
-    __shared__ size_t rdst[PRB];             // k rows: element offset of the cache row
-    constexpr int PTK = PRB / 2 + 2;         // tokens a block's rows can span (nslot >= 2)
-    __shared__ int tpos[PTK], thd[PTK];      // their positions and block-table rows
+    uint16_t *xs = L.xs, *rcs = L.rcs;
+    float *rs = L.rs;
+    size_t *rdst = L.rdst;
+    int *tpos = L.tpos, *thd = L.thd;
     // The block's tokens' metadata first (a lookup chain of a few dependent
     // loads, with nothing else in flight yet), then every row and cos/sin
     // load of the block unconditionally (rows clamped into the block), so
@@ -224,24 +233,22 @@ __global__ __launch_bounds__(256) void k_attn_prep(
     }
 }
 
-// k_attn_vappend: the new tokens' v rows (raw, c/layer.h:315-316) into the
+// The V append blocks: the new tokens' v rows (raw, c/layer.h:315-316) into the
 // transposed V blocks [kv head][d][32]. One block per
 // (sequence, kv head, 32-position block the new tokens touch): the rows are
 // staged in LDS, then thread d writes its 32 keys -- one 64-byte run, so
 // the block is written as contiguous 16 KiB (a block only partly covered
 // by new tokens keeps its other keys: element stores for those).
-__global__ __launch_bounds__(256) void k_attn_vappend(
-    AttnSeqs sq, const int32_t *__restrict__ dmeta, const uint16_t *__restrict__ vin,
-    KvRef kv, int nkv, int maxnb) {
-    const Meta mt = meta_of(sq, dmeta);
-    const int s = blockIdx.x / (nkv * maxnb), rem = blockIdx.x % (nkv * maxnb);
+__device__ __forceinline__ void vappend_block(int bid, uint16_t *vt, const Meta &mt,
+                                              const uint16_t *__restrict__ vin, const KvRef &kv,
+                                              int nkv, int maxnb) {
+    const int s = bid / (nkv * maxnb), rem = bid % (nkv * maxnb);
     const int kvh = rem / maxnb, bi = rem % maxnb;
     const int t0 = mt.cu[s], ns = mt.cu[s + 1] - t0, p0 = mt.pos0[s];
     if (ns <= 0) return;
     const int b = p0 / 32 + bi;
     if (b > (p0 + ns - 1) / 32) return;
     const int klo = max(p0, b * 32) - b * 32, khi = min(p0 + ns, b * 32 + 32) - b * 32;
-    __shared__ __attribute__((aligned(16))) uint16_t vt[32 * PRS];
     const int tid = threadIdx.x;
     u16x8 v4[32 * (D / 8) / 256];               // every load in flight at once
 #pragma unroll
@@ -271,6 +278,25 @@ __global__ __launch_bounds__(256) void k_attn_vappend(
     } else {
         for (int k = klo; k < khi; k++) blk[d * 32 + k] = vt[k * PRS + d];
     }
+}
+
+// One launch for both: blocks [0, nprep) are prep blocks of rpb rows,
+// the rest V append blocks (B * nkv * maxnb of them). Neither reads what
+// the other writes (the K and V caches, qn), so they need no order.
+__global__ __launch_bounds__(256) void k_attn_prep(
+    AttnSeqs sq, const int32_t *__restrict__ dmeta, const uint16_t *__restrict__ qg,
+    const uint16_t *__restrict__ kin, const uint16_t *__restrict__ vin,
+    const uint16_t *__restrict__ qn_w, const uint16_t *__restrict__ kn_w,
+    const uint16_t *__restrict__ rope, KvRef kv, uint16_t *__restrict__ qn, int nh, int nkv,
+    int nrows, int rpb, int nprep, int maxnb, uint16_t *__restrict__ tr_kf) {
+    __shared__ __attribute__((aligned(16))) char lds[kPrepKernLds];
+    const Meta mt = meta_of(sq, dmeta);
+    if ((int)blockIdx.x < nprep)
+        prep_block((int)blockIdx.x, *reinterpret_cast<PrepLds *>(lds), mt, sq, qg, kin, qn_w,
+                   kn_w, rope, kv, qn, nh, nkv, nrows, rpb, tr_kf);
+    else
+        vappend_block((int)blockIdx.x - nprep, reinterpret_cast<uint16_t *>(lds), mt, vin, kv,
+                      nkv, maxnb);
 }
 
 // Row n of the 32 MFMA rows is (token n / GRP, q head n % GRP of the kv
@@ -635,7 +661,10 @@ __global__ __launch_bounds__(64 * (ScoresShape<NRB>::W + 1)) void k_attn_scores(
                 if (rd <= nxt[w]) continue;
                 compiler_fence();
                 // slot layout [row][64 keys]: lane l stores 16 bytes (8 keys)
-                // of row 8*i + l/8, two 64-byte runs a row
+                // of row 8*i + l/8, two 64-byte runs a row. The streaming
+                // policy: with the default one the dirty score lines were
+                // written back from L2 while P.V streamed V (config 4: P.V
+                // 222 -> 204 us, scores 206 -> 214 us)
                 for (int g = nxt[w]; g < rd; g++) {
                     const uint4 *sl = ring[w][g % kScRing];
                     const RingHdr h = hdr[w][g % kScRing];
@@ -645,7 +674,9 @@ __global__ __launch_bounds__(64 * (ScoresShape<NRB>::W + 1)) void k_attn_scores(
                     for (int i = 0; i < 2 * NRB; i++) {
                         const int row = 8 * i + (l >> 3);
                         if (row / GRP < h.tq && kq < h.k1)
-                            *reinterpret_cast<uint4 *>(Ab + a_index(row, kq, h.cap)) = sl[i * 64 + l];
+                            __builtin_nontemporal_store(
+                                __builtin_bit_cast(u16x8, sl[i * 64 + l]),
+                                reinterpret_cast<u16x8 *>(Ab + a_index(row, kq, h.cap)));
                     }
                 }
                 compiler_fence();
@@ -985,10 +1016,11 @@ int attn_prep(const ApusHipAttnLayer *L, const AttnSeqs &sq, const int32_t *dmet
     const size_t nrows = Ttot * (L->nh + L->nkv);
     // few rows (decode): small blocks, so they spread over the chip
     const int rpb = nrows < (size_t)8 * PRB * cu_count() ? 8 : PRB;
+    const unsigned nprep = cdiv(nrows, rpb), nvapp = (unsigned)(sq.n * L->nkv * maxnb);
     APUS_TIMED("k_attn_prep",
-               k_attn_prep<<<cdiv(nrows, rpb), 256, 0, stream()>>>(
-        sq, dmeta, qg, k, L->qn_w, L->kn_w, rope, kv, qn, (int)L->nh, (int)L->nkv, (int)nrows,
-        rpb, attn_trace() ? attn_trace()->kf : nullptr));
+               k_attn_prep<<<nprep + nvapp, 256, 0, stream()>>>(
+        sq, dmeta, qg, k, v, L->qn_w, L->kn_w, rope, kv, qn, (int)L->nh, (int)L->nkv,
+        (int)nrows, rpb, (int)nprep, maxnb, attn_trace() ? attn_trace()->kf : nullptr));
     if (int r = launch_check("k_attn_prep")) return r;
     if (const ApusHipAttnTrace *tr = attn_trace()) {
         if (tr->qf)
@@ -1003,10 +1035,7 @@ int attn_prep(const ApusHipAttnLayer *L, const AttnSeqs &sq, const int32_t *dmet
             if (int r = launch_check("k_trace_mgate")) return r;
         }
     }
-    APUS_TIMED("k_attn_vappend",
-               k_attn_vappend<<<(unsigned)(sq.n * L->nkv * maxnb), 256, 0, stream()>>>(
-        sq, dmeta, v, kv, (int)L->nkv, maxnb));
-    return launch_check("k_attn_vappend");
+    return kOk;
 }
 
 // the most 32-position cache blocks one sequence's new tokens touch

@@ -488,8 +488,7 @@ def bench_attn_decode(torch, B, ctx, steps, warmup, seed, leg=None):
     flops = B * NH * 4 * AD * ctx
     kbytes = B * ctx * NKV * AD * 2           # one of the K / V caches
     table = {"k_attn_scores": ("hbm", kbytes, HBM_PEAK), "k_attn_pv": ("hbm", kbytes, HBM_PEAK),
-             "k_attn_prep": ("hbm", B * (NH * AD * 2 * 2 + NKV * AD * 2 * 2), HBM_PEAK),
-             "k_attn_vappend": ("hbm", B * NKV * AD * 2 * 2, HBM_PEAK),
+             "k_attn_prep": ("hbm", B * (NH * AD * 2 * 2 + 2 * NKV * AD * 2 * 2), HBM_PEAK),
              "k_attn_combine": ("hbm", B * NH * AD * 2 * 2, HBM_PEAK)}
     total, per, kt = time_steps(torch, step, steps, warmup, nsets, table)
     st = float(np.mean(per))
@@ -542,8 +541,7 @@ def bench_attn_prefill(torch, T, steps, warmup, seed, leg=None):
     bytes_ = T * (NH * 2 * AD * 2 + 2 * NKV * AD * 2 + 2 * NKV * AD * 2 + NH * AD * 2)
     table = {"k_attn_fa": ("mfma", flops, BF16_PEAK),
              # q and k rows read and written (normed, roped), v rows appended
-             "k_attn_prep": ("hbm", T * (NH * AD * 2 * 2 + NKV * AD * 2 * 2), HBM_PEAK),
-             "k_attn_vappend": ("hbm", T * NKV * AD * 2 * 2, HBM_PEAK)}
+             "k_attn_prep": ("hbm", T * (NH * AD * 2 * 2 + 2 * NKV * AD * 2 * 2), HBM_PEAK)}
     total, per, kt = time_steps(torch, step, steps, warmup, nsets, table)
     st = float(np.mean(per))
     wl = f"attn_prefill_t{T}"
@@ -635,8 +633,7 @@ def bench_mixed_block(torch, B, steps, warmup, seed, leg=None):
     kv1 = int(sum((int(c) + int(x)) * NKV * AD * 2 for c, x in zip(ctx, k)))   # one of K / V
     table = {"k_gdn_decode": ("hbm", gdn_bytes, HBM_PEAK),
              "k_attn_scores": ("hbm", kv1, HBM_PEAK), "k_attn_pv": ("hbm", kv1, HBM_PEAK),
-             "k_attn_prep": ("hbm", T * (NH * AD * 2 * 2 + NKV * AD * 2 * 2), HBM_PEAK),
-             "k_attn_vappend": ("hbm", T * NKV * AD * 2 * 2, HBM_PEAK),
+             "k_attn_prep": ("hbm", T * (NH * AD * 2 * 2 + 2 * NKV * AD * 2 * 2), HBM_PEAK),
              "k_attn_combine": ("hbm", T * NH * AD * 2 * 2, HBM_PEAK)}
     total, per, kt = time_steps(torch, step, steps, warmup, 1, table)
     st = float(np.mean(per))
