@@ -871,34 +871,53 @@ __global__ __launch_bounds__(64) void k_attn_pv(
     }
 }
 
-// ---- k_attn_combine: one block per (token, q head), d threads ----------
-__global__ __launch_bounds__(D) void k_attn_combine(
+// ---- k_attn_combine: one block per (token, kv head, 4 of its q heads) --
+// A thread owns 4 consecutive d of one (token, q head) row: its gate codes
+// are loaded first, then up to 16 of the pair's run partials at once
+// (float4 each), summed in run order from 0.0f; rnd, times
+// rnd(sigmoid(gate)). One block per (token, q head) with a thread per d
+// needed three rounds of resident waves on config 4, each a chain of
+// dependent loads.
+__global__ __launch_bounds__(256) void k_attn_combine(
     AttnSeqs sq, const int32_t *__restrict__ dmeta, const float *__restrict__ Op,
     const uint16_t *__restrict__ qg, int nh, int nkv, uint16_t *__restrict__ y,
     const uint16_t *__restrict__ sig_bf, uint16_t *__restrict__ tr_attno) {
     const Meta mt = meta_of(sq, dmeta);
-    const int32_t *cu = mt.cu;
-    const int tt = blockIdx.x / nh, h = blockIdx.x % nh;
-    const int s = seq_of(cu, sq.n, tt), t = tt - cu[s];
-    const int kvh = h / GRP, n = t * GRP + h % GRP;
-    const int dd = threadIdx.x;
+    const int half = blockIdx.x & 1, tk = blockIdx.x >> 1;
+    const int tt = tk / nkv, kvh = tk % nkv;
+    const int s = seq_of(mt.cu, sq.n, tt), t = tt - mt.cu[s];
+    const int g = half * (GRP / 2) + (threadIdx.x >> 6), h = kvh * GRP + g, n = t * GRP + g;
+    const int d = (threadIdx.x & 63) * 4;
+    const size_t row = (size_t)tt * nh + h;
+    const uint2 gc = *reinterpret_cast<const uint2 *>(qg + row * 2 * D + D + d);
     int w0, w1;
     pair_runs(mt, nkv, s, kvh, sq.T2, &w0, &w1);
-    const int p = s * nkv + kvh;
-    float sum = 0.0f;
-    for (int w = w0; w <= w1; w += 8) {          // eight partials in flight, summed in order
-        float v[8];
+    const int nw = w1 - w0;
+    const float *P0 = Op + ((size_t)(s * nkv + kvh + w0) * kRows + n) * D + d;
+    f32x4 sum = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int w = 0; w <= nw; w += 16) {
+        f32x4 v[16];
 #pragma unroll
-        for (int i = 0; i < 8; i++)
-            v[i] = w + i <= w1 ? Op[((size_t)(p + w + i) * kRows + n) * D + dd] : 0.0f;
+        for (int i = 0; i < 16; i++)
+            v[i] = *reinterpret_cast<const f32x4 *>(P0 + (size_t)min(w + i, nw) * kRows * D);
 #pragma unroll
-        for (int i = 0; i < 8; i++)
-            if (w + i <= w1) sum += v[i];
+        for (int i = 0; i < 16; i++)
+            if (w + i <= nw) sum += v[i];
     }
-    const float o = rndf(sum);
-    const float gt = bf2f(sig_bf[qg[((size_t)tt * nh + h) * 2 * D + D + dd]]);  // rnd(sigmoid)
-    y[((size_t)tt * nh + h) * D + dd] = f2bf(o * gt);
-    if (tr_attno) tr_attno[((size_t)tt * nh + h) * D + dd] = f2bf(o);      // (trace)
+    const uint16_t code[4] = {(uint16_t)gc.x, (uint16_t)(gc.x >> 16), (uint16_t)gc.y,
+                              (uint16_t)(gc.y >> 16)};
+    uint16_t yo[4], ao[4];
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+        const float o = rndf(sum[e]);
+        ao[e] = f2bf(o);
+        yo[e] = f2bf(o * bf2f(sig_bf[code[e]]));       // rnd(sigmoid(gate))
+    }
+    *reinterpret_cast<uint2 *>(y + row * D + d) =
+        make_uint2(yo[0] | (uint32_t)yo[1] << 16, yo[2] | (uint32_t)yo[3] << 16);
+    if (tr_attno)                                        // (trace)
+        *reinterpret_cast<uint2 *>(tr_attno + row * D + d) =
+            make_uint2(ao[0] | (uint32_t)ao[1] << 16, ao[2] | (uint32_t)ao[3] << 16);
 }
 
 // (trace) mgate = rnd(sigmoid(gate)) for every (token, head, d)
@@ -1101,7 +1120,7 @@ int attn_decode_kv(const ApusHipAttnLayer *L, size_t B, const int32_t *cu, const
         APUS_LAUNCHED("k_attn_pv");
     }
     APUS_TIMED("k_attn_combine",
-               k_attn_combine<<<(unsigned)(Ttot * L->nh), D, 0, stream()>>>(
+               k_attn_combine<<<(unsigned)(Ttot * nkv * 2), 256, 0, stream()>>>(
                    sq, dmeta, Op, qg, (int)L->nh, (int)nkv, y, tabs->sig_bf,
                    attn_trace() ? attn_trace()->attno : nullptr));
     APUS_LAUNCHED("k_attn_combine");
