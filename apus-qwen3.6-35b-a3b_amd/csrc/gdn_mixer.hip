@@ -51,21 +51,6 @@ __device__ __forceinline__ int seq_of(const int32_t *cu, int B, int t) {
     return lo;
 }
 
-// Ascending sum of squares of n (multiple of 4) LDS floats, one rounding
-// per mul and add; 16-byte LDS reads keep the dependent add chain fed.
-__device__ __forceinline__ float seq_sumsq(const float *x, int n) {
-    float ss = 0.0f;
-    for (int i = 0; i < n; i += 4) {
-        const float4 v = *reinterpret_cast<const float4 *>(x + i);
-        ss = ss + v.x * v.x;
-        ss = ss + v.y * v.y;
-        ss = ss + v.z * v.z;
-        ss = ss + v.w * v.w;
-    }
-    return ss;
-}
-
-
 // ---- state layout conversion -------------------------------------------
 __device__ __forceinline__ size_t packed_index(int i, int j) {
     return ((size_t)((j >> 6) * 32 + (i >> 2)) * 64 + (j & 63)) * 4 + (i & 3);

@@ -133,26 +133,22 @@ __device__ __forceinline__ ChunkPos chunk_pos(const int32_t *cu, const int32_t *
 //   F  fp32 [3][C]: F[0][t] = G_t rq_t qscale (the scale of row t of
 //      Q S0, Q as codes), F[1][s] = exp(gamma_C - gamma_s) rk_s (the scale
 //      of key s in the state update, K as codes), F[2][0] = G_C.
-// Per (chunk, K head), written by the v-head of even index (both v-heads
-// of a K head hold the same q and k), the conv codes themselves (exact in
-// bf16, so one MFMA per product against a split operand's two parts):
-//   Q  the codes in W's lane order (the A operand of Q S0);
-//   K  the codes as a B operand: lane g*16 + i%16 holds key rows
-//      s = 8g..8g+7 of state row i.
 __device__ __forceinline__ size_t bx_a_index(int t, int c, int nkb) {
     return ((size_t)((t >> 4) * nkb + (c >> 5)) * 64 + ((c & 31) >> 3) * 16 + (t & 15)) * 16 + (c & 7);
-}
-__device__ __forceinline__ size_t bx_b_index(int s, int i) {
-    return ((size_t)((i >> 4) * 2 + (s >> 5)) * 64 + ((s & 31) >> 3) * 16 + (i & 15)) * 16 + (s & 7);
 }
 __device__ __forceinline__ size_t wy_u_index(int t, int j) {
     return ((size_t)((j >> 4) * 4 + (t >> 4)) * 64 + ((t & 15) >> 2) * 16 + (j & 15)) * 4 + (t & 3);
 }
 
-// q and k travel to the scan as code planes (exact bf16, no lo part) in
-// the same lane order, 1 KiB blocks of 64 lanes x 8 codes:
-//   Q  [4 row blocks][4 column blocks][64][8];
-//   K  [8 state-row blocks][2 key blocks][64][8].
+// Per (chunk, K head), written by the v-head of even index (both v-heads
+// of a K head hold the same q and k), q and k travel to the scan as the
+// conv codes themselves (exact in bf16, so one MFMA per product against a
+// split operand's two parts), as code planes in the same lane order, 1 KiB
+// blocks of 64 lanes x 8 codes:
+//   Q  [4 row blocks][4 column blocks][64][8], W's lane order (the A
+//      operand of Q S0);
+//   K  [8 state-row blocks][2 key blocks][64][8], a B operand: lane
+//      g*16 + i%16 holds key rows s = 8g..8g+7 of state row i.
 __device__ __forceinline__ size_t bx1_a_index(int t, int c, int nkb) {
     return ((size_t)((t >> 4) * nkb + (c >> 5)) * 64 + ((c & 31) >> 3) * 16 + (t & 15)) * 8 + (c & 7);
 }
@@ -209,9 +205,6 @@ __device__ __forceinline__ f32x4 mfma_x2a(u16x8 c, u16x8 xh, u16x8 xl, f32x4 acc
     return __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf(c), as_bf(xh), acc, 0, 0, 0);
 }
 
-__device__ __forceinline__ float4 lds4_(const float *p) {
-    return *reinterpret_cast<const float4 *>(p);
-}
 // hi/lo bf16 codes of 8 fp32 values: one split-precision MFMA operand
 __device__ __forceinline__ void split8(const float (&x)[8], u16x8 &hi, u16x8 &lo) {
 #pragma unroll
@@ -221,41 +214,6 @@ __device__ __forceinline__ void split8(const float (&x)[8], u16x8 &hi, u16x8 &lo
         hi[i] = h;
         lo[i] = l;
     }
-}
-// the same for 8 consecutive fp32 values in LDS
-__device__ __forceinline__ void lds_split8(const float *p, u16x8 &hi, u16x8 &lo) {
-    const float4 a0 = lds4_(p), a1 = lds4_(p + 4);
-    const float v[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
-    split8(v, hi, lo);
-}
-
-// Three-way split: x = hi + mid + lo to 24 bits (hi = rnd(x), mid =
-// rnd(x - hi), lo = rnd(x - hi - mid)), and the product keeping every
-// term down to 2^-16 relative (hh, hm, mh, hl, lh, mm; the dropped terms
-// are below 2^-24), smallest first.
-__device__ __forceinline__ void lds_split8x3(const float *p, u16x8 &hi, u16x8 &mid, u16x8 &lo) {
-    const float4 a0 = lds4_(p), a1 = lds4_(p + 4);
-    const float v[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
-#pragma unroll
-    for (int i = 0; i < 8; i++) {
-        const __bf16 h = (__bf16)v[i];
-        const float r = v[i] - (float)h;
-        const __bf16 m = (__bf16)r;
-        const __bf16 l = (__bf16)(r - (float)m);
-        hi[i] = __builtin_bit_cast(uint16_t, h);
-        mid[i] = __builtin_bit_cast(uint16_t, m);
-        lo[i] = __builtin_bit_cast(uint16_t, l);
-    }
-}
-__device__ __forceinline__ f32x4 mfma_x6(u16x8 ah, u16x8 am, u16x8 al, u16x8 bh, u16x8 bm,
-                                         u16x8 bl, f32x4 c) {
-    c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf(am), as_bf(bm), c, 0, 0, 0);
-    c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf(al), as_bf(bh), c, 0, 0, 0);
-    c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf(ah), as_bf(bl), c, 0, 0, 0);
-    c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf(am), as_bf(bh), c, 0, 0, 0);
-    c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf(ah), as_bf(bm), c, 0, 0, 0);
-    c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf(ah), as_bf(bh), c, 0, 0, 0);
-    return c;
 }
 
 // k_gdn_chunk_wy: one workgroup per (chunk, v-head), up to three per CU.
@@ -967,7 +925,7 @@ static PrefillWs prefill_ws_carve(char *base, size_t Ttot, size_t nch, size_t B,
         off += (n + 255) / 256 * 256;
         return q;
     };
-    const size_t kd = hk * DK, vd = hv * DV, units = nch * hv;
+    const size_t vd = hv * DV, units = nch * hv;
     p.w.ob = (uint16_t *)take(Ttot * vd * 2);
     p.Ub = (float *)take(units * C * DV * 4);
     p.Wb = (uint16_t *)take(units * C * DK * 4);

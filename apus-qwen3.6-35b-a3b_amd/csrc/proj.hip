@@ -109,13 +109,6 @@ __global__ __launch_bounds__(64) void k_gemm_seq(const uint16_t *__restrict__ w,
     if (o < O) y[(size_t)m * O + o] = f2bf(acc);
 }
 
-// 16 consecutive codes of row r at k (zeros past the row or past K)
-__device__ __forceinline__ bf16x8 ld_op(const uint16_t *base, int r, int nrows, int K, int k) {
-    u16x8 v = u16x8{0, 0, 0, 0, 0, 0, 0, 0};
-    if (r < nrows && k < K) v = *reinterpret_cast<const u16x8 *>(base + (size_t)r * K + k);
-    return __builtin_bit_cast(bf16x8, v);
-}
-
 // One workgroup per (64 outputs, up to 64 rows); its 4 wavefronts split K
 // (32-wide k step st goes to wavefront st % 4), each with all 4 x 4
 // 16x16 output blocks, the next step's operands in flight, and add their
