@@ -19,10 +19,12 @@
 // Padding a chunk with tokens of g = 0, b = 0, k = q = 0 leaves S and the
 // real rows unchanged, so ragged sequences need no special case.
 //
-// Kernels (after k_gdn_prep, before k_gdn_post of gdn_mixer.hip):
+// Kernels (before k_gdn_post of gdn_mixer.hip):
+//   k_gdn_chunk_qk    one workgroup per (chunk, K head): the q, k conv
+//                     codes, l2norm factors, K K^T and Q K^T.
 //   k_gdn_chunk_wy    one workgroup per (chunk, v-head), all chunks in
-//                     parallel: K K^T and Q K^T, L and A with their decay
-//                     factors, then U and W as T [b V | b G K] with
+//                     parallel: the v codes and gates, L and A with their
+//                     decay factors, then U and W as T [b V | b G K] with
 //                     T = (I+L)^-1 built in 32x32 blocks.
 //   k_gdn_chunk_scan  one workgroup per (sequence, v-head, 16-column block
 //                     of S): the delta rule is separable by value column,
@@ -216,12 +218,13 @@ __device__ __forceinline__ void split8(const float (&x)[8], u16x8 &hi, u16x8 &lo
     }
 }
 
-// k_gdn_chunk_wy: one workgroup per (chunk, v-head), up to three per CU.
-// It forms the chunk's q, k, v conv+SiLU codes, l2norm factors and gates
-// from the layer inputs itself. The normalised rows are q_t = rq_t qscale
-// cq_t and k_s = rk_s ck_s with cq, ck the codes, so q.k and k.k are the
-// factors times the exact dot products of the codes: one bf16 MFMA per
-// product, fp32 accumulation, no operand splitting.
+// The normalised rows are q_t = rq_t qscale cq_t and k_s = rk_s ck_s with
+// cq, ck the conv codes, so q.k and k.k are the factors times the exact
+// dot products of the codes: one bf16 MFMA per product, fp32
+// accumulation, no operand splitting. k_gdn_chunk_qk forms the codes,
+// factors and products once per (chunk, K head); k_gdn_chunk_wy, one
+// workgroup per (chunk, v-head) and up to three per CU, forms the v codes
+// and gates of its head from the layer inputs and the rest of the WY form.
 constexpr int CKP = DK + 8;            // bf16 row stride of the code copies
 
 // Two channels' 4-tap conv sums (tap order, one rounding per mul and add,
@@ -246,6 +249,168 @@ __device__ __forceinline__ uint32_t conv_sum4_pair(const float (&w0)[4], const f
     c = c + w1[3] * hi(x3);
     return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_t{a, c}, bf16x2_t));
 }
+constexpr int TG = 16;                         // tokens per conv work item
+
+// The conv+SiLU codes of channels gcol and gcol + 1 (c/gdn.h:19-33,
+// 220-228) for the 16 tokens tg .. tg+15 of chunk P: the item reads its
+// tokens' inputs and the 3 before them (from the sequence's old conv state
+// in its first chunk). Loads are unconditional (rows clamped into the
+// chunk); the codes of padding rows (t >= nt) are 0.
+__device__ __forceinline__ void conv_codes16(const uint16_t *__restrict__ qkv, size_t cd,
+                                             size_t gcol, const ChunkPos &P, int tg, bool first,
+                                             const uint16_t *__restrict__ cst,
+                                             const uint16_t *__restrict__ conv_w,
+                                             const uint16_t *__restrict__ silu_bf,
+                                             uint16_t (&c0)[TG], uint16_t (&c1)[TG]) {
+    // inputs of rows t0 + tg - 3 .. t0 + tg + 15, two channels a word
+    uint32_t x[TG + 3];
+#pragma unroll
+    for (int r = 0; r < TG + 3; r++) {
+        const int t = tg - 3 + r;               // chunk-relative token
+        const uint32_t vq = *reinterpret_cast<const uint32_t *>(
+            qkv + (size_t)(P.t0 + max(min(t, P.nt - 1), first ? 0 : -3)) * cd + gcol);
+        if (r < 3 && tg == 0) {
+            const uint32_t vs = (uint32_t)cst[gcol * 3 + r] | ((uint32_t)cst[(gcol + 1) * 3 + r] << 16);
+            x[r] = first ? vs : vq;
+        } else {
+            x[r] = vq;
+        }
+    }
+    float w0[4], w1[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        w0[i] = bf2f(conv_w[gcol * 4 + i]);
+        w1[i] = bf2f(conv_w[(gcol + 1) * 4 + i]);
+    }
+    // conv sums, then SiLU through the fp32 fast path; the few results it
+    // cannot vouch for come from the bf16-code table, all gathered after
+    uint32_t redo = 0;
+#pragma unroll
+    for (int j = 0; j < TG; j++) {
+        const uint32_t cc = conv_sum4_pair(w0, w1, x[j], x[j + 1], x[j + 2], x[j + 3]);
+        c0[j] = (uint16_t)cc;
+        c1[j] = (uint16_t)(cc >> 16);
+        bool ok0, ok1;
+        const uint16_t r0 = silu_fast(bf2f(c0[j]), ok0), r1 = silu_fast(bf2f(c1[j]), ok1);
+        redo |= (ok0 ? 0u : 1u << j) | (ok1 ? 0u : 1u << (TG + j));
+        if (ok0) c0[j] = r0;
+        if (ok1) c1[j] = r1;
+    }
+    if (redo) {
+#pragma unroll
+        for (int j = 0; j < TG; j++) {
+            if (redo >> j & 1u) c0[j] = silu_bf[c0[j]];
+            if (redo >> (TG + j) & 1u) c1[j] = silu_bf[c1[j]];
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < TG; j++)
+        if (tg + j >= P.nt) c0[j] = c1[j] = 0;
+}
+
+// Q K^T and K K^T of a (chunk, K head) as the MFMA left them: the 10 lower
+// 16x16 tiles (rb, cb <= rb) of each, tile index rb (rb + 1) / 2 + cb,
+// 64 lanes x 4 floats a tile. Q K^T is formed transposed (K Q^T: lane
+// (g, r) holds keys s = 16 cb + 4 g .. +3 of row t = 16 rb + r); K K^T
+// lane (g, r) holds rows t = 16 rb + 4 g .. +3 of key s = 16 cb + r.
+constexpr int kQkTiles = 10;
+__device__ __forceinline__ size_t qk_tile(size_t ku, int which, int rb, int cb, int lane) {
+    return (((ku * 2 + which) * kQkTiles + rb * (rb + 1) / 2 + cb) * 64 + lane) * 4;
+}
+
+// k_gdn_chunk_qk: one workgroup per (chunk, K head). The q and k conv+SiLU
+// codes of the chunk (formed once per K head: both of its v-heads use
+// them), their l2norm factors (rq with the 1/sqrt(dk) query scale, rk:
+// QKR[(chunk, K head)][2C]), the scan's code planes Q and K, and the
+// v-head-independent products Q K^T and K K^T on the codes (one MFMA per
+// product, qk_tile layout) for k_gdn_chunk_wy.
+__global__ __launch_bounds__(512) void k_gdn_chunk_qk(
+    ChunkSeqs sq, const int32_t *__restrict__ dmeta, const uint16_t *__restrict__ qkv,
+    const uint16_t *__restrict__ conv_w, const uint16_t *__restrict__ conv_state,
+    const int32_t *__restrict__ slots, const uint16_t *__restrict__ silu_bf,
+    uint16_t *__restrict__ Qp, uint16_t *__restrict__ Kp, float *__restrict__ QKt,
+    float *__restrict__ QKR, int hk, float qscale) {
+    const int hv = hk * REP;
+    const size_t kd = (size_t)hk * DK, vd = (size_t)hv * DV, cd = 2 * kd + vd;
+    const int ku = blockIdx.x, ci = ku / hk, kh = ku % hk;
+    const int32_t *cu = dmeta ? dmeta : sq.cu;
+    const int32_t *coff = dmeta ? dmeta + sq.n + 1 : sq.coff;
+    const ChunkPos P = chunk_pos(cu, coff, sq.n, ci);
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    __shared__ __attribute__((aligned(16))) uint16_t Qc[C * CKP], Kc[C * CKP];
+    const bool first = ci == coff[P.s];
+    const uint16_t *cst = conv_state + (size_t)(slots ? slots[P.s] : P.s) * cd * 3;
+    // work items: (two adjacent channels of the 2 DK q|k channels, 16
+    // tokens), one per thread
+    for (int it = tid; it < DK * (C / TG); it += 512) {
+        const int lc = 2 * (it % DK), tg = (it / DK) * TG;
+        const size_t gcol = lc < DK ? (size_t)kh * DK + lc : kd + (size_t)kh * DK + (lc - DK);
+        uint16_t c0[TG], c1[TG];
+        conv_codes16(qkv, cd, gcol, P, tg, first, cst, conv_w, silu_bf, c0, c1);
+        uint16_t *dst = (lc < DK ? Qc : Kc) + (lc & (DK - 1));
+#pragma unroll
+        for (int j = 0; j < TG; j++)
+            *reinterpret_cast<uint32_t *>(dst + (tg + j) * CKP) = (uint32_t)c0[j] | ((uint32_t)c1[j] << 16);
+    }
+    __syncthreads();
+    if (tid < 2 * C) {                          // l2norm factors, one lane per row
+        const int t = tid & (C - 1);
+        const float f = t < P.nt ? 1.0f / sqrtf(row_sumsq((tid < C ? Qc : Kc) + t * CKP) + kL2Eps) : 0.0f;
+        QKR[(size_t)ku * 2 * C + tid] = tid < C ? f * qscale : f;
+    }
+    // the scan's Q (rows t, 8 consecutive dims a piece) and K (dim i, 8
+    // consecutive keys a piece) as code planes
+    uint16_t *Qpu = Qp + (size_t)ku * C * DK, *Kpu = Kp + (size_t)ku * C * DK;
+#pragma unroll
+    for (int u = 0; u < C * DK / 8 / 512; u++) {
+        const int e = tid + 512 * u;
+        {
+            const int t = e / (DK / 8), c0 = (e % (DK / 8)) * 8;
+            *reinterpret_cast<u16x8 *>(Qpu + bx1_a_index(t, c0, DK / 32)) =
+                *reinterpret_cast<const u16x8 *>(Qc + t * CKP + c0);
+        }
+        {
+            const int i = e % DK, s0 = (e / DK) * 8;
+            u16x8 x;
+#pragma unroll
+            for (int j = 0; j < 8; j++) x[j] = Kc[(s0 + j) * CKP + i];
+            *reinterpret_cast<u16x8 *>(Kpu + bx1_b_index(s0, i)) = x;
+        }
+    }
+    // products on the bf16 MFMA 16x16x32 (lane: row / column r16, reduction
+    // indices g8 .. g8+7): wavefront w < 4 takes row block 3 - w of Q K^T,
+    // wavefront 4 + w row block w of K K^T
+    const int r16 = lane & 15, g8 = (lane >> 4) * 8;
+    if (wave < 4) {
+        const int rb = 3 - wave;
+        u16x8 qf[DK / 32];
+#pragma unroll
+        for (int ks = 0; ks < DK / 32; ks++) qf[ks] = ld8(Qc + (rb * 16 + r16) * CKP + ks * 32 + g8);
+        for (int cb = 0; cb <= rb; cb++) {
+            f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int ks = 0; ks < DK / 32; ks++)
+                acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                    as_bf(ld8(Kc + (cb * 16 + r16) * CKP + ks * 32 + g8)), as_bf(qf[ks]), acc, 0, 0, 0);
+            *reinterpret_cast<f32x4 *>(QKt + qk_tile(ku, 0, rb, cb, lane)) = acc;
+        }
+    } else {
+        const int rb = wave - 4;
+        u16x8 kw[DK / 32];
+#pragma unroll
+        for (int ks = 0; ks < DK / 32; ks++) kw[ks] = ld8(Kc + (rb * 16 + r16) * CKP + ks * 32 + g8);
+        for (int cb = 0; cb <= rb; cb++) {
+            f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int ks = 0; ks < DK / 32; ks++)
+                acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                    as_bf(kw[ks]), as_bf(ld8(Kc + (cb * 16 + r16) * CKP + ks * 32 + g8)), acc, 0, 0, 0);
+            *reinterpret_cast<f32x4 *>(QKt + qk_tile(ku, 1, rb, cb, lane)) = acc;
+        }
+    }
+}
+
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void k_gdn_chunk_wy(
     ChunkSeqs sq, const int32_t *__restrict__ dmeta, const uint16_t *__restrict__ qkv,
     const uint16_t *__restrict__ a, const uint16_t *__restrict__ b,
@@ -254,51 +419,46 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void k
     const int32_t *__restrict__ slots, const uint16_t *__restrict__ silu_bf,
     const uint16_t *__restrict__ sig_bf, float *__restrict__ Ub,
     uint16_t *__restrict__ Wb, uint16_t *__restrict__ Ab, float *__restrict__ Fb,
-    uint16_t *__restrict__ Qp, uint16_t *__restrict__ Kp, int hk, int pair_map, float qscale) {
+    const uint16_t *__restrict__ Kp, const float *__restrict__ QKt,
+    const float *__restrict__ QKR, int hk, int pair_map) {
     const int hv = hk * REP;
     const size_t kd = (size_t)hk * DK, vd = (size_t)hv * DV;
     // unit = ci * hv + h. With pair_map the two v-heads of one K head (units
     // 2P, 2P+1) run as blocks 8 apart: blocks are dealt round-robin over the
-    // 8 XCDs, so both land on one XCD and the second reads q, k from its L2.
+    // 8 XCDs, so both land on one XCD and the second reads the K head's
+    // products and codes from its L2.
     int unit = blockIdx.x;
     if (pair_map) {
         const int b = blockIdx.x;
         unit = ((b >> 4) * 8 + (b & 7)) * 2 + ((b >> 3) & 1);
     }
     const int ci = unit / hv, h = unit % hv, kh = h / REP;
-    const bool wqk = h % REP == 0;              // this v-head writes Qp / Kp
-    uint16_t *Qpu = Qp + ((size_t)ci * hk + kh) * C * DK;
-    uint16_t *Kpu = Kp + ((size_t)ci * hk + kh) * C * DK;
+    const size_t ku = (size_t)ci * hk + kh;     // the (chunk, K head) of k_gdn_chunk_qk
+    const uint16_t *Kpu = Kp + ku * C * DK;
     const int32_t *cu = dmeta ? dmeta : sq.cu;
     const int32_t *coff = dmeta ? dmeta + sq.n + 1 : sq.coff;
     const ChunkPos P = chunk_pos(cu, coff, sq.n, ci);
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
 
-    // LDS: q codes (later L, then W's staging together with the k codes),
-    // k codes, the V codes transposed ([column][token]: the B operand of
-    // T R; the 16-byte pieces of row n XOR-swizzled by n % 8, so the MFMA
-    // operand reads spread over the banks), per-token factors (three
-    // workgroups per CU)
-    constexpr int QC_B = C * CKP * 2, L_B = C * CP * 4;
-    static_assert(QC_B >= L_B, "L does not fit over the q codes");
-    static_assert(2 * QC_B >= C * KP * 4, "W's staging does not fit over the code copies");
-    __shared__ __attribute__((aligned(16))) char wy_lds[2 * QC_B + DV * C * 2];
-    uint16_t *Qc = reinterpret_cast<uint16_t *>(wy_lds);
+    // LDS: L (later W's staging), the V codes transposed ([column][token]:
+    // the B operand of T R; the 16-byte pieces of row n XOR-swizzled by
+    // n % 8, so the MFMA operand reads spread over the banks), per-token
+    // factors (three workgroups per CU)
+    constexpr int W_B = C * KP * 4, L_B = C * CP * 4;
+    static_assert(W_B >= L_B, "L does not fit in W's staging");
+    __shared__ __attribute__((aligned(16))) char wy_lds[W_B + DV * C * 2];
     float *Ls = reinterpret_cast<float *>(wy_lds);
-    uint16_t *Kc = reinterpret_cast<uint16_t *>(wy_lds + QC_B);
-    uint16_t *Vt = reinterpret_cast<uint16_t *>(wy_lds + 2 * QC_B);
+    uint16_t *Vt = reinterpret_cast<uint16_t *>(wy_lds + W_B);
     __shared__ float graw_s[C], gam[C], bet[C], Gs[C], rq[C], rk[C];
 
     // ---- the token-parallel front (c/layer.h:427-492 up to the
-    // recurrence) for this chunk: causal conv1d k=4 + SiLU of the q, k
-    // channels of K head kh and the v channels of head h (c/gdn.h:19-33,
-    // 220-228), the l2norm factors (c/gdn.h:402-416) and the gates
-    // (c/gdn.h:34-40). Work items are (two adjacent channels of the 384,
-    // 16 tokens), three per thread; an item reads its 16 tokens' inputs and
-    // the 3 before them (from the sequence's old conv state in its first
-    // chunk). Loads are unconditional (rows clamped into the chunk); codes
-    // of padding rows (t >= nt) are 0, as are their gates.
+    // recurrence) for this chunk and v-head: causal conv1d k=4 + SiLU of the
+    // v channels of head h (c/gdn.h:19-33, 220-228) and the gates
+    // (c/gdn.h:34-40); the q, k codes, their l2norm factors (c/gdn.h:402-416)
+    // and their products come from k_gdn_chunk_qk. Work items are (two
+    // adjacent v channels, 16 tokens), one per thread; the gates of padding
+    // rows (t >= nt) are 0.
     const size_t cd = 2 * kd + vd;
     const bool first = ci == coff[P.s];
     const uint16_t *cst = conv_state + (size_t)(slots ? slots[P.s] : P.s) * cd * 3;
@@ -312,106 +472,27 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void k
         graw_s[tid] = g;
         bet[tid] = bt;
     }
-    constexpr int TG = 16;                      // tokens per work item
-    for (int it = tid; it < (3 * DK / 2) * (C / TG); it += 256) {
-        const int lc = 2 * (it % (3 * DK / 2)), tg = (it / (3 * DK / 2)) * TG;
-        const size_t gcol = lc < DK ? (size_t)kh * DK + lc
-                          : lc < 2 * DK ? kd + (size_t)kh * DK + (lc - DK)
-                                        : 2 * kd + (size_t)h * DV + (lc - 2 * DK);
-        // inputs of rows t0 + tg - 3 .. t0 + tg + 15, two channels a word
-        uint32_t x[TG + 3];
-#pragma unroll
-        for (int r = 0; r < TG + 3; r++) {
-            const int t = tg - 3 + r;           // chunk-relative token
-            const uint32_t vq = *reinterpret_cast<const uint32_t *>(
-                qkv + (size_t)(P.t0 + max(min(t, P.nt - 1), first ? 0 : -3)) * cd + gcol);
-            if (r < 3 && tg == 0) {
-                const uint32_t vs = (uint32_t)cst[gcol * 3 + r] | ((uint32_t)cst[(gcol + 1) * 3 + r] << 16);
-                x[r] = first ? vs : vq;
-            } else {
-                x[r] = vq;
-            }
-        }
-        float w0[4], w1[4];
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            w0[i] = bf2f(conv_w[gcol * 4 + i]);
-            w1[i] = bf2f(conv_w[(gcol + 1) * 4 + i]);
-        }
-        // conv sums, then SiLU through the fp32 fast path; the few results it
-        // cannot vouch for come from the bf16-code table, all gathered after
+    for (int it = tid; it < (DV / 2) * (C / TG); it += 256) {
+        const int n0 = 2 * (it % (DV / 2)), tg = (it / (DV / 2)) * TG;
         uint16_t c0[TG], c1[TG];
-        uint32_t redo = 0;
+        conv_codes16(qkv, cd, 2 * kd + (size_t)h * DV + n0, P, tg, first, cst, conv_w, silu_bf,
+                     c0, c1);
+        // rows n0, n0 + 1 of Vt
 #pragma unroll
-        for (int j = 0; j < TG; j++) {
-            const uint32_t cc = conv_sum4_pair(w0, w1, x[j], x[j + 1], x[j + 2], x[j + 3]);
-            c0[j] = (uint16_t)cc;
-            c1[j] = (uint16_t)(cc >> 16);
-            bool ok0, ok1;
-            const uint16_t r0 = silu_fast(bf2f(c0[j]), ok0), r1 = silu_fast(bf2f(c1[j]), ok1);
-            redo |= (ok0 ? 0u : 1u << j) | (ok1 ? 0u : 1u << (TG + j));
-            if (ok0) c0[j] = r0;
-            if (ok1) c1[j] = r1;
-        }
-        if (redo) {
+        for (int h8 = 0; h8 < TG / 8; h8++) {
+            u16x8 a0, a1;
 #pragma unroll
-            for (int j = 0; j < TG; j++) {
-                if (redo >> j & 1u) c0[j] = silu_bf[c0[j]];
-                if (redo >> (TG + j) & 1u) c1[j] = silu_bf[c1[j]];
+            for (int j = 0; j < 8; j++) {
+                a0[j] = c0[h8 * 8 + j];
+                a1[j] = c1[h8 * 8 + j];
             }
-        }
-#pragma unroll
-        for (int j = 0; j < TG; j++)
-            if (tg + j >= P.nt) c0[j] = c1[j] = 0;
-        if (lc < 2 * DK) {                      // q or k: rows of Qc / Kc
-            uint16_t *dst = (lc < DK ? Qc : Kc) + (lc & (DK - 1));
-#pragma unroll
-            for (int j = 0; j < TG; j++)
-                *reinterpret_cast<uint32_t *>(dst + (tg + j) * CKP) = (uint32_t)c0[j] | ((uint32_t)c1[j] << 16);
-        } else {                                // v: rows n0, n0 + 1 of Vt
-            const int n0 = lc - 2 * DK;
-#pragma unroll
-            for (int h8 = 0; h8 < TG / 8; h8++) {
-                u16x8 a0, a1;
-#pragma unroll
-                for (int j = 0; j < 8; j++) {
-                    a0[j] = c0[h8 * 8 + j];
-                    a1[j] = c1[h8 * 8 + j];
-                }
-                const int t8 = tg / 8 + h8;
-                *reinterpret_cast<u16x8 *>(Vt + n0 * C + ((t8 ^ (n0 & 7)) << 3)) = a0;
-                *reinterpret_cast<u16x8 *>(Vt + (n0 + 1) * C + ((t8 ^ ((n0 + 1) & 7)) << 3)) = a1;
-            }
+            const int t8 = tg / 8 + h8;
+            *reinterpret_cast<u16x8 *>(Vt + n0 * C + ((t8 ^ (n0 & 7)) << 3)) = a0;
+            *reinterpret_cast<u16x8 *>(Vt + (n0 + 1) * C + ((t8 ^ ((n0 + 1) & 7)) << 3)) = a1;
         }
     }
+    if (tid < 2 * C) (tid < C ? rq : rk)[tid & (C - 1)] = QKR[ku * 2 * C + tid];
     __syncthreads();
-    if (tid < 2 * C) {                          // l2norm factors, one lane per row
-        const int t = tid & (C - 1);
-        const float f = t < P.nt ? 1.0f / sqrtf(row_sumsq((tid < C ? Qc : Kc) + t * CKP) + kL2Eps) : 0.0f;
-        if (tid < C) rq[t] = f * qscale;
-        else rk[t] = f;
-    }
-    __syncthreads();
-    if (wqk) {
-        // the scan's Q (rows t, 8 consecutive dims a piece) and K (dim i,
-        // 8 consecutive keys a piece) as code planes
-#pragma unroll
-        for (int u = 0; u < C * DK / 8 / 256; u++) {
-            const int e = tid + 256 * u;
-            {
-                const int t = e / (DK / 8), c0 = (e % (DK / 8)) * 8;
-                *reinterpret_cast<u16x8 *>(Qpu + bx1_a_index(t, c0, DK / 32)) =
-                    *reinterpret_cast<const u16x8 *>(Qc + t * CKP + c0);
-            }
-            {
-                const int i = e % DK, s0 = (e / DK) * 8;
-                u16x8 x;
-#pragma unroll
-                for (int j = 0; j < 8; j++) x[j] = Kc[(s0 + j) * CKP + i];
-                *reinterpret_cast<u16x8 *>(Kpu + bx1_b_index(s0, i)) = x;
-            }
-        }
-    }
     if (tid < C) {                     // gamma_t = g_0 + .. + g_t, in token order
         float acc = 0.0f;
         for (int t = 0; t <= tid; t++) acc = acc + graw_s[t];
@@ -431,9 +512,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void k
     // products on the bf16 MFMA 16x16x32 (lane: row / column r16,
     // reduction indices g8 .. g8+7; result rows kq .. kq+3)
     const int r16 = lane & 15, kq = (lane >> 4) * 4, g8 = (lane >> 4) * 8;
-    // Q K^T, row block 3-w: A = decayed lower triangle, to global. The
-    // product is formed transposed (K Q^T) so each lane holds 4 consecutive
-    // key columns s of one row t: 4 hi and 4 lo codes, two 8-byte stores.
+    // Q K^T (from k_gdn_chunk_qk), row block 3-w: A = decayed lower
+    // triangle, to global. The product was formed transposed (K Q^T) so
+    // each lane holds 4 consecutive key columns s of one row t: 4 hi and 4
+    // lo codes, two 8-byte stores.
     uint16_t *A = Ab + (size_t)unit * C * C * 2;
     {
         typedef unsigned short u16x4_t __attribute__((ext_vector_type(4)));
@@ -456,16 +538,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void k
             const float z[4] = {0.f, 0.f, 0.f, 0.f};
             put4((rb + 1) * 16 + kq, z);
         }
-        u16x8 qf[DK / 32];
-#pragma unroll
-        for (int ks = 0; ks < DK / 32; ks++) qf[ks] = ld8(Qc + t * CKP + ks * 32 + g8);
         const float qt = rq[t];
         for (int cb = 0; cb <= rb; cb++) {
-            f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-            for (int ks = 0; ks < DK / 32; ks++)
-                acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-                    as_bf(ld8(Kc + (cb * 16 + r16) * CKP + ks * 32 + g8)), as_bf(qf[ks]), acc, 0, 0, 0);
+            const f32x4 acc = *reinterpret_cast<const f32x4 *>(QKt + qk_tile(ku, 0, rb, cb, lane));
             float v[4];
 #pragma unroll
             for (int i = 0; i < 4; i++) {
@@ -475,32 +550,16 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void k
             put4(cb * 16 + kq, v);
         }
     }
-    // K K^T, row block w, kept in registers until Q's LDS copy is free
-    f32x4 g[4];
-    {
-        u16x8 kw[DK / 32];
-#pragma unroll
-        for (int ks = 0; ks < DK / 32; ks++) kw[ks] = ld8(Kc + (wave * 16 + r16) * CKP + ks * 32 + g8);
-#pragma unroll
-        for (int cb = 0; cb < 4; cb++) {
-            g[cb] = f32x4{0.f, 0.f, 0.f, 0.f};
-            if (cb <= wave) {
-#pragma unroll
-                for (int ks = 0; ks < DK / 32; ks++)
-                    g[cb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-                        as_bf(kw[ks]), as_bf(ld8(Kc + (cb * 16 + r16) * CKP + ks * 32 + g8)), g[cb], 0, 0, 0);
-            }
-        }
-    }
-    __syncthreads();                   // every reader of the q codes is done
+    // K K^T (from k_gdn_chunk_qk), row block w: L
 #pragma unroll
     for (int cb = 0; cb < 4; cb++) {
         if (cb <= wave) {
+            const f32x4 gk = *reinterpret_cast<const f32x4 *>(QKt + qk_tile(ku, 1, wave, cb, lane));
             const int s = cb * 16 + r16;
 #pragma unroll
             for (int i = 0; i < 4; i++) {
                 const int t = wave * 16 + kq + i;
-                Ls[t * CP + s] = s < t ? bet[t] * (exp_fast(gam[t] - gam[s]) * ((rk[t] * rk[s]) * g[cb][i])) : 0.0f;
+                Ls[t * CP + s] = s < t ? bet[t] * (exp_fast(gam[t] - gam[s]) * ((rk[t] * rk[s]) * gk[i])) : 0.0f;
             }
         }
     }
@@ -588,7 +647,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void k
     for (int rt = 0; rt < 4; rt++)
 #pragma unroll
         for (int ct = 0; ct < 4; ct++) xacc[rt][ct] = f32x4{0.f, 0.f, 0.f, 0.f};
-    // R = [diag(b) V | diag(b G rk) Kc] with V and Kc exact codes: a
+    // R = [diag(b) V | diag(b G rk) K] with V and K exact codes: a
     // wavefront's 64 columns are of one kind, so its T operand carries that
     // kind's row factors (T diag(f), split hi/lo) and the codes are the B
     // operand as they are: two MFMAs per product
@@ -613,8 +672,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void k
             if (isv) {
                 bc[ct] = ld8(Vt + n * C + (((k0 >> 3) ^ (n & 7)) << 3));
             } else {
-#pragma unroll
-                for (int j = 0; j < 8; j++) bc[ct][j] = Kc[(k0 + j) * CKP + (n - DV)];
+                bc[ct] = ld8(Kpu + bx1_b_index(k0, n - DV));   // keys k0 .. k0+7 of dim n - DV
             }
         }
 #pragma unroll
@@ -913,6 +971,7 @@ struct PrefillWs {
     GdnScratch w;
     float *Ub = nullptr, *Fb = nullptr;
     uint16_t *Wb = nullptr, *Ab = nullptr, *Qp = nullptr, *Kp = nullptr;
+    float *QKt = nullptr, *QKR = nullptr;
     int32_t *meta = nullptr;
     size_t bytes = 0;
 };
@@ -933,6 +992,8 @@ static PrefillWs prefill_ws_carve(char *base, size_t Ttot, size_t nch, size_t B,
     p.Fb = (float *)take(units * 3 * C * 4);
     p.Qp = (uint16_t *)take(nch * hk * C * DK * 2);
     p.Kp = (uint16_t *)take(nch * hk * C * DK * 2);
+    p.QKt = (float *)take(nch * hk * 2 * kQkTiles * 64 * 4 * 4);
+    p.QKR = (float *)take(nch * hk * 2 * C * 4);
     p.meta = (int32_t *)take(2 * (B + 1) * 4);
     p.bytes = off;
     return p;
@@ -1027,12 +1088,20 @@ static int gdn_prefill_run(const ApusHipGdnLayer *L, size_t B, const int32_t *cu
     float *Fb = ws ? pw.Fb : (float *)scratch(kScratchGdnChunk5, units * 3 * C * 4);
     uint16_t *Qp = ws ? pw.Qp : (uint16_t *)scratch(kScratchGdnChunk6, nch * L->hk * C * DK * 2);
     uint16_t *Kp = ws ? pw.Kp : (uint16_t *)scratch(kScratchGdnChunk7, nch * L->hk * C * DK * 2);
-    if (!Ub || !Wb || !Ab || !Fb || !Qp || !Kp) return kErrHip;
+    float *QKt = ws ? pw.QKt
+                    : (float *)scratch(kScratchGdnChunk8, nch * L->hk * 2 * kQkTiles * 64 * 4 * 4);
+    float *QKR = ws ? pw.QKR : (float *)scratch(kScratchGdnChunk9, nch * L->hk * 2 * C * 4);
+    if (!Ub || !Wb || !Ab || !Fb || !Qp || !Kp || !QKt || !QKR) return kErrHip;
+    APUS_TIMED("k_gdn_chunk_qk",
+               k_gdn_chunk_qk<<<(unsigned)(nch * L->hk), 512, 0, stream()>>>(
+        sq, kmeta, qkv, L->conv_w, conv_state, slots, tabs->silu_bf, Qp, Kp, QKt, QKR,
+        (int)L->hk, (float)pow((double)L->dk, -0.5)));
+    APUS_LAUNCHED("k_gdn_chunk_qk");
     APUS_TIMED("k_gdn_chunk_wy",
                k_gdn_chunk_wy<<<(unsigned)units, 256, 0, stream()>>>(
         sq, kmeta, qkv, a, b, L->conv_w, L->A_log, L->dt_bias, conv_state, slots,
-        tabs->silu_bf, tabs->sig_bf, Ub, Wb, Ab, Fb, Qp, Kp, (int)L->hk,
-        units % 16 == 0 ? 1 : 0, (float)pow((double)L->dk, -0.5)));
+        tabs->silu_bf, tabs->sig_bf, Ub, Wb, Ab, Fb, Kp, QKt, QKR, (int)L->hk,
+        units % 16 == 0 ? 1 : 0));
     APUS_LAUNCHED("k_gdn_chunk_wy");
     APUS_TIMED("k_gdn_chunk_scan",
                k_gdn_chunk_scan<<<(unsigned)(B * L->hv * NCB), 512, 0, stream()>>>(
