@@ -55,8 +55,7 @@ enum ScratchSlot { kScratchIn = 0, kScratchIn2, kScratchIn3, kScratchIn4,
                    kScratchGdnQK, kScratchGdnQKR, kScratchGdnV, kScratchGdnGate, kScratchGdnOB,
                    kScratchGdnChunk, kScratchGdnChunk2, kScratchGdnChunk3,
                    kScratchGdnChunk4, kScratchGdnChunk5,
-                   kScratchGdnChunk6, kScratchGdnChunk7, kScratchGdnChunk8,
-                   kScratchGdnChunk9,
+                   kScratchGdnChunk6, kScratchGdnChunk7,
                    // batched attention mixer intermediates
                    kScratchAttnQ, kScratchAttnA, kScratchAttnStat,
                    kScratchAttnPart,

@@ -20,11 +20,11 @@
 // real rows unchanged, so ragged sequences need no special case.
 //
 // Kernels (before k_gdn_post of gdn_mixer.hip):
-//   k_gdn_chunk_qk    one workgroup per (chunk, K head): the q, k conv
-//                     codes, l2norm factors, K K^T and Q K^T.
-//   k_gdn_chunk_wy    one workgroup per (chunk, v-head), all chunks in
-//                     parallel: the v codes and gates, L and A with their
-//                     decay factors, then U and W as T [b V | b G K] with
+//   k_gdn_chunk_wy    one workgroup per (chunk, K head), all chunks in
+//                     parallel: the q, k, v conv codes, gates and l2norm
+//                     factors, K K^T and Q K^T once for the K head's two
+//                     v-heads, then per v-head L and A with their decay
+//                     factors and U and W as T [b V | b G K] with
 //                     T = (I+L)^-1 built in 32x32 blocks.
 //   k_gdn_chunk_scan  one workgroup per (sequence, v-head, 16-column block
 //                     of S): the delta rule is separable by value column,
@@ -221,10 +221,9 @@ __device__ __forceinline__ void split8(const float (&x)[8], u16x8 &hi, u16x8 &lo
 // The normalised rows are q_t = rq_t qscale cq_t and k_s = rk_s ck_s with
 // cq, ck the conv codes, so q.k and k.k are the factors times the exact
 // dot products of the codes: one bf16 MFMA per product, fp32
-// accumulation, no operand splitting. k_gdn_chunk_qk forms the codes,
-// factors and products once per (chunk, K head); k_gdn_chunk_wy, one
-// workgroup per (chunk, v-head) and up to three per CU, forms the v codes
-// and gates of its head from the layer inputs and the rest of the WY form.
+// accumulation, no operand splitting. k_gdn_chunk_wy forms the codes of a
+// (chunk, K head) and their products once; per (chunk, v-head) work runs on
+// half of its wavefronts each.
 constexpr int CKP = DK + 8;            // bf16 row stride of the code copies
 
 // Two channels' 4-tap conv sums (tap order, one rounding per mul and add,
@@ -308,28 +307,15 @@ __device__ __forceinline__ void conv_codes16(const uint16_t *__restrict__ qkv, s
         if (tg + j >= P.nt) c0[j] = c1[j] = 0;
 }
 
-// Q K^T and K K^T of a (chunk, K head) as the MFMA left them: the 10 lower
-// 16x16 tiles (rb, cb <= rb) of each, tile index rb (rb + 1) / 2 + cb,
-// 64 lanes x 4 floats a tile. Q K^T is formed transposed (K Q^T: lane
-// (g, r) holds keys s = 16 cb + 4 g .. +3 of row t = 16 rb + r); K K^T
-// lane (g, r) holds rows t = 16 rb + 4 g .. +3 of key s = 16 cb + r.
-constexpr int kQkTiles = 10;
-__device__ __forceinline__ size_t qk_tile(size_t ku, int which, int rb, int cb, int lane) {
-    return (((ku * 2 + which) * kQkTiles + rb * (rb + 1) / 2 + cb) * 64 + lane) * 4;
-}
-
-// k_gdn_chunk_qk: one workgroup per (chunk, K head). The q and k conv+SiLU
-// codes of the chunk (formed once per K head: both of its v-heads use
-// them), their l2norm factors (rq with the 1/sqrt(dk) query scale, rk:
-// QKR[(chunk, K head)][2C]), the scan's code planes Q and K, and the
-// v-head-independent products Q K^T and K K^T on the codes (one MFMA per
-// product, qk_tile layout) for k_gdn_chunk_wy.
-__global__ __launch_bounds__(512) void k_gdn_chunk_qk(
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void k_gdn_chunk_wy(
     ChunkSeqs sq, const int32_t *__restrict__ dmeta, const uint16_t *__restrict__ qkv,
-    const uint16_t *__restrict__ conv_w, const uint16_t *__restrict__ conv_state,
+    const uint16_t *__restrict__ a, const uint16_t *__restrict__ b,
+    const uint16_t *__restrict__ conv_w, const float *__restrict__ A_log,
+    const float *__restrict__ dt_bias, const uint16_t *__restrict__ conv_state,
     const int32_t *__restrict__ slots, const uint16_t *__restrict__ silu_bf,
-    uint16_t *__restrict__ Qp, uint16_t *__restrict__ Kp, float *__restrict__ QKt,
-    float *__restrict__ QKR, int hk, float qscale) {
+    const uint16_t *__restrict__ sig_bf, float *__restrict__ Ub,
+    uint16_t *__restrict__ Wb, uint16_t *__restrict__ Ab, float *__restrict__ Fb,
+    uint16_t *__restrict__ Qp, uint16_t *__restrict__ Kp, int hk, float qscale) {
     const int hv = hk * REP;
     const size_t kd = (size_t)hk * DK, vd = (size_t)hv * DV, cd = 2 * kd + vd;
     const int ku = blockIdx.x, ci = ku / hk, kh = ku % hk;
@@ -338,26 +324,91 @@ __global__ __launch_bounds__(512) void k_gdn_chunk_qk(
     const ChunkPos P = chunk_pos(cu, coff, sq.n, ci);
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    __shared__ __attribute__((aligned(16))) uint16_t Qc[C * CKP], Kc[C * CKP];
+    // wavefronts 4 grp .. 4 grp + 3 work on v-head 2 kh + grp (unit unitg)
+    // once the q, k work is done
+    const int grp = wave >> 2, gw = wave & 3, gtid = tid & 255;
+    const int unitg = ci * hv + kh * REP + grp;
+
+    // LDS (two workgroups per CU): the q and k codes (rows t, CKP pitch),
+    // then the V codes of each v-head transposed ([column][token]: the B
+    // operand of T R; the 16-byte pieces of row n XOR-swizzled by n % 8, so
+    // the MFMA operand reads spread over the banks). L of each v-head
+    // replaces the codes once the products are formed; W's staging of each
+    // v-head replaces L and V once T R is done.
+    constexpr int QC_B = C * CKP * 2, L_B = C * CP * 4, W_B = C * KP * 4, V_B = DV * C * 2;
+    static_assert(L_B <= QC_B, "L does not fit over the codes");
+    static_assert(2 * W_B <= 2 * QC_B + 2 * V_B, "W's staging does not fit over L and V");
+    __shared__ __attribute__((aligned(16))) char wy_lds[2 * QC_B + 2 * V_B];
+    uint16_t *Qc = reinterpret_cast<uint16_t *>(wy_lds);
+    uint16_t *Kc = reinterpret_cast<uint16_t *>(wy_lds + QC_B);
+    float *Lg = reinterpret_cast<float *>(wy_lds + grp * QC_B);
+    uint16_t *Vg = reinterpret_cast<uint16_t *>(wy_lds + 2 * QC_B + grp * V_B);
+    __shared__ float graw_s[REP][C], gam[REP][C], bet[REP][C], Gs[REP][C], rq[C], rk[C];
+    const float *betg = bet[grp], *Gsg = Gs[grp];
+
+    // ---- the token-parallel front (c/layer.h:427-492 up to the
+    // recurrence) for this chunk and K head: causal conv1d k=4 + SiLU
+    // (c/gdn.h:19-33, 220-228) of the q, k channels of K head kh and the v
+    // channels of its two v-heads, the l2norm factors (c/gdn.h:402-416) and
+    // the gates (c/gdn.h:34-40). Work items are (two adjacent channels, 16
+    // tokens): 512 of q|k, then 256 of v per v-head, two per thread. The
+    // gates of padding rows (t >= nt) are 0.
     const bool first = ci == coff[P.s];
     const uint16_t *cst = conv_state + (size_t)(slots ? slots[P.s] : P.s) * cd * 3;
-    // work items: (two adjacent channels of the 2 DK q|k channels, 16
-    // tokens), one per thread
-    for (int it = tid; it < DK * (C / TG); it += 512) {
-        const int lc = 2 * (it % DK), tg = (it / DK) * TG;
-        const size_t gcol = lc < DK ? (size_t)kh * DK + lc : kd + (size_t)kh * DK + (lc - DK);
+    if (tid < REP * C) {                        // the gates of token t, v-head 2 kh + g
+        const int g = tid / C, t = tid % C, h = kh * REP + g;
+        float gg = 0.0f, bt = 0.0f;
+        if (t < P.nt) {
+            const size_t i = (size_t)(P.t0 + t) * hv + h;
+            gg = decay_of(a[i], A_log[h], dt_bias[h]);
+            bt = bf2f(sig_bf[b[i]]);
+        }
+        graw_s[g][t] = gg;
+        bet[g][t] = bt;
+    }
+    for (int it = tid; it < 2 * DK * (C / TG) / 2 + REP * (DV / 2) * (C / TG); it += 512) {
         uint16_t c0[TG], c1[TG];
-        conv_codes16(qkv, cd, gcol, P, tg, first, cst, conv_w, silu_bf, c0, c1);
-        uint16_t *dst = (lc < DK ? Qc : Kc) + (lc & (DK - 1));
+        if (it < DK * (C / TG)) {               // q | k channels 2 lc, 2 lc + 1
+            const int lc = 2 * (it % DK), tg = (it / DK) * TG;
+            const size_t gcol = lc < DK ? (size_t)kh * DK + lc : kd + (size_t)kh * DK + (lc - DK);
+            conv_codes16(qkv, cd, gcol, P, tg, first, cst, conv_w, silu_bf, c0, c1);
+            uint16_t *dst = (lc < DK ? Qc : Kc) + (lc & (DK - 1));
 #pragma unroll
-        for (int j = 0; j < TG; j++)
-            *reinterpret_cast<uint32_t *>(dst + (tg + j) * CKP) = (uint32_t)c0[j] | ((uint32_t)c1[j] << 16);
+            for (int j = 0; j < TG; j++)
+                *reinterpret_cast<uint32_t *>(dst + (tg + j) * CKP) =
+                    (uint32_t)c0[j] | ((uint32_t)c1[j] << 16);
+        } else {                                // v channels n0, n0 + 1 of v-head 2 kh + g
+            const int iv = it - DK * (C / TG), g = iv / ((DV / 2) * (C / TG));
+            const int jv = iv % ((DV / 2) * (C / TG));
+            const int n0 = 2 * (jv % (DV / 2)), tg = (jv / (DV / 2)) * TG;
+            conv_codes16(qkv, cd, 2 * kd + (size_t)(kh * REP + g) * DV + n0, P, tg, first, cst,
+                         conv_w, silu_bf, c0, c1);
+            uint16_t *V = reinterpret_cast<uint16_t *>(wy_lds + 2 * QC_B + g * V_B);
+#pragma unroll
+            for (int h8 = 0; h8 < TG / 8; h8++) {
+                u16x8 a0, a1;
+#pragma unroll
+                for (int j = 0; j < 8; j++) {
+                    a0[j] = c0[h8 * 8 + j];
+                    a1[j] = c1[h8 * 8 + j];
+                }
+                const int t8 = tg / 8 + h8;
+                *reinterpret_cast<u16x8 *>(V + n0 * C + ((t8 ^ (n0 & 7)) << 3)) = a0;
+                *reinterpret_cast<u16x8 *>(V + (n0 + 1) * C + ((t8 ^ ((n0 + 1) & 7)) << 3)) = a1;
+            }
+        }
     }
     __syncthreads();
     if (tid < 2 * C) {                          // l2norm factors, one lane per row
         const int t = tid & (C - 1);
         const float f = t < P.nt ? 1.0f / sqrtf(row_sumsq((tid < C ? Qc : Kc) + t * CKP) + kL2Eps) : 0.0f;
-        QKR[(size_t)ku * 2 * C + tid] = tid < C ? f * qscale : f;
+        if (tid < C) rq[t] = f * qscale;
+        else rk[t] = f;
+    } else if (tid >= 256 && tid < 256 + REP * C) {   // gamma_t = g_0 + .. + g_t, in token order
+        const int g = (tid - 256) / C, t = (tid - 256) % C;
+        float acc = 0.0f;
+        for (int u = 0; u <= t; u++) acc = acc + graw_s[g][u];
+        gam[g][t] = acc;
     }
     // the scan's Q (rows t, 8 consecutive dims a piece) and K (dim i, 8
     // consecutive keys a piece) as code planes
@@ -378,149 +429,32 @@ __global__ __launch_bounds__(512) void k_gdn_chunk_qk(
             *reinterpret_cast<u16x8 *>(Kpu + bx1_b_index(s0, i)) = x;
         }
     }
-    // products on the bf16 MFMA 16x16x32 (lane: row / column r16, reduction
-    // indices g8 .. g8+7): wavefront w < 4 takes row block 3 - w of Q K^T,
-    // wavefront 4 + w row block w of K K^T
-    const int r16 = lane & 15, g8 = (lane >> 4) * 8;
-    if (wave < 4) {
-        const int rb = 3 - wave;
-        u16x8 qf[DK / 32];
-#pragma unroll
-        for (int ks = 0; ks < DK / 32; ks++) qf[ks] = ld8(Qc + (rb * 16 + r16) * CKP + ks * 32 + g8);
-        for (int cb = 0; cb <= rb; cb++) {
-            f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-            for (int ks = 0; ks < DK / 32; ks++)
-                acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-                    as_bf(ld8(Kc + (cb * 16 + r16) * CKP + ks * 32 + g8)), as_bf(qf[ks]), acc, 0, 0, 0);
-            *reinterpret_cast<f32x4 *>(QKt + qk_tile(ku, 0, rb, cb, lane)) = acc;
-        }
-    } else {
-        const int rb = wave - 4;
-        u16x8 kw[DK / 32];
-#pragma unroll
-        for (int ks = 0; ks < DK / 32; ks++) kw[ks] = ld8(Kc + (rb * 16 + r16) * CKP + ks * 32 + g8);
-        for (int cb = 0; cb <= rb; cb++) {
-            f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-            for (int ks = 0; ks < DK / 32; ks++)
-                acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-                    as_bf(kw[ks]), as_bf(ld8(Kc + (cb * 16 + r16) * CKP + ks * 32 + g8)), acc, 0, 0, 0);
-            *reinterpret_cast<f32x4 *>(QKt + qk_tile(ku, 1, rb, cb, lane)) = acc;
-        }
-    }
-}
-
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void k_gdn_chunk_wy(
-    ChunkSeqs sq, const int32_t *__restrict__ dmeta, const uint16_t *__restrict__ qkv,
-    const uint16_t *__restrict__ a, const uint16_t *__restrict__ b,
-    const uint16_t *__restrict__ conv_w, const float *__restrict__ A_log,
-    const float *__restrict__ dt_bias, const uint16_t *__restrict__ conv_state,
-    const int32_t *__restrict__ slots, const uint16_t *__restrict__ silu_bf,
-    const uint16_t *__restrict__ sig_bf, float *__restrict__ Ub,
-    uint16_t *__restrict__ Wb, uint16_t *__restrict__ Ab, float *__restrict__ Fb,
-    const uint16_t *__restrict__ Kp, const float *__restrict__ QKt,
-    const float *__restrict__ QKR, int hk, int pair_map) {
-    const int hv = hk * REP;
-    const size_t kd = (size_t)hk * DK, vd = (size_t)hv * DV;
-    // unit = ci * hv + h. With pair_map the two v-heads of one K head (units
-    // 2P, 2P+1) run as blocks 8 apart: blocks are dealt round-robin over the
-    // 8 XCDs, so both land on one XCD and the second reads the K head's
-    // products and codes from its L2.
-    int unit = blockIdx.x;
-    if (pair_map) {
-        const int b = blockIdx.x;
-        unit = ((b >> 4) * 8 + (b & 7)) * 2 + ((b >> 3) & 1);
-    }
-    const int ci = unit / hv, h = unit % hv, kh = h / REP;
-    const size_t ku = (size_t)ci * hk + kh;     // the (chunk, K head) of k_gdn_chunk_qk
-    const uint16_t *Kpu = Kp + ku * C * DK;
-    const int32_t *cu = dmeta ? dmeta : sq.cu;
-    const int32_t *coff = dmeta ? dmeta + sq.n + 1 : sq.coff;
-    const ChunkPos P = chunk_pos(cu, coff, sq.n, ci);
-    const int tid = threadIdx.x, lane = tid & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-
-    // LDS: L (later W's staging), the V codes transposed ([column][token]:
-    // the B operand of T R; the 16-byte pieces of row n XOR-swizzled by
-    // n % 8, so the MFMA operand reads spread over the banks), per-token
-    // factors (three workgroups per CU)
-    constexpr int W_B = C * KP * 4, L_B = C * CP * 4;
-    static_assert(W_B >= L_B, "L does not fit in W's staging");
-    __shared__ __attribute__((aligned(16))) char wy_lds[W_B + DV * C * 2];
-    float *Ls = reinterpret_cast<float *>(wy_lds);
-    uint16_t *Vt = reinterpret_cast<uint16_t *>(wy_lds + W_B);
-    __shared__ float graw_s[C], gam[C], bet[C], Gs[C], rq[C], rk[C];
-
-    // ---- the token-parallel front (c/layer.h:427-492 up to the
-    // recurrence) for this chunk and v-head: causal conv1d k=4 + SiLU of the
-    // v channels of head h (c/gdn.h:19-33, 220-228) and the gates
-    // (c/gdn.h:34-40); the q, k codes, their l2norm factors (c/gdn.h:402-416)
-    // and their products come from k_gdn_chunk_qk. Work items are (two
-    // adjacent v channels, 16 tokens), one per thread; the gates of padding
-    // rows (t >= nt) are 0.
-    const size_t cd = 2 * kd + vd;
-    const bool first = ci == coff[P.s];
-    const uint16_t *cst = conv_state + (size_t)(slots ? slots[P.s] : P.s) * cd * 3;
-    if (tid < C) {                              // the gates of token tid
-        float g = 0.0f, bt = 0.0f;
-        if (tid < P.nt) {
-            const size_t i = (size_t)(P.t0 + tid) * hv + h;
-            g = decay_of(a[i], A_log[h], dt_bias[h]);
-            bt = bf2f(sig_bf[b[i]]);
-        }
-        graw_s[tid] = g;
-        bet[tid] = bt;
-    }
-    for (int it = tid; it < (DV / 2) * (C / TG); it += 256) {
-        const int n0 = 2 * (it % (DV / 2)), tg = (it / (DV / 2)) * TG;
-        uint16_t c0[TG], c1[TG];
-        conv_codes16(qkv, cd, 2 * kd + (size_t)h * DV + n0, P, tg, first, cst, conv_w, silu_bf,
-                     c0, c1);
-        // rows n0, n0 + 1 of Vt
-#pragma unroll
-        for (int h8 = 0; h8 < TG / 8; h8++) {
-            u16x8 a0, a1;
-#pragma unroll
-            for (int j = 0; j < 8; j++) {
-                a0[j] = c0[h8 * 8 + j];
-                a1[j] = c1[h8 * 8 + j];
-            }
-            const int t8 = tg / 8 + h8;
-            *reinterpret_cast<u16x8 *>(Vt + n0 * C + ((t8 ^ (n0 & 7)) << 3)) = a0;
-            *reinterpret_cast<u16x8 *>(Vt + (n0 + 1) * C + ((t8 ^ ((n0 + 1) & 7)) << 3)) = a1;
-        }
-    }
-    if (tid < 2 * C) (tid < C ? rq : rk)[tid & (C - 1)] = QKR[ku * 2 * C + tid];
     __syncthreads();
-    if (tid < C) {                     // gamma_t = g_0 + .. + g_t, in token order
-        float acc = 0.0f;
-        for (int t = 0; t <= tid; t++) acc = acc + graw_s[t];
-        gam[tid] = acc;
-    }
-    __syncthreads();
-    // F: the output scale G_t rq_t, the state-update scale
+    // F of each v-head: the output scale G_t rq_t, the state-update scale
     // exp(gamma_C - gamma_s) rk_s, and G_C
-    float *F = Fb + (size_t)unit * 3 * C;
-    if (tid < C) {
-        Gs[tid] = exp_fast(gam[tid]);
-        F[tid] = Gs[tid] * rq[tid];
-        F[C + tid] = exp_fast(gam[C - 1] - gam[tid]) * rk[tid];
-        F[2 * C + tid] = tid == 0 ? exp_fast(gam[C - 1]) : 0.0f;
+    if (tid < REP * C) {
+        const int g = tid / C, t = tid % C;
+        float *F = Fb + (size_t)(ci * hv + kh * REP + g) * 3 * C;
+        Gs[g][t] = exp_fast(gam[g][t]);
+        F[t] = Gs[g][t] * rq[t];
+        F[C + t] = exp_fast(gam[g][C - 1] - gam[g][t]) * rk[t];
+        F[2 * C + t] = t == 0 ? exp_fast(gam[g][C - 1]) : 0.0f;
     }
 
-    // products on the bf16 MFMA 16x16x32 (lane: row / column r16,
-    // reduction indices g8 .. g8+7; result rows kq .. kq+3)
+    // products on the bf16 MFMA 16x16x32 on the codes (lane: row / column
+    // r16, reduction indices g8 .. g8+7; result rows kq .. kq+3). Each
+    // group of four wavefronts forms them for its v-head: wavefront gw takes
+    // row block 3 - gw of Q K^T and row block gw of K K^T (5 tiles each; the
+    // MFMAs are repeated per group, the decay and gate factors differ).
     const int r16 = lane & 15, kq = (lane >> 4) * 4, g8 = (lane >> 4) * 8;
-    // Q K^T (from k_gdn_chunk_qk), row block 3-w: A = decayed lower
-    // triangle, to global. The product was formed transposed (K Q^T) so
-    // each lane holds 4 consecutive key columns s of one row t: 4 hi and 4
-    // lo codes, two 8-byte stores.
-    uint16_t *A = Ab + (size_t)unit * C * C * 2;
     {
+        // Q K^T: A = decayed lower triangle, to global. The product is
+        // formed transposed (K Q^T) so each lane holds 4 consecutive key
+        // columns s of one row t: 4 hi and 4 lo codes, two 8-byte stores.
         typedef unsigned short u16x4_t __attribute__((ext_vector_type(4)));
-        const int rb = 3 - wave;
+        const int rb = 3 - gw;
         const int t = rb * 16 + r16;
+        uint16_t *A = Ab + (size_t)unitg * C * C * 2;
         auto put4 = [&](int s0, const float (&v)[4]) {
             u16x4_t hi, lo;
 #pragma unroll
@@ -538,44 +472,63 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void k
             const float z[4] = {0.f, 0.f, 0.f, 0.f};
             put4((rb + 1) * 16 + kq, z);
         }
+        u16x8 qf[DK / 32];
+#pragma unroll
+        for (int ks = 0; ks < DK / 32; ks++) qf[ks] = ld8(Qc + t * CKP + ks * 32 + g8);
         const float qt = rq[t];
+        const float *gm = gam[grp];
         for (int cb = 0; cb <= rb; cb++) {
-            const f32x4 acc = *reinterpret_cast<const f32x4 *>(QKt + qk_tile(ku, 0, rb, cb, lane));
+            f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int ks = 0; ks < DK / 32; ks++)
+                acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                    as_bf(ld8(Kc + (cb * 16 + r16) * CKP + ks * 32 + g8)), as_bf(qf[ks]), acc, 0, 0, 0);
             float v[4];
 #pragma unroll
             for (int i = 0; i < 4; i++) {
                 const int s = cb * 16 + kq + i;
-                v[i] = s <= t ? exp_fast(gam[t] - gam[s]) * ((qt * rk[s]) * acc[i]) : 0.0f;
+                v[i] = s <= t ? exp_fast(gm[t] - gm[s]) * ((qt * rk[s]) * acc[i]) : 0.0f;
             }
             put4(cb * 16 + kq, v);
         }
     }
-    // K K^T (from k_gdn_chunk_qk), row block w: L
+    // K K^T, row block gw: L, kept in registers until every reader of the
+    // codes is done, then written over them
+    float lv[4][4];
+    {
+        const float *gm = gam[grp];
+        u16x8 kw[DK / 32];
 #pragma unroll
-    for (int cb = 0; cb < 4; cb++) {
-        if (cb <= wave) {
-            const f32x4 gk = *reinterpret_cast<const f32x4 *>(QKt + qk_tile(ku, 1, wave, cb, lane));
-            const int s = cb * 16 + r16;
+        for (int ks = 0; ks < DK / 32; ks++) kw[ks] = ld8(Kc + (gw * 16 + r16) * CKP + ks * 32 + g8);
 #pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const int t = wave * 16 + kq + i;
-                Ls[t * CP + s] = s < t ? bet[t] * (exp_fast(gam[t] - gam[s]) * ((rk[t] * rk[s]) * gk[i])) : 0.0f;
+        for (int cb = 0; cb < 4; cb++) {
+            if (cb <= gw) {
+                f32x4 gk = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int ks = 0; ks < DK / 32; ks++)
+                    gk = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                        as_bf(kw[ks]), as_bf(ld8(Kc + (cb * 16 + r16) * CKP + ks * 32 + g8)), gk, 0, 0, 0);
+                const int s = cb * 16 + r16;
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const int t = gw * 16 + kq + i;
+                    lv[cb][i] = s < t ? betg[t] * (exp_fast(gm[t] - gm[s]) * ((rk[t] * rk[s]) * gk[i])) : 0.0f;
+                }
             }
         }
     }
+    __syncthreads();                   // every reader of the codes is done
+#pragma unroll
+    for (int cb = 0; cb < 4; cb++)
+        if (cb <= gw)
+#pragma unroll
+            for (int i = 0; i < 4; i++) Lg[(gw * 16 + kq + i) * CP + cb * 16 + r16] = lv[cb][i];
     __syncthreads();
 
-    // X = (I + L)^-1 R for the 256 right-hand-side columns R = [b V | b G K]
-    // as T R, T = (I + L)^-1, in 32x32 blocks: T00 = (I + L00)^-1 and T11 =
-    // (I + L11)^-1 by substitution (wavefront w < 2, lane j < 32 substitutes
-    // the unit vector e_j: x_t = e_j[t] - sum_{s<t} L[t][s] x_s, four partial
-    // sums shortening the dependent chain), written over their L blocks;
-    // then T10 = -T11 (L10 T00) as two split-precision MFMA products (the
-    // intermediate in the unused upper-right block), and T R on the MFMA
-    // (T's blocks above the diagonal are skipped).
+    // ---- per v-head (wavefronts 4 grp .. 4 grp + 3)
     constexpr int H = C / 2;
-    if (wave < 2) {
-        const int o = wave * H;                  // this diagonal block's first row / column
+    if (gw < 2) {
+        const int o = gw * H;                  // this diagonal block's first row / column
         float x[H];
 #pragma unroll
         for (int t = 0; t < H; t++) x[t] = t == lane ? 1.0f : 0.0f;
@@ -584,7 +537,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void k
             float p0 = 0.f, p1 = 0.f, p2 = 0.f, p3 = 0.f;
 #pragma unroll
             for (int s0 = 0; s0 < t; s0 += 4) {
-                const float4 l4 = lds4(Ls + (o + t) * CP + o + s0);
+                const float4 l4 = lds4(Lg + (o + t) * CP + o + s0);
                 p0 = fmaf(l4.x, x[s0], p0);
                 if (s0 + 1 < t) p1 = fmaf(l4.y, x[s0 + 1], p1);
                 if (s0 + 2 < t) p2 = fmaf(l4.z, x[s0 + 2], p2);
@@ -595,52 +548,52 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void k
         // (this wavefront's reads of L are all issued: DS operations run in order)
         if (lane < H) {
 #pragma unroll
-            for (int t = 0; t < H; t++) Ls[(o + t) * CP + o + lane] = x[t];
+            for (int t = 0; t < H; t++) Lg[(o + t) * CP + o + lane] = x[t];
         }
     }
     __syncthreads();
     {
         // wavefront w: output tile (w / 2, w % 2) of the 32x32 products
-        const int tr = (wave >> 1) * 16, tc = (wave & 1) * 16;
+        const int tr = (gw >> 1) * 16, tc = (gw & 1) * 16;
         const int rr = lane & 15, kk = (lane >> 4) * 8;
         // Y = L10 T00: A = L rows H + tr + rr, k = kk..; B = T00 column tc + rr
         u16x8 ah, al, bh, bl;
         {
-            const float4 a0 = lds4(Ls + (H + tr + rr) * CP + kk), a1 = lds4(Ls + (H + tr + rr) * CP + kk + 4);
+            const float4 a0 = lds4(Lg + (H + tr + rr) * CP + kk), a1 = lds4(Lg + (H + tr + rr) * CP + kk + 4);
             const float va[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
             split8(va, ah, al);
             float vb[8];
 #pragma unroll
-            for (int j = 0; j < 8; j++) vb[j] = Ls[(kk + j) * CP + tc + rr];
+            for (int j = 0; j < 8; j++) vb[j] = Lg[(kk + j) * CP + tc + rr];
             split8(vb, bh, bl);
         }
         f32x4 y = mfma_x3(ah, al, bh, bl, f32x4{0.f, 0.f, 0.f, 0.f});
         // Y to the upper-right block [k = row][n]: rows tr + 4(l/16) + i, column tc + rr
 #pragma unroll
-        for (int i = 0; i < 4; i++) Ls[(tr + (lane >> 4) * 4 + i) * CP + H + tc + rr] = y[i];
+        for (int i = 0; i < 4; i++) Lg[(tr + (lane >> 4) * 4 + i) * CP + H + tc + rr] = y[i];
         __syncthreads();
         // T10 = -T11 Y: A = T11 rows H + tr + rr, k = H + kk..; B = Y column tc + rr
         {
-            const float4 a0 = lds4(Ls + (H + tr + rr) * CP + H + kk), a1 = lds4(Ls + (H + tr + rr) * CP + H + kk + 4);
+            const float4 a0 = lds4(Lg + (H + tr + rr) * CP + H + kk), a1 = lds4(Lg + (H + tr + rr) * CP + H + kk + 4);
             const float va[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
             split8(va, ah, al);
             float vb[8];
 #pragma unroll
-            for (int j = 0; j < 8; j++) vb[j] = Ls[(kk + j) * CP + H + tc + rr];
+            for (int j = 0; j < 8; j++) vb[j] = Lg[(kk + j) * CP + H + tc + rr];
             split8(vb, bh, bl);
         }
         const f32x4 t10 = mfma_x3(ah, al, bh, bl, f32x4{0.f, 0.f, 0.f, 0.f});
         __syncthreads();                         // every read of L10 and Y is done
 #pragma unroll
-        for (int i = 0; i < 4; i++) Ls[(H + tr + (lane >> 4) * 4 + i) * CP + tc + rr] = -t10[i];
+        for (int i = 0; i < 4; i++) Lg[(H + tr + (lane >> 4) * 4 + i) * CP + tc + rr] = -t10[i];
         // the upper-right block back to zero (T is lower triangular; T R reads
         // only k below its row block, but keep the matrix clean)
 #pragma unroll
-        for (int i = 0; i < 4; i++) Ls[(tr + (lane >> 4) * 4 + i) * CP + H + tc + rr] = 0.0f;
+        for (int i = 0; i < 4; i++) Lg[(tr + (lane >> 4) * 4 + i) * CP + H + tc + rr] = 0.0f;
     }
     __syncthreads();
     const int g4 = kq;
-    const int cbase = wave * 64;                // this wavefront's 64 columns of R
+    const int cbase = gw * 64;                // this wavefront's 64 columns of R
     const bool isv = cbase < DV;
     f32x4 xacc[4][4];
 #pragma unroll
@@ -656,12 +609,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void k
         const int k0 = ks * 32 + g8;             // this lane's 8 reduction indices
         float f[8];
 #pragma unroll
-        for (int j = 0; j < 8; j++) f[j] = isv ? bet[k0 + j] : (bet[k0 + j] * Gs[k0 + j]) * rk[k0 + j];
+        for (int j = 0; j < 8; j++) f[j] = isv ? betg[k0 + j] : (betg[k0 + j] * Gsg[k0 + j]) * rk[k0 + j];
         u16x8 ah[4], al[4], bc[4];
 #pragma unroll
         for (int rt = 2 * ks; rt < 4; rt++) {    // T rows 16 rt + r16
-            const float4 a0 = lds4(Ls + (rt * 16 + r16) * CP + k0);
-            const float4 a1 = lds4(Ls + (rt * 16 + r16) * CP + k0 + 4);
+            const float4 a0 = lds4(Lg + (rt * 16 + r16) * CP + k0);
+            const float4 a1 = lds4(Lg + (rt * 16 + r16) * CP + k0 + 4);
             const float v[8] = {a0.x * f[0], a0.y * f[1], a0.z * f[2], a0.w * f[3],
                                 a1.x * f[4], a1.y * f[5], a1.z * f[6], a1.w * f[7]};
             split8(v, ah[rt], al[rt]);
@@ -670,7 +623,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void k
         for (int ct = 0; ct < 4; ct++) {         // R column n, rows k0 .. k0 + 7
             const int n = cbase + ct * 16 + r16;
             if (isv) {
-                bc[ct] = ld8(Vt + n * C + (((k0 >> 3) ^ (n & 7)) << 3));
+                bc[ct] = ld8(Vg + n * C + (((k0 >> 3) ^ (n & 7)) << 3));
             } else {
                 bc[ct] = ld8(Kpu + bx1_b_index(k0, n - DV));   // keys k0 .. k0+7 of dim n - DV
             }
@@ -683,7 +636,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void k
                 xacc[rt][ct] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf(ah[rt]), as_bf(bc[ct]), xacc[rt][ct], 0, 0, 0);
             }
     }
-    const size_t ub = (size_t)unit * C * DV;
+    const size_t ub = (size_t)unitg * C * DV;
     if (isv) {                         // U: the accumulator order is U's layout
 #pragma unroll
         for (int rt = 0; rt < 4; rt++)
@@ -695,7 +648,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void k
     // W through LDS (L is no longer read): column tid - DV of every row in,
     // then 32-byte units of 8 consecutive columns of one row out
     __syncthreads();                   // every reader of T, V and the k codes is done
-    float *Wl = reinterpret_cast<float *>(wy_lds);
+    float *Wl = reinterpret_cast<float *>(wy_lds + grp * W_B);   // over both Ls and Vs
     if (!isv) {
 #pragma unroll
         for (int rt = 0; rt < 4; rt++)
@@ -708,7 +661,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void k
     __syncthreads();
 #pragma unroll
     for (int u = 0; u < C * DK / 8 / 256; u++) {
-        const int e = tid + 256 * u, t = e / (DK / 8), c0 = (e % (DK / 8)) * 8;
+        const int e = gtid + 256 * u, t = e / (DK / 8), c0 = (e % (DK / 8)) * 8;
         float w8[8];
         const float4 a0 = lds4(Wl + t * KP + c0), a1 = lds4(Wl + t * KP + c0 + 4);
         w8[0] = a0.x; w8[1] = a0.y; w8[2] = a0.z; w8[3] = a0.w;
@@ -971,7 +924,6 @@ struct PrefillWs {
     GdnScratch w;
     float *Ub = nullptr, *Fb = nullptr;
     uint16_t *Wb = nullptr, *Ab = nullptr, *Qp = nullptr, *Kp = nullptr;
-    float *QKt = nullptr, *QKR = nullptr;
     int32_t *meta = nullptr;
     size_t bytes = 0;
 };
@@ -992,8 +944,6 @@ static PrefillWs prefill_ws_carve(char *base, size_t Ttot, size_t nch, size_t B,
     p.Fb = (float *)take(units * 3 * C * 4);
     p.Qp = (uint16_t *)take(nch * hk * C * DK * 2);
     p.Kp = (uint16_t *)take(nch * hk * C * DK * 2);
-    p.QKt = (float *)take(nch * hk * 2 * kQkTiles * 64 * 4 * 4);
-    p.QKR = (float *)take(nch * hk * 2 * C * 4);
     p.meta = (int32_t *)take(2 * (B + 1) * 4);
     p.bytes = off;
     return p;
@@ -1088,20 +1038,12 @@ static int gdn_prefill_run(const ApusHipGdnLayer *L, size_t B, const int32_t *cu
     float *Fb = ws ? pw.Fb : (float *)scratch(kScratchGdnChunk5, units * 3 * C * 4);
     uint16_t *Qp = ws ? pw.Qp : (uint16_t *)scratch(kScratchGdnChunk6, nch * L->hk * C * DK * 2);
     uint16_t *Kp = ws ? pw.Kp : (uint16_t *)scratch(kScratchGdnChunk7, nch * L->hk * C * DK * 2);
-    float *QKt = ws ? pw.QKt
-                    : (float *)scratch(kScratchGdnChunk8, nch * L->hk * 2 * kQkTiles * 64 * 4 * 4);
-    float *QKR = ws ? pw.QKR : (float *)scratch(kScratchGdnChunk9, nch * L->hk * 2 * C * 4);
-    if (!Ub || !Wb || !Ab || !Fb || !Qp || !Kp || !QKt || !QKR) return kErrHip;
-    APUS_TIMED("k_gdn_chunk_qk",
-               k_gdn_chunk_qk<<<(unsigned)(nch * L->hk), 512, 0, stream()>>>(
-        sq, kmeta, qkv, L->conv_w, conv_state, slots, tabs->silu_bf, Qp, Kp, QKt, QKR,
-        (int)L->hk, (float)pow((double)L->dk, -0.5)));
-    APUS_LAUNCHED("k_gdn_chunk_qk");
+    if (!Ub || !Wb || !Ab || !Fb || !Qp || !Kp) return kErrHip;
     APUS_TIMED("k_gdn_chunk_wy",
-               k_gdn_chunk_wy<<<(unsigned)units, 256, 0, stream()>>>(
+               k_gdn_chunk_wy<<<(unsigned)(nch * L->hk), 512, 0, stream()>>>(
         sq, kmeta, qkv, a, b, L->conv_w, L->A_log, L->dt_bias, conv_state, slots,
-        tabs->silu_bf, tabs->sig_bf, Ub, Wb, Ab, Fb, Kp, QKt, QKR, (int)L->hk,
-        units % 16 == 0 ? 1 : 0));
+        tabs->silu_bf, tabs->sig_bf, Ub, Wb, Ab, Fb, Qp, Kp, (int)L->hk,
+        (float)pow((double)L->dk, -0.5)));
     APUS_LAUNCHED("k_gdn_chunk_wy");
     APUS_TIMED("k_gdn_chunk_scan",
                k_gdn_chunk_scan<<<(unsigned)(B * L->hv * NCB), 512, 0, stream()>>>(

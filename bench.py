@@ -391,7 +391,6 @@ def bench_gdn_prefill(torch, T, steps, warmup, seed, leg=None):
              "k_gdn_chunk_wy": ("mfma", nu * WY_FLOPS_PER_UNIT, BF16_PEAK,
                                 {"split_roof_tflops": BF16_PEAK * WY_FLOPS_PER_UNIT
                                  / WY_EXEC_PER_UNIT / 1e12}),
-             "k_gdn_chunk_qk": ("mfma", (nu // 2) * QK_FLOPS_PER_KUNIT, BF16_PEAK),
              "k_gdn_post": ("hbm", gdn_post_bytes(T), HBM_PEAK)}
     total, per, kt = time_steps(torch, step, steps, warmup, nsets, table)
     st = float(np.mean(per))
@@ -418,16 +417,15 @@ def bench_gdn_prefill(torch, T, steps, warmup, seed, leg=None):
 # the WY build does K K^T, Q K^T (64x64x128) and the two 64x64x128
 # triangular applications giving U and W, plus the triangular solve.
 SCAN_FLOPS_PER_UNIT = 3 * 2 * 64 * 128 * 128 + 2 * 64 * 64 * 128
-# WY per (chunk, v-head): T [b V | b G K] and the triangular solve; Q K^T
-# and K K^T are formed once per (chunk, K head) by k_gdn_chunk_qk
-WY_FLOPS_PER_UNIT = 2 * 2 * 64 * 64 * 128 + (2 * 64 ** 3) // 3
-QK_FLOPS_PER_KUNIT = 2 * 2 * 64 * 64 * 128
+# WY per (chunk, v-head): T [b V | b G K], the triangular solve, and half
+# of Q K^T and K K^T (formed once per (chunk, K head) for its two v-heads)
+WY_FLOPS_PER_UNIT = 2 * 2 * 64 * 64 * 128 + (2 * 64 ** 3) // 3 + 2 * 64 * 64 * 128
 # MFMA flops the kernels execute for them: the scan's W S0 and A D take
 # three MFMAs per product (both operands split), Q S0 and K^T D two (q, k
-# as exact codes); WY's T R two, and the 32x32 off-diagonal block of T two
-# split products
+# as exact codes); WY's T R two, the 32x32 off-diagonal block of T two
+# split products, Q K^T and K K^T one (codes, shared by two v-heads)
 SCAN_EXEC_PER_UNIT = 3 * 2 * 64 * 128 * 128 + 2 * 2 * 2 * 64 * 128 * 128 + 3 * 2 * 64 * 64 * 128
-WY_EXEC_PER_UNIT = 2 * 2 * 2 * 64 * 64 * 128 + 3 * 2 * 2 * 32 ** 3
+WY_EXEC_PER_UNIT = 2 * 2 * 2 * 64 * 64 * 128 + 3 * 2 * 2 * 32 ** 3 + 2 * 64 * 64 * 128
 
 
 def gdn_post_bytes(T):
