@@ -417,15 +417,13 @@ def bench_gdn_prefill(torch, T, steps, warmup, seed, leg=None):
 # the WY build does K K^T, Q K^T (64x64x128) and the two 64x64x128
 # triangular applications giving U and W, plus the triangular solve.
 SCAN_FLOPS_PER_UNIT = 3 * 2 * 64 * 128 * 128 + 2 * 64 * 64 * 128
-# WY per (chunk, v-head): T [b V | b G K], the triangular solve, and half
-# of Q K^T and K K^T (formed once per (chunk, K head) for its two v-heads)
-WY_FLOPS_PER_UNIT = 2 * 2 * 64 * 64 * 128 + (2 * 64 ** 3) // 3 + 2 * 64 * 64 * 128
+WY_FLOPS_PER_UNIT = 4 * 2 * 64 * 64 * 128 + (2 * 64 ** 3) // 3
 # MFMA flops the kernels execute for them: the scan's W S0 and A D take
 # three MFMAs per product (both operands split), Q S0 and K^T D two (q, k
-# as exact codes); WY's T R two, the 32x32 off-diagonal block of T two
-# split products, Q K^T and K K^T one (codes, shared by two v-heads)
+# as exact codes); WY's K K^T and Q K^T one (codes), T R two, and the
+# 32x32 off-diagonal block of T two split products
 SCAN_EXEC_PER_UNIT = 3 * 2 * 64 * 128 * 128 + 2 * 2 * 2 * 64 * 128 * 128 + 3 * 2 * 64 * 64 * 128
-WY_EXEC_PER_UNIT = 2 * 2 * 2 * 64 * 64 * 128 + 3 * 2 * 2 * 32 ** 3 + 2 * 64 * 64 * 128
+WY_EXEC_PER_UNIT = 2 * 2 * 64 * 64 * 128 + 2 * 2 * 2 * 64 * 64 * 128 + 3 * 2 * 2 * 32 ** 3
 
 
 def gdn_post_bytes(T):
