@@ -138,8 +138,9 @@ __device__ __forceinline__ int sload_i32(const int32_t *base, uint32_t bytes, in
 __device__ __forceinline__ void dma16(i32x4 r, int voff, int soff, uint32_t lds) {
     soff = __builtin_amdgcn_readfirstlane(soff);
     lds = __builtin_amdgcn_readfirstlane(lds);
-    asm volatile("s_mov_b32 m0, %3\n\tbuffer_load_dwordx4 %0, %1, %2 offen lds"
-                 :: "v"(voff), "s"(r), "s"(soff), "s"(lds) : "memory", "m0");
+    // (M0 is bound as an operand, so the compiler sets it and knows it changed)
+    asm volatile("buffer_load_dwordx4 %0, %1, %2 offen lds"
+                 :: "v"(voff), "s"(r), "s"(soff), "{m0}"(lds) : "memory");
 }
 
 // Exact IEEE single ops that the compiler may not fuse or reorder. The
