@@ -272,12 +272,14 @@ void k_gdn_decode(
     uint32_t c0x = cwq.x, c0y = cwq.y, c1x = cwv.x, c1y = cwv.y;
     const int voff = (half * 32 * 64 + lane) * 16;
     float sr[DK];
-    // This wave's 128x64 state tile (32 x 16-byte loads per lane). With one
-    // token it is loaded before phase A, whose gate math then runs under
-    // the loads; with several it is loaded after phase A, so that its 128
-    // registers are not live through phase A's per-token gate and silu
-    // code. (The descriptor is made where si and h are known uniform.)
-    constexpr bool kEarlyTile = MODE == 0;
+    // This wave's 128x64 state tile (32 x 16-byte loads per lane). With the
+    // tokens in one chunk (modes 0 and 1) it is loaded before phase A, whose
+    // conv, gate and silu math then runs under the loads (186 VGPRs with up
+    // to KT tokens, no spills at two waves per SIMD; loading it after phase
+    // A cost 7 us per config-4 layer). With several chunks (mode 2) it is
+    // loaded after phase A of the first. (The descriptor is made where si
+    // and h are known uniform.)
+    constexpr bool kEarlyTile = MODE != 2;
     auto load_tile = [&]() {
         const int tix = __builtin_amdgcn_readfirstlane(si * hv + h);
         const auto Sr = buf_rsrc(S + (size_t)tix * DK * DV, DK * DV * 4);
