@@ -50,7 +50,7 @@ EXPORTS = [
     "apus_hip_st_open", "apus_hip_st_close", "apus_hip_st_ntensors", "apus_hip_st_find",
     "apus_hip_st_read", "apus_hip_gdn_layer_load", "apus_hip_attn_layer_load",
     "apus_hip_gdn_layer_free", "apus_hip_attn_layer_free", "apus_hip_trace_set",
-    "apus_hip_gdn_prefill_noalloc",
+    "apus_hip_gdn_prefill_noalloc", "apus_hip_set_spin_limit", "apus_hip_attn_split_check",
 ]
 
 
@@ -69,7 +69,8 @@ class GdnLayer(C.Structure):
 
 class KvCache(C.Structure):
     """ApusHipKvCache (include/apus_hip.h): a paged KV cache."""
-    _fields_ = [("k", _vp), ("v", _vp), ("block_table", _vp), ("max_blocks", _sz)]
+    _fields_ = [("k", _vp), ("v", _vp), ("block_table", _vp), ("max_blocks", _sz),
+                ("max_rows", _sz), ("row_blocks", _vp)]
 
 
 class AttnLayer(C.Structure):
@@ -118,6 +119,26 @@ def last_error():
 def _chk(rc):
     if rc != 0:
         raise ApusHipError(rc, last_error())
+
+
+def set_spin_limit(polls):
+    """Polls a bounded device wait makes before it gives up (0: default)."""
+    _chk(load().apus_hip_set_spin_limit(C.c_uint32(int(polls))))
+
+
+def attn_split_check(cu, pos0, nkv=2, cus=256):
+    """Host walk of the decode split plan (apus_hip_attn_split_check):
+    returns its 12 counters as a dict."""
+    cu = np.ascontiguousarray(cu, np.int32)
+    pos0 = np.ascontiguousarray(pos0, np.int32)
+    out = np.zeros(12, np.int64)
+    _chk(load().apus_hip_attn_split_check(_sz(len(pos0)), cu.ctypes.data_as(_i32p),
+                                          pos0.ctypes.data_as(_i32p), _sz(nkv), _sz(cus),
+                                          out.ctypes.data_as(C.POINTER(C.c_int64))))
+    keys = ("runs", "group_mismatch", "writer_groups", "stream_groups", "bad_keys",
+            "bad_slots", "bad_pair_runs", "T1", "pv_runs", "pv_bad_keys", "pv_bad_slots",
+            "pv_bad_pair_runs")
+    return dict(zip(keys, (int(x) for x in out)))
 
 
 def _u16(a):

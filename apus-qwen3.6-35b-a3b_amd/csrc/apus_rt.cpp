@@ -21,6 +21,8 @@ int g_ready = 0;
 int g_device = 0;
 int g_cus = 256;
 hipStream_t g_stream = nullptr;
+uint32_t *g_fault = nullptr;           // device fault word of the current device
+uint32_t g_spin = kDefaultSpinLimit;
 
 struct Buf {
     void *p = nullptr;
@@ -123,8 +125,19 @@ int ensure_ready() {
         g_ready = 0;
         return kErrHip;
     }
+    if (!g_fault) {
+        if (hipMalloc((void **)&g_fault, 256) != hipSuccess ||
+            hipMemset(g_fault, 0, 256) != hipSuccess) {
+            g_ready = 0;
+            g_fault = nullptr;
+            return set_error(kErrHip, "allocation of the device fault word failed");
+        }
+    }
     return kOk;
 }
+
+uint32_t *fault_word() { return g_fault; }
+uint32_t spin_limit() { return g_spin; }
 
 int cu_count() { return g_cus; }
 int current_device() { return g_device; }
@@ -323,6 +336,7 @@ using namespace apus;
 extern "C" {
 
 int apus_hip_init(int device, char *err, size_t errcap) {
+    if (device != g_device) g_fault = nullptr;   // each device gets its own word
     g_device = device;
     g_ready = 0;
     int r = ensure_ready();
@@ -347,6 +361,19 @@ int apus_hip_set_stream(void *s) {
 int apus_hip_synchronize(void) {
     APUS_READY();
     APUS_HIP_TRY(hipStreamSynchronize(g_stream));
+    uint32_t f = 0;
+    APUS_HIP_TRY(hipMemcpy(&f, g_fault, 4, hipMemcpyDeviceToHost));
+    if (f) {
+        APUS_HIP_TRY(hipMemset(g_fault, 0, 4));
+        return set_error(kErrHip, "a kernel's bounded wait expired (fault bits 0x%x: %s); the "
+                         "results of the work since the last synchronize are invalid", f,
+                         (f & kFaultScoresWait) ? "k_attn_scores score ring" : "unknown");
+    }
+    return kOk;
+}
+
+int apus_hip_set_spin_limit(uint32_t polls) {
+    g_spin = polls ? polls : kDefaultSpinLimit;
     return kOk;
 }
 

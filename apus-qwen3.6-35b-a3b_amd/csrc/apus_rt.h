@@ -84,6 +84,17 @@ constexpr size_t kNoAllocScratchBytes = (size_t)96 << 20;
 int noalloc_setup(int dev);
 void *noalloc_scratch();
 
+// Device fault word: kernels with bounded waits (k_attn_scores' producer /
+// consumer ring) OR a kFault* bit into it when a wait expires, then run on
+// to a normal exit; apus_hip_synchronize reads and clears it and reports
+// a set bit as an error. spin_limit(): the polls such a wait makes before
+// it gives up (apus_hip_set_spin_limit; default kDefaultSpinLimit, about
+// a quarter of a second of polling).
+constexpr uint32_t kFaultScoresWait = 1u;
+constexpr uint32_t kDefaultSpinLimit = 1u << 22;
+uint32_t *fault_word();
+uint32_t spin_limit();
+
 // The trace sinks set by apus_hip_trace_set (nullptr when tracing is off).
 const ApusHipGdnTrace *gdn_trace();
 const ApusHipAttnTrace *attn_trace();

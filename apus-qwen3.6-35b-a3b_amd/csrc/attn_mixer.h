@@ -79,6 +79,14 @@ int attn_max_vblocks(size_t B, const int32_t *cu, const int32_t *pos0);
 // Flat-layout KvRef of B sequences of max_seq positions each.
 KvRef kv_flat(uint16_t *kcache, uint16_t *vcache, size_t max_seq);
 
+// The KvRef of a paged cache for a call of B sequences at table rows
+// rows[s] writing positions up to pos0[s] + (cu[s+1] - cu[s]): refuses a
+// row outside the table and, when the descriptor carries the rows'
+// reserved block counts, a closed row or one that has not reserved the
+// blocks the call writes.
+int kv_paged_ref(const ApusHipKvCache *c, size_t B, const int32_t *rows, const int32_t *cu,
+                 const int32_t *pos0, KvRef *r);
+
 // Prefill on a cache given as a KvRef (flat or paged).
 int attn_prefill_kv(const ApusHipAttnLayer *L, size_t B, const int32_t *cu, const int32_t *pos0,
                     const int32_t *rows, const uint16_t *qg, const uint16_t *k,

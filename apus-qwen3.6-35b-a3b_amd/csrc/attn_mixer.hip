@@ -70,7 +70,7 @@ __device__ __forceinline__ bf16x8 ld_bf16x8(const uint16_t *p) {
     return __builtin_bit_cast(bf16x8, gld16(p));
 }
 
-__device__ __forceinline__ int seq_of(const int32_t *off, int n, int x) {
+__host__ __device__ inline int seq_of(const int32_t *off, int n, int x) {
     int lo = 0, hi = n - 1;          // largest s with off[s] <= x
     while (lo < hi) {
         int mid = (lo + hi + 1) >> 1;
@@ -316,10 +316,21 @@ __device__ __forceinline__ size_t a_index(int row, int key, int cap) {
     return ((size_t)((row >> 4) * (cap >> 5) + (key >> 5)) * 16 + (row & 15)) * 32 + (key & 31);
 }
 
+// a wave-uniform value held in a scalar register (the identity on the
+// host, where the split plan is checked)
+__host__ __device__ inline int uni(int x) {
+#if defined(__HIP_DEVICE_COMPILE__)
+    return __builtin_amdgcn_readfirstlane(x);
+#else
+    return x;
+#endif
+}
+
 // The segment of run w (keys x1 > x of the padded pair space) starting at
 // x; *xn is where the next one starts. False for a segment that holds only
-// padding keys (nothing to compute or store).
-__device__ __forceinline__ bool seg_at(const Meta &mt, int n, int nkv, int w, int x, int x1,
+// padding keys (nothing to compute or store). Host and device: the split
+// plan is also walked on the host (apus_hip_attn_split_check).
+__host__ __device__ inline bool seg_at(const Meta &mt, int n, int nkv, int w, int x, int x1,
                                        Seg &g, int *xn) {
     const int s = seq_of(mt.ccap, n, x / nkv);
     const int base = nkv * mt.ccap[s], cap = mt.ccap[s + 1] - mt.ccap[s];
@@ -332,14 +343,14 @@ __device__ __forceinline__ bool seg_at(const Meta &mt, int n, int nkv, int w, in
     g.pos0 = mt.pos0[s];
     g.k0 = k0;
     g.k1 = min(k0 + (xe - x), g.pos0 + g.tq);
-    g.cap = __builtin_amdgcn_readfirstlane(cap);
-    g.abase = (size_t)kRows * (size_t)__builtin_amdgcn_readfirstlane(base + kvh * cap);
+    g.cap = uni(cap);
+    g.abase = (size_t)kRows * (size_t)uni(base + kvh * cap);
     *xn = xe;
     return g.k0 < g.k1;
 }
 
 // The runs of T keys a pair's real keys fall in: w0 .. w1 (inclusive).
-__device__ __forceinline__ void pair_runs(const Meta &mt, int nkv, int s, int kvh, int T,
+__host__ __device__ inline void pair_runs(const Meta &mt, int nkv, int s, int kvh, int T,
                                           int *w0, int *w1) {
     const int cap = mt.ccap[s + 1] - mt.ccap[s];
     const int ps = nkv * mt.ccap[s] + kvh * cap;
@@ -348,6 +359,23 @@ __device__ __forceinline__ void pair_runs(const Meta &mt, int nkv, int s, int kv
     *w1 = (ps + ctx - 1) / T;
 }
 
+
+// The 64-key groups run `run` (keys [run*T, min(run*T + T, total)) of the
+// padded pair space) publishes through the score ring: the writer's count,
+// formed before it stores anything. The streaming wavefront walks the same
+// segments and steps each one's keys by 64 (scores_seg).
+__host__ __device__ inline int run_groups(const Meta &mt, int n, int nkv, int run, int T,
+                                          int total) {
+    int x = run * T, ng = 0;
+    const int x1 = min(x + T, total);
+    while (x < x1) {
+        Seg g;
+        int xn;
+        if (seg_at(mt, n, nkv, run, x, x1, g, &xn)) ng += (g.k1 - g.k0 + 63) / 64;
+        x = xn;
+    }
+    return ng;
+}
 
 // ---- k_attn_scores: W streaming wavefronts + 1 writer per workgroup ------
 // Each streaming wavefront owns one run of T1 keys (one or more segments).
@@ -392,6 +420,16 @@ __device__ __forceinline__ void lds_count_store(int *p, int v) {
 }
 __device__ __forceinline__ void compiler_fence() { asm volatile("" ::: "memory"); }
 
+// a bounded wait of k_attn_scores expired: tell the workgroup's other
+// waves (LDS flag) and the host (the device fault word, read by
+// apus_hip_synchronize); vector atomics from one lane
+__device__ __forceinline__ void scores_abort(int *abortp, uint32_t *__restrict__ fault) {
+    if ((threadIdx.x & 63) == 0) {
+        lds_count_store(abortp, 1);
+        __hip_atomic_fetch_or(fault, kFaultScoresWait, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+}
+
 // a wave-uniform pointer held in scalar registers
 __device__ __forceinline__ const uint16_t *uniform_ptr(const uint16_t *p) {
     const uint64_t a = (uint64_t)p;
@@ -417,7 +455,8 @@ __device__ __forceinline__ void scores_seg(const Meta &mt, const Seg &c,
                                            int nh, int nkv, float scale,
                                            float2 *__restrict__ stats, uint4 *ringw,
                                            RingHdr *hdrw, int *readyw, int *donew, int &grp,
-                                           uint4 *stg) {
+                                           uint4 *stg, int *abortp, uint32_t spin,
+                                           uint32_t *__restrict__ fault) {
     const int32_t *cu = mt.cu;
     const int l = threadIdx.x & 63, c16 = l & 15, q4 = l >> 4;
 
@@ -549,9 +588,21 @@ __device__ __forceinline__ void scores_seg(const Meta &mt, const Seg &c,
         qA = rA;
         qB = rB;
 
-        // publish the group's scores to the writer through the ring
-        if (grp >= kScRing && dn <= grp - kScRing)
-            while (lds_count_load(donew) <= grp - kScRing) __builtin_amdgcn_s_sleep(1);
+        // publish the group's scores to the writer through the ring. The
+        // wait is bounded: past `spin` polls (or once another wavefront of
+        // the workgroup gave up) the call is marked failed in the device
+        // fault word and the wavefront runs on without waiting, so every
+        // wave still exits
+        if (grp >= kScRing && dn <= grp - kScRing) {
+            uint32_t polls = 0;
+            while (lds_count_load(donew) <= grp - kScRing) {
+                if (lds_count_load(abortp) || ++polls > spin) {
+                    scores_abort(abortp, fault);
+                    break;
+                }
+                __builtin_amdgcn_s_sleep(1);
+            }
+        }
         compiler_fence();
         const int rs = grp % kScRing;
         uint4 *sl = ringw + rs * SLOT;
@@ -616,17 +667,18 @@ template <int NRB>
 __global__ __launch_bounds__(64 * (ScoresShape<NRB>::W + 1)) void k_attn_scores(
     AttnSeqs sq, const int32_t *__restrict__ dmeta, const uint16_t *__restrict__ qn, KvRef kv,
     int nh, int nkv, float scale, uint16_t *__restrict__ As, float2 *__restrict__ stats,
-    int nruns) {
+    int nruns, uint32_t spin, uint32_t *__restrict__ fault) {
     constexpr int W = ScoresShape<NRB>::W, SLOT = ScoresShape<NRB>::SLOT;
     __shared__ uint4 ring[W][kScRing][SLOT];
     __shared__ uint4 kstage[W][16 * 33];            // per wavefront: one 16-key K block
     __shared__ RingHdr hdr[W][kScRing];
-    __shared__ int ready[W], done[W];
+    __shared__ int ready[W], done[W], abort_flag;
     const int wave = threadIdx.x >> 6, l = threadIdx.x & 63;
     if (threadIdx.x < W) {
         ready[threadIdx.x] = 0;
         done[threadIdx.x] = 0;
     }
+    if (threadIdx.x == 0) abort_flag = 0;
     __syncthreads();
     const Meta mt = meta_of(sq, dmeta);
     const int n = sq.n, T = sq.T1, total = nkv * mt.ccap[n];
@@ -639,18 +691,13 @@ __global__ __launch_bounds__(64 * (ScoresShape<NRB>::W + 1)) void k_attn_scores(
 #pragma unroll
         for (int w = 0; w < W; w++) {
             nxt[w] = 0;
-            ng[w] = 0;
             const int run = blockIdx.x * W + w;
-            if (run >= nruns) continue;
-            int x = run * T;
-            const int x1 = min(x + T, total);
-            while (x < x1) {
-                Seg g;
-                int xn;
-                if (seg_at(mt, n, nkv, run, x, x1, g, &xn)) ng[w] += (g.k1 - g.k0 + 63) / 64;
-                x = xn;
-            }
+            ng[w] = run < nruns ? run_groups(mt, n, nkv, run, T, total) : 0;
         }
+        // the writer's polls over its life, bounded like the streaming
+        // wavefronts' waits (a normal launch makes a few thousand at most;
+        // a run of more groups than the ring holds always needs two)
+        uint32_t polls = 0;
         for (;;) {
             bool left = false, moved = false;
 #pragma unroll
@@ -685,6 +732,10 @@ __global__ __launch_bounds__(64 * (ScoresShape<NRB>::W + 1)) void k_attn_scores(
                 moved = true;
             }
             if (!left) break;
+            if (lds_count_load(&abort_flag) || ++polls > spin) {
+                scores_abort(&abort_flag, fault);
+                break;
+            }
             if (!moved) __builtin_amdgcn_s_sleep(2);
         }
         return;
@@ -702,10 +753,12 @@ __global__ __launch_bounds__(64 * (ScoresShape<NRB>::W + 1)) void k_attn_scores(
             // a sequence with at most 2 tokens fills one row block
             if (NRB == 2 && g.tq <= 2)
                 scores_seg<1, SLOT>(mt, g, qn, kv, nh, nkv, scale, stats, ring[wave][0],
-                                    hdr[wave], &ready[wave], &done[wave], grp, kstage[wave]);
+                                    hdr[wave], &ready[wave], &done[wave], grp, kstage[wave],
+                                    &abort_flag, spin, fault);
             else
                 scores_seg<NRB, SLOT>(mt, g, qn, kv, nh, nkv, scale, stats, ring[wave][0],
-                                      hdr[wave], &ready[wave], &done[wave], grp, kstage[wave]);
+                                      hdr[wave], &ready[wave], &done[wave], grp, kstage[wave],
+                                      &abort_flag, spin, fault);
         }
         x = xn;
     }
@@ -974,6 +1027,17 @@ KvRef kv_flat(uint16_t *kcache, uint16_t *vcache, size_t max_seq) {
 
 static size_t ceil64(size_t x) { return (x + 63) / 64 * 64; }
 
+// decode: balanced runs of T keys per wavefront over `total` padded keys,
+// each kernel's grid one round of resident wavefronts (scores: W streaming
+// wavefronts per CU; P.V: two wavefronts per run, each owning half of d,
+// at three wavefronts per SIMD for one row block, two for two)
+static void attn_split_sizes(size_t total, size_t max_tok, size_t cus, int32_t *T1, int32_t *T2) {
+    const size_t w1 = (max_tok <= 2 ? scores_waves_per_block<1>() : scores_waves_per_block<2>()) * cus;
+    const size_t w2 = (max_tok <= 2 ? 3 : 2) * 4 * cus / 2;
+    *T1 = (int32_t)std::max<size_t>(64, ceil64((total + w1 - 1) / w1));
+    *T2 = (int32_t)std::max<size_t>(64, ceil64((total + w2 - 1) / w2));
+}
+
 int attn_meta(size_t B, const int32_t *cu, const int32_t *pos0, const int32_t *rows,
               size_t bstride, size_t nkv, int max_new, AttnSeqs *sq, const int32_t **dmeta,
               size_t *max_tok) {
@@ -997,8 +1061,8 @@ int attn_meta(size_t B, const int32_t *cu, const int32_t *pos0, const int32_t *r
         if ((size_t)tq > mt) mt = (size_t)tq;
     }
     *max_tok = mt;
+    attn_split_sizes(nkv * (size_t)ccap[B], mt, (size_t)cu_count(), &sq->T1, &sq->T2);
     sq->n = (int32_t)B;
-    sq->T1 = sq->T2 = 64;
     *dmeta = nullptr;
     if (B <= (size_t)kAttnInlineSeqs) {
         memcpy(sq->cu, cu, (B + 1) * 4);
@@ -1014,16 +1078,6 @@ int attn_meta(size_t B, const int32_t *cu, const int32_t *pos0, const int32_t *r
         *dmeta = (const int32_t *)upload_async(m.data(), m.size() * 4);
         if (!*dmeta) return kErrHip;
     }
-    // decode: balanced runs of T keys per wavefront, each kernel's grid one
-    // round of resident wavefronts (scores: W streaming wavefronts per CU;
-    // P.V: two wavefronts per run, each owning half of d, at three
-    // wavefronts per SIMD for one row block, two for two)
-    const size_t total = nkv * (size_t)ccap[B];
-    const size_t w1 = (mt <= 2 ? scores_waves_per_block<1>() : scores_waves_per_block<2>()) *
-                      (size_t)cu_count();
-    const size_t w2 = (mt <= 2 ? 3 : 2) * 4 * (size_t)cu_count() / 2;
-    sq->T1 = (int32_t)std::max<size_t>(64, ceil64((total + w1 - 1) / w1));
-    sq->T2 = (int32_t)std::max<size_t>(64, ceil64((total + w2 - 1) / w2));
     return kOk;
 }
 
@@ -1102,7 +1156,8 @@ int attn_decode_kv(const ApusHipAttnLayer *L, size_t B, const int32_t *cu, const
         APUS_TIMED("k_attn_scores",
                    k_attn_scores<1><<<cdiv(nruns1, scores_waves_per_block<1>()),
                                       64 * (scores_waves_per_block<1>() + 1), 0, stream()>>>(
-                       sq, dmeta, qn, kv, (int)L->nh, (int)nkv, scale, As, st, (int)nruns1));
+                       sq, dmeta, qn, kv, (int)L->nh, (int)nkv, scale, As, st, (int)nruns1,
+                       spin_limit(), fault_word()));
         APUS_LAUNCHED("k_attn_scores");
         APUS_TIMED("k_attn_pv",
                    k_attn_pv<1, 2><<<(unsigned)(2 * nruns2), 64, 0, stream()>>>(
@@ -1112,7 +1167,8 @@ int attn_decode_kv(const ApusHipAttnLayer *L, size_t B, const int32_t *cu, const
         APUS_TIMED("k_attn_scores",
                    k_attn_scores<2><<<cdiv(nruns1, scores_waves_per_block<2>()),
                                       64 * (scores_waves_per_block<2>() + 1), 0, stream()>>>(
-                       sq, dmeta, qn, kv, (int)L->nh, (int)nkv, scale, As, st, (int)nruns1));
+                       sq, dmeta, qn, kv, (int)L->nh, (int)nkv, scale, As, st, (int)nruns1,
+                       spin_limit(), fault_word()));
         APUS_LAUNCHED("k_attn_scores");
         APUS_TIMED("k_attn_pv",
                    k_attn_pv<2, 2><<<(unsigned)(2 * nruns2), 64, 0, stream()>>>(
@@ -1127,10 +1183,28 @@ int attn_decode_kv(const ApusHipAttnLayer *L, size_t B, const int32_t *cu, const
     return kOk;
 }
 
-static int kv_of(const ApusHipKvCache *c, KvRef *r) {
+int kv_paged_ref(const ApusHipKvCache *c, size_t B, const int32_t *rows, const int32_t *cu,
+                 const int32_t *pos0, KvRef *r) {
     if (!c || !c->k || !c->v || !c->block_table || c->max_blocks == 0 ||
-        c->max_blocks > 0x7fffffff)
+        c->max_blocks > 0x7fffffff || c->max_rows == 0 || c->max_rows > 0x7fffffff)
         return set_error(kErrArgument, "bad paged KV cache descriptor");
+    if (!rows) return set_error(kErrArgument, "NULL block-table rows");
+    if (B && (!cu || !pos0)) return set_error(kErrArgument, "NULL offsets");
+    for (size_t s = 0; s < B; s++) {
+        if (rows[s] < 0 || (size_t)rows[s] >= c->max_rows)
+            return set_error(kErrArgument, "block-table row %d of sequence %zu is outside the "
+                             "table's %zu rows", rows[s], s, c->max_rows);
+        if (!c->row_blocks) continue;
+        // positions 0 .. pos0 + new - 1 must lie in blocks the row holds
+        const int64_t end = (int64_t)pos0[s] + (int64_t)(cu[s + 1] - cu[s]);
+        const int32_t held = c->row_blocks[rows[s]];
+        if (held < 0)
+            return set_error(kErrArgument, "block-table row %d of sequence %zu is not open",
+                             rows[s], s);
+        if (end > (int64_t)held * KVB)
+            return set_error(kErrArgument, "sequence %zu reaches position %lld but row %d has "
+                             "reserved %d positions", s, (long long)end, rows[s], held * KVB);
+    }
     *r = KvRef{c->k, c->v, c->block_table, (int32_t)c->max_blocks};
     return kOk;
 }
@@ -1154,9 +1228,97 @@ int apus_hip_attn_decode_paged(const ApusHipAttnLayer *L, size_t B, const int32_
                                uint16_t *y) {
     APUS_READY();
     KvRef r;
-    if (int e = kv_of(kv, &r)) return e;
-    if (!rows) return set_error(kErrArgument, "NULL block-table rows");
+    if (int e = kv_paged_ref(kv, B, rows, cu, pos0, &r)) return e;
     return attn_decode_kv(L, B, cu, pos0, rows, qg, k, v, r, y);
+}
+
+// Host walk of the decode split plan for a batch (no device needed): the
+// scores kernel's two enumerations of each run's 64-key groups, the
+// writer's (run_groups) and the streaming wavefront's (its segments' keys
+// stepped by 64), must agree or the ring's producer / consumer waits would
+// not meet; every real key of every (sequence, kv head) pair must fall in
+// exactly one segment; segment slots must be distinct and inside the
+// statistics buffer; and the runs P.V folds for a pair (pair_runs) must be
+// exactly the runs holding one of its segments. out[12]: runs, runs whose
+// two counts differ, writer groups, streaming groups, keys missed or
+// covered twice, slot collisions or overflows, pair_runs mismatches, T1,
+// and (the same for P.V's runs of T2) runs, keys missed or covered twice,
+// slot problems, pair_runs mismatches.
+int apus_hip_attn_split_check(size_t B, const int32_t *cu, const int32_t *pos0, size_t nkv,
+                              size_t cus, int64_t *out) {
+    if (!cu || !pos0 || !out || B == 0 || nkv == 0 || cus == 0 || cu[0] != 0)
+        return set_error(kErrArgument, "bad split-check arguments");
+    std::vector<int32_t> ccap(B + 1, 0), hd(B);
+    size_t mt = 0;
+    for (size_t s = 0; s < B; s++) {
+        const int32_t tq = cu[s + 1] - cu[s];
+        if (tq < 1 || tq > kRows / GRP || pos0[s] < 0)
+            return set_error(kErrArgument, "sequence %zu: 1..4 new tokens after pos0 >= 0", s);
+        ccap[s + 1] = ccap[s] + (int32_t)ceil64((size_t)pos0[s] + tq);
+        mt = std::max<size_t>(mt, (size_t)tq);
+        hd[s] = (int32_t)s;
+    }
+    const size_t total = nkv * (size_t)ccap[B];
+    if (total > (size_t)0x7ff00000) return set_error(kErrArgument, "too many keys");
+    int32_t T[2];
+    attn_split_sizes(total, mt, cus, &T[0], &T[1]);
+    const Meta m{cu, pos0, ccap.data(), hd.data()};
+    const int n = (int)B;
+    for (int i = 0; i < 12; i++) out[i] = 0;
+    out[7] = T[0];
+    for (int k = 0; k < 2; k++) {
+        const int Tk = T[k];
+        const size_t nruns = (total + Tk - 1) / Tk;
+        int64_t *o = k == 0 ? out : out + 8;       // runs, keys, slots, pair_runs
+        std::vector<uint8_t> cover(total, 0), slot_used(nruns + B * nkv, 0);
+        std::vector<std::vector<int>> pair_seg_runs(B * nkv);
+        o[0] = (int64_t)nruns;
+        for (size_t run = 0; run < nruns; run++) {
+            int x = (int)(run * Tk), sg = 0;
+            const int x1 = (int)std::min<size_t>((size_t)x + Tk, total);
+            while (x < x1) {
+                Seg g;
+                int xn;
+                if (seg_at(m, n, (int)nkv, (int)run, x, x1, g, &xn)) {
+                    for (int g0 = g.k0; g0 < g.k1; g0 += 64) sg++;   // scores_seg's loop
+                    const size_t base = (size_t)g.abase / kRows;       // the pair's first key
+                    for (int key = g.k0; key < g.k1; key++) cover[base + key]++;
+                    if ((size_t)g.slot >= slot_used.size() || slot_used[g.slot]++)
+                        o[k == 0 ? 5 : 2]++;
+                    pair_seg_runs[(size_t)g.s * nkv + g.kvh].push_back((int)run);
+                }
+                x = xn;
+            }
+            if (k == 0) {
+                const int wg = run_groups(m, n, (int)nkv, (int)run, Tk, (int)total);
+                out[2] += wg;
+                out[3] += sg;
+                if (wg != sg) out[1]++;
+            }
+        }
+        int64_t bad_keys = 0, bad_pairs = 0;
+        for (size_t s = 0; s < B; s++)
+            for (size_t h = 0; h < nkv; h++) {
+                const int cap = ccap[s + 1] - ccap[s], ctx = pos0[s] + cu[s + 1] - cu[s];
+                const size_t base = nkv * (size_t)ccap[s] + h * cap;
+                for (int key = 0; key < cap; key++)
+                    if (cover[base + key] != (key < ctx ? 1 : 0)) bad_keys++;
+                int w0, w1;
+                pair_runs(m, (int)nkv, (int)s, (int)h, Tk, &w0, &w1);
+                const auto &r = pair_seg_runs[s * nkv + h];
+                bool ok = (int)r.size() == w1 - w0 + 1;
+                for (size_t i = 0; ok && i < r.size(); i++) ok = r[i] == w0 + (int)i;
+                if (!ok) bad_pairs++;
+            }
+        if (k == 0) {
+            out[4] = bad_keys;
+            out[6] = bad_pairs;
+        } else {
+            out[9] = bad_keys;
+            out[11] = bad_pairs;
+        }
+    }
+    return kOk;
 }
 
 static int cache_xfer(bool pack, const uint16_t *kc_ref, const uint16_t *vc_ref, uint16_t *ko,
@@ -1199,8 +1361,8 @@ int apus_hip_attn_cache_pack_paged(const uint16_t *kc_ref, const uint16_t *vc_re
                                    size_t nkv, size_t d, const ApusHipKvCache *kv, int32_t row) {
     APUS_READY();
     KvRef r;
-    if (int e = kv_of(kv, &r)) return e;
-    if (row < 0) return set_error(kErrArgument, "negative block-table row");
+    const int32_t cu1[2] = {0, (int32_t)std::min<size_t>(ntok, 0x7fffffff)}, p0[1] = {0};
+    if (int e = kv_paged_ref(kv, 1, &row, cu1, p0, &r)) return e;
     return cache_xfer(true, kc_ref, vc_ref, nullptr, nullptr, ntok, nkv, d, r, row);
 }
 
@@ -1208,8 +1370,8 @@ int apus_hip_attn_cache_unpack_paged(const ApusHipKvCache *kv, int32_t row, size
                                      size_t nkv, size_t d, uint16_t *kc_ref, uint16_t *vc_ref) {
     APUS_READY();
     KvRef r;
-    if (int e = kv_of(kv, &r)) return e;
-    if (row < 0) return set_error(kErrArgument, "negative block-table row");
+    const int32_t cu1[2] = {0, (int32_t)std::min<size_t>(ntok, 0x7fffffff)}, p0[1] = {0};
+    if (int e = kv_paged_ref(kv, 1, &row, cu1, p0, &r)) return e;
     return cache_xfer(false, nullptr, nullptr, kc_ref, vc_ref, ntok, nkv, d, r, row);
 }
 

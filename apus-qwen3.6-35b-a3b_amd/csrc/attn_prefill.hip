@@ -710,12 +710,9 @@ int apus_hip_attn_prefill_paged(const ApusHipAttnLayer *L, size_t B, const int32
                                 const uint16_t *k, const uint16_t *v, const ApusHipKvCache *kv,
                                 uint16_t *y) {
     APUS_READY();
-    if (!kv || !kv->k || !kv->v || !kv->block_table || kv->max_blocks == 0 ||
-        kv->max_blocks > 0x7fffffff)
-        return set_error(kErrArgument, "bad paged KV cache descriptor");
-    if (!rows) return set_error(kErrArgument, "NULL block-table rows");
-    return attn_prefill_kv(L, B, cu, pos0, rows, qg, k, v,
-                           KvRef{kv->k, kv->v, kv->block_table, (int32_t)kv->max_blocks}, y);
+    KvRef r;
+    if (int e = kv_paged_ref(kv, B, rows, cu, pos0, &r)) return e;
+    return attn_prefill_kv(L, B, cu, pos0, rows, qg, k, v, r, y);
 }
 
 }  // extern "C"

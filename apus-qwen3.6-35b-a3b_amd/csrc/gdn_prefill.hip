@@ -1066,6 +1066,11 @@ int apus_hip_gdn_prefill_noalloc(const ApusHipGdnLayer *L, size_t B, const int32
     APUS_READY();
     char *ws = (char *)noalloc_scratch();
     if (!ws) return set_error(kErrHip, "the allocation-free scratch of this device is not set up");
+    // a trace's intermediates would need library scratch (an allocation)
+    if (gdn_trace())
+        return set_error(kErrUnsupported,
+                         "the allocation-free prefill does not capture traces (clear the trace "
+                         "with apus_hip_trace_set first)");
     return gdn_prefill_run(L, B, cu, qkv, z, a, b, conv_state, S, y, nullptr, ws,
                            kNoAllocScratchBytes);
 }

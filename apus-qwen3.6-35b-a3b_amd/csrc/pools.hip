@@ -128,6 +128,8 @@ int apus_hip_kv_pool_cache(const ApusHipKvPool *p, size_t layer, ApusHipKvCache 
     out->v = p->v[layer];
     out->block_table = p->dtab;
     out->max_blocks = p->max_blocks;
+    out->max_rows = p->max_rows;
+    out->row_blocks = p->nused.data();
     return kOk;
 }
 
@@ -153,13 +155,16 @@ int apus_hip_kv_seq_reserve(ApusHipKvPool *p, int32_t row, size_t ntok) {
         return set_error(kErrUnsupported, "KV pool exhausted (%zu blocks free, %zu needed)",
                          p->free_blocks.size(), need - have);
     int32_t *ent = p->htab.data() + (size_t)row * p->max_blocks;
-    for (size_t b = have; b < need; b++) {
-        ent[b] = p->free_blocks.back();
-        p->free_blocks.pop_back();
-    }
+    const size_t nfree = p->free_blocks.size();
+    for (size_t b = have; b < need; b++) ent[b] = p->free_blocks[nfree - 1 - (b - have)];
+    // the device table first: if its update cannot be enqueued, the host
+    // bookkeeping stays as it was (the blocks remain free, the row its size)
+    if (int r = copy_to_device_async(p->dtab + (size_t)row * p->max_blocks + have, ent + have,
+                                     (need - have) * 4))
+        return r;
+    p->free_blocks.resize(nfree - (need - have));
     p->nused[row] = (int32_t)need;
-    return copy_to_device_async(p->dtab + (size_t)row * p->max_blocks + have, ent + have,
-                                (need - have) * 4);
+    return kOk;
 }
 
 int apus_hip_kv_seq_close(ApusHipKvPool *p, int32_t row) {

@@ -315,24 +315,35 @@ int open_shard(const std::string &path, std::unique_ptr<Shard> &out) {
         if (shp->arr.size() > APUS_HIP_ST_MAX_NDIM)
             return set_error(kErrArgument, "too many dimensions for %s", e.info.name);
         e.info.ndim = (int)shp->arr.size();
+        // JSON numbers are doubles: a dimension or an offset is accepted
+        // only as an integer below 2^53 (exact in a double, and the cast
+        // below is then defined), and the element count must not overflow
+        const double kMaxInt = 9007199254740992.0;   // 2^53
+        auto is_index = [&](const Json &x) {
+            return x.kind == Json::Num && x.num >= 0 && x.num < kMaxInt &&
+                   x.num == (double)(uint64_t)x.num;
+        };
         uint64_t nel = 1;
         for (int i = 0; i < e.info.ndim; i++) {
             const Json &x = shp->arr[i];
-            if (x.kind != Json::Num || x.num < 0 || x.num != (double)(int64_t)x.num)
-                return set_error(kErrArgument, "bad shape for %s", e.info.name);
+            if (!is_index(x)) return set_error(kErrArgument, "bad shape for %s", e.info.name);
             e.info.shape[i] = (int64_t)x.num;
-            nel *= (uint64_t)e.info.shape[i];
+            if (__builtin_mul_overflow(nel, (uint64_t)e.info.shape[i], &nel))
+                return set_error(kErrArgument, "element count of %s overflows", e.info.name);
         }
-        const double a = offs->arr[0].num, b = offs->arr[1].num;
-        if (offs->arr[0].kind != Json::Num || offs->arr[1].kind != Json::Num || a < 0 || b < a ||
-            base + (uint64_t)b > fsz)
+        if (!is_index(offs->arr[0]) || !is_index(offs->arr[1]))
+            return set_error(kErrArgument, "bad data_offsets for %s", e.info.name);
+        const uint64_t a = (uint64_t)offs->arr[0].num, b = (uint64_t)offs->arr[1].num;
+        if (b < a || base > fsz || b > fsz - base)
             return set_error(kErrArgument, "tensor %s lies past the end of %s", e.info.name,
                              path.c_str());
-        e.info.nbytes = (size_t)((uint64_t)b - (uint64_t)a);
-        if (esize && (uint64_t)e.info.nbytes != nel * (uint64_t)esize)
+        e.info.nbytes = (size_t)(b - a);
+        uint64_t want = 0;
+        if (esize && (__builtin_mul_overflow(nel, (uint64_t)esize, &want) ||
+                      (uint64_t)e.info.nbytes != want))
             return set_error(kErrArgument, "tensor %s: %zu bytes for %llu elements of %s",
                              e.info.name, e.info.nbytes, (unsigned long long)nel, dt->str.c_str());
-        e.off = base + (uint64_t)a;
+        e.off = base + a;
         sh->tensors[kv.first] = e;
     }
     out = std::move(sh);

@@ -31,11 +31,12 @@ The CPU leg (skipped with --no-cpu) does two things per configuration:
     (oracle/, the C restatement of the reference anchors); the line reports
     the measured worst case (normwise relative error, bf16 ulps, fraction of
     bit-identical outputs, state error) against the north star's bars;
-  * cpu_baseline: the reference's own scalar anchors (oracle/_ref, built
-    from the reference sources; the repo's restatement when absent or above
-    the reference pool's 32 lanes) timed on the host cores on a bounded
-    sample of each configuration, at min(32, cores) threads and at all the
-    cores this process may use.
+  * cpu_baseline: the repo's C restatement of the reference's scalar
+    anchors (oracle/apus_oracle.c, pinned bitwise to the reference's own
+    c/gdn.h / c/attn.h by the CPU tests; kind "port") timed on the host
+    cores on a bounded sample of each configuration, at min(32, cores)
+    threads (the reference pool's lane cap) and at all the cores this
+    process may use.
 """
 import argparse
 import json
@@ -49,7 +50,7 @@ import numpy as np
 
 ROOT = os.path.dirname(os.path.abspath(__file__))
 PKG = os.path.join(ROOT, "apus-qwen3.6-35b-a3b_amd")
-for p in (PKG, os.path.join(ROOT, "oracle")):
+for p in (PKG, os.path.join(ROOT, "oracle"), os.path.join(ROOT, "tests")):
     if p not in sys.path:
         sys.path.insert(0, p)
 
@@ -414,10 +415,12 @@ def bench_gdn_prefill(torch, T, steps, warmup, seed, leg=None):
 
 # Algorithmic flops per (chunk of 64, v-head) of the two chunk kernels:
 # the scan does W S0, Q S0, K^T D (64x128x128 each) and A D (64x64x128);
-# the WY build does K K^T, Q K^T (64x64x128) and the two 64x64x128
-# triangular applications giving U and W, plus the triangular solve.
+# the WY build does K K^T, Q K^T (64x64x128, on the q/k codes shared by the
+# two v-heads of a K head, so half of each per v-head unit) and the two
+# 64x64x128 triangular applications giving U and W, plus the triangular
+# solve.
 SCAN_FLOPS_PER_UNIT = 3 * 2 * 64 * 128 * 128 + 2 * 64 * 64 * 128
-WY_FLOPS_PER_UNIT = 4 * 2 * 64 * 64 * 128 + (2 * 64 ** 3) // 3
+WY_FLOPS_PER_UNIT = 3 * 2 * 64 * 64 * 128 + (2 * 64 ** 3) // 3
 # MFMA flops the kernels execute for them: the scan's W S0 and A D take
 # three MFMAs per product (both operands split), Q S0 and K^T D two (q, k
 # as exact codes); WY's K K^T and Q K^T one (codes), T R two, and the
@@ -780,16 +783,18 @@ def _code_pool(rng, n):
 
 def cpu_worker(threads):
     """Child process (APUS_THREADS / OMP_NUM_THREADS = threads): time each
-    configuration's bounded sample on the reference's anchors (or the
-    oracle port above the reference pool's 32 lanes) and print one JSON
+    configuration's bounded sample on the oracle port (the C restatement
+    of the reference's anchors) and print one JSON
     line per configuration: seconds measured, and the config's tokens per
     second derived from them (rule in "rule")."""
     import oracle
     import synth
-    use_ref = oracle.Reference.available() and threads <= REF_POOL_MAX
-    lib = oracle.Reference() if use_ref else oracle.Oracle()
-    kind = "reference" if use_ref else "port"
-    kw = {} if use_ref else dict(nthreads=threads)
+    # the repo's C restatement of the anchors (pinned bitwise to the
+    # reference's own c/gdn.h / c/attn.h in the CPU tests); reference code
+    # itself never travels to the GPU box
+    lib = oracle.Oracle()
+    kind = "port"
+    kw = dict(nthreads=threads)
     rng = np.random.default_rng(1)
     w = synth.gdn_weights(rng)
     aw = synth.attn_weights(rng)
@@ -896,7 +901,7 @@ def cpu_baseline(head):
     c = first["configs"][head]
     return dict(value=c["tok_s"], unit="tok/s", cores=first["threads"], kind=first["kind"],
                 sample=(f"config {head}: {c['rule']}; "
-                        f"{'the reference c/gdn.h + c/attn.h anchors (oracle/_ref)' if first['kind'] == 'reference' else 'the repo oracle port'}"
+                        "the repo oracle port (oracle/apus_oracle.c, bitwise-pinned to c/gdn.h + c/attn.h)"
                         f" with {first['threads']} threads on {cpu_model()}"),
                 nproc=os.cpu_count(), usable_cores=n, cgroup_cpus=_cgroup_cpus(),
                 cpu_model=cpu_model(),

@@ -51,6 +51,23 @@ size_t apus_hip_last_error(char *buf, size_t cap);
 /* stream is a hipStream_t passed as void* (NULL = the null stream) */
 int    apus_hip_set_stream(void *stream);
 int    apus_hip_synchronize(void);
+/* Bounded device waits (no counterpart in the reference, whose ops run on
+ * one host thread): a kernel whose wavefronts wait on each other (the
+ * decode score ring) gives up after `polls` polls, marks the call failed
+ * and exits normally; apus_hip_synchronize then returns APUS_HIP_ERR_HIP
+ * naming the kernel. 0 restores the default (2^22 polls, about a quarter
+ * of a second). A tiny limit exists to test the error path. */
+int    apus_hip_set_spin_limit(uint32_t polls);
+/* Host-only check of the decode split plan (no device needed; no
+ * counterpart in the reference): for B sequences of 1..4 new tokens after
+ * pos0[s] cached, nkv kv heads and `cus` compute units, walks the runs the
+ * decode kernels would be given and fills out[12] (see attn_mixer.hip):
+ * out[1] counts runs whose two group enumerations of the score ring
+ * disagree, out[4]/out[9] keys missed or covered twice, out[5]/out[10]
+ * slot collisions, out[6]/out[11] mismatched pair run ranges -- all zero
+ * for a sound plan. */
+int    apus_hip_attn_split_check(size_t B, const int32_t *cu, const int32_t *pos0,
+                                 size_t nkv, size_t cus, int64_t *out);
 /* Device memory for hosts that do not link HIP themselves (state, KV). */
 int    apus_hip_malloc(void **dptr, size_t bytes);
 int    apus_hip_free(void *dptr);
@@ -239,12 +256,14 @@ int apus_hip_gdn_decode_slots(const ApusHipGdnLayer *L, size_t B,
 /* Chunked GDN prefill: the same layer and arguments as apus_hip_gdn_decode
  * for sequences of any length (c/layer.h:427-492, the prompt path; the
  * reference steps the recurrence token by token, c/gdn.h:627-635). The
- * recurrence runs in chunks of 64 tokens in the WY/UT form on fp32 MFMA:
- * conv_state and the token-parallel ops equal the reference anchors up to
- * libm ulps; S and y are a tolerance class of the sequential recurrence
- * (state within 1e-4 relative, y within bf16 rounding of the sequential
- * result). Library scratch grows with the token count (about 80 KiB per
- * chunk of 64 tokens per v-head). */
+ * recurrence runs in chunks of 64 tokens in the WY/UT form on the bf16
+ * MFMA with fp32 accumulation, every fp32 operand split into hi/lo bf16
+ * parts (q and k enter as their exact bf16 conv codes): conv_state and the
+ * token-parallel ops equal the reference anchors up to libm ulps; S and y
+ * are a tolerance class of the sequential recurrence (state within 1e-4
+ * relative, y within bf16 rounding of the sequential result). Library
+ * scratch grows with the token count: about 96 KiB per (chunk of 64
+ * tokens, v-head) plus 8 KiB per token. */
 int apus_hip_gdn_prefill(const ApusHipGdnLayer *L, size_t B,
                          const int32_t *cu, const uint16_t *qkv,
                          const uint16_t *z, const uint16_t *a,
@@ -261,7 +280,8 @@ int apus_hip_gdn_prefill(const ApusHipGdnLayer *L, size_t B,
  * (sequence, chunk of 64 tokens), so one sequence of up to ~1700 tokens
  * (longer prompts are prefilled in successive calls: the state carries
  * over); at most 400 sequences and no slot map. A larger call returns
- * APUS_HIP_ERR_UNSUPPORTED with the size it needs. Calls on one GPU share
+ * APUS_HIP_ERR_UNSUPPORTED with the size it needs; so does a call made
+ * while a GDN trace is set (capturing it would allocate). Calls on one GPU share
  * that GPU's scratch: calls that overlap (two streams) race. */
 int apus_hip_gdn_prefill_noalloc(const ApusHipGdnLayer *L, size_t B,
                                  const int32_t *cu, const uint16_t *qkv,
@@ -310,11 +330,18 @@ int apus_hip_attn_cache_unpack(const uint16_t *kcache, const uint16_t *vcache,
  * entry [h][b] is the id of block b of the sequence at table row h. The
  * *_paged calls take, per sequence of the batch, its table row (HOST array
  * rows[B]); a sequence may use blocks 0 .. ceil((pos0+new)/32) - 1 of its
- * row. apus_hip_kv_pool_* below manage such a cache. */
+ * row. apus_hip_kv_pool_* below manage such a cache. The table has
+ * max_rows rows; a call naming a row >= max_rows is refused. row_blocks
+ * (HOST array [max_rows], nullable) holds the blocks each row has
+ * reserved (-1: row closed); when set, a call whose new tokens reach past
+ * a row's reserved blocks is refused instead of writing through stale
+ * table entries. apus_hip_kv_pool_cache fills both. */
 typedef struct {
     uint16_t *k, *v;
     const int32_t *block_table;
     size_t max_blocks;
+    size_t max_rows;
+    const int32_t *row_blocks;
 } ApusHipKvCache;
 int apus_hip_attn_cache_pack_paged(const uint16_t *kc_ref, const uint16_t *vc_ref,
                                    size_t ntok, size_t nkv, size_t d,

@@ -60,13 +60,13 @@ def attn_esc_rows(qf_rows, K, V, qpos, nh, nkv, d, chunk=128, flips=True, rel=BF
             Kf = bf16_f32(K[:npos, hk]).astype(np.float64)
             Vf = np.abs(bf16_f32(V[:npos, hk]).astype(np.float64))
             qh = q[:, hk * grp:(hk + 1) * grp]
-            s = np.einsum("thd,kd->thk", qh, Kf)
+            s = qh @ Kf.T                       # (BLAS; same values as the einsum)
             A = np.where(masked, -np.inf, s * scale)
             P = np.exp(A - A.max(2, keepdims=True))
             P /= P.sum(2, keepdims=True)
             e = P @ Vf
             if flips:
-                tabs = np.einsum("thd,kd->thk", np.abs(qh), np.abs(Kf))
+                tabs = np.abs(qh) @ np.abs(Kf).T
                 dist, ulp = _midpoint_dist(s)
                 sflip = dist <= 2.0 * d * _U * tabs
                 dS = np.where(sflip & ~masked, P * np.expm1(ulp * scale), 0.0)

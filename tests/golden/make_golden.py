@@ -17,7 +17,8 @@ import numpy as np
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(os.path.dirname(HERE))
-sys.path[:0] = [os.path.join(ROOT, "oracle"), os.path.join(ROOT, "apus-qwen3.6-35b-a3b_amd")]
+sys.path[:0] = [os.path.join(ROOT, "oracle"), os.path.join(ROOT, "apus-qwen3.6-35b-a3b_amd"),
+                os.path.dirname(HERE)]
 
 import oracle  # noqa: E402
 import synth   # noqa: E402

@@ -78,3 +78,43 @@ def test_decode_config2_shape(hip, orc):
     """BASELINE config 2 per sequence: 32K-token cache, one new token
     (two sequences here; the bench runs 64)."""
     _run(hip, orc, np.random.default_rng(3), [0, 1, 2], [32767, 32767], 32768)
+
+
+
+def test_scores_wait_limit_reports_error(hip, orc):
+    """The score ring's producer / consumer waits are bounded: with the
+    limit forced to one poll from the host the waits give up, every wave
+    still exits, and apus_hip_synchronize reports the failed call (its
+    output is not checked: the scores were never stored). Ten sequences of
+    32000 cached keys give every scores wavefront a run of at least four
+    64-key groups, more than its 3-slot ring holds, so the writer needs a
+    second poll and the limit of one expires on every launch. With the
+    default limit restored a small call is correct again (and the fault
+    word was cleared by the report)."""
+    import torch
+    dims = synth.ATTN_DIMS
+    nh, nkv, d, rot, theta = dims
+    rng = np.random.default_rng(11)
+    B, max_seq = 10, 32768
+    cu, pos0 = list(range(B + 1)), [32000] * B
+    plan = hip.attn_split_check(np.array(cu, np.int32), np.array(pos0, np.int32))
+    assert plan["T1"] >= 4 * 64, plan
+    dev = torch.device("cuda")
+    td = lambda a: torch.from_numpy(np.ascontiguousarray(a).view(np.int16)).to(dev)
+    layer = hip.attn_layer(dims, {k: td(v) for k, v in synth.attn_weights(rng).items()})
+    t = {k: td(v) for k, v in synth.attn_tokens(rng, B).items()}
+    dk = torch.zeros((B, nkv, max_seq, d), dtype=torch.int16, device=dev)
+    dv = torch.zeros((B, nkv, max_seq // 32, d, 32), dtype=torch.int16, device=dev)
+    y = torch.empty((B, nh * d), dtype=torch.int16, device=dev)
+    hip.synchronize()
+    hip.set_spin_limit(1)
+    try:
+        hip.attn_decode(layer, cu, pos0, t["qg"], t["k"], t["v"], dk, dv, max_seq, y)
+        with pytest.raises(hip.ApusHipError, match="bounded wait"):
+            hip.synchronize()
+    finally:
+        hip.set_spin_limit(0)
+    hip.synchronize()                     # the report cleared the fault word
+    del dk, dv
+    _run(hip, orc, np.random.default_rng(11), [0, 1, 3], [3000, 1700], 3072)
+    hip.synchronize()

@@ -175,9 +175,16 @@ def test_attn_prefill_b260(hip, orc):
     print(f"[attn prefill B=260] {st}", flush=True)
 
 
-SAMPLE_BLOCKS = ((0, 64), (2047, 2111), (4096, 4160), (8128, 8192))
+# 17 blocks of 64 query rows over the whole prompt (every 8th 64-row tile
+# and its odd 32-row offsets, so both halves of the kernel's 32-token query
+# tiles are sampled): the first tile, rows just past every 2048 boundary,
+# a block straddling one (2016..2079), and the last diagonal tile, with
+# all 16 heads (both kv heads) of each row checked.
+SAMPLE_BLOCKS = tuple((r, r + 64) for r in (0, 544, 1056, 1568, 2016, 2048, 2592, 3104, 3616,
+                                             4096, 4640, 5152, 6144, 6688, 7200, 7712, 8128))
 
 
+@pytest.mark.timeout(400)
 def test_config3_full_sampled(hip, orc):
     """T=8192 causal prefill from position 0. The whole
     cache fill bit-exact; outputs of all 16 heads on the sampled row
