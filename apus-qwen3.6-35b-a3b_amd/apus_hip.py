@@ -51,6 +51,8 @@ EXPORTS = [
     "apus_hip_st_read", "apus_hip_gdn_layer_load", "apus_hip_attn_layer_load",
     "apus_hip_gdn_layer_free", "apus_hip_attn_layer_free", "apus_hip_trace_set",
     "apus_hip_gdn_prefill_noalloc", "apus_hip_set_spin_limit", "apus_hip_attn_split_check",
+    "apus_hip_gdn_layer_decode", "apus_hip_gdn_layer_decode_slots",
+    "apus_hip_attn_layer_decode", "apus_hip_attn_layer_decode_paged",
 ]
 
 
@@ -77,6 +79,18 @@ class AttnLayer(C.Structure):
     """ApusHipAttnLayer (include/apus_hip.h)."""
     _fields_ = [("nh", _sz), ("nkv", _sz), ("d", _sz), ("rot", _sz), ("theta", C.c_double),
                 ("qn_w", _vp), ("kn_w", _vp)]
+
+
+class GdnProj(C.Structure):
+    """ApusHipGdnProj (include/apus_hip.h): a GDN layer's projections."""
+    _fields_ = [("hidden", _sz), ("w_qkv", _vp), ("w_z", _vp), ("w_b", _vp), ("w_a", _vp),
+                ("w_out", _vp)]
+
+
+class AttnProj(C.Structure):
+    """ApusHipAttnProj (include/apus_hip.h): a full-attention layer's
+    projections."""
+    _fields_ = [("hidden", _sz), ("wq", _vp), ("wk", _vp), ("wv", _vp), ("wo", _vp)]
 
 
 _lib = None
@@ -497,6 +511,63 @@ def gdn_decode_slots(layer, slot_in, slot_out, cu, qkv, z, a, b, conv, S, y):
     _chk(load().apus_hip_gdn_decode_slots(C.byref(layer), _sz(B), sip, sop, cup, _dp(qkv), _dp(z),
                                           _dp(a), _dp(b), C.c_void_p(conv), C.c_void_p(S),
                                           _dp(y)))
+
+
+def gdn_proj(hidden, w):
+    """ApusHipGdnProj from a dict of device tensors w_qkv, w_z, w_b, w_a,
+    w_out (int16 views of bf16, reference layouts); keeps them alive."""
+    for k in ("w_qkv", "w_z", "w_b", "w_a", "w_out"):
+        assert w[k].is_cuda and w[k].is_contiguous(), k
+    p = GdnProj(hidden, w["w_qkv"].data_ptr(), w["w_z"].data_ptr(), w["w_b"].data_ptr(),
+                w["w_a"].data_ptr(), w["w_out"].data_ptr())
+    p._tensors = dict(w)
+    return p
+
+
+def attn_proj(hidden, w):
+    """ApusHipAttnProj from device tensors wq, wk, wv, wo."""
+    for k in ("wq", "wk", "wv", "wo"):
+        assert w[k].is_cuda and w[k].is_contiguous(), k
+    p = AttnProj(hidden, w["wq"].data_ptr(), w["wk"].data_ptr(), w["wv"].data_ptr(),
+                 w["wo"].data_ptr())
+    p._tensors = dict(w)
+    return p
+
+
+def gdn_layer_decode(layer, proj, cu, ln1, conv, S, ao):
+    """GDN layer with projections: ln1 [T, H] -> ao [T, H] (flat states)."""
+    cu, cup, B = _cu_arr(cu)
+    _chk(load().apus_hip_gdn_layer_decode(C.byref(layer), C.byref(proj), _sz(B), cup, _dp(ln1),
+                                          _dp(conv), _dp(S), _dp(ao)))
+
+
+def gdn_layer_decode_slots(layer, proj, slot_in, slot_out, cu, ln1, conv, S, ao):
+    """As gdn_layer_decode on a state pool (conv, S: the slot arrays' base
+    addresses as ints)."""
+    cu, cup, B = _cu_arr(cu)
+    si, sip = _i32arr(slot_in)
+    so, sop = _i32arr(slot_out)
+    _chk(load().apus_hip_gdn_layer_decode_slots(C.byref(layer), C.byref(proj), _sz(B), sip, sop,
+                                                cup, _dp(ln1), C.c_void_p(conv), C.c_void_p(S),
+                                                _dp(ao)))
+
+
+def attn_layer_decode(layer, proj, cu, pos0, ln1, kcache, vcache, max_seq, ao):
+    """Full-attention layer with projections on a flat cache."""
+    cu, cup, B = _cu_arr(cu)
+    pos0, pp = _i32arr(pos0)
+    _chk(load().apus_hip_attn_layer_decode(C.byref(layer), C.byref(proj), _sz(B), cup, pp,
+                                           _dp(ln1), _dp(kcache), _dp(vcache), _sz(max_seq),
+                                           _dp(ao)))
+
+
+def attn_layer_decode_paged(layer, proj, rows, cu, pos0, ln1, kv, ao):
+    """Full-attention layer with projections on a paged cache."""
+    cu, cup, B = _cu_arr(cu)
+    rows, rp = _i32arr(rows)
+    pos0, pp = _i32arr(pos0)
+    _chk(load().apus_hip_attn_layer_decode_paged(C.byref(layer), C.byref(proj), _sz(B), rp, cup,
+                                                 pp, _dp(ln1), C.byref(kv), _dp(ao)))
 
 
 def gdn_prefill_slots(layer, slots, cu, qkv, z, a, b, conv, S, y):

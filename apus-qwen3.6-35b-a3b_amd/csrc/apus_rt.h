@@ -59,6 +59,9 @@ enum ScratchSlot { kScratchIn = 0, kScratchIn2, kScratchIn3, kScratchIn4,
                    // batched attention mixer intermediates
                    kScratchAttnQ, kScratchAttnA, kScratchAttnStat,
                    kScratchAttnPart,
+                   // layer entry points: projection outputs, mixer output
+                   kScratchLayerA, kScratchLayerB, kScratchLayerC, kScratchLayerD,
+                   kScratchLayerY,
                    kScratchSlots };
 void *scratch(int slot, size_t bytes);
 

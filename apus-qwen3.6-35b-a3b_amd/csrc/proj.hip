@@ -12,13 +12,15 @@
 //                against the reference. The weight row is read 16 bytes
 //                at a time, 16 to 32 pieces ahead of the add chain; the x row
 //                is staged in LDS once per wavefront.
-//   k_gemm_mfma  the 16x16x32 bf16 MFMA with fp32 accumulation for
-//                decode batches (up to kMfmaRows rows): one workgroup per
-//                (64 outputs, 64 rows), its 4 wavefronts splitting K, so
-//                each weight piece is loaded once per row tile. Larger
-//                batches (prefill) go to rocBLAS's bf16 GEMM (fp32
-//                compute), a plain library GEMM. Both sum in their own order:
-//                the tolerance class of the attention kernels (|c - r| <=
+//   k_gemm_tile  the 32x32x16 bf16 MFMA with fp32 accumulation, for every
+//                row count: a workgroup computes a (BO outputs x BM rows)
+//                tile, its operands copied global -> LDS by buffer_load ...
+//                lds in stages of 32 k through a 4-deep ring; each
+//                wavefront reads the next k16 step's fragments while the
+//                current step's MFMAs issue. Tile shapes are chosen per call
+//                shape (decode batches: small tiles, many workgroups;
+//                prefill: 256 x 256). It sums in its own order: the
+//                tolerance class of the attention kernels (|c - r| <=
 //                2e-3 (|r| + esc), esc = sum_k |w x|).
 // Host-pointer drop-ins keep device copies of the weights keyed by their
 // host address, as the reference's Metal backend keys weights by stable
@@ -28,11 +30,10 @@
 
 #include <unordered_map>
 
-#include <rocblas/rocblas.h>
-
 #include "../../include/apus_hip.h"
 #include "apus_dev.h"
 #include "apus_host.h"
+#include "proj.h"
 
 using namespace apus;
 
@@ -109,99 +110,223 @@ __global__ __launch_bounds__(64) void k_gemm_seq(const uint16_t *__restrict__ w,
     if (o < O) y[(size_t)m * O + o] = f2bf(acc);
 }
 
-// One workgroup per (64 outputs, up to 64 rows); its 4 wavefronts split K
-// (32-wide k step st goes to wavefront st % 4), each with all 4 x 4
-// 16x16 output blocks, the next step's operands in flight, and add their
-// partial sums through LDS. Operands come through buffer loads whose rows
-// past M or O sit out of the buffer's range and read as zero, so every
-// load and MFMA is unconditional (no branch joins for the compiler to
-// drain the memory counter at). Needs K % 32 == 0.
-constexpr int MT = 64, OT = 64, MB = MT / 16, OB = OT / 16, NWV = 4;
-constexpr int kOutOfRange = 0x40000000;   // a byte offset past every operand
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 
-__global__ __launch_bounds__(256) void k_gemm_mfma(const uint16_t *__restrict__ w,
-                                                   const uint16_t *__restrict__ x,
-                                                   uint16_t *__restrict__ y, int M, int O, int K) {
+__device__ __forceinline__ uint32_t pk2(float a, float b) {
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{a, b}, bf16x2));
+}
+int check_dims(size_t M, size_t O, size_t K) {
+    if (M > 0x7fffffffu || O > 0x7fffffffu || K > 0x7fffffffu)
+        return set_error(kErrUnsupported, "gemm dims past 2^31");
+    return kOk;
+}
+
+// byte offset of 16-byte chunk c (0..3) of row r in a stage's 64-byte rows:
+// chunks are XOR-swizzled by (r / 4) % 4, so the 32 rows one MFMA operand
+// read touches spread over the LDS banks
+__device__ __forceinline__ int tile_slot(int r, int c) { return r * 64 + ((c ^ ((r >> 2) & 3)) << 4); }
+
+constexpr int kTileStages = 4;            // LDS ring depth (stages of 32 k)
+
+__device__ __forceinline__ int seg_of(const GemmSegs &g, int o) {
+    int i = 0;
+#pragma unroll
+    for (int j = 1; j < kMaxSegs; j++)
+        if (j < g.n && o >= g.row0[j]) i = j;
+    return i;
+}
+
+// y[m][o] = rnd(sum_k w[o][k] x[m][k]) on the 32x32x16 bf16 MFMA. The
+// workgroup has WO x WM wavefronts; wavefront (wo, wm) = (wave / WM,
+// wave % WM) -- so the WM wavefronts sharing output columns sit on
+// different SIMDs -- computes TO x TMM MFMA tiles: outputs
+// o0 + 32 (TO wo + t) .., rows m0 + 32 (TMM wm + u) ... The product is
+// formed transposed (D[o][m]: A = w rows, B = x rows) so that a lane holds
+// 4 consecutive outputs of one row and stores them as 8 bytes.
+// Stages: each stage's w rows (BO x 64 B) and x rows (BM x 64 B) are copied
+// global -> LDS in 1 KiB pieces (16 rows each; lane L fills byte 16 L of
+// the piece: row L / 4, chunk (L % 4) ^ ((row / 4) % 4)); rows past O or M
+// lie past their buffer's end and read zero. Stage s is issued ST - 1
+// stages ahead, unconditionally (past the last stage the copy re-reads
+// it), so every wait is a constant count; one barrier per stage. MFMAs of
+// tiles wholly past O or M are skipped (wave-uniform).
+// Workgroup order: the row tiles of an output tile are dealt to one XCD
+// (block ids congruent mod 8), so they share its w rows in that XCD's L2.
+template <int WO, int WM, int TO, int TMM>
+__global__ __launch_bounds__(64 * WO * WM) void k_gemm_tile(GemmSegs sg,
+                                                       const uint16_t *__restrict__ x, int M,
+                                                       int K) {
+    const int O = sg.row0[sg.n];
+    constexpr int ST = kTileStages;
+    constexpr int NW = WO * WM, BO = 32 * TO * WO, BM = 32 * TMM * WM;
+    constexpr int PB = BO * 64, SB = (BO + BM) * 64;
+    constexpr int NPIECE = (BO + BM) / 16;
+    static_assert(NPIECE % NW == 0, "copy pieces must split evenly over the wavefronts");
+    constexpr int PPW = NPIECE / NW;
+    __shared__ __attribute__((aligned(16))) char sm[ST * SB];
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int r16 = lane & 15, g8 = (lane >> 4) * 8, kq = (lane >> 4) * 4;
-    const int o0 = blockIdx.x * OT, m0 = blockIdx.y * MT;
-    const auto wr = buf_rsrc(w, (uint32_t)((size_t)O * K * 2));
-    const auto xr = buf_rsrc(x, (uint32_t)((size_t)M * K * 2));
-    int woff[OB], xoff[MB];
+    const int wo = wave / WM, wm = wave % WM;
+    const int nbo = (O + BO - 1) / BO, nbm = (M + BM - 1) / BM;
+    const int id = blockIdx.x;
+    const int band = id / (8 * nbm), rem = id % (8 * nbm);
+    const int mb = rem / 8, ob = band * 8 + rem % 8;
+    if (ob >= nbo) return;                      // (the grid rounds bands up to 8)
+    const int o0 = ob * BO, m0 = mb * BM;
+    const uint32_t lds0 = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(lds_void *)sm);
+    // this wave's copy pieces: the buffer of each (x, or its weight
+    // segment; wave-uniform) and each lane's byte offset in it
+    i32x4 rs[PPW];
+    int voff[PPW];
+    uint32_t loff[PPW];
 #pragma unroll
-    for (int c = 0; c < OB; c++) {
-        const int o = o0 + c * 16 + r16;
-        woff[c] = o < O ? (o * K + g8) * 2 : kOutOfRange;
+    for (int i = 0; i < PPW; i++) {
+        const int p = wave * PPW + i;
+        const bool pw = p < BO / 16;
+        const int pr = pw ? p : p - BO / 16;
+        const int r = pr * 16 + lane / 4;
+        const int c = (lane & 3) ^ ((r >> 2) & 3);
+        if (pw) {
+            const int si = __builtin_amdgcn_readfirstlane(seg_of(sg, o0 + pr * 16));
+            const int rows = sg.row0[si + 1] - sg.row0[si], gr = o0 + r - sg.row0[si];
+            rs[i] = dma_rsrc(sg.w[si], (uint32_t)((size_t)rows * K * 2));
+            voff[i] = gr < rows ? (gr * K + c * 8) * 2 : 0x7fffffff;
+        } else {
+            rs[i] = dma_rsrc(x, (uint32_t)((size_t)M * K * 2));
+            voff[i] = m0 + r < M ? ((m0 + r) * K + c * 8) * 2 : 0x7fffffff;
+        }
+        loff[i] = pw ? pr * 1024 : PB + pr * 1024;
     }
+    const int nk = K / 32;
+    auto issue = [&](int st) {
+        const int kb = min(st, nk - 1) * 64;
+        const uint32_t base = lds0 + (st % ST) * SB;
 #pragma unroll
-    for (int b = 0; b < MB; b++) {
-        const int m = m0 + b * 16 + r16;
-        xoff[b] = m < M ? (m * K + g8) * 2 : kOutOfRange;
-    }
-    f32x4 acc[MB][OB];
-#pragma unroll
-    for (int b = 0; b < MB; b++)
-#pragma unroll
-        for (int c = 0; c < OB; c++) acc[b][c] = f32x4{0.f, 0.f, 0.f, 0.f};
-    const int nsteps = K / 32;
-    bf16x8 bw[OB], ax[MB];
-    // step st's operands; steps past K are clamped to the last (loaded,
-    // not used)
-    auto load = [&](int st) {
-        const int kb = min(st, nsteps - 1) * 64;
-#pragma unroll
-        for (int c = 0; c < OB; c++)
-            bw[c] = __builtin_bit_cast(bf16x8, llvm_raw_ptr_buffer_load_v4f32(wr, woff[c] + kb, 0, 0));
-#pragma unroll
-        for (int b = 0; b < MB; b++)
-            ax[b] = __builtin_bit_cast(bf16x8, llvm_raw_ptr_buffer_load_v4f32(xr, xoff[b] + kb, 0, 0));
+        for (int i = 0; i < PPW; i++) dma16(rs[i], voff[i], kb, base + loff[i]);
     };
-    load(wave);
-    for (int st = wave; st < nsteps; st += NWV) {
-        bf16x8 bc[OB], ac[MB];
+    f32x16 acc[TO][TMM];
 #pragma unroll
-        for (int c = 0; c < OB; c++) bc[c] = bw[c];
+    for (int t = 0; t < TO; t++)
 #pragma unroll
-        for (int b = 0; b < MB; b++) ac[b] = ax[b];
-        load(st + NWV);
-        asm volatile("" ::: "memory");
-        __builtin_amdgcn_sched_barrier(0);
+        for (int u = 0; u < TMM; u++) acc[t][u] = f32x16{};
+    auto rd = [&](int kt, int s, bf16x8 (&af)[TO], bf16x8 (&bf)[TMM]) {
+        const char *Wl = sm + (kt % ST) * SB;
+        const char *Xl = Wl + PB;
+        const int c = s * 2 + (lane >> 5);
 #pragma unroll
-        for (int b = 0; b < MB; b++)
+        for (int t = 0; t < TO; t++)
+            af[t] = *reinterpret_cast<const bf16x8 *>(Wl + tile_slot(wo * TO * 32 + t * 32 + (lane & 31), c));
 #pragma unroll
-            for (int c = 0; c < OB; c++)
-                acc[b][c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ac[b], bc[c], acc[b][c], 0, 0, 0);
-    }
-    // the partial sums of the 4 wavefronts through LDS, added in wavefront
-    // order; wavefront v then finishes row block v
-    __shared__ f32x4 part[NWV][MB][OB][64];
+        for (int u = 0; u < TMM; u++)
+            bf[u] = *reinterpret_cast<const bf16x8 *>(Xl + tile_slot(wm * TMM * 32 + u * 32 + (lane & 31), c));
+    };
+    const int tv = min(TO, max(0, (O - (o0 + wo * TO * 32) + 31) / 32));
+    const int uv = min(TMM, max(0, (M - (m0 + wm * TMM * 32) + 31) / 32));
+    auto mma = [&](const bf16x8 (&af)[TO], const bf16x8 (&bf)[TMM]) {
 #pragma unroll
-    for (int b = 0; b < MB; b++)
+        for (int t = 0; t < TO; t++)
 #pragma unroll
-        for (int c = 0; c < OB; c++) part[wave][b][c][lane] = acc[b][c];
+            for (int u = 0; u < TMM; u++)
+                if (t < tv && u < uv)
+                    acc[t][u] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[t], bf[u], acc[t][u], 0, 0, 0);
+    };
+#pragma unroll
+    for (int s = 0; s < ST - 1; s++) issue(s);
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(PPW * (ST - 2)) : "memory");
     __syncthreads();
-    const int b = wave;
+    issue(ST - 1);
+    bf16x8 fa0[TO], fb0[TMM], fa1[TO], fb1[TMM];
+    rd(0, 0, fa0, fb0);
+    // the scheduling barriers keep each phase's LDS reads ahead of the
+    // MFMAs that do not need them (left free, the scheduler sank them to
+    // their first use)
+    for (int kt = 0; kt < nk; kt++) {
+        rd(kt, 1, fa1, fb1);
+        __builtin_amdgcn_sched_barrier(0);
+        mma(fa0, fb0);
+        __builtin_amdgcn_sched_barrier(0);
+        // stage kt+1 landed (this wave's copies), then visible to all; every
+        // wave is past its reads of stage kt, whose slot the next issue fills
+        asm volatile("s_waitcnt vmcnt(%0)" ::"n"(PPW * (ST - 2)) : "memory");
+        __syncthreads();
+        issue(kt + ST);
+        rd(kt + 1, 0, fa0, fb0);
+        __builtin_amdgcn_sched_barrier(0);
+        mma(fa1, fb1);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    // D[o][m]: lane -> m = lane % 32, o = 8 (i / 4) + 4 (lane / 32) + i % 4;
+    // each 32-output tile lies in one segment
 #pragma unroll
-    for (int c = 0; c < OB; c++) {
-        f32x4 s = part[0][b][c][lane];
+    for (int t = 0; t < TO; t++) {
+        const int ot = o0 + wo * TO * 32 + t * 32;
+        if (ot >= O) continue;
+        const int si = seg_of(sg, ot);
+        uint16_t *yb = sg.y[si] - sg.row0[si];
+        const int ld = sg.ldy[si];
+        const bool vec = ((ld | sg.row0[si]) & 3) == 0 && ((uintptr_t)sg.y[si] & 7) == 0;
 #pragma unroll
-        for (int v = 1; v < NWV; v++) s += part[v][b][c][lane];
-        // D[row kq + i][column r16]: row m0 + 16b + kq + i, output o0 + 16c + r16
-        const int o = o0 + c * 16 + r16;
-        if (o < O) {
+        for (int u = 0; u < TMM; u++) {
+            const int m = m0 + wm * TMM * 32 + u * 32 + (lane & 31);
+            if (m >= M) continue;
+            const f32x16 &a = acc[t][u];
 #pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const int m = m0 + b * 16 + kq + i;
-                if (m < M) y[(size_t)m * O + o] = f2bf(s[i]);
+            for (int q = 0; q < 4; q++) {
+                const int o = ot + 8 * q + 4 * (lane >> 5);
+                if (vec) {
+                    if (o < O)
+                        *reinterpret_cast<uint2 *>(yb + (size_t)m * ld + o) =
+                            make_uint2(pk2(a[4 * q], a[4 * q + 1]), pk2(a[4 * q + 2], a[4 * q + 3]));
+                } else {
+#pragma unroll
+                    for (int i = 0; i < 4; i++)
+                        if (o + i < O) yb[(size_t)m * ld + o + i] = f2bf(a[4 * q + i]);
+                }
             }
         }
     }
 }
 
-int check_dims(size_t M, size_t O, size_t K) {
-    if (M > 0x7fffffffu || O > 0x7fffffffu || K > 0x7fffffffu)
-        return set_error(kErrUnsupported, "gemm dims past 2^31");
+template <int WO, int WM, int TO, int TMM>
+int launch_tile(const GemmSegs &sg, const uint16_t *x, int M, int K, const char *name) {
+    constexpr int BO = 32 * TO * WO, BM = 32 * TMM * WM;
+    const int O = sg.row0[sg.n];
+    const int nbo = (O + BO - 1) / BO, nbm = (M + BM - 1) / BM;
+    const unsigned grid = (unsigned)(((nbo + 7) / 8) * 8 * nbm);
+    APUS_TIMED(name, k_gemm_tile<WO, WM, TO, TMM><<<grid, 64 * WO * WM, 0, stream()>>>(sg, x, M, K));
+    return launch_check(name);
+}
+
+}  // namespace
+
+namespace apus {
+
+// Tile shape per call shape (measured on MI355X for the model's projection
+// shapes, K = 2048 / 4096): decode batches want many small workgroups
+// (the weights stream once; x is re-read from L2), prefill the 256 x 256
+// tile (operand traffic M O K (1/BO + 1/BM) through L2).
+int gemm_tile(const GemmSegs &sg, const uint16_t *x, size_t M, size_t K, const char *nm) {
+    const int m = (int)M, k = (int)K;
+    const size_t O = (size_t)sg.row0[sg.n];
+    if (M > 512) return launch_tile<2, 4, 4, 2>(sg, x, m, k, nm);                 // 256 x 256
+    if (M > 64 && O > 10000) return launch_tile<2, 2, 2, 4>(sg, x, m, k, nm);     // 128 x 256
+    if (M > 64 && O > 4096) return launch_tile<4, 1, 1, 4>(sg, x, m, k, nm);      // 128 x 128
+    return launch_tile<2, 1, 1, 2>(sg, x, m, k, nm);                             // 64 x 64
+}
+
+// checks shared by the MFMA entry points: K a multiple of 32 (stages),
+// 16-byte aligned operands (16-byte copies), byte offsets under 2 GiB
+int gemm_tile_check(const uint16_t *x, size_t M, size_t O, size_t K) {
+    if (int r = check_dims(M, O, K)) return r;
+    if (!x) return set_error(kErrArgument, "NULL operand");
+    if (K == 0 || K % 32 != 0 || (uintptr_t)x % 16 != 0)
+        return set_error(kErrUnsupported, "MFMA gemm needs K a multiple of 32 and 16-byte "
+                         "aligned operands (K=%zu)", K);
+    if (O * K * 2 >= 0x7fff0000u || M * K * 2 >= 0x7fff0000u)
+        return set_error(kErrUnsupported, "MFMA gemm operands must stay under 2 GiB");
     return kOk;
 }
 
@@ -267,34 +392,7 @@ int host_gemm(const uint16_t *w, const uint16_t *x, uint16_t *y, size_t M, size_
     return stage_out(y, dy, M * O * 2);
 }
 
-// rocBLAS for prefill-sized row counts: y (column-major O x M, ldc O) =
-// w^T (w is column-major K x O) . x (column-major K x M), bf16 in and
-// out, fp32 compute. One handle per device, on the library's stream.
-constexpr size_t kMfmaRows = 256;
-std::unordered_map<int, rocblas_handle> g_blas;
-
-int blas_gemm(const uint16_t *w, const uint16_t *x, uint16_t *y, size_t M, size_t O, size_t K) {
-    const int dev = current_device();
-    rocblas_handle &h = g_blas[dev];
-    if (!h && rocblas_create_handle(&h) != rocblas_status_success) {
-        h = nullptr;
-        return set_error(kErrHip, "rocblas_create_handle failed");
-    }
-    if (rocblas_set_stream(h, stream()) != rocblas_status_success)
-        return set_error(kErrHip, "rocblas_set_stream failed");
-    const float one = 1.0f, zero = 0.0f;
-    const rocblas_status st = rocblas_gemm_ex(
-        h, rocblas_operation_transpose, rocblas_operation_none, (rocblas_int)O, (rocblas_int)M,
-        (rocblas_int)K, &one, w, rocblas_datatype_bf16_r, (rocblas_int)K, x,
-        rocblas_datatype_bf16_r, (rocblas_int)K, &zero, y, rocblas_datatype_bf16_r,
-        (rocblas_int)O, y, rocblas_datatype_bf16_r, (rocblas_int)O, rocblas_datatype_f32_r,
-        rocblas_gemm_algo_standard, 0, 0);
-    if (st != rocblas_status_success)
-        return set_error(kErrHip, "rocblas_gemm_ex failed (%d)", (int)st);
-    return kOk;
-}
-
-}  // namespace
+}  // namespace apus
 
 extern "C" {
 
@@ -326,20 +424,18 @@ int apus_hip_bf16_gemm_dev(const uint16_t *w, const uint16_t *x, uint16_t *y, si
 int apus_hip_bf16_gemm_mfma_dev(const uint16_t *w, const uint16_t *x, uint16_t *y, size_t M,
                                 size_t O, size_t K) {
     APUS_READY();
-    if (int r = check_dims(M, O, K)) return r;
-    if (M == 0 || O == 0) return kOk;
-    // the hand kernel: decode-sized M, K % 32 == 0, 16-byte aligned rows,
-    // operands under 1 GiB; everything else (prefill) through rocBLAS
-    if (M > kMfmaRows || K % 32 != 0 || ((uintptr_t)w | (uintptr_t)x) % 16 != 0 ||
-        O * K * 2 >= (size_t)kOutOfRange || M * K * 2 >= (size_t)kOutOfRange) {
-        int r = kOk;
-        APUS_TIMED("rocblas_gemm_bf16", r = blas_gemm(w, x, y, M, O, K));
-        return r;
-    }
-    const dim3 grid(cdiv(O, OT), cdiv(M, MT));
-    APUS_TIMED("k_gemm_mfma",
-               k_gemm_mfma<<<grid, 256, 0, stream()>>>(w, x, y, (int)M, (int)O, (int)K));
-    return launch_check("k_gemm_mfma");
+    if (M == 0 || O == 0) return check_dims(M, O, K);
+    if (!w || !y) return set_error(kErrArgument, "NULL operand");
+    if (int r = gemm_tile_check(x, M, O, K)) return r;
+    if ((uintptr_t)w % 16 != 0)
+        return set_error(kErrUnsupported, "MFMA gemm needs 16-byte aligned operands");
+    GemmSegs sg{};
+    sg.n = 1;
+    sg.row0[1] = (int)O;
+    sg.w[0] = w;
+    sg.y[0] = y;
+    sg.ldy[0] = (int)O;
+    return gemm_tile(sg, x, M, K, "k_gemm_tile");
 }
 
 }  // extern "C"

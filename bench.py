@@ -712,7 +712,7 @@ def bench_proj(torch, M, exact, steps, warmup, seed):
         w, x, y = sets[i]
         apus_hip.bf16_gemm_dev(w, x, y, exact=exact)
 
-    kname = "k_gemm_seq" if exact else ("k_gemm_mfma" if M <= 256 else "rocblas_gemm_bf16")
+    kname = "k_gemm_seq" if exact else "k_gemm_tile"
     bytes_ = O * K * 2 + M * K * 2 + M * O * 2
     flops = 2 * M * O * K
     table = {kname: ("hbm", bytes_, HBM_PEAK) if M <= 256 else ("mfma", flops, BF16_PEAK)}

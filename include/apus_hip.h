@@ -504,15 +504,67 @@ int apus_hip_bf16_weights_release(void);
 
 /* Device-pointer forms (no counterpart in the reference; the tier-2 calls
  * around the device-resident mixers). _dev: the reference's order, bitwise,
- * one lane per output (decode-sized M). _mfma_dev: the 16x16x32 bf16 MFMA
- * for decode batches up to 256 rows (K % 32 == 0, 16-byte aligned w, x),
- * rocBLAS's bf16 GEMM (fp32 compute) otherwise (prefill); both sum in their
- * own order, a tolerance class of the reference (|c - r| <= 2e-3 (|r| +
- * sum_k |w x|)). */
+ * one lane per output (decode-sized M). _mfma_dev: a hand-written
+ * 32x32x16 bf16 MFMA GEMM with fp32 accumulation for any M (tile shape
+ * chosen per call shape; K % 32 == 0, 16-byte aligned w and x, else
+ * APUS_HIP_ERR_UNSUPPORTED); it sums in its own order, a tolerance class of
+ * the reference (|c - r| <= 2e-3 (|r| + sum_k |w x|)), and its result does
+ * not depend on the tile shape (every element accumulates its k16 steps
+ * in order). */
 int apus_hip_bf16_gemm_dev(const uint16_t *w, const uint16_t *x, uint16_t *y,
                            size_t M, size_t O, size_t K);
 int apus_hip_bf16_gemm_mfma_dev(const uint16_t *w, const uint16_t *x,
                                 uint16_t *y, size_t M, size_t O, size_t K);
+
+/* ---- one layer's mixer with its projections (c/layer.h:236-331) --------
+ * The reference's per-token layer body around the mixer: the input
+ * projections of the normed input ln1, the mixer, the output projection.
+ * Device pointers; the weights keep the reference's layouts
+ * (ApusLayerW, c/layer.h:133-157), [rows][hidden] bf16, 16-byte aligned. */
+typedef struct {
+    size_t hidden;                  /* H = 2048 */
+    const uint16_t *w_qkv;          /* [conv_dim][H] */
+    const uint16_t *w_z;            /* [value_dim][H] */
+    const uint16_t *w_b, *w_a;      /* [hv][H] */
+    const uint16_t *w_out;          /* [H][value_dim] */
+} ApusHipGdnProj;
+typedef struct {
+    size_t hidden;                  /* H = 2048 */
+    const uint16_t *wq;             /* [nh*2d][H] ([q|gate] per head) */
+    const uint16_t *wk, *wv;        /* [nkv*d][H] */
+    const uint16_t *wo;             /* [H][nh*d] */
+} ApusHipAttnProj;
+
+/* GDN layer decode / verify with its projections (c/layer.h:236-286 per
+ * token): ln1 [Ttot][H] -> ao [Ttot][H]; the state arguments as
+ * apus_hip_gdn_decode / _decode_slots. The four input projections (w_qkv,
+ * w_z, w_b, w_a, c/layer.h:250-253) run as one MFMA GEMM launch whose
+ * epilogue writes qkv, z, b, a in the mixer's layouts; then the fused
+ * decode mixer; then w_out (c/layer.h:274). The GEMMs are the tolerance
+ * class of apus_hip_bf16_gemm_mfma_dev; with the same projections the
+ * mixer is bitwise apus_hip_gdn_decode. Needs hidden, value_dim and hv
+ * multiples of 32. Library scratch holds the intermediates. */
+int apus_hip_gdn_layer_decode(const ApusHipGdnLayer *L, const ApusHipGdnProj *P,
+                              size_t B, const int32_t *cu, const uint16_t *ln1,
+                              uint16_t *conv_state, float *S, uint16_t *ao);
+int apus_hip_gdn_layer_decode_slots(const ApusHipGdnLayer *L, const ApusHipGdnProj *P,
+                                    size_t B, const int32_t *slot_in,
+                                    const int32_t *slot_out, const int32_t *cu,
+                                    const uint16_t *ln1, uint16_t *conv, float *S,
+                                    uint16_t *ao);
+/* Full-attention layer decode / verify with its projections (c/layer.h:
+ * 288-331 per token): wq | wk | wv as one MFMA GEMM launch writing qg, k, v
+ * (c/layer.h:300-302), the split-K decode mixer on the flat or paged cache
+ * (arguments as apus_hip_attn_decode / _decode_paged), then wo
+ * (c/layer.h:322). */
+int apus_hip_attn_layer_decode(const ApusHipAttnLayer *L, const ApusHipAttnProj *P,
+                               size_t B, const int32_t *cu, const int32_t *pos0,
+                               const uint16_t *ln1, uint16_t *kcache,
+                               uint16_t *vcache, size_t max_seq, uint16_t *ao);
+int apus_hip_attn_layer_decode_paged(const ApusHipAttnLayer *L, const ApusHipAttnProj *P,
+                                     size_t B, const int32_t *rows, const int32_t *cu,
+                                     const int32_t *pos0, const uint16_t *ln1,
+                                     const ApusHipKvCache *kv, uint16_t *ao);
 
 #ifdef __cplusplus
 }

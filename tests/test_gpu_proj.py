@@ -3,8 +3,8 @@
 reference's x86 hot path, tests/test_oracle_ref.py).
 
 The hook drop-ins (host pointers) and the device-pointer sequential kernel
-keep the reference's order and must be bitwise. The MFMA GEMM sums in the
-MFMA's order: every element within 2e-3 (|r| + esc), esc = sum_k |w x|
+keep the reference's order and must be bitwise. The MFMA GEMM (hand-written,
+every row count) sums in the MFMA's order: every element within 2e-3 (|r| + esc), esc = sum_k |w x|
 (the attention kernels' class), and normwise within 2e-3.
 """
 import numpy as np
@@ -63,10 +63,14 @@ def test_gemm_dev_bitwise(hip, orc, M, O, K):
     assert np.array_equal(y.cpu().numpy().view(np.uint16), orc.bf16_gemm(w, x))
 
 
-@pytest.mark.parametrize("M,O,K", [(64, 12352, 2048), (200, 1000, 4096), (5, 70, 40),
-                                   (300, 517, 2048),    # M > 256: rocBLAS
-                                   (1000, 1000, 512),   # rocBLAS, ragged edges
-                                   (7, 90, 40)])        # K % 32 != 0: rocBLAS
+# one shape per tile configuration of the MFMA GEMM (64 x 64, 128 x 128,
+# 128 x 256, 256 x 256), with ragged row / output edges and an output count
+# that is not a multiple of 4 (the element-store epilogue)
+@pytest.mark.parametrize("M,O,K", [(64, 12352, 2048), (200, 1000, 4096), (1, 70, 32),
+                                   (300, 5000, 512),    # 128 x 128 tiles
+                                   (260, 10240, 256),   # 128 x 256 tiles
+                                   (1000, 1000, 512),   # 256 x 256, ragged edges
+                                   (700, 517, 64)])     # O % 4 != 0
 def test_gemm_mfma_tolerance(hip, orc, M, O, K):
     import torch
     rng = np.random.default_rng(M * 31 + K)
@@ -84,3 +88,15 @@ def test_gemm_mfma_tolerance(hip, orc, M, O, K):
     same = float(np.mean(c == r))
     print(f"[proj] mfma normwise {nrm:.3g}, identical {same:.4f}", flush=True)
     assert nrm <= 2e-3 and same > 0.9
+
+
+def test_gemm_mfma_refuses_unaligned_k(hip):
+    """K not a multiple of 32: the MFMA GEMM returns "unsupported" (the
+    caller runs the exact kernel or its CPU op), never a wrong result."""
+    import torch
+    w = torch.zeros((90, 40), dtype=torch.int16, device="cuda")
+    x = torch.zeros((7, 40), dtype=torch.int16, device="cuda")
+    y = torch.empty((7, 90), dtype=torch.int16, device="cuda")
+    with pytest.raises(hip.ApusHipError) as e:
+        hip.bf16_gemm_dev(w, x, y, exact=False)
+    assert e.value.code == 1
