@@ -445,6 +445,7 @@ def gdn_prefill_flops(T, C=64):
 
 ATTN = (16, 2, 256, 64, 1e7)
 NH, NKV, AD = 16, 2, 256
+HID = 2048                  # hidden size (the projections' K / output)
 
 
 def attn_decode_bytes(ctx, tq=1):
@@ -563,7 +564,7 @@ def bench_attn_prefill(torch, T, steps, warmup, seed, leg=None):
     return r
 
 
-def bench_mixed_block(torch, B, steps, warmup, seed, leg=None):
+def bench_mixed_block(torch, B, steps, warmup, seed, leg=None, proj=False):
     """Config 4: one hybrid decode block in the model's 3:1 ratio -- three
     Gated DeltaNet layers (each with its own weights, conv state and
     recurrent state per sequence) and one gated-GQA layer (a bf16 KV cache
@@ -610,20 +611,37 @@ def bench_mixed_block(torch, B, steps, warmup, seed, leg=None):
                 kpool.reserve(rows[s], int(have[s]) * 32)
     kv = kpool.cache(0)
 
-    # caches filled with finite random bf16 codes, |x| in [2^-8, 2) with
-    # random signs
-    def codes(shape):
-        x = torch.randint(0x3B80, 0x4000, shape, dtype=torch.int16, device="cuda", generator=g)
-        sign = torch.randint(0, 2, shape, dtype=torch.int16, device="cuda", generator=g) << 15
-        return x.bitwise_or_(sign)
+    # caches filled with N(0, 1) bf16 values (config 2's distribution)
     for s in range(B):
-        apus_hip.attn_cache_pack_paged(codes((int(ctx[s]), NKV, AD)), codes((int(ctx[s]), NKV, AD)),
+        apus_hip.attn_cache_pack_paged(bf((int(ctx[s]), NKV, AD)), bf((int(ctx[s]), NKV, AD)),
                                        int(ctx[s]), NKV, AD, kv, rows[s])
     att = dict(qg=bf((T, NH, 2 * AD)), k=bf((T, NKV, AD)), v=bf((T, NKV, AD)),
                y=torch.empty((T, NH * AD), dtype=torch.int16, device="cuda"))
+    if proj:
+        # each layer's projections (c/layer.h:133-157 layouts), its normed
+        # input ln1 and its projected output ao
+        sH = HID ** -0.5
+        for L in gdn:
+            L["pw"] = dict(w_qkv=bf((CD, HID), sH), w_z=bf((VD, HID), sH), w_b=bf((HV, HID), sH),
+                           w_a=bf((HV, HID), sH), w_out=bf((HID, VD), VD ** -0.5))
+            L["proj"] = apus_hip.gdn_proj(HID, L["pw"])
+            L["ln1"] = bf((T, HID))
+            L["ao"] = torch.empty((T, HID), dtype=torch.int16, device="cuda")
+        att["pw"] = dict(wq=bf((NH * 2 * AD, HID), sH), wk=bf((NKV * AD, HID), sH),
+                         wv=bf((NKV * AD, HID), sH), wo=bf((HID, NH * AD), (NH * AD) ** -0.5))
+        att["proj"] = apus_hip.attn_proj(HID, att["pw"])
+        att["ln1"] = bf((T, HID))
+        att["ao"] = torch.empty((T, HID), dtype=torch.int16, device="cuda")
     torch.cuda.synchronize()
 
     def step(i):
+        if proj:
+            for L in gdn:
+                apus_hip.gdn_layer_decode_slots(L["layer"], L["proj"], slots, slots, cu, L["ln1"],
+                                                L["conv"], L["S"], L["ao"])
+            apus_hip.attn_layer_decode_paged(alayer, att["proj"], rows, cu, ctx, att["ln1"], kv,
+                                             att["ao"])
+            return
         for L in gdn:
             apus_hip.gdn_decode_slots(L["layer"], slots, slots, cu, L["qkv"], L["z"], L["a"],
                                       L["b"], L["conv"], L["S"], L["y"])
@@ -638,9 +656,23 @@ def bench_mixed_block(torch, B, steps, warmup, seed, leg=None):
              "k_attn_scores": ("hbm", kv1, HBM_PEAK), "k_attn_pv": ("hbm", kv1, HBM_PEAK),
              "k_attn_prep": ("hbm", T * (NH * AD * 2 * 2 + 2 * NKV * AD * 2 * 2), HBM_PEAK),
              "k_attn_combine": ("hbm", T * NH * AD * 2 * 2, HBM_PEAK)}
+    if proj:
+        # the projections' compulsory bytes: every weight once, ln1 in and
+        # ao out per layer (the projection outputs the mixers read are
+        # intermediates); the mixers' own terms already count their in/out
+        # activations, which here are those intermediates
+        w_gdn = ((CD + VD + 2 * HV) * HID + HID * VD) * 2
+        w_att = ((NH * 2 * AD + 2 * NKV * AD) * HID + HID * NH * AD) * 2
+        bytes_ += 3 * w_gdn + w_att + 4 * 2 * T * HID * 2
+        flops_in = 2 * T * HID * (3 * (CD + VD + 2 * HV) + NH * 2 * AD + 2 * NKV * AD)
+        flops_out = 2 * T * HID * (3 * VD + NH * AD)
+        table["k_gemm_tile_in"] = ("hbm", (3 * (CD + VD + 2 * HV) + NH * 2 * AD + 2 * NKV * AD)
+                                   * HID * 2 // 4 + T * HID * 2, HBM_PEAK)
+        table["k_gemm_tile_out"] = ("hbm", (3 * HID * VD + HID * NH * AD) * 2 // 4
+                                    + T * HID * 2, HBM_PEAK)
     total, per, kt = time_steps(torch, step, steps, warmup, 1, table)
     st = float(np.mean(per))
-    wl = f"mixed_block_3gdn_1gqa_b{B}"
+    wl = f"mixed_block_3gdn_1gqa_b{B}" + ("_proj" if proj else "")
     r = dict(workload=wl, tokens_per_step=T, ms_per_step=total / steps * 1e3,
              step_event_ms=st * 1e3, kernels_ms=kt, alg_bytes=bytes_,
              ctx_mean=float(ctx.mean()), ctx_max=int(ctx.max()), verify_tokens=T,
@@ -651,6 +683,15 @@ def bench_mixed_block(torch, B, steps, warmup, seed, leg=None):
              tok_s=T * steps / total, layer_hbm_gbs=bytes_ / st / 1e9,
              layer_hbm_frac=bytes_ / st / HBM_PEAK,
              roofline=kernel_roofline(kt, table, wl))
+    if proj:
+        r["proj_flops"] = flops_in + flops_out
+        r["proj_weight_bytes"] = 3 * w_gdn + w_att
+        if leg:
+            r["parity"] = _proj_block_parity(torch, apus_hip, gdn, att, alayer, gpool, slots, rows,
+                                             kv, cu, ctx, B, T)
+        kpool.destroy()
+        gpool.destroy()
+        return r
     if leg:
         def slot_states(li):
             conv = torch.empty((B, CD * 3), dtype=torch.int16, device="cuda")
@@ -687,6 +728,72 @@ def bench_mixed_block(torch, B, steps, warmup, seed, leg=None):
     kpool.destroy()
     gpool.destroy()
     return r
+
+
+def _proj_block_parity(torch, apus_hip, gdn, att, alayer, gpool, slots, rows, kv, cu, ctx, B, T):
+    """The block with projections against the same block composed of the
+    separately checked entry points: from one snapshot of the GDN states
+    (and the KV cache, whose appended rows are rewritten with the same
+    values), the fused layer calls and the composition (separate MFMA
+    GEMMs per weight matrix, the mixer, the output GEMM) must give
+    bit-identical outputs and states. The mixers are held to the oracle
+    by the c4 line and the GEMMs by the test suite; the layer calls are
+    held to both, stage by stage, in tests/test_gpu_layer.py."""
+    snaps = []
+    for li in range(3):
+        conv = torch.empty((B, CD * 3), dtype=torch.int16, device="cuda")
+        S = torch.empty((B, HV, DK, DV), dtype=torch.float32, device="cuda")
+        for i, sl in enumerate(slots):
+            gpool.store_state(li, sl, conv[i], S[i])
+        snaps.append((conv, S))
+
+    def restore():
+        for li, (conv, S) in enumerate(snaps):
+            for i, sl in enumerate(slots):
+                gpool.load_state(li, sl, conv[i], S[i])
+
+    def run_fused():
+        for L in gdn:
+            apus_hip.gdn_layer_decode_slots(L["layer"], L["proj"], slots, slots, cu, L["ln1"],
+                                            L["conv"], L["S"], L["ao"])
+        apus_hip.attn_layer_decode_paged(alayer, att["proj"], rows, cu, ctx, att["ln1"], kv,
+                                         att["ao"])
+        return [L["ao"].clone() for L in gdn] + [att["ao"].clone()]
+
+    def run_composed():
+        outs = []
+        for L in gdn:
+            P = L["pw"]
+            for wn, dst in (("w_qkv", "qkv"), ("w_z", "z"), ("w_b", "b"), ("w_a", "a")):
+                apus_hip.bf16_gemm_dev(P[wn], L["ln1"], L[dst], exact=False)
+            apus_hip.gdn_decode_slots(L["layer"], slots, slots, cu, L["qkv"], L["z"], L["a"],
+                                      L["b"], L["conv"], L["S"], L["y"])
+            o = torch.empty_like(L["ao"])
+            apus_hip.bf16_gemm_dev(P["w_out"], L["y"], o, exact=False)
+            outs.append(o)
+        P = att["pw"]
+        for wn, dst in (("wq", "qg"), ("wk", "k"), ("wv", "v")):
+            apus_hip.bf16_gemm_dev(P[wn], att["ln1"], att[dst].view(T, -1), exact=False)
+        apus_hip.attn_decode_paged(alayer, rows, cu, ctx, att["qg"], att["k"], att["v"], kv,
+                                   att["y"])
+        o = torch.empty_like(att["ao"])
+        apus_hip.bf16_gemm_dev(P["wo"], att["y"], o, exact=False)
+        outs.append(o)
+        return outs
+
+    restore()
+    fused = run_fused()
+    fused_states = [(L["conv"].clone(), L["S"].clone()) for L in gdn]
+    restore()
+    comp = run_composed()
+    torch.cuda.synchronize()
+    same = [bool(torch.equal(a, b)) for a, b in zip(fused, comp)]
+    same_state = all(bool(torch.equal(a[0], L["conv"]) and torch.equal(a[1], L["S"]))
+                     for a, L in zip(fused_states, gdn))
+    return {"pass": all(same) and same_state, "layers_bitwise": same,
+            "states_bitwise": same_state,
+            "check": "fused layer calls == separate GEMM + mixer + GEMM launches, bit for bit "
+                     "(every stage held to the oracle in tests/test_gpu_layer.py)"}
 
 
 PROJ_O, PROJ_K = CD + VD + 2 * HV, 2048   # GDN in_proj: qkv | z | a | b (12352 x 2048)
@@ -934,7 +1041,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--only", default="c0,c0b,c1,c2,c3,c4,p1,p64,p4096")
+    ap.add_argument("--only", default="c0,c0b,c1,c2,c3,c4,c4p,p1,p64,p4096")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-threads", type=int, default=0)
     ap.add_argument("--cpu-worker", action="store_true")
@@ -961,6 +1068,8 @@ def main():
             ("c2", lambda: bench_attn_decode(torch, 64, 32768, args.steps, args.warmup, 13, leg)),
             ("c3", lambda: bench_attn_prefill(torch, 8192, args.steps, args.warmup, 14, leg)),
             ("c4", lambda: bench_mixed_block(torch, 128, args.steps, args.warmup, 15, leg)),
+            ("c4p", lambda: bench_mixed_block(torch, 128, args.steps, args.warmup, 15, leg,
+                                              proj=True)),
             ("p1", lambda: bench_proj(torch, 1, True, args.steps, args.warmup, 16)),
             ("p64", lambda: bench_proj(torch, 64, False, args.steps, args.warmup, 16)),
             ("p4096", lambda: bench_proj(torch, 4096, False, args.steps, args.warmup, 16)),
