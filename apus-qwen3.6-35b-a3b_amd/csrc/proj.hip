@@ -28,6 +28,7 @@
 #include <stdint.h>
 #include <string.h>
 
+#include <algorithm>
 #include <unordered_map>
 
 #include "../../include/apus_hip.h"
@@ -154,10 +155,13 @@ __device__ __forceinline__ int seg_of(const GemmSegs &g, int o) {
 // tiles wholly past O or M are skipped (wave-uniform).
 // Workgroup order: the row tiles of an output tile are dealt to one XCD
 // (block ids congruent mod 8), so they share its w rows in that XCD's L2.
+// Split K (part != nullptr): block b works on k stages of split b / nb
+// (nb: the blocks of one split) and stores its fp32 partial tile to
+// part[split][m][o]; k_gemm_reduce then sums the splits in order.
 template <int WO, int WM, int TO, int TMM>
 __global__ __launch_bounds__(64 * WO * WM) void k_gemm_tile(GemmSegs sg,
                                                        const uint16_t *__restrict__ x, int M,
-                                                       int K) {
+                                                       int K, float *__restrict__ part, int nsplit) {
     const int O = sg.row0[sg.n];
     constexpr int ST = kTileStages;
     constexpr int NW = WO * WM, BO = 32 * TO * WO, BM = 32 * TMM * WM;
@@ -170,7 +174,8 @@ __global__ __launch_bounds__(64 * WO * WM) void k_gemm_tile(GemmSegs sg,
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int wo = wave / WM, wm = wave % WM;
     const int nbo = (O + BO - 1) / BO, nbm = (M + BM - 1) / BM;
-    const int id = blockIdx.x;
+    const int nb = ((nbo + 7) / 8) * 8 * nbm;
+    const int id = blockIdx.x % nb, ks = blockIdx.x / nb;
     const int band = id / (8 * nbm), rem = id % (8 * nbm);
     const int mb = rem / 8, ob = band * 8 + rem % 8;
     if (ob >= nbo) return;                      // (the grid rounds bands up to 8)
@@ -199,9 +204,11 @@ __global__ __launch_bounds__(64 * WO * WM) void k_gemm_tile(GemmSegs sg,
         }
         loff[i] = pw ? pr * 1024 : PB + pr * 1024;
     }
-    const int nk = K / 32;
+    // this block's k stages: [kt0, kt0 + nk)
+    const int nkall = K / 32;
+    const int kt0 = ks * nkall / nsplit, nk = (ks + 1) * nkall / nsplit - kt0;
     auto issue = [&](int st) {
-        const int kb = min(st, nk - 1) * 64;
+        const int kb = (kt0 + min(st, nk - 1)) * 64;
         const uint32_t base = lds0 + (st % ST) * SB;
 #pragma unroll
         for (int i = 0; i < PPW; i++) dma16(rs[i], voff[i], kb, base + loff[i]);
@@ -260,6 +267,28 @@ __global__ __launch_bounds__(64 * WO * WM) void k_gemm_tile(GemmSegs sg,
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     // D[o][m]: lane -> m = lane % 32, o = 8 (i / 4) + 4 (lane / 32) + i % 4;
     // each 32-output tile lies in one segment
+    if (part) {                                 // fp32 partials, [split][m][O]
+        float *pb = part + (size_t)ks * M * O;
+#pragma unroll
+        for (int t = 0; t < TO; t++) {
+            const int ot = o0 + wo * TO * 32 + t * 32;
+            if (ot >= O) continue;
+#pragma unroll
+            for (int u = 0; u < TMM; u++) {
+                const int m = m0 + wm * TMM * 32 + u * 32 + (lane & 31);
+                if (m >= M) continue;
+                const f32x16 &a = acc[t][u];
+#pragma unroll
+                for (int q = 0; q < 4; q++) {
+                    const int o = ot + 8 * q + 4 * (lane >> 5);
+                    if (o < O)
+                        *reinterpret_cast<float4 *>(pb + (size_t)m * O + o) =
+                            make_float4(a[4 * q], a[4 * q + 1], a[4 * q + 2], a[4 * q + 3]);
+                }
+            }
+        }
+        return;
+    }
 #pragma unroll
     for (int t = 0; t < TO; t++) {
         const int ot = o0 + wo * TO * 32 + t * 32;
@@ -290,14 +319,48 @@ __global__ __launch_bounds__(64 * WO * WM) void k_gemm_tile(GemmSegs sg,
     }
 }
 
+// y = rnd(sum over the splits of part, in split order), scattered to the
+// segments; a thread owns 4 consecutive outputs of one row (O % 4 == 0)
+__global__ __launch_bounds__(256) void k_gemm_reduce(GemmSegs sg, const float *__restrict__ part,
+                                                     int M, int nsplit) {
+    const int O = sg.row0[sg.n], O4 = O / 4;
+    const size_t e = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (e >= (size_t)M * O4) return;
+    const int m = (int)(e / O4), o = (int)(e % O4) * 4;
+    float4 sm = *reinterpret_cast<const float4 *>(part + (size_t)m * O + o);
+    for (int s = 1; s < nsplit; s++) {
+        const float4 v = *reinterpret_cast<const float4 *>(part + ((size_t)s * M + m) * O + o);
+        sm.x += v.x; sm.y += v.y; sm.z += v.z; sm.w += v.w;
+    }
+    const int si = seg_of(sg, o);
+    uint16_t *yr = sg.y[si] + (size_t)m * sg.ldy[si] + (o - sg.row0[si]);
+    yr[0] = f2bf(sm.x);
+    yr[1] = f2bf(sm.y);
+    yr[2] = f2bf(sm.z);
+    yr[3] = f2bf(sm.w);
+}
+
 template <int WO, int WM, int TO, int TMM>
-int launch_tile(const GemmSegs &sg, const uint16_t *x, int M, int K, const char *name) {
+int launch_tile(const GemmSegs &sg, const uint16_t *x, int M, int K, const char *name,
+                int nsplit) {
     constexpr int BO = 32 * TO * WO, BM = 32 * TMM * WM;
     const int O = sg.row0[sg.n];
     const int nbo = (O + BO - 1) / BO, nbm = (M + BM - 1) / BM;
     const unsigned grid = (unsigned)(((nbo + 7) / 8) * 8 * nbm);
-    APUS_TIMED(name, k_gemm_tile<WO, WM, TO, TMM><<<grid, 64 * WO * WM, 0, stream()>>>(sg, x, M, K));
-    return launch_check(name);
+    float *part = nullptr;
+    if (nsplit > 1) {
+        part = (float *)scratch(kScratchWork3, (size_t)nsplit * M * O * 4);
+        if (!part) return kErrHip;
+    }
+    APUS_TIMED(name, k_gemm_tile<WO, WM, TO, TMM><<<grid * nsplit, 64 * WO * WM, 0, stream()>>>(
+                         sg, x, M, K, part, nsplit));
+    if (int r = launch_check(name)) return r;
+    if (nsplit > 1) {
+        APUS_TIMED("k_gemm_reduce", k_gemm_reduce<<<cdiv((size_t)M * O / 4, 256), 256, 0,
+                                                    stream()>>>(sg, part, M, nsplit));
+        return launch_check("k_gemm_reduce");
+    }
+    return kOk;
 }
 
 }  // namespace
@@ -308,13 +371,29 @@ namespace apus {
 // shapes, K = 2048 / 4096): decode batches want many small workgroups
 // (the weights stream once; x is re-read from L2), prefill the 256 x 256
 // tile (operand traffic M O K (1/BO + 1/BM) through L2).
-int gemm_tile(const GemmSegs &sg, const uint16_t *x, size_t M, size_t K, const char *nm) {
+int gemm_tile_split(const GemmSegs &sg, const uint16_t *x, size_t M, size_t K, const char *nm,
+                    int cfg, int nsplit) {
     const int m = (int)M, k = (int)K;
     const size_t O = (size_t)sg.row0[sg.n];
-    if (M > 512) return launch_tile<2, 4, 4, 2>(sg, x, m, k, nm);                 // 256 x 256
-    if (M > 64 && O > 10000) return launch_tile<2, 2, 2, 4>(sg, x, m, k, nm);     // 128 x 256
-    if (M > 64 && O > 4096) return launch_tile<4, 1, 1, 4>(sg, x, m, k, nm);      // 128 x 128
-    return launch_tile<2, 1, 1, 2>(sg, x, m, k, nm);                             // 64 x 64
+    if (nsplit > 1 && O % 4) nsplit = 1;
+    nsplit = std::max(1, std::min(nsplit, (int)(K / 32)));
+    if (cfg < 0)
+        cfg = M > 512 ? 3 : (M > 64 && O > 10000) ? 2 : (M > 64 && O > 4096) ? 1 : 0;
+    switch (cfg) {
+    case 3: return launch_tile<2, 4, 4, 2>(sg, x, m, k, nm, nsplit);      // 256 x 256
+    case 2: return launch_tile<2, 2, 2, 4>(sg, x, m, k, nm, nsplit);      // 128 x 256
+    case 1: return launch_tile<4, 1, 1, 4>(sg, x, m, k, nm, nsplit);      // 128 x 128
+    default: return launch_tile<2, 1, 1, 2>(sg, x, m, k, nm, nsplit);     // 64 x 64
+    }
+}
+
+// Decode-sized row counts with a long K (the output projections, K =
+// 4096) split K in two: twice the workgroups for the few output tiles
+// (w_out at 325 rows: 27 -> 21 us). The split depends on M and K only, so
+// a product's summation order is the same whichever launch (segmented or
+// not) computes it.
+int gemm_tile(const GemmSegs &sg, const uint16_t *x, size_t M, size_t K, const char *nm) {
+    return gemm_tile_split(sg, x, M, K, nm, -1, (M <= 512 && K >= 4096) ? 2 : 1);
 }
 
 // checks shared by the MFMA entry points: K a multiple of 32 (stages),
