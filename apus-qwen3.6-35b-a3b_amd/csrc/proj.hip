@@ -131,6 +131,47 @@ __device__ __forceinline__ int tile_slot(int r, int c) { return r * 64 + ((c ^ (
 
 constexpr int kTileStages = 4;            // LDS ring depth (stages of 32 k)
 
+// Workgroup -> (output tile, row tile). Workgroups are dealt round-robin
+// to the 8 XCDs (id % 8), each XCD running its ids in order. The tiles are
+// grouped into blocks of GO output tiles x GM row tiles (GO GM = 32, GM =
+// 8 for 8 or more row tiles); block g goes to XCD g % 8 as its (g / 8)-th group of
+// 32 ids. The 32 workgroups an XCD runs together then share GO weight
+// tiles and GM x tiles, which stay in that XCD's L2 while they walk K in
+// step (prefill: 12 distinct 256-row operand tiles per XCD instead of 18
+// with whole row-tile columns per XCD).
+__host__ __device__ inline void tile_groups(int nbo, int nbm, int &go, int &gm, int &ngo,
+                                            int &ngm) {
+    gm = nbm < 8 ? nbm : 8;
+    go = 32 / gm;
+    ngo = (nbo + go - 1) / go;
+    ngm = (nbm + gm - 1) / gm;
+}
+// Fewer than 8 row tiles (decode batches): output tile ob's row tiles all
+// go to XCD ob % 8 instead (ids ((ob / 8) nbm + mb) 8 + ob % 8), which
+// measured faster there (w_out at 325 rows: 27 vs 29 us).
+__host__ __device__ inline int tile_grid(int nbo, int nbm) {
+    if (nbm < 8) return (nbo + 7) / 8 * 8 * nbm;
+    int go, gm, ngo, ngm;
+    tile_groups(nbo, nbm, go, gm, ngo, ngm);
+    return (ngo * ngm + 7) / 8 * 8 * 32;
+}
+__host__ __device__ inline void tile_of(int id, int nbo, int nbm, int &ob, int &mb) {
+    if (nbm < 8) {
+        const int band = id / (8 * nbm), rem = id % (8 * nbm);
+        mb = rem / 8;
+        ob = band * 8 + rem % 8;
+        return;
+    }
+    int go, gm, ngo, ngm;
+    tile_groups(nbo, nbm, go, gm, ngo, ngm);
+    const int x = id % 8, slot = id / 8;
+    const int g = (slot / 32) * 8 + x, p = slot % 32;
+    const int gi = g / ngm, gj = g % ngm;          // group (output, row)
+    ob = gi * go + p % go;
+    mb = gj * gm + p / go;
+    if (gi >= ngo) ob = nbo;                       // past the last group
+}
+
 __device__ __forceinline__ int seg_of(const GemmSegs &g, int o) {
     int i = 0;
 #pragma unroll
@@ -174,11 +215,11 @@ __global__ __launch_bounds__(64 * WO * WM) void k_gemm_tile(GemmSegs sg,
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int wo = wave / WM, wm = wave % WM;
     const int nbo = (O + BO - 1) / BO, nbm = (M + BM - 1) / BM;
-    const int nb = ((nbo + 7) / 8) * 8 * nbm;
+    const int nb = tile_grid(nbo, nbm);
     const int id = blockIdx.x % nb, ks = blockIdx.x / nb;
-    const int band = id / (8 * nbm), rem = id % (8 * nbm);
-    const int mb = rem / 8, ob = band * 8 + rem % 8;
-    if (ob >= nbo) return;                      // (the grid rounds bands up to 8)
+    int ob, mb;
+    tile_of(id, nbo, nbm, ob, mb);
+    if (ob >= nbo || mb >= nbm) return;         // (the grid rounds up to whole groups)
     const int o0 = ob * BO, m0 = mb * BM;
     const uint32_t lds0 = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(lds_void *)sm);
     // this wave's copy pieces: the buffer of each (x, or its weight
@@ -346,7 +387,7 @@ int launch_tile(const GemmSegs &sg, const uint16_t *x, int M, int K, const char 
     constexpr int BO = 32 * TO * WO, BM = 32 * TMM * WM;
     const int O = sg.row0[sg.n];
     const int nbo = (O + BO - 1) / BO, nbm = (M + BM - 1) / BM;
-    const unsigned grid = (unsigned)(((nbo + 7) / 8) * 8 * nbm);
+    const unsigned grid = (unsigned)tile_grid(nbo, nbm);
     float *part = nullptr;
     if (nsplit > 1) {
         part = (float *)scratch(kScratchWork3, (size_t)nsplit * M * O * 4);
