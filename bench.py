@@ -19,9 +19,12 @@ peaks (HBM 8 TB/s, dense bf16 MFMA 2.5 PFLOP/s):
   c3   config 3   gated-GQA causal prefill, T=8192 (cache fill + attention)
   c4   config 4   hybrid decode block, 3 GDN + 1 GQA layers, 128 sequences
                   (headline)
+  c4p  config 4   the same block with every layer's projections (layer
+                  entry points: one input-projection launch, mixer, output
+                  projection)
   p1, p64, p4096  the GDN input projection (2048 -> 12352) beside the path:
-                  1 token (reference-order kernel, bitwise), 64 tokens
-                  (MFMA GEMM), 4096 tokens (rocBLAS bf16 GEMM)
+                  1 token (reference-order kernel, bitwise), 64 and 4096
+                  tokens (the hand-written MFMA GEMM)
 Input buffer sets rotate (at least 4 where the inputs are smaller than the
 256 MB Infinity Cache) so repeated reads come from HBM.
 
