@@ -202,6 +202,38 @@ def test_kv_pool_bookkeeping(hip):
     pool.destroy()
 
 
+def test_paged_rows_checked(hip):
+    """A paged call naming a row outside the block table, a closed row, or
+    positions past the blocks its row reserved is refused before any
+    kernel runs (the stale table entries of a closed row would otherwise
+    point into another sequence's blocks)."""
+    import torch
+    rng = np.random.default_rng(77)
+    layer = hip.attn_layer(synth.ATTN_DIMS, {n: torch.from_numpy(v.view(np.int16)).cuda()
+                                            for n, v in synth.attn_weights(rng).items()})
+    tok = {n: torch.from_numpy(v.view(np.int16)).cuda() for n, v in synth.attn_tokens(rng, 1).items()}
+    y = torch.empty((1, synth.ATTN_DIMS[0] * D), dtype=torch.int16, device="cuda")
+    pool = hip.KvPool(1, NKV, D, 8, 3, 4)
+    a, b = pool.open(), pool.open()
+    pool.reserve(a, 64)                      # 2 blocks: positions 0..63
+    pool.reserve(b, 40)
+    kv = pool.cache(0)
+    hip.attn_decode_paged(layer, [a], [0, 1], [63], tok["qg"], tok["k"], tok["v"], kv, y)
+    torch.cuda.synchronize()
+    for rows, pos0, why in (([3], [0], "row past the table"), ([-1], [0], "negative row"),
+                            ([a], [64], "position past the reserved blocks"),
+                            ([b], [64], "position past the reserved blocks")):
+        with pytest.raises(hip.ApusHipError) as e:
+            hip.attn_decode_paged(layer, rows, [0, 1], pos0, tok["qg"], tok["k"], tok["v"], kv, y)
+        assert e.value.code == 3, why
+    pool.close(b)
+    with pytest.raises(hip.ApusHipError):
+        hip.attn_decode_paged(layer, [b], [0, 1], [0], tok["qg"], tok["k"], tok["v"], kv, y)
+    with pytest.raises(hip.ApusHipError):      # the prefill form checks the same
+        hip.attn_prefill_paged(layer, [a], [0, 1], [64], tok["qg"], tok["k"], tok["v"], kv, y)
+    pool.destroy()
+
+
 def _gdn_inputs(rng, T):
     return synth.gdn_tokens(rng, T)
 

@@ -116,6 +116,43 @@ def test_broken_containers_refused(tmp_path):
         apus_hip.Container(d)
 
 
+def _hand_written(path, entry, payload=b"\0" * 64):
+    """A container whose header is written by hand (one tensor "x")."""
+    hdr = json.dumps({"x": entry}).encode()
+    path.write_bytes(len(hdr).to_bytes(8, "little") + hdr + payload)
+
+
+@pytest.mark.parametrize("entry", [
+    # element count overflows 64 bits (2^40 x 2^40 x 2^40), a payload of 8 bytes
+    {"dtype": "BF16", "shape": [2 ** 40, 2 ** 40, 2 ** 40], "data_offsets": [0, 8]},
+    # 2^63 x 2 wraps to 0 bytes with an unchecked multiply
+    {"dtype": "BF16", "shape": [2 ** 53 - 1, 2 ** 10], "data_offsets": [0, 0]},
+    # non-integral dimension and offsets
+    {"dtype": "BF16", "shape": [2.5], "data_offsets": [0, 5]},
+    {"dtype": "U8", "shape": [4], "data_offsets": [0.5, 4.5]},
+    # offsets past 2^53 (not exact as JSON doubles) and past the file
+    {"dtype": "U8", "shape": [8], "data_offsets": [2 ** 60, 2 ** 60 + 8]},
+    {"dtype": "U8", "shape": [8], "data_offsets": [60, 68]},
+    # negative dimension
+    {"dtype": "U8", "shape": [-8], "data_offsets": [0, 8]},
+])
+def test_header_numbers_refused(tmp_path, entry):
+    """Dimensions and offsets must be integers below 2^53 and the element
+    count and byte size must not overflow: a crafted header is refused
+    rather than reporting a bogus shape or reading past the payload."""
+    f = tmp_path / "x.safetensors"
+    _hand_written(f, entry)
+    with pytest.raises(apus_hip.ApusHipError):
+        apus_hip.Container(f)
+
+
+def test_hand_written_header_accepted(tmp_path):
+    f = tmp_path / "x.safetensors"
+    _hand_written(f, {"dtype": "U8", "shape": [2, 4], "data_offsets": [8, 16]})
+    c = apus_hip.Container(f)
+    assert c is not None
+
+
 @pytest.mark.gpu
 @pytest.mark.parametrize("a_log_bf16", [False, True])
 def test_layer_loaders(tmp_path, hip, a_log_bf16):
