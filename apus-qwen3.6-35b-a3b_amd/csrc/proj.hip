@@ -29,6 +29,7 @@
 #include <string.h>
 
 #include <algorithm>
+#include <type_traits>
 #include <unordered_map>
 
 #include "../../include/apus_hip.h"
@@ -180,6 +181,43 @@ __device__ __forceinline__ int seg_of(const GemmSegs &g, int o) {
     return i;
 }
 
+// bf16 stores of a wavefront's TO x TMM accumulator tiles (D[o][m]): tile
+// (t, u) holds outputs ob0 + 32 t .. and rows mb0 + 32 u + lane % 32; lane
+// -> o = 8 (i / 4) + 4 (lane / 32) + i % 4 of register i. Each 32-output
+// tile lies in one segment.
+template <int TO, int TMM>
+__device__ __forceinline__ void store_tiles(const GemmSegs &sg, const f32x16 (&acc)[TO][TMM],
+                                            int ob0, int mb0, int O, int M, int lane) {
+#pragma unroll
+    for (int t = 0; t < TO; t++) {
+        const int ot = ob0 + t * 32;
+        if (ot >= O) continue;
+        const int si = seg_of(sg, ot);
+        uint16_t *yb = sg.y[si] - sg.row0[si];
+        const int ld = sg.ldy[si];
+        const bool vec = ((ld | sg.row0[si]) & 3) == 0 && ((uintptr_t)sg.y[si] & 7) == 0;
+#pragma unroll
+        for (int u = 0; u < TMM; u++) {
+            const int m = mb0 + u * 32 + (lane & 31);
+            if (m >= M) continue;
+            const f32x16 &a = acc[t][u];
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                const int o = ot + 8 * q + 4 * (lane >> 5);
+                if (vec) {
+                    if (o < O)
+                        *reinterpret_cast<uint2 *>(yb + (size_t)m * ld + o) =
+                            make_uint2(pk2(a[4 * q], a[4 * q + 1]), pk2(a[4 * q + 2], a[4 * q + 3]));
+                } else {
+#pragma unroll
+                    for (int i = 0; i < 4; i++)
+                        if (o + i < O) yb[(size_t)m * ld + o + i] = f2bf(a[4 * q + i]);
+                }
+            }
+        }
+    }
+}
+
 // y[m][o] = rnd(sum_k w[o][k] x[m][k]) on the 32x32x16 bf16 MFMA. The
 // workgroup has WO x WM wavefronts; wavefront (wo, wm) = (wave / WM,
 // wave % WM) -- so the WM wavefronts sharing output columns sit on
@@ -199,12 +237,11 @@ __device__ __forceinline__ int seg_of(const GemmSegs &g, int o) {
 // Split K (part != nullptr): block b works on k stages of split b / nb
 // (nb: the blocks of one split) and stores its fp32 partial tile to
 // part[split][m][o]; k_gemm_reduce then sums the splits in order.
-template <int WO, int WM, int TO, int TMM>
+template <int WO, int WM, int TO, int TMM, int ST>
 __global__ __launch_bounds__(64 * WO * WM) void k_gemm_tile(GemmSegs sg,
                                                        const uint16_t *__restrict__ x, int M,
                                                        int K, float *__restrict__ part, int nsplit) {
     const int O = sg.row0[sg.n];
-    constexpr int ST = kTileStages;
     constexpr int NW = WO * WM, BO = 32 * TO * WO, BM = 32 * TMM * WM;
     constexpr int PB = BO * 64, SB = (BO + BM) * 64;
     constexpr int NPIECE = (BO + BM) / 16;
@@ -272,39 +309,49 @@ __global__ __launch_bounds__(64 * WO * WM) void k_gemm_tile(GemmSegs sg,
     };
     const int tv = min(TO, max(0, (O - (o0 + wo * TO * 32) + 31) / 32));
     const int uv = min(TMM, max(0, (M - (m0 + wm * TMM * 32) + 31) / 32));
-    auto mma = [&](const bf16x8 (&af)[TO], const bf16x8 (&bf)[TMM]) {
+    // MFMAs of tiles past O or M are skipped; a wavefront whose tiles are
+    // all inside runs the loop without the per-MFMA tests (as uniform
+    // branches they split the loop into a block per MFMA and cost ~10 %)
+    auto loop = [&](auto edge) {
+        auto mma = [&](const bf16x8 (&af)[TO], const bf16x8 (&bf)[TMM]) {
 #pragma unroll
-        for (int t = 0; t < TO; t++)
+            for (int t = 0; t < TO; t++)
 #pragma unroll
-            for (int u = 0; u < TMM; u++)
-                if (t < tv && u < uv)
-                    acc[t][u] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[t], bf[u], acc[t][u], 0, 0, 0);
-    };
+                for (int u = 0; u < TMM; u++)
+                    if (!decltype(edge)::value || (t < tv && u < uv))
+                        acc[t][u] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[t], bf[u], acc[t][u], 0, 0, 0);
+        };
 #pragma unroll
-    for (int s = 0; s < ST - 1; s++) issue(s);
-    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(PPW * (ST - 2)) : "memory");
-    __syncthreads();
-    issue(ST - 1);
-    bf16x8 fa0[TO], fb0[TMM], fa1[TO], fb1[TMM];
-    rd(0, 0, fa0, fb0);
-    // the scheduling barriers keep each phase's LDS reads ahead of the
-    // MFMAs that do not need them (left free, the scheduler sank them to
-    // their first use)
-    for (int kt = 0; kt < nk; kt++) {
-        rd(kt, 1, fa1, fb1);
-        __builtin_amdgcn_sched_barrier(0);
-        mma(fa0, fb0);
-        __builtin_amdgcn_sched_barrier(0);
-        // stage kt+1 landed (this wave's copies), then visible to all; every
-        // wave is past its reads of stage kt, whose slot the next issue fills
+        for (int s = 0; s < ST - 1; s++) issue(s);
         asm volatile("s_waitcnt vmcnt(%0)" ::"n"(PPW * (ST - 2)) : "memory");
         __syncthreads();
-        issue(kt + ST);
-        rd(kt + 1, 0, fa0, fb0);
-        __builtin_amdgcn_sched_barrier(0);
-        mma(fa1, fb1);
-        __builtin_amdgcn_sched_barrier(0);
-    }
+        issue(ST - 1);
+        bf16x8 fa0[TO], fb0[TMM], fa1[TO], fb1[TMM];
+        rd(0, 0, fa0, fb0);
+        // the scheduling barriers keep each phase's LDS reads ahead of the
+        // MFMAs that do not need them (left free, the scheduler sank them
+        // to their first use)
+        for (int kt = 0; kt < nk; kt++) {
+            rd(kt, 1, fa1, fb1);
+            __builtin_amdgcn_sched_barrier(0);
+            mma(fa0, fb0);
+            __builtin_amdgcn_sched_barrier(0);
+            // stage kt+1 landed (this wave's copies), then visible to all;
+            // every wave is past its reads of stage kt, whose slot the next
+            // issue fills
+            asm volatile("s_waitcnt vmcnt(%0)" ::"n"(PPW * (ST - 2)) : "memory");
+            __syncthreads();
+            issue(kt + ST);
+            rd(kt + 1, 0, fa0, fb0);
+            __builtin_amdgcn_sched_barrier(0);
+            mma(fa1, fb1);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    };
+    if (tv == TO && uv == TMM)
+        loop(std::false_type{});
+    else
+        loop(std::true_type{});
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     // D[o][m]: lane -> m = lane % 32, o = 8 (i / 4) + 4 (lane / 32) + i % 4;
     // each 32-output tile lies in one segment
@@ -330,36 +377,19 @@ __global__ __launch_bounds__(64 * WO * WM) void k_gemm_tile(GemmSegs sg,
         }
         return;
     }
-#pragma unroll
-    for (int t = 0; t < TO; t++) {
-        const int ot = o0 + wo * TO * 32 + t * 32;
-        if (ot >= O) continue;
-        const int si = seg_of(sg, ot);
-        uint16_t *yb = sg.y[si] - sg.row0[si];
-        const int ld = sg.ldy[si];
-        const bool vec = ((ld | sg.row0[si]) & 3) == 0 && ((uintptr_t)sg.y[si] & 7) == 0;
-#pragma unroll
-        for (int u = 0; u < TMM; u++) {
-            const int m = m0 + wm * TMM * 32 + u * 32 + (lane & 31);
-            if (m >= M) continue;
-            const f32x16 &a = acc[t][u];
-#pragma unroll
-            for (int q = 0; q < 4; q++) {
-                const int o = ot + 8 * q + 4 * (lane >> 5);
-                if (vec) {
-                    if (o < O)
-                        *reinterpret_cast<uint2 *>(yb + (size_t)m * ld + o) =
-                            make_uint2(pk2(a[4 * q], a[4 * q + 1]), pk2(a[4 * q + 2], a[4 * q + 3]));
-                } else {
-#pragma unroll
-                    for (int i = 0; i < 4; i++)
-                        if (o + i < O) yb[(size_t)m * ld + o + i] = f2bf(a[4 * q + i]);
-                }
-            }
-        }
-    }
+    store_tiles<TO, TMM>(sg, acc, o0 + wo * TO * 32, m0 + wm * TMM * 32, O, M, lane);
 }
 
+// Decode-sized row counts: one BO x BM tile per workgroup (BO = 32 TO
+// outputs, BM = 32 TMM rows), its NW wavefronts each over a contiguous
+// 1/NW share of the k stages. Each wavefront copies its own stages into a
+// private R-deep LDS ring (the same 1 KiB pieces and swizzle as
+// k_gemm_tile) and waits only for its own copies: no barrier in the k loop,
+// where the shared-ring kernel's per-stage barrier left a decode tile's
+// two wavefronts waiting on each other for every 32 k. The NW partial
+// tiles are then summed through LDS in a fixed tree (NW = 4: (p0 + p2) +
+// (p1 + p3), p_w the partial of share w), and wavefront 0 stores the
+// tile. An element's sum order depends on K and NW only.
 // y = rnd(sum over the splits of part, in split order), scattered to the
 // segments; a thread owns 4 consecutive outputs of one row (O % 4 == 0)
 __global__ __launch_bounds__(256) void k_gemm_reduce(GemmSegs sg, const float *__restrict__ part,
@@ -381,7 +411,7 @@ __global__ __launch_bounds__(256) void k_gemm_reduce(GemmSegs sg, const float *_
     yr[3] = f2bf(sm.w);
 }
 
-template <int WO, int WM, int TO, int TMM>
+template <int WO, int WM, int TO, int TMM, int ST = kTileStages>
 int launch_tile(const GemmSegs &sg, const uint16_t *x, int M, int K, const char *name,
                 int nsplit) {
     constexpr int BO = 32 * TO * WO, BM = 32 * TMM * WM;
@@ -393,7 +423,7 @@ int launch_tile(const GemmSegs &sg, const uint16_t *x, int M, int K, const char 
         part = (float *)scratch(kScratchWork3, (size_t)nsplit * M * O * 4);
         if (!part) return kErrHip;
     }
-    APUS_TIMED(name, k_gemm_tile<WO, WM, TO, TMM><<<grid * nsplit, 64 * WO * WM, 0, stream()>>>(
+    APUS_TIMED(name, k_gemm_tile<WO, WM, TO, TMM, ST><<<grid * nsplit, 64 * WO * WM, 0, stream()>>>(
                          sg, x, M, K, part, nsplit));
     if (int r = launch_check(name)) return r;
     if (nsplit > 1) {
