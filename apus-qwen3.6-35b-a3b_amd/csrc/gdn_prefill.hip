@@ -754,27 +754,33 @@ __global__ __launch_bounds__(512) void k_gdn_chunk_scan(
     const int r16 = lane & 15, g4 = lane >> 4;  // MFMA row / column, lane group
     const int kq = g4 * 4;
 
-    __shared__ __attribute__((aligned(16))) float S0T[CB * KP];        // S slice [col][row]
-    __shared__ __attribute__((aligned(16))) uint16_t S0h[CB * SB];     // its hi / lo codes
-    __shared__ __attribute__((aligned(16))) uint16_t S0l[CB * SB];
+    // The state slice and the decay factors are double-buffered by chunk
+    // parity: step ci reads copy ci & 1 and writes step ci + 1's into the
+    // other, so a step needs two barriers (state in place; D complete).
+    __shared__ __attribute__((aligned(16))) float S0Tb[2][CB * KP];    // S slice [col][row]
+    __shared__ __attribute__((aligned(16))) uint16_t S0hb[2][CB * SB]; // its hi / lo codes
+    __shared__ __attribute__((aligned(16))) uint16_t S0lb[2][CB * SB];
     __shared__ __attribute__((aligned(16))) uint16_t Dh[CB * DB];      // D [col][t], hi / lo
     __shared__ __attribute__((aligned(16))) uint16_t Dl[CB * DB];
     __shared__ __attribute__((aligned(16))) uint16_t Dph[CB * DB];     // decayed D
     __shared__ __attribute__((aligned(16))) uint16_t Dpl[CB * DB];
-    __shared__ float Fs[3 * C];
+    __shared__ float Fsb[2][3 * C];
     __shared__ __attribute__((aligned(16))) uint16_t Ost[4][16 * CB];   // output role: rnd(o) tiles
 
     // state slice in: packed layout ((j/64*32 + i/4)*64 + j%64)*4 + i%4
     float *Sm = S + ((size_t)(slots ? slots[s] : s) * hv + h) * DK * DV;
     const int jb = (cb * CB) / 64 * 32, jl = (cb * CB) % 64;
-    for (int e = tid; e < CB * DK; e += 512) {
-        const int q = e / 64, rem = e % 64, jj = rem / 4, r = rem % 4;
-        const float x = Sm[((size_t)(jb + q) * 64 + jl + jj) * 4 + r];
-        S0T[jj * KP + 4 * q + r] = x;
-        split_bf(x, S0h[jj * SB + 4 * q + r], S0l[jj * SB + 4 * q + r]);
+    const int c0 = coff[s], c1 = coff[s + 1];
+    {
+        const int p0 = c0 & 1;
+        for (int e = tid; e < CB * DK; e += 512) {
+            const int q = e / 64, rem = e % 64, jj = rem / 4, r = rem % 4;
+            const float x = Sm[((size_t)(jb + q) * 64 + jl + jj) * 4 + r];
+            S0Tb[p0][jj * KP + 4 * q + r] = x;
+            split_bf(x, S0hb[p0][jj * SB + 4 * q + r], S0lb[p0][jj * SB + 4 * q + r]);
+        }
     }
 
-    const int c0 = coff[s], c1 = coff[s + 1];
     const int tS = cu[s], tE = cu[s + 1];
     // Prefetches are unconditional, their chunk clamped to the sequence's
     // last (re-read, unused): with no branch around them, and the two roles
@@ -791,13 +797,16 @@ __global__ __launch_bounds__(512) void k_gdn_chunk_scan(
             scan_load_wu(nx, Wb, Ub, u, wr, lane, cb);
         };
         load_wu(ring0, c0);
-        if (tid < 3 * C) Fs[tid] = ring0.f;
+        if (tid < 3 * C) Fsb[c0 & 1][tid] = ring0.f;
         scan_load_k(kf, Kp, cl(c0) * hk + kh, wr, lane);
         load_wu(ring1, c0 + 1);
         auto step = [&](ScanOps &cur, const ScanOps &oth, int ci) {
             const bool more = ci + 1 < c1;
+            const float *S0T = S0Tb[ci & 1], *Fs = Fsb[ci & 1];
+            const uint16_t *S0h = S0hb[ci & 1], *S0l = S0lb[ci & 1];
             if (tid < 3 * C) cur.f = Fb[(cl(ci + 2) * hv + h) * 3 * C + tid];
-            __syncthreads();           // the state slice and Fs of this chunk are in place
+            __syncthreads();           // the state slice and Fs of this chunk are in place;
+                                       // every reader of the last step's D is done
             f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int kb = 0; kb < DK / 32; kb++)
@@ -827,18 +836,22 @@ __global__ __launch_bounds__(512) void k_gdn_chunk_scan(
                                      ld8(Dpl + r16 * DB + kb * 32 + g4 * 8), sn[r], true);
             }
             scan_load_k(kf, Kp, cl(ci + 1) * hk + kh, wr, lane);
-            __syncthreads();           // every reader of the state slice and Fs is done
+            // the next step's state and factors go to the other copies
+            // (their last readers were in step ci - 1, before this step's
+            // first barrier)
+            float *S1T = S0Tb[(ci + 1) & 1];
+            uint16_t *S1h = S0hb[(ci + 1) & 1], *S1l = S0lb[(ci + 1) & 1];
 #pragma unroll
             for (int r = 0; r < 2; r++) {
                 const int i0 = wr * 32 + r * 16;
 #pragma unroll
                 for (int i = 0; i < 4; i++) {
                     const int n = kq + i, col = i0 + r16;
-                    S0T[n * KP + col] = sn[r][i];
-                    split_bf(sn[r][i], S0h[n * SB + col], S0l[n * SB + col]);
+                    S1T[n * KP + col] = sn[r][i];
+                    split_bf(sn[r][i], S1h[n * SB + col], S1l[n * SB + col]);
                 }
             }
-            if (more && tid < 3 * C) Fs[tid] = oth.f;
+            if (more && tid < 3 * C) Fsb[(ci + 1) & 1][tid] = oth.f;
         };
         for (int ci = c0; ci < c1; ci += 2) {
             step(ring0, ring1, ci);
@@ -856,6 +869,8 @@ __global__ __launch_bounds__(512) void k_gdn_chunk_scan(
         scan_load_a(af1, Ab, cl(c0 + 1) * hv + h, wr, lane);
         auto step = [&](ScanOps &cur, ScanOps2 &af, int ci) {
             const int t0 = tS + (ci - c0) * C, nt = min(C, tE - t0);
+            const float *Fs = Fsb[ci & 1];
+            const uint16_t *S0h = S0hb[ci & 1], *S0l = S0lb[ci & 1];
             __syncthreads();           // the state slice and Fs of this chunk are in place
             f32x4 o = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -887,7 +902,6 @@ __global__ __launch_bounds__(512) void k_gdn_chunk_scan(
                     *reinterpret_cast<u16x8 *>(ob + (size_t)(t0 + t) * vd + (size_t)h * DV +
                                                cb * CB + half * 8) = v8;
             }
-            __syncthreads();           // every reader of the state slice and Fs is done
         };
         for (int ci = c0; ci < c1; ci += 2) {
             step(ring0, af0, ci);
@@ -895,9 +909,10 @@ __global__ __launch_bounds__(512) void k_gdn_chunk_scan(
         }
     }
     __syncthreads();
+    const float *S1T = S0Tb[c1 & 1];   // the state after the last chunk
     for (int e = tid; e < CB * DK; e += 512) {
         const int q = e / 64, rem = e % 64, jj = rem / 4, r = rem % 4;
-        Sm[((size_t)(jb + q) * 64 + jl + jj) * 4 + r] = S0T[jj * KP + 4 * q + r];
+        Sm[((size_t)(jb + q) * 64 + jl + jj) * 4 + r] = S1T[jj * KP + 4 * q + r];
     }
 }
 
