@@ -166,6 +166,16 @@ def test_gdn_decode_config0(hip, orc):
     print(f"config0 y: {st} state rel {e:.3g}")
 
 
+@pytest.mark.parametrize("k", [[1, 1, 1], [1, 0, 1, 1, 1, 1, 1, 1, 1], [1] * 8])
+def test_gdn_decode_small_batches(hip, orc, k):
+    """One token per sequence at small batch sizes (the latency-oriented
+    one-token kernel: up to 8 sequences of 16 K heads), an empty sequence
+    included."""
+    cu = np.concatenate([[0], np.cumsum(k)]).astype(np.int32)
+    st, e = _run_decode(hip, orc, np.random.default_rng(len(k)), cu)
+    print(f"B={len(k)} y: {st} state rel {e:.3g}")
+
+
 def test_gdn_decode_batch64(hip, orc):
     """Config 0 at batch 64 (the HBM-bound decode shape)."""
     cu = np.arange(65, dtype=np.int32)
