@@ -251,50 +251,58 @@ __device__ __forceinline__ uint32_t conv_sum4_pair(const float (&w0)[4], const f
 constexpr int TG = 16;                         // tokens per conv work item
 
 // The conv+SiLU codes of channels gcol and gcol + 1 (c/gdn.h:19-33,
-// 220-228) for the 16 tokens tg .. tg+15 of chunk P: the item reads its
-// tokens' inputs and the 3 before them (from the sequence's old conv state
-// in its first chunk). Loads are unconditional (rows clamped into the
-// chunk); the codes of padding rows (t >= nt) are 0.
-__device__ __forceinline__ void conv_codes16(const uint16_t *__restrict__ qkv, size_t cd,
-                                             size_t gcol, const ChunkPos &P, int tg, bool first,
-                                             const uint16_t *__restrict__ cst,
-                                             const uint16_t *__restrict__ conv_w,
-                                             const uint16_t *__restrict__ silu_bf,
-                                             uint16_t (&c0)[TG], uint16_t (&c1)[TG]) {
-    // inputs of rows t0 + tg - 3 .. t0 + tg + 15, two channels a word
-    uint32_t x[TG + 3];
+// 220-228) for the 16 tokens tg .. tg+15 of chunk P, in two parts so that
+// a thread's two items have their loads in flight together:
+// conv_rows16 reads the item's tokens' inputs and the 3 before them (from
+// the sequence's old conv state in its first chunk) and the two channels'
+// taps; conv_codes16 forms the codes. Loads are unconditional (rows
+// clamped into the chunk); the codes of padding rows (t >= nt) are 0.
+struct ConvRows {
+    uint32_t x[TG + 3];                         // inputs, two channels a word
+    float w0[4], w1[4];                         // the two channels' taps
+};
+__device__ __forceinline__ void conv_rows16(const uint16_t *__restrict__ qkv, size_t cd,
+                                            size_t gcol, const ChunkPos &P, int tg, bool first,
+                                            const uint16_t *__restrict__ cst,
+                                            const uint16_t *__restrict__ conv_w, ConvRows &R) {
+    // (tg, P and first are wave-uniform: the row addresses are scalar)
+    const uint32_t cofs = (uint32_t)gcol * 2;   // the lane's byte offset in a row
+    const int t0 = __builtin_amdgcn_readfirstlane(P.t0), nt = __builtin_amdgcn_readfirstlane(P.nt);
 #pragma unroll
     for (int r = 0; r < TG + 3; r++) {
         const int t = tg - 3 + r;               // chunk-relative token
-        const uint32_t vq = *reinterpret_cast<const uint32_t *>(
-            qkv + (size_t)(P.t0 + max(min(t, P.nt - 1), first ? 0 : -3)) * cd + gcol);
+        const int row = t0 + max(min(t, nt - 1), first ? 0 : -3);
+        const char *rowp = reinterpret_cast<const char *>(qkv) + (size_t)row * cd * 2;
+        const uint32_t vq = *reinterpret_cast<const uint32_t *>(rowp + cofs);
         if (r < 3 && tg == 0) {
             const uint32_t vs = (uint32_t)cst[gcol * 3 + r] | ((uint32_t)cst[(gcol + 1) * 3 + r] << 16);
-            x[r] = first ? vs : vq;
+            R.x[r] = first ? vs : vq;
         } else {
-            x[r] = vq;
+            R.x[r] = vq;
         }
     }
-    float w0[4], w1[4];
 #pragma unroll
     for (int i = 0; i < 4; i++) {
-        w0[i] = bf2f(conv_w[gcol * 4 + i]);
-        w1[i] = bf2f(conv_w[(gcol + 1) * 4 + i]);
+        R.w0[i] = bf2f(conv_w[gcol * 4 + i]);
+        R.w1[i] = bf2f(conv_w[(gcol + 1) * 4 + i]);
     }
-    // conv sums, then the SiLU of each code from the bf16-code table
-    // (rnd(co sigmoid(co)) is a function of the code co; the table holds the
-    // reference's value for every code). Gathering it costs less than the
-    // fp32 fast path with its exponential and reciprocal (config 1: WY
-    // 95 -> 90 us).
+}
+// conv sums, then the SiLU of each code from the bf16-code table
+// (rnd(co sigmoid(co)) is a function of the code co; the table holds the
+// reference's value for every code). Gathering it costs less than the fp32
+// fast path with its exponential and reciprocal (config 1: WY 95 -> 90 us).
+__device__ __forceinline__ void conv_codes16(const ConvRows &R, int tg, int nt,
+                                             const uint16_t *__restrict__ silu_bf,
+                                             uint16_t (&c0)[TG], uint16_t (&c1)[TG]) {
 #pragma unroll
     for (int j = 0; j < TG; j++) {
-        const uint32_t cc = conv_sum4_pair(w0, w1, x[j], x[j + 1], x[j + 2], x[j + 3]);
+        const uint32_t cc = conv_sum4_pair(R.w0, R.w1, R.x[j], R.x[j + 1], R.x[j + 2], R.x[j + 3]);
         c0[j] = silu_bf[cc & 0xffffu];
         c1[j] = silu_bf[cc >> 16];
     }
 #pragma unroll
     for (int j = 0; j < TG; j++)
-        if (tg + j >= P.nt) c0[j] = c1[j] = 0;
+        if (tg + j >= nt) c0[j] = c1[j] = 0;
 }
 
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void k_gdn_chunk_wy(
@@ -343,7 +351,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void k
     // the gates (c/gdn.h:34-40). Work items are (two adjacent channels, 16
     // tokens): 512 of q|k, then 256 of v per v-head, two per thread. The
     // gates of padding rows (t >= nt) are 0.
-    const bool first = ci == coff[P.s];
+    const bool first = __builtin_amdgcn_readfirstlane(ci == coff[P.s] ? 1 : 0) != 0;
     const uint16_t *cst = conv_state + (size_t)(slots ? slots[P.s] : P.s) * cd * 3;
     if (tid < REP * C) {                        // the gates of token t, v-head 2 kh + g
         const int g = tid / C, t = tid % C, h = kh * REP + g;
@@ -356,36 +364,40 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void k
         graw_s[g][t] = gg;
         bet[g][t] = bt;
     }
-    for (int it = tid; it < 2 * DK * (C / TG) / 2 + REP * (DV / 2) * (C / TG); it += 512) {
+    static_assert(2 * DK * (C / TG) / 2 == 512 && REP * (DV / 2) * (C / TG) == 512,
+                  "two conv items per thread");
+    {
+        // item A: q | k channels 2 lc, 2 lc + 1, tokens tgA ..; item B: v
+        // channels n0, n0 + 1 of v-head 2 kh + g, tokens tgB .. (both
+        // items' inputs are loaded before either's codes are formed)
+        const int lc = 2 * (tid % DK), tgA = __builtin_amdgcn_readfirstlane((tid / DK) * TG);
+        const size_t gA = lc < DK ? (size_t)kh * DK + lc : kd + (size_t)kh * DK + (lc - DK);
+        const int g = tid / ((DV / 2) * (C / TG)), jv = tid % ((DV / 2) * (C / TG));
+        const int n0 = 2 * (jv % (DV / 2)), tgB = __builtin_amdgcn_readfirstlane((jv / (DV / 2)) * TG);
+        const size_t gB = 2 * kd + (size_t)(kh * REP + g) * DV + n0;
+        ConvRows RA, RB;
+        conv_rows16(qkv, cd, gA, P, tgA, first, cst, conv_w, RA);
+        conv_rows16(qkv, cd, gB, P, tgB, first, cst, conv_w, RB);
+        const int nt = __builtin_amdgcn_readfirstlane(P.nt);
         uint16_t c0[TG], c1[TG];
-        if (it < DK * (C / TG)) {               // q | k channels 2 lc, 2 lc + 1
-            const int lc = 2 * (it % DK), tg = (it / DK) * TG;
-            const size_t gcol = lc < DK ? (size_t)kh * DK + lc : kd + (size_t)kh * DK + (lc - DK);
-            conv_codes16(qkv, cd, gcol, P, tg, first, cst, conv_w, silu_bf, c0, c1);
-            uint16_t *dst = (lc < DK ? Qc : Kc) + (lc & (DK - 1));
+        conv_codes16(RA, tgA, nt, silu_bf, c0, c1);
+        uint16_t *dst = (lc < DK ? Qc : Kc) + (lc & (DK - 1));
 #pragma unroll
-            for (int j = 0; j < TG; j++)
-                *reinterpret_cast<uint32_t *>(dst + (tg + j) * CKP) =
-                    (uint32_t)c0[j] | ((uint32_t)c1[j] << 16);
-        } else {                                // v channels n0, n0 + 1 of v-head 2 kh + g
-            const int iv = it - DK * (C / TG), g = iv / ((DV / 2) * (C / TG));
-            const int jv = iv % ((DV / 2) * (C / TG));
-            const int n0 = 2 * (jv % (DV / 2)), tg = (jv / (DV / 2)) * TG;
-            conv_codes16(qkv, cd, 2 * kd + (size_t)(kh * REP + g) * DV + n0, P, tg, first, cst,
-                         conv_w, silu_bf, c0, c1);
-            uint16_t *V = reinterpret_cast<uint16_t *>(wy_lds + 2 * QC_B + g * V_B);
+        for (int j = 0; j < TG; j++)
+            *reinterpret_cast<uint32_t *>(dst + (tgA + j) * CKP) = (uint32_t)c0[j] | ((uint32_t)c1[j] << 16);
+        conv_codes16(RB, tgB, nt, silu_bf, c0, c1);
+        uint16_t *V = reinterpret_cast<uint16_t *>(wy_lds + 2 * QC_B + g * V_B);
 #pragma unroll
-            for (int h8 = 0; h8 < TG / 8; h8++) {
-                u16x8 a0, a1;
+        for (int h8 = 0; h8 < TG / 8; h8++) {
+            u16x8 a0, a1;
 #pragma unroll
-                for (int j = 0; j < 8; j++) {
-                    a0[j] = c0[h8 * 8 + j];
-                    a1[j] = c1[h8 * 8 + j];
-                }
-                const int t8 = tg / 8 + h8;
-                *reinterpret_cast<u16x8 *>(V + n0 * C + ((t8 ^ (n0 & 7)) << 3)) = a0;
-                *reinterpret_cast<u16x8 *>(V + (n0 + 1) * C + ((t8 ^ ((n0 + 1) & 7)) << 3)) = a1;
+            for (int j = 0; j < 8; j++) {
+                a0[j] = c0[h8 * 8 + j];
+                a1[j] = c1[h8 * 8 + j];
             }
+            const int t8 = tgB / 8 + h8;
+            *reinterpret_cast<u16x8 *>(V + n0 * C + ((t8 ^ (n0 & 7)) << 3)) = a0;
+            *reinterpret_cast<u16x8 *>(V + (n0 + 1) * C + ((t8 ^ ((n0 + 1) & 7)) << 3)) = a1;
         }
     }
     __syncthreads();
