@@ -2,11 +2,10 @@
 
 - config 2: gated-GQA decode, all 64 sequences with a 32768-token cache;
 - config 3: gated-GQA causal prefill at T=8192 from position 0; the whole
-  cache fill is checked bit-exact and the outputs of every head are checked
-  on four sampled blocks of 64 query rows (0-63, 2047-2110, 4096-4159,
-  8128-8191: the first tile, a block straddling the 2048 boundary, the
-  middle and the last tile), each recomputed by the oracle's ordered GQA
-  rows over the full causal key range;
+  cache fill is checked bit-exact; the outputs of every head on 17 sampled
+  blocks of 64 query rows are recomputed by the oracle's ordered GQA rows
+  over the full causal key range, and all 8192 rows of every head against
+  a float64 torch reference with the reference's rounding points;
 - config 4: the hybrid 3 GDN + 1 GQA decode block on the benchmark's own
   ragged batch (128 sequences, log-normal contexts mu = ln 4096, sigma = 1,
   up to 36066 cached tokens, 1..4 verify tokens each), every layer against
@@ -184,6 +183,69 @@ SAMPLE_BLOCKS = tuple((r, r + 64) for r in (0, 544, 1056, 1568, 2016, 2048, 2592
                                              4096, 4640, 5152, 6144, 6688, 7200, 7712, 8128))
 
 
+def _gqa_rows_f64(torch, qn, K, V, gate, T, chunk=512, rel=2e-3):
+    """Every row of a causal GQA prefill from position 0 in float64 on the
+    GPU (a torch reference, for the all-rows sweep; the ordered oracle
+    checks the sampled blocks): the reference's rounding points
+    (c/attn.h:337-368, 524-531) -- A = rnd(rnd(q.k) * scale), P =
+    rnd(e^{A-m} / sum e), o = rnd(sum P V), y = rnd(o * rnd(sigmoid(g)))
+    -- with float64 sums in place of the ordered fp32 ones. Returns y codes
+    [T, NH*D] and esc_y = |rnd(sigmoid(g))| * (sum_j P_j |V_jd| + the
+    rounding-flip allowance of attn_util.attn_esc_rows: scores within the
+    fp32 summation bound of a bf16 midpoint and probabilities within the
+    exp / divide window of one may round the other way)."""
+    dev = torch.device("cuda")
+
+    def f64(a):
+        return torch.from_numpy(np.ascontiguousarray(a).view(np.int16)).to(dev).view(
+            torch.bfloat16).double()
+
+    def rnd(x):
+        return x.float().bfloat16().double()
+
+    def mid(x):                      # distance to the nearest bf16 midpoint, and the ulp
+        ax = x.abs()
+        ulp = torch.exp2(torch.floor(torch.log2(ax.clamp_min(1e-300))) - 7)
+        f = ax / ulp
+        return (f - torch.floor(f) - 0.5).abs() * ulp, ulp
+
+    grp = NH // NKV
+    scale = 1.0 / 16.0
+    q = f64(qn).reshape(T, NH, D)
+    Kd, Vd = f64(K), f64(V)
+    g = rnd(torch.sigmoid(f64(gate).reshape(T, NH, D)))
+    y = torch.empty((T, NH, D), dtype=torch.float64, device=dev)
+    esc = torch.empty_like(y)
+    for r0 in range(0, T, chunk):
+        r1 = min(T, r0 + chunk)
+        pos = torch.arange(r0, r1, device=dev)
+        keys = torch.arange(r1, device=dev)
+        masked = keys[None, None, :] > pos[:, None, None]
+        for hk in range(NKV):
+            qh = q[r0:r1, hk * grp:(hk + 1) * grp]                      # [n, grp, D]
+            Kh, Vh = Kd[:r1, hk], Vd[:r1, hk]
+            Va = Vh.abs()
+            s = torch.einsum("ngd,kd->ngk", qh, Kh)
+            A = rnd(rnd(s) * scale).masked_fill(masked, float("-inf"))
+            e = torch.exp(A - A.amax(2, keepdim=True))
+            Pu = e / e.sum(2, keepdim=True)
+            o = rnd(torch.einsum("ngk,kd->ngd", rnd(Pu), Vh))
+            sl = slice(hk * grp, (hk + 1) * grp)
+            y[r0:r1, sl] = rnd(o * g[r0:r1, sl])
+            ee = torch.einsum("ngk,kd->ngd", Pu, Va)
+            tabs = torch.einsum("ngd,kd->ngk", qh.abs(), Kh.abs())
+            dist, ulp = mid(s)
+            sflip = (dist <= 2.0 * D * 2.0 ** -24 * tabs) & ~masked
+            dS = torch.where(sflip, Pu * torch.expm1(ulp * scale), torch.zeros_like(Pu))
+            pd, pulp = mid(Pu)
+            pflip = (pd <= 4e-6 * Pu) & ~masked
+            dP = dS + torch.where(pflip, pulp, torch.zeros_like(Pu))
+            allow = torch.einsum("ngk,kd->ngd", dP, Va) + dS.sum(2, keepdim=True) * ee
+            esc[r0:r1, sl] = (ee + allow * (1.02 / rel)) * g[r0:r1, sl].abs()
+    yc = y.float().bfloat16().view(torch.int16).cpu().numpy().view(np.uint16)
+    return yc.reshape(T, NH * D), esc.cpu().numpy().reshape(T, NH * D)
+
+
 @pytest.mark.timeout(400)
 def test_config3_full_sampled(hip, orc):
     """T=8192 causal prefill from position 0. The whole
@@ -224,6 +286,12 @@ def test_config3_full_sampled(hip, orc):
         st = assert_bf16_esc(yh[r0:r1], y_o.reshape(n, NH * D), esc, ulps=2,
                              what=f"config3 rows {r0}..{r1 - 1}")
         print(f"[config3] rows {r0}..{r1 - 1}: {st}", flush=True)
+    # every row and head against the float64 torch reference (its sums in
+    # another order than the reference's ascending fp32 ones: the same esc
+    # tolerance class with the same rounding-flip allowance)
+    y_t, esc_t = _gqa_rows_f64(torch, qn, K, V, gate, T)
+    st = assert_bf16_esc(yh, y_t, esc_t, ulps=2, what="config3 all rows (float64 reference)")
+    print(f"[config3] all {T} rows: {st}", flush=True)
 
 
 def test_config4_full(hip, orc):
