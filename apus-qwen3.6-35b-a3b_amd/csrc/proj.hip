@@ -46,8 +46,11 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 // One output per lane: outputs blockIdx.x*64 + lane of row blockIdx.y.
-// VEC: K is a multiple of 8 and the rows are 16-byte aligned.
-template <bool VEC>
+// VEC: K is a multiple of 8 and the rows are 16-byte aligned. XF: the x
+// row is staged in LDS as fp32 (widened once per wavefront instead of once
+// per output; K up to 16384), so a k costs the weight's widening, one
+// multiply and one add.
+template <bool VEC, bool XF = false>
 __global__ __launch_bounds__(64) void k_gemm_seq(const uint16_t *__restrict__ w,
                                                  const uint16_t *__restrict__ x,
                                                  uint16_t *__restrict__ y, int O, int K) {
@@ -61,11 +64,32 @@ __global__ __launch_bounds__(64) void k_gemm_seq(const uint16_t *__restrict__ w,
         // counter, so the vector-memory waits count weight loads only
         extern __shared__ __attribute__((aligned(16))) u16x8 xs_lds[];
         const int n8 = K / 8;
-        for (int i = threadIdx.x; i < n8; i += 64)
-            xs_lds[i] = reinterpret_cast<const u16x8 *>(xr)[i];
+        if (XF) {
+            float4 *xf = reinterpret_cast<float4 *>(xs_lds);
+            for (int i = threadIdx.x; i < n8; i += 64) {
+                const u16x8 v = reinterpret_cast<const u16x8 *>(xr)[i];
+                xf[2 * i] = make_float4(bf2f(v[0]), bf2f(v[1]), bf2f(v[2]), bf2f(v[3]));
+                xf[2 * i + 1] = make_float4(bf2f(v[4]), bf2f(v[5]), bf2f(v[6]), bf2f(v[7]));
+            }
+        } else {
+            for (int i = threadIdx.x; i < n8; i += 64)
+                xs_lds[i] = reinterpret_cast<const u16x8 *>(xr)[i];
+        }
         __syncthreads();
+        // k values 8i .. 8i+7 of x as floats
+        auto xk = [&](int i, float (&f)[8]) {
+            if (XF) {
+                const float4 *xf = reinterpret_cast<const float4 *>(xs_lds);
+                const float4 a = xf[2 * i], b = xf[2 * i + 1];
+                f[0] = a.x; f[1] = a.y; f[2] = a.z; f[3] = a.w;
+                f[4] = b.x; f[5] = b.y; f[6] = b.z; f[7] = b.w;
+            } else {
+                const u16x8 v = xs_lds[i];
+#pragma unroll
+                for (int j = 0; j < 8; j++) f[j] = bf2f(v[j]);
+            }
+        };
         const u16x8 *w8 = reinterpret_cast<const u16x8 *>(wr);
-        const u16x8 *x8 = xs_lds;
         constexpr int R = 16;          // pieces per round; two register sets
         // rounds alternate between the sets: while one set is summed the
         // next round's loads are in flight into the other. Prefetch indices
@@ -86,9 +110,10 @@ __global__ __launch_bounds__(64) void k_gemm_seq(const uint16_t *__restrict__ w,
             __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
             for (int i = 0; i < R; i++) {
-                const u16x8 xv = x8[p + i];
+                float xv[8];
+                xk(p + i, xv);
 #pragma unroll
-                for (int j = 0; j < 8; j++) acc = acc + bf2f(qa[i][j]) * bf2f(xv[j]);
+                for (int j = 0; j < 8; j++) acc = acc + bf2f(qa[i][j]) * xv[j];
             }
 #pragma unroll
             for (int i = 0; i < R; i++) qa[i] = w8[min(p + 2 * R + i, n8 - 1)];
@@ -96,15 +121,18 @@ __global__ __launch_bounds__(64) void k_gemm_seq(const uint16_t *__restrict__ w,
             __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
             for (int i = 0; i < R; i++) {
-                const u16x8 xv = x8[p + R + i];
+                float xv[8];
+                xk(p + R + i, xv);
 #pragma unroll
-                for (int j = 0; j < 8; j++) acc = acc + bf2f(qb[i][j]) * bf2f(xv[j]);
+                for (int j = 0; j < 8; j++) acc = acc + bf2f(qb[i][j]) * xv[j];
             }
         }
         for (int i = 0; p + i < n8; i++) {
-            const u16x8 wv = w8[p + i], xv = x8[p + i];
+            const u16x8 wv = w8[p + i];
+            float xv[8];
+            xk(p + i, xv);
 #pragma unroll
-            for (int j = 0; j < 8; j++) acc = acc + bf2f(wv[j]) * bf2f(xv[j]);
+            for (int j = 0; j < 8; j++) acc = acc + bf2f(wv[j]) * xv[j];
         }
     } else {
         for (int k = 0; k < K; k++) acc = acc + bf2f(wr[k]) * bf2f(xr[k]);
@@ -489,8 +517,12 @@ int launch_seq(const uint16_t *w, const uint16_t *x, uint16_t *y, size_t M, size
     const dim3 grid(cdiv(O, 64), (unsigned)M);
     if (vec) {
         if (K * 2 > 64 * 1024) return set_error(kErrUnsupported, "sequential gemm takes K up to 32768");
-        APUS_TIMED("k_gemm_seq",
-                   k_gemm_seq<true><<<grid, 64, K * 2, stream()>>>(w, x, y, (int)O, (int)K));
+        if (K * 4 <= 64 * 1024)
+            APUS_TIMED("k_gemm_seq",
+                       k_gemm_seq<true, true><<<grid, 64, K * 4, stream()>>>(w, x, y, (int)O, (int)K));
+        else
+            APUS_TIMED("k_gemm_seq",
+                       k_gemm_seq<true><<<grid, 64, K * 2, stream()>>>(w, x, y, (int)O, (int)K));
     } else {
         APUS_TIMED("k_gemm_seq", k_gemm_seq<false><<<grid, 64, 0, stream()>>>(w, x, y, (int)O, (int)K));
     }
