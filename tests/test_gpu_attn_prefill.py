@@ -117,3 +117,40 @@ def test_prefill_config3_vs_decode(hip):
     st = assert_bf16_esc(a, b, np.full(a.shape, mag), ulps=2,
                          what="config3 prefill vs decode")
     print(f"[attn_prefill config3] last rows vs decode {st}", flush=True)
+
+
+@pytest.mark.parametrize("T,cut", [(12, 7), (300, 173), (1000, 513)])
+def test_prefill_split_equals_oneshot(hip, T, cut):
+    """The reference's chunking invariance (its one-shot T=12 prefill must
+    equal a 7 + 5 chunking bitwise, tests/m4c/README.md): T tokens
+    prefilled in one call and the same tokens in two calls (the second
+    starting at position `cut` over the cache the first filled) give the
+    same outputs and the same cache, bit for bit. A row's scores, its
+    running max / sum and its P.V run over keys 0..pos in the same 32-key
+    steps whichever call holds it."""
+    import torch
+    dims = synth.ATTN_DIMS
+    nh, nkv, d, rot, theta = dims
+    rng = np.random.default_rng(T)
+    w = synth.attn_weights(rng)
+    tok = synth.attn_tokens(rng, T)
+    layer = hip.attn_layer(dims, {k: _td(torch, v) for k, v in w.items()})
+    max_seq = -(-T // 32) * 32
+    t = {k: _td(torch, v) for k, v in tok.items()}
+
+    def fresh():
+        return (torch.zeros((1, nkv, max_seq, d), dtype=torch.int16, device="cuda"),
+                torch.zeros((1, nkv, max_seq // 32, d, 32), dtype=torch.int16, device="cuda"))
+
+    dk1, dv1 = fresh()
+    y1 = torch.empty((T, nh * d), dtype=torch.int16, device="cuda")
+    hip.attn_prefill(layer, [0, T], [0], t["qg"], t["k"], t["v"], dk1, dv1, max_seq, y1)
+    dk2, dv2 = fresh()
+    y2 = torch.empty((T, nh * d), dtype=torch.int16, device="cuda")
+    hip.attn_prefill(layer, [0, cut], [0], t["qg"][:cut], t["k"][:cut], t["v"][:cut], dk2, dv2,
+                     max_seq, y2[:cut])
+    hip.attn_prefill(layer, [0, T - cut], [cut], t["qg"][cut:], t["k"][cut:], t["v"][cut:],
+                     dk2, dv2, max_seq, y2[cut:])
+    torch.cuda.synchronize()
+    assert torch.equal(dk1, dk2) and torch.equal(dv1, dv2), "cache"
+    assert torch.equal(y1, y2), "outputs"

@@ -323,3 +323,42 @@ def test_gdn_decode_into_rejects_partial_overlap(hip):
     with pytest.raises(RuntimeError, match="disjoint"):
         hip.gdn_decode_into(layer, [0, 1, 2], t["qkv"], t["z"], t["a"], t["b"],
                             c, Sb[:2 * dims[1]], c.clone(), Sb[dims[1]:], y)
+
+
+def test_gdn_decode_tokens_equal_steps(hip):
+    """The reference's step-loop invariance (recurrent == step loop,
+    bitwise; tests/m4a): sequences decoding 9, 4 and 1 tokens in one call
+    leave the same outputs, conv state and recurrent state, bit for bit, as
+    the same tokens fed one decode call per token."""
+    import torch
+    rng = np.random.default_rng(91)
+    dims = synth.GDN_DIMS
+    k = [9, 4, 1]
+    cu = np.concatenate([[0], np.cumsum(k)]).astype(np.int32)
+    B, T = len(k), int(cu[-1])
+    w = synth.gdn_weights(rng)
+    tok = synth.gdn_tokens(rng, T)
+    conv, S = synth.gdn_state(rng, B)
+    dev = torch.device("cuda")
+    tw = {n: torch.from_numpy(v.view(np.int16) if v.dtype == np.uint16 else v).to(dev)
+          for n, v in w.items()}
+    layer = hip.gdn_layer(dims, tw)
+    t = {n: torch.from_numpy(v.view(np.int16)).to(dev) for n, v in tok.items()}
+    dS0 = torch.empty((B,) + S.shape[1:], dtype=torch.float32, device=dev)
+    hip.gdn_state_pack(torch.from_numpy(S).to(dev), dS0)
+    vd = dims[1] * dims[3]
+    # one call
+    c1, S1 = torch.from_numpy(conv.view(np.int16)).to(dev), dS0.clone()
+    y1 = torch.empty((T, vd), dtype=torch.int16, device=dev)
+    hip.gdn_decode(layer, cu, t["qkv"], t["z"], t["a"], t["b"], c1, S1, y1)
+    # one call per token of each sequence
+    c2, S2 = torch.from_numpy(conv.view(np.int16)).to(dev), dS0.clone()
+    y2 = torch.empty((T, vd), dtype=torch.int16, device=dev)
+    for s in range(B):
+        for j in range(int(cu[s]), int(cu[s + 1])):
+            hip.gdn_decode(layer, [0, 1], t["qkv"][j:j + 1], t["z"][j:j + 1], t["a"][j:j + 1],
+                           t["b"][j:j + 1], c2[s:s + 1], S2[s:s + 1], y2[j:j + 1])
+    torch.cuda.synchronize()
+    assert torch.equal(y1, y2), "outputs"
+    assert torch.equal(c1, c2), "conv state"
+    assert torch.equal(S1, S2), "recurrent state"
