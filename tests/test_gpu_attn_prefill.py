@@ -154,3 +154,45 @@ def test_prefill_split_equals_oneshot(hip, T, cut):
     torch.cuda.synchronize()
     assert torch.equal(dk1, dk2) and torch.equal(dv1, dv2), "cache"
     assert torch.equal(y1, y2), "outputs"
+
+
+def test_prefill_batched_equals_alone(hip):
+    """The reference's batch invariance (batched prefill == sequential,
+    bitwise; tests/m9c): a ragged batch with cached prefixes and each
+    sequence prefilled alone over its own cache give the same outputs and
+    caches, bit for bit."""
+    import torch
+    dims = synth.ATTN_DIMS
+    nh, nkv, d, rot, theta = dims
+    rng = np.random.default_rng(96)
+    lens, pos0 = [37, 1, 64, 100], [0, 50, 31, 200]
+    cu = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+    B, T = len(lens), int(cu[-1])
+    max_seq = 320
+    w = synth.attn_weights(rng)
+    tok = synth.attn_tokens(rng, T)
+    kc = synth.normal_bf16(rng, (B, max_seq, nkv, d))
+    vc = synth.normal_bf16(rng, (B, max_seq, nkv, d))
+    layer = hip.attn_layer(dims, {k: _td(torch, v) for k, v in w.items()})
+    t = {k: _td(torch, v) for k, v in tok.items()}
+
+    def caches():
+        dk = torch.empty((B, nkv, max_seq, d), dtype=torch.int16, device="cuda")
+        dv = torch.empty((B, nkv, max_seq // 32, d, 32), dtype=torch.int16, device="cuda")
+        for s in range(B):
+            hip.attn_cache_pack(_td(torch, kc[s]), _td(torch, vc[s]), max_seq, nkv, d, dk[s],
+                                dv[s], max_seq)
+        return dk, dv
+
+    dk1, dv1 = caches()
+    y1 = torch.empty((T, nh * d), dtype=torch.int16, device="cuda")
+    hip.attn_prefill(layer, cu, pos0, t["qg"], t["k"], t["v"], dk1, dv1, max_seq, y1)
+    dk2, dv2 = caches()
+    y2 = torch.empty((T, nh * d), dtype=torch.int16, device="cuda")
+    for s in range(B):
+        a, b = int(cu[s]), int(cu[s + 1])
+        hip.attn_prefill(layer, [0, b - a], [pos0[s]], t["qg"][a:b], t["k"][a:b], t["v"][a:b],
+                         dk2[s:s + 1], dv2[s:s + 1], max_seq, y2[a:b])
+    torch.cuda.synchronize()
+    assert torch.equal(dk1, dk2) and torch.equal(dv1, dv2), "caches"
+    assert torch.equal(y1, y2), "outputs"

@@ -122,3 +122,38 @@ def test_prefill_many_sequences(hip, orc, B):
     lens = rng.integers(1, 5, B)
     cu = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
     _run_prefill(hip, orc, rng, cu, tag=f"B{B}")
+
+
+def test_prefill_batched_equals_alone(hip):
+    """The reference's batch invariance (batched prefill == sequential,
+    bitwise; tests/m9c): a ragged batch of 5 sequences and each sequence
+    prefilled alone give the same outputs, conv state and recurrent state,
+    bit for bit (a sequence's chunks start at its own first token either
+    way)."""
+    import torch
+    rng = np.random.default_rng(95)
+    dims = synth.GDN_DIMS
+    k = [1, 63, 64, 65, 130]
+    cu = np.concatenate([[0], np.cumsum(k)]).astype(np.int32)
+    B, T = len(k), int(cu[-1])
+    w = synth.gdn_weights(rng)
+    tok = synth.gdn_tokens(rng, T)
+    conv, S = synth.gdn_state(rng, B)
+    layer = hip.gdn_layer(dims, {n: _dev(torch, v) for n, v in w.items()})
+    t = {n: _dev(torch, v) for n, v in tok.items()}
+    dS0 = torch.empty((B,) + S.shape[1:], dtype=torch.float32, device="cuda")
+    hip.gdn_state_pack(torch.from_numpy(S).cuda(), dS0)
+    vd = dims[1] * dims[3]
+    c1, S1 = _dev(torch, conv), dS0.clone()
+    y1 = torch.empty((T, vd), dtype=torch.int16, device="cuda")
+    hip.gdn_prefill(layer, cu, t["qkv"], t["z"], t["a"], t["b"], c1, S1, y1)
+    c2, S2 = _dev(torch, conv), dS0.clone()
+    y2 = torch.empty((T, vd), dtype=torch.int16, device="cuda")
+    for s in range(B):
+        a, b = int(cu[s]), int(cu[s + 1])
+        hip.gdn_prefill(layer, [0, b - a], t["qkv"][a:b], t["z"][a:b], t["a"][a:b], t["b"][a:b],
+                        c2[s:s + 1], S2[s:s + 1], y2[a:b])
+    torch.cuda.synchronize()
+    assert torch.equal(y1, y2), "outputs"
+    assert torch.equal(c1, c2), "conv state"
+    assert torch.equal(S1, S2), "recurrent state"
