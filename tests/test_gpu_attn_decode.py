@@ -118,3 +118,34 @@ def test_scores_wait_limit_reports_error(hip, orc):
     del dk, dv
     _run(hip, orc, np.random.default_rng(11), [0, 1, 3], [3000, 1700], 3072)
     hip.synchronize()
+
+
+def test_decode_repeat_bitwise(hip):
+    """The split-K decode is deterministic: every partial lands in a slot of
+    its own and the combine sums them in run order (no atomics), so the
+    same call on the same inputs gives the same outputs, bit for bit, call
+    after call (the reference's thread-count independence, tests/m4a, in
+    its GPU form). A ragged batch of long contexts with 1..4 tokens."""
+    import torch
+    dims = synth.ATTN_DIMS
+    nh, nkv, d, rot, theta = dims
+    rng = np.random.default_rng(97)
+    k = [1, 4, 2, 3, 1, 1]
+    pos0 = [7000, 300, 12000, 64, 5000, 9999]
+    cu = np.concatenate([[0], np.cumsum(k)]).astype(np.int32)
+    B, T, max_seq = len(k), int(cu[-1]), 12032
+    dev = torch.device("cuda")
+    td = lambda a: torch.from_numpy(np.ascontiguousarray(a).view(np.int16)).to(dev)
+    layer = hip.attn_layer(dims, {n: td(v) for n, v in synth.attn_weights(rng).items()})
+    t = {n: td(v) for n, v in synth.attn_tokens(rng, T).items()}
+    g = torch.Generator(device=dev).manual_seed(97)
+    kc = torch.randn((B, nkv, max_seq, d), generator=g, device=dev).to(torch.bfloat16).view(torch.int16)
+    vc = torch.randn((B, nkv, max_seq // 32, d, 32), generator=g, device=dev).to(torch.bfloat16).view(torch.int16)
+    ys = []
+    for _ in range(3):
+        dk, dv = kc.clone(), vc.clone()
+        y = torch.empty((T, nh * d), dtype=torch.int16, device=dev)
+        hip.attn_decode(layer, cu, pos0, t["qg"], t["k"], t["v"], dk, dv, max_seq, y)
+        ys.append(y)
+    torch.cuda.synchronize()
+    assert torch.equal(ys[0], ys[1]) and torch.equal(ys[0], ys[2])
