@@ -383,7 +383,7 @@ def bench_gdn_decode(torch, B, steps, warmup, seed, leg=None):
     st = float(np.mean(per))
     wl = f"gdn_decode_b{B}"
     r = dict(workload=wl, tokens_per_step=B, ms_per_step=total / steps * 1e3,
-             step_event_ms=st * 1e3, kernels_ms=kt, alg_bytes=bytes_,
+             step_event_ms=st * 1e3, step_event_median_ms=float(np.median(per)) * 1e3, kernels_ms=kt, alg_bytes=bytes_,
              tok_s=B * steps / total, roofline=kernel_roofline(kt, table, wl))
     if leg:
         s = d.sets[0]
@@ -429,7 +429,7 @@ def bench_gdn_prefill(torch, T, steps, warmup, seed, leg=None):
     if "split_roof_tflops" in roof:
         roof["split_roof_frac"] = roof["achieved"] / roof["split_roof_tflops"]
     r = dict(workload=wl, tokens_per_step=T, ms_per_step=total / steps * 1e3,
-             step_event_ms=st * 1e3, kernels_ms=kt, alg_bytes=bytes_, alg_flops=flops,
+             step_event_ms=st * 1e3, step_event_median_ms=float(np.median(per)) * 1e3, kernels_ms=kt, alg_bytes=bytes_, alg_flops=flops,
              tok_s=T * steps / total, layer_hbm_frac=bytes_ / st / HBM_PEAK,
              layer_tflops=flops / st / 1e12, layer_mfma_frac=flops / st / BF16_PEAK,
              roofline=roof)
@@ -527,7 +527,7 @@ def bench_attn_decode(torch, B, ctx, steps, warmup, seed, leg=None):
     st = float(np.mean(per))
     wl = f"attn_decode_b{B}_ctx{ctx}"
     r = dict(workload=wl, tokens_per_step=B, ms_per_step=total / steps * 1e3,
-             step_event_ms=st * 1e3, kernels_ms=kt, alg_bytes=bytes_, alg_flops=flops,
+             step_event_ms=st * 1e3, step_event_median_ms=float(np.median(per)) * 1e3, kernels_ms=kt, alg_bytes=bytes_, alg_flops=flops,
              tok_s=B * steps / total, layer_hbm_gbs=bytes_ / st / 1e9,
              layer_hbm_frac=bytes_ / st / HBM_PEAK, roofline=kernel_roofline(kt, table, wl))
     if leg:
@@ -579,7 +579,7 @@ def bench_attn_prefill(torch, T, steps, warmup, seed, leg=None):
     st = float(np.mean(per))
     wl = f"attn_prefill_t{T}"
     r = dict(workload=wl, tokens_per_step=T, ms_per_step=total / steps * 1e3,
-             step_event_ms=st * 1e3, kernels_ms=kt, alg_bytes=bytes_, alg_flops=flops,
+             step_event_ms=st * 1e3, step_event_median_ms=float(np.median(per)) * 1e3, kernels_ms=kt, alg_bytes=bytes_, alg_flops=flops,
              tok_s=T * steps / total, layer_tflops=flops / st / 1e12,
              layer_mfma_frac=flops / st / BF16_PEAK, roofline=kernel_roofline(kt, table, wl))
     if leg:
@@ -703,7 +703,7 @@ def bench_mixed_block(torch, B, steps, warmup, seed, leg=None, proj=False):
     st = float(np.mean(per))
     wl = f"mixed_block_3gdn_1gqa_b{B}" + ("_proj" if proj else "")
     r = dict(workload=wl, tokens_per_step=T, ms_per_step=total / steps * 1e3,
-             step_event_ms=st * 1e3, kernels_ms=kt, alg_bytes=bytes_,
+             step_event_ms=st * 1e3, step_event_median_ms=float(np.median(per)) * 1e3, kernels_ms=kt, alg_bytes=bytes_,
              ctx_mean=float(ctx.mean()), ctx_max=int(ctx.max()), verify_tokens=T,
              shape="ctx ~ LogNormal(ln 4096, 1.0) clipped to [256, 65536], 1..4 verify tokens, "
                    f"seed {seed}",
@@ -866,7 +866,7 @@ def bench_proj(torch, M, exact, steps, warmup, seed):
     total, per, kt = time_steps(torch, step, steps, warmup, nsets, table)
     wl = f"gdn_in_proj_m{M}"
     return dict(workload=wl, tokens_per_step=M, ms_per_step=total / steps * 1e3,
-                step_event_ms=float(np.mean(per)) * 1e3, kernels_ms=kt, alg_bytes=bytes_,
+                step_event_ms=float(np.mean(per)) * 1e3, step_event_median_ms=float(np.median(per)) * 1e3, kernels_ms=kt, alg_bytes=bytes_,
                 alg_flops=flops, exact=exact, tok_s=M * steps / total,
                 roofline=kernel_roofline(kt, table, wl))
 
@@ -886,7 +886,7 @@ def bench_copy(torch, steps, warmup):
 
     total, per, _ = time_steps(torch, step, steps, warmup, 2)
     st = float(np.mean(per))
-    return dict(workload="copy_1GiB", ms_per_step=total / steps * 1e3, step_event_ms=st * 1e3,
+    return dict(workload="copy_1GiB", ms_per_step=total / steps * 1e3, step_event_ms=st * 1e3, step_event_median_ms=float(np.median(per)) * 1e3,
                 alg_bytes=2 * n, hbm_gbs=2 * n / st / 1e9, tok_s=0.0)
 
 
