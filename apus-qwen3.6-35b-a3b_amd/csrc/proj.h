@@ -26,9 +26,10 @@ struct GemmSegs {
 // of x [M][K]; name: the timing / error name of the launch. Call
 // gemm_tile_check first.
 int gemm_tile(const GemmSegs &sg, const uint16_t *x, size_t M, size_t K, const char *name);
-// the same with an explicit tile configuration (cfg 0..3: 64x64, 128x128,
-// 128x256, 256x256; -1: by shape) and nsplit k splits (fp32 partials in
-// library scratch, summed in split order by k_gemm_reduce)
+// the same with an explicit tile configuration (cfg 0: 64x64, or 128x64
+// past 64 rows; 1: 128x128; 2: 128x128 up to 128 rows, 128x192 up to 384,
+// else 128x256; 3: 256x256; -1: by shape) and nsplit k splits (fp32
+// partials in library scratch, summed in split order by k_gemm_reduce)
 int gemm_tile_split(const GemmSegs &sg, const uint16_t *x, size_t M, size_t K, const char *name,
                     int cfg, int nsplit);
 // K a multiple of 32, x 16-byte aligned, operands under 2 GiB (weights:

@@ -478,11 +478,23 @@ int gemm_tile_split(const GemmSegs &sg, const uint16_t *x, size_t M, size_t K, c
     nsplit = std::max(1, std::min(nsplit, (int)(K / 32)));
     if (cfg < 0)
         cfg = M > 512 ? 3 : (M > 64 && O > 10000) ? 2 : (M > 64 && O > 4096) ? 1 : 0;
+    // Within a configuration the row tile follows M (measured on the
+    // model's shapes: the slowest workgroup sets the time, so a row tile
+    // that is mostly past M wastes its CU): M <= 128 with long outputs
+    // runs 128 x 128 tiles on 8 wavefronts (39 -> 31 us at M = 128), M <=
+    // 384 128 x 192 (the in-projection at M = 325: 42 -> 39 us), and
+    // decode rows past 64 with short outputs 128 x 64 (the out-projection
+    // at M = 325: 21 -> 19 us).
     switch (cfg) {
     case 3: return launch_tile<2, 4, 4, 2>(sg, x, m, k, nm, nsplit);      // 256 x 256
-    case 2: return launch_tile<2, 2, 2, 4>(sg, x, m, k, nm, nsplit);      // 128 x 256
+    case 2:
+        if (m <= 128) return launch_tile<2, 4, 2, 1>(sg, x, m, k, nm, nsplit);   // 128 x 128
+        if (m <= 384) return launch_tile<2, 2, 2, 3>(sg, x, m, k, nm, nsplit);   // 128 x 192
+        return launch_tile<2, 2, 2, 4>(sg, x, m, k, nm, nsplit);                 // 128 x 256
     case 1: return launch_tile<4, 1, 1, 4>(sg, x, m, k, nm, nsplit);      // 128 x 128
-    default: return launch_tile<2, 1, 1, 2>(sg, x, m, k, nm, nsplit);     // 64 x 64
+    default:
+        if (m > 64) return launch_tile<2, 2, 2, 1>(sg, x, m, k, nm, nsplit);     // 128 x 64
+        return launch_tile<2, 1, 1, 2>(sg, x, m, k, nm, nsplit);                 // 64 x 64
     }
 }
 
