@@ -14,7 +14,9 @@
 //           the row max / sum need one exchange between the lane halves
 //           (v_permlane32_swap). A = rnd(rnd(q.k) * scale) as the
 //           reference rounds it (c/attn.h:340-347), causal mask key <=
-//           query; running max m and sum s = sum_j e^{A_j - m} per query;
+//           query; a reference point m and sum s = sum_j e^{A_j - m} per
+//           query, m a running max that is raised only when the sum would
+//           leave the fp32 range (s e^{m} and so P do not depend on m);
 //   pass 2: S^T again, then the reference's normalised probabilities
 //           P = rnd(e^{A-m} / s) (c/attn.h:354-360) in bf16, straight from
 //           the S^T accumulator registers into O^T += V^T P^T on MFMA.
@@ -226,7 +228,7 @@ __device__ __forceinline__ i32x4 fa_vrsrc(const FaCtx &c, int kt, int id) {
 // running softmax state of one query row (per lane)
 struct FaRow {
     int qpos;                          // query position
-    float M, lsum;                     // max (units of rnd(q.k)), sum of e^{A - m}
+    float M, lsum;                     // reference point (a running max), sum of e^{A - M}
     float K2;                          // pass 2: M * scale * log2(e) + log2(sum)
 };
 
@@ -327,7 +329,15 @@ __device__ __forceinline__ f32x16 fa_s(const FaCtx &c, int Kn, const bf16x8 (&q)
 }
 
 // pass-1 step j: S(j+1) from the K block at Kn (when NEXT), interleaved
-// with folding S(j) = sc (keys from kj) into the row's running max / sum.
+// with folding S(j) = sc (keys from kj) into the row's sum. The terms are
+// taken against the row's current reference point M, with no max over the
+// step: a sum taken against any M < max A is the sum against the max times
+// e^{max A - M}, and pass 2's exponent M c2 + log2(s) is the same either
+// way. M starts at -inf, so the first step's sum is +inf and takes the
+// slow path, which sets M to the running max as before; it is raised
+// again only if the sum reaches 2^100 (scores ~100 / c2 above M),
+// so the terms never overflow and none underflows that would not against
+// the true max.
 template <bool NEXT, bool MASK>
 __device__ __forceinline__ void fa_p1_step(const FaCtx &c, int Kn, int kj,
                                            const bf16x8 (&q)[D / 16], f32x16 &sc, FaRow &w) {
@@ -348,23 +358,28 @@ __device__ __forceinline__ void fa_p1_step(const FaCtx &c, int Kn, int kj,
             nx = mfma32(k, q[ks], nx);
         }
     }
-    float mx = -INFINITY;
-#pragma unroll
-    for (int i = 0; i < 16; i++) mx = fmaxf(mx, !MASK || fa_keep(i, lim) ? sc[i] : -INFINITY);
-    const float mn = fmaxf(w.M, rnd_hw(max32(mx)));
     float e[16];
-    fa_exp16<MASK>(e, sc, c.c2, mn * c.c2, lim);
+    fa_exp16<MASK>(e, sc, c.c2, w.M * c.c2, lim);
     float ps = 0.0f;
 #pragma unroll
     for (int i = 0; i < 16; i++) ps += e[i];
-    // first step: M = -inf, lsum = 0 (exp2(-inf) = 0); key 0 is in every
-    // row's first step, so M is finite from then on
-    w.lsum = w.lsum * __builtin_amdgcn_exp2f((w.M - mn) * c.c2) + sum32(ps);
-    w.M = mn;
-    if (NEXT) {
-        fa_groups16<4, 4>();
-        sc = nx;
+    const float ls = w.lsum + sum32(ps);
+    if (NEXT) fa_groups16<4, 4>();
+    if (__builtin_expect(__builtin_amdgcn_ballot_w64(!(ls < 0x1p100f)) != 0, 0)) {
+        float mx = -INFINITY;
+#pragma unroll
+        for (int i = 0; i < 16; i++) mx = fmaxf(mx, !MASK || fa_keep(i, lim) ? sc[i] : -INFINITY);
+        const float mn = fmaxf(w.M, rnd_hw(max32(mx)));
+        fa_exp16<MASK>(e, sc, c.c2, mn * c.c2, lim);
+        ps = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 16; i++) ps += e[i];
+        w.lsum = w.lsum * __builtin_amdgcn_exp2f((w.M - mn) * c.c2) + sum32(ps);
+        w.M = mn;
+    } else {
+        w.lsum = ls;
     }
+    if (NEXT) sc = nx;
     fa_split(c.nkeys);
 }
 

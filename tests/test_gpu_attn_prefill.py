@@ -28,7 +28,7 @@ def _td(torch, a):
     return torch.from_numpy(np.ascontiguousarray(a).view(np.int16)).to("cuda")
 
 
-def _run(hip, orc, rng, cu, pos0, max_seq, tag=""):
+def _run(hip, orc, rng, cu, pos0, max_seq, tag="", edit=None):
     import torch
     dims = synth.ATTN_DIMS
     nh, nkv, d, rot, theta = dims
@@ -39,6 +39,8 @@ def _run(hip, orc, rng, cu, pos0, max_seq, tag=""):
     tok = synth.attn_tokens(rng, T)
     kc = synth.normal_bf16(rng, (B, max_seq, nkv, d))
     vc = synth.normal_bf16(rng, (B, max_seq, nkv, d))
+    if edit:
+        edit(tok, kc)
     k_o, v_o = kc.copy(), vc.copy()
     y_o, qf, _ = orc.attn_mixer(dims, w, np.asarray(cu, np.int32), np.asarray(pos0, np.int32),
                                 tok["qg"], tok["k"], tok["v"], k_o, v_o, max_seq * nkv * d,
@@ -69,6 +71,23 @@ def _run(hip, orc, rng, cu, pos0, max_seq, tag=""):
 def test_prefill_small(hip, orc):
     """Two sequences: 37 tokens from position 0, 20 tokens after 50 cached."""
     _run(hip, orc, np.random.default_rng(11), [0, 37, 57], [0, 50], 128, tag="small")
+
+
+def test_prefill_score_growth(hip, orc):
+    """Scores that rise far above the first key step's: pass 1 takes its
+    sums against a reference point that it raises only when a sum would
+    leave the fp32 range, and this case makes every row raise it. Every q
+    row is all ones (after the (1+w) norm all its unrotated dims have one
+    sign) and the cached keys 0..31 are all -250, so their scores lie near
+    -2,000 while the later keys' scores are O(1): ~2,000 above the first
+    step's max, past the ~1,100 at which the sum against it would
+    overflow. The reference's terms for keys 0..31 underflow to 0 as the
+    kernel's do."""
+    def edit(tok, kc):
+        tok["qg"][:, :, :synth.ATTN_DIMS[2]] = synth.bf16_bits(np.float32(1.0))
+        kc[:, :32] = synth.bf16_bits(np.float32(-250.0))
+    _run(hip, orc, np.random.default_rng(14), [0, 40, 75], [64, 96], 192, tag="growth",
+         edit=edit)
 
 
 def test_prefill_tile_edges(hip, orc):
