@@ -138,31 +138,31 @@ __device__ __forceinline__ int fa_lane() {
 }
 
 // K rows of key tile kt -> the K buffer at LDS address kb (row pitch
-// KROW): wavefront w copies tile rows 8w..8w+7, one row (32 pieces, lanes
-// 0..31) per instruction, from cache block 2kt + w/4 (its rows
-// 8(w%4)..+7) at byte offset soff of the resource kr, which ends at the
+// KROW): copy part p is tile rows 8p..8p+7, one row (32 pieces, lanes
+// 0..31) per instruction, from cache block 2kt + p/4 (its rows
+// 8(p%4)..+7) at byte offset soff of the resource kr, which ends at the
 // last key: rows past it read zero (and their scores are masked).
-__device__ __forceinline__ void fa_dma_k(uint32_t kb, i32x4 kr, int soff, int wave) {
+__device__ __forceinline__ void fa_dma_k(uint32_t kb, i32x4 kr, int soff, int part) {
     const int lane = fa_lane();
     if (lane < 32) {
 #pragma unroll
         for (int j = 0; j < 8; j++) {
-            const int r = 8 * wave + j, rb = 8 * (wave & 3) + j;
+            const int r = 8 * part + j, rb = 8 * (part & 3) + j;
             dma16(kr, (rb * D + lane * 8) * 2, soff, kb + r * KROW);
         }
     }
 }
 
 // V^T blocks 2kt, 2kt+1 -> the LDS blocks at vb0, vb1 ([d][32 keys]):
-// wavefront w copies the 1 KiB groups 4w..4w+3 of block w / 4 (16 d-rows
+// copy part p is the 1 KiB groups 4p..4p+3 of block p / 4 (16 d-rows
 // of 4 pieces each) from the cache block at byte offset soff of vr (a
 // block past the last key lies past the resource's end: it reads zero). Keys past the last one inside its
 // block are zeroed in LDS before use.
-__device__ __forceinline__ void fa_dma_v(uint32_t vb0, uint32_t vb1, i32x4 vr, int soff, int wave) {
+__device__ __forceinline__ void fa_dma_v(uint32_t vb0, uint32_t vb1, i32x4 vr, int soff, int part) {
     const int lane = fa_lane();
 #pragma unroll
     for (int j = 0; j < 4; j++) {
-        const int q = 4 * wave + j, bb = q >> 4, g = q & 15;
+        const int q = 4 * part + j, bb = q >> 4, g = q & 15;
         const int r = 16 * g + (lane >> 2);
         const int c = (lane & 3) ^ ((r >> 2) & 3);
         dma16(vr, (r * VB + c * 8) * 2, soff, (bb ? vb1 : vb0) + g * 16 * VB * 2);
@@ -205,22 +205,22 @@ struct FaCtx {
     uint32_t lds;                      // LDS address of fa_lds
 };
 
-// The cache block wavefront w copies for key tile kt (clamped to the last
-// block holding keys), its id (a block-table load for a paged cache), and
-// the buffer resources of its K rows and V^T block.
-__device__ __forceinline__ int fa_block(const FaCtx &c, int kt) {
-    return min(2 * kt + (c.wave >> 2), c.nblk - 1);
+// Cache block 2 kt + half of key tile kt (clamped to the last block
+// holding keys), its id (a block-table load for a paged cache), and the
+// buffer resources of its K rows and V^T block.
+__device__ __forceinline__ int fa_block(const FaCtx &c, int kt, int half) {
+    return min(2 * kt + half, c.nblk - 1);
 }
 __device__ __forceinline__ int fa_block_id(const FaCtx &c, int b) {
     return (int)kv_block_id_u(c.kv, c.hd, b);
 }
-__device__ __forceinline__ i32x4 fa_krsrc(const FaCtx &c, int kt, int id) {
-    const int b = 2 * kt + (c.wave >> 2);
+__device__ __forceinline__ i32x4 fa_krsrc(const FaCtx &c, int kt, int half, int id) {
+    const int b = 2 * kt + half;
     const int valid = max(0, min(KVB, c.nkeys - KVB * b));
     return dma_rsrc(c.kv.k + ((size_t)id * c.nkv + c.kvh) * KVB * D, (uint32_t)valid * D * 2);
 }
-__device__ __forceinline__ i32x4 fa_vrsrc(const FaCtx &c, int kt, int id) {
-    const int b = 2 * kt + (c.wave >> 2);
+__device__ __forceinline__ i32x4 fa_vrsrc(const FaCtx &c, int kt, int half, int id) {
+    const int b = 2 * kt + half;
     return dma_rsrc(c.kv.v + ((size_t)id * c.nkv + c.kvh) * D * KVB,
                    b < c.nblk ? (uint32_t)(D * KVB * 2) : 0u);
 }
@@ -482,12 +482,10 @@ __global__ __launch_bounds__(64 * NW) void k_attn_fa(
     auto vbuf = [&](int u, int half) { return 2 * KBUF + ((2 * u + half) % 5) * VHALF; };
 
     // tile u = 0 .. 2nkt-1 of the key stream: pass u / nkt, key tile u %
-    // nkt. idn: this wavefront's block id for the next tile to copy, read
-    // a tile ahead (its load completes under the tile's copies).
-    // An identity (flat) table puts the sequence's blocks of this kv head
+    // nkt. An identity (flat) table puts the sequence's blocks of this kv head
     // at a fixed stride: one resource per cache covers them all and a tile
-    // only moves a scalar offset. A paged table builds each wavefront's
-    // resources from the block id, read a tile ahead.
+    // only moves a scalar offset. A paged table builds each block's
+    // resources from its block id, read a tile ahead.
     const bool flat = kv.btab == nullptr;
     const int blk_bytes = nkv * KVB * D * 2;
     i32x4 kflat = {0, 0, 0, 0}, vflat = {0, 0, 0, 0};
@@ -497,13 +495,42 @@ __global__ __launch_bounds__(64 * NW) void k_attn_fa(
                          (uint32_t)((c.nblk - 1) * blk_bytes + (c.nkeys - KVB * (c.nblk - 1)) * D * 2));
         vflat = dma_rsrc(kv.v + b0 * D * KVB, (uint32_t)((c.nblk - 1) * blk_bytes + D * KVB * 2));
     }
-    auto wblock = [&](int kt) { return 2 * kt + (c.wave >> 2); };   // this wave's (unclamped) block
-    int idn = 0;
-    if (flat) {
-        fa_dma_k(c.lds + kbuf(0), kflat, wblock(0) * blk_bytes, c.wave);
-    } else {
-        fa_dma_k(c.lds + kbuf(0), fa_krsrc(c, 0, fa_block_id(c, fa_block(c, 0))), 0, c.wave);
-        idn = fa_block_id(c, fa_block(c, 1 % nkt));
+    // A tile's copy is in 8 parts: part p is K rows 8p..8p+7 and V^T
+    // groups 4p..4p+3, from cache block 2 kt + p / 4. Wavefronts 0..3 (one
+    // per SIMD) issue parts w and w + 4, wavefronts 4..7 none: a wavefront
+    // issuing copies stalls while the address unit takes them, and with
+    // every wavefront copying both wavefronts of a SIMD stalled at each
+    // tile start; with one copier per SIMD the other keeps issuing MFMAs
+    // (T=8192: 0.96 -> 0.92 ms). idn[half]: the block ids of the next tile
+    // to copy, read a tile ahead (the loads complete under the copies).
+    const bool copier = c.wave < 4;
+    int idn[2] = {0, 0};
+    auto copy_tile = [&](int u, int kt, bool withv) {
+#pragma unroll
+        for (int half = 0; half < 2; half++) {
+            const int part = c.wave + 4 * half;
+            i32x4 kr = kflat, vr = vflat;
+            int off = (2 * kt + half) * blk_bytes;
+            if (!flat) {
+                const int id = __builtin_amdgcn_readfirstlane(idn[half]);
+                kr = fa_krsrc(c, kt, half, id);
+                vr = fa_vrsrc(c, kt, half, id);
+                off = 0;
+            }
+            fa_dma_k(c.lds + kbuf(u), kr, off, part);
+            if (withv) fa_dma_v(c.lds + vbuf(u, 0), c.lds + vbuf(u, 1), vr, off, part);
+        }
+    };
+    auto next_ids = [&](int kt) {
+        if (!flat) {
+            idn[0] = fa_block_id(c, fa_block(c, kt, 0));
+            idn[1] = fa_block_id(c, fa_block(c, kt, 1));
+        }
+    };
+    if (copier) {
+        next_ids(0);
+        copy_tile(0, 0, false);
+        next_ids(1 % nkt);
     }
 
     // query row of this lane: token 4w + l32/8, head l32%8 of the kv head
@@ -521,21 +548,9 @@ __global__ __launch_bounds__(64 * NW) void k_attn_fa(
     // u % nkt. begin_tile(u) publishes tile u and starts the copy of u+1.
     auto begin_tile = [&](int u) {
         fa_publish();
-        if (u + 1 < 2 * nkt) {
-            const int kt1 = (u + 1) % nkt;
-            if (flat) {
-                const int off = wblock(kt1) * blk_bytes;
-                fa_dma_k(c.lds + kbuf(u + 1), kflat, off, c.wave);
-                if (u + 1 >= nkt)
-                    fa_dma_v(c.lds + vbuf(u + 1, 0), c.lds + vbuf(u + 1, 1), vflat, off, c.wave);
-            } else {
-                const int id = __builtin_amdgcn_readfirstlane(idn);
-                fa_dma_k(c.lds + kbuf(u + 1), fa_krsrc(c, kt1, id), 0, c.wave);
-                if (u + 1 >= nkt)
-                    fa_dma_v(c.lds + vbuf(u + 1, 0), c.lds + vbuf(u + 1, 1), fa_vrsrc(c, kt1, id),
-                             0, c.wave);
-                idn = fa_block_id(c, fa_block(c, (u + 2) % nkt));
-            }
+        if (u + 1 < 2 * nkt && copier) {
+            copy_tile(u + 1, (u + 1) % nkt, u + 1 >= nkt);
+            next_ids((u + 2) % nkt);
         }
         // the last tile's V keys past nkeys: zero (P is 0 there, but
         // 0 * NaN from unwritten cache memory would not be)
