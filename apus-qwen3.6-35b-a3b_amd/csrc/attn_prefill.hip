@@ -208,11 +208,19 @@ struct FaCtx {
 // Cache block 2 kt + half of key tile kt (clamped to the last block
 // holding keys), its id (a block-table load for a paged cache), and the
 // buffer resources of its K rows and V^T block.
+// The id is read by a vector load (the address is uniform; the value is
+// taken with readfirstlane a tile later, after the tile barrier's wait for
+// the vector memory counter). A scalar load would be counted by lgkmcnt,
+// which LDS reads share and which does not retire scalar loads in order:
+// with one pending, every LDS operand read would have to wait for all
+// reads in flight (lgkmcnt(0)) instead of just its own.
 __device__ __forceinline__ int fa_block(const FaCtx &c, int kt, int half) {
     return min(2 * kt + half, c.nblk - 1);
 }
 __device__ __forceinline__ int fa_block_id(const FaCtx &c, int b) {
-    return (int)kv_block_id_u(c.kv, c.hd, b);
+    if (!c.kv.btab) return (int)kv_block_id_u(c.kv, c.hd, b);
+    typedef const __attribute__((address_space(1))) int32_t *gi32p;
+    return *(gi32p)(c.kv.btab + (size_t)c.hd * c.kv.bstride + b);
 }
 __device__ __forceinline__ i32x4 fa_krsrc(const FaCtx &c, int kt, int half, int id) {
     const int b = 2 * kt + half;
@@ -343,6 +351,9 @@ __device__ __forceinline__ void fa_p1_step(const FaCtx &c, int Kn, int kj,
                                            const bf16x8 (&q)[D / 16], f32x16 &sc, FaRow &w) {
     const int lim = w.qpos - kj - 8 * (fa_lane() >> 5);
     f32x16 nx;
+    float e[16];
+    float ps = 0.0f;
+    const float Kc = w.M * c.c2;
     if (NEXT) {
         const int kbase = fa_kbase();
         const char *Kp = fa_lds + Kn;
@@ -351,20 +362,26 @@ __device__ __forceinline__ void fa_p1_step(const FaCtx &c, int Kn, int kj,
         u16x8 kq[4];
 #pragma unroll
         for (int i = 0; i < 4; i++) kq[i] = lds16(fa_kaddr(Kp, kbase, i));
+        uint32_t pk = 0;
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int ks = 0; ks < D / 16; ks++) {
-            const bf16x8 k = __builtin_bit_cast(bf16x8, kq[ks & 3]);
-            if (ks + 4 < D / 16) kq[ks & 3] = lds16(fa_kaddr(Kp, kbase, ks + 4));
+            const bf16x8 k = __builtin_bit_cast(bf16x8, kq[ks % 4]);
+            if (ks + 4 < D / 16) kq[ks % 4] = lds16(fa_kaddr(Kp, kbase, ks + 4));
             nx = mfma32(k, q[ks], nx);
+            if ((ks & 1) == 0) pk = pack2(sc[ks], sc[ks + 1]);
+            const float r = __uint_as_float((ks & 1) ? (pk & 0xffff0000u) : (pk << 16));
+            float ev = __builtin_amdgcn_exp2f(fmaf(r, c.c2, -Kc));
+            if (MASK) ev = fa_keep(ks, lim) ? ev : 0.0f;
+            ps += ev;
+            __builtin_amdgcn_sched_barrier(0);
         }
-    }
-    float e[16];
-    fa_exp16<MASK>(e, sc, c.c2, w.M * c.c2, lim);
-    float ps = 0.0f;
+    } else {
+        fa_exp16<MASK>(e, sc, c.c2, Kc, lim);
 #pragma unroll
-    for (int i = 0; i < 16; i++) ps += e[i];
+        for (int i = 0; i < 16; i++) ps += e[i];
+    }
     const float ls = w.lsum + sum32(ps);
-    if (NEXT) fa_groups16<4, 4>();
     if (__builtin_expect(__builtin_amdgcn_ballot_w64(!(ls < 0x1p100f)) != 0, 0)) {
         float mx = -INFINITY;
 #pragma unroll
