@@ -22,7 +22,7 @@
 //           the S^T accumulator registers into O^T += V^T P^T on MFMA.
 // Each pass is a software pipeline over 32-key steps that keeps the MFMA
 // pipe fed while the softmax runs on the VALU: in pass 1 step j issues
-// the MFMAs of S(j+1) interleaved with the max / sum fold of S(j); in
+// the MFMAs of S(j+1) interleaved with the sum fold of S(j); in
 // pass 2 step j computes S(j), then the MFMAs of P(j-1).V(j-1)
 // interleaved with forming P(j) (one set of scores and one of packed
 // probabilities live at a time: the O^T accumulators take half of the
@@ -243,10 +243,14 @@ struct FaRow {
 // Instruction order. Each phase below is its own basic block (fa_split:
 // a uniform branch on a runtime value the compiler cannot fold), so the
 // scheduler cannot mix the K reads of an S block with the V reads of a
-// P.V block or pull a later step's reads forward; inside a block,
-// scheduling-group barriers lay out (operand read DEPTH ahead, MFMA,
-// VALU slice) groups. Left free, the scheduler issues all operand reads of
-// a step first and spills Q.
+// P.V block or pull a later step's reads forward. Inside the pass-1 step
+// and the P.V half of a pass-2 step, each (operand read DEPTH ahead, MFMA,
+// softmax work of one score) slice is fenced by a scheduling barrier:
+// under this register pressure the scheduler otherwise moves every
+// operand read to just before its MFMA (each MFMA then waits for its
+// read) and the softmax work after the last MFMA, and scheduling-group
+// barriers did not keep the slices. The S-only block (fa_s) keeps
+// scheduling-group barriers, which it follows.
 __device__ __forceinline__ void fa_split(int opaque) {
     if (__builtin_expect(opaque == -12345, 0)) asm volatile("s_nop 0");
 }
@@ -411,25 +415,35 @@ __device__ __forceinline__ void fa_p2_step(const FaCtx &c, int Kn, int Vp, int k
                                            bf16x8 (&pp)[2], f32x16 (&o)[D / 32]) {
     const f32x16 sc = fa_s(c, Kn, q);
     const int lim = w.qpos - kj - 8 * (fa_lane() >> 5);
+    uint32_t pw[8];
     if (PV) {
         const int vbase = fa_vbase();
         const char *Vb = fa_lds + Vp;
         u16x8 vq[2];
 #pragma unroll
         for (int i = 0; i < 2; i++) vq[i] = lds16(fa_vaddr(Vb, vbase, i));
+        uint32_t pk = 0;
+        float ep = 0.0f;
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int jj = 0; jj < 2 * (D / 32); jj++) {
-            const bf16x8 va = __builtin_bit_cast(bf16x8, vq[jj & 1]);
-            if (jj + 2 < 2 * (D / 32)) vq[jj & 1] = lds16(fa_vaddr(Vb, vbase, jj + 2));
+            const bf16x8 va = __builtin_bit_cast(bf16x8, vq[jj % 2]);
+            if (jj + 2 < 2 * (D / 32)) vq[jj % 2] = lds16(fa_vaddr(Vb, vbase, jj + 2));
             o[jj & 7] = mfma32(va, pp[jj >> 3], o[jj & 7]);
+            if ((jj & 1) == 0) pk = pack2(sc[jj], sc[jj + 1]);
+            const float r = __uint_as_float((jj & 1) ? (pk & 0xffff0000u) : (pk << 16));
+            float ev = __builtin_amdgcn_exp2f(fmaf(r, c.c2, -w.K2));
+            if (MASK) ev = fa_keep(jj, lim) ? ev : 0.0f;
+            if (jj & 1) pw[jj >> 1] = pack2(ep, ev);
+            else ep = ev;
+            __builtin_amdgcn_sched_barrier(0);
         }
-    }
-    float e[16];
-    fa_exp16<MASK>(e, sc, c.c2, w.K2, lim);
-    uint32_t pw[8];
+    } else {
+        float e[16];
+        fa_exp16<MASK>(e, sc, c.c2, w.K2, lim);
 #pragma unroll
-    for (int i = 0; i < 8; i++) pw[i] = pack2(e[2 * i], e[2 * i + 1]);
-    if (PV) fa_groups16<2, 4>();
+        for (int i = 0; i < 8; i++) pw[i] = pack2(e[2 * i], e[2 * i + 1]);
+    }
     // keep P(j) in this block (else it is sunk past the next step's S)
     asm volatile("" : "+v"(pw[0]), "+v"(pw[1]), "+v"(pw[2]), "+v"(pw[3]), "+v"(pw[4]),
                  "+v"(pw[5]), "+v"(pw[6]), "+v"(pw[7]));
