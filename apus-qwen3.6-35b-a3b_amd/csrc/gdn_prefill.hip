@@ -183,6 +183,7 @@ __device__ __forceinline__ void put_split8(uint16_t *p, const float (&x)[8]) {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef unsigned short u16x8 __attribute__((ext_vector_type(8)));
+typedef unsigned short u16x4 __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ bf16x8 as_bf(u16x8 v) { return __builtin_bit_cast(bf16x8, v); }
 __device__ __forceinline__ u16x8 ld8(const uint16_t *p) {
@@ -826,26 +827,41 @@ __global__ __launch_bounds__(512) void k_gdn_chunk_scan(
                               ld8(S0h + r16 * SB + kb * 32 + g4 * 8),
                               ld8(S0l + r16 * SB + kb * 32 + g4 * 8), acc);
             const float uu[4] = {cur.u.x, cur.u.y, cur.u.z, cur.u.w};
+            {
+                // tokens rw + kq .. + 3 of column r16: 8-byte pieces
+                u16x4 dh, dl, ph, pl;
 #pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const int t = rw + kq + i;
-                const float d = uu[i] - acc[i];
-                split_bf(d, Dh[r16 * DB + t], Dl[r16 * DB + t]);
-                split_bf(Fs[C + t] * d, Dph[r16 * DB + t], Dpl[r16 * DB + t]);
+                for (int i = 0; i < 4; i++) {
+                    const int t = rw + kq + i;
+                    const float d = uu[i] - acc[i];
+                    uint16_t a0, a1, b0, b1;
+                    split_bf(d, a0, a1);
+                    split_bf(Fs[C + t] * d, b0, b1);
+                    dh[i] = a0; dl[i] = a1; ph[i] = b0; pl[i] = b1;
+                }
+                const int o = r16 * DB + rw + kq;
+                *reinterpret_cast<u16x4 *>(Dh + o) = dh;
+                *reinterpret_cast<u16x4 *>(Dl + o) = dl;
+                *reinterpret_cast<u16x4 *>(Dph + o) = ph;
+                *reinterpret_cast<u16x4 *>(Dpl + o) = pl;
             }
             scan_load_wu(cur, Wb, Ub, cl(ci + 2) * hv + h, wr, lane, cb);
             __syncthreads();           // D complete
+            // S1 = G_C S0 + K^T Dp, formed as [state row][column] (the codes
+            // as the A operand): a lane holds rows i0 + kq .. + 3 of column
+            // r16, so its S0 reads and S1 writes are 16- and 8-byte pieces
             f32x4 sn[2];
             const float gc = Fs[2 * C];
 #pragma unroll
             for (int r = 0; r < 2; r++) {
                 const int i0 = wr * 32 + r * 16;
+                const f32x4 s0 = *reinterpret_cast<const f32x4 *>(S0T + r16 * KP + i0 + kq);
 #pragma unroll
-                for (int i = 0; i < 4; i++) sn[r][i] = gc * S0T[(kq + i) * KP + i0 + r16];
+                for (int i = 0; i < 4; i++) sn[r][i] = gc * s0[i];
 #pragma unroll
                 for (int kb = 0; kb < C / 32; kb++)
                     sn[r] = mfma_x2a(kf.b[2 * r + kb], ld8(Dph + r16 * DB + kb * 32 + g4 * 8),
-                                     ld8(Dpl + r16 * DB + kb * 32 + g4 * 8), sn[r], true);
+                                     ld8(Dpl + r16 * DB + kb * 32 + g4 * 8), sn[r], false);
             }
             scan_load_k(kf, Kp, cl(ci + 1) * hk + kh, wr, lane);
             // the next step's state and factors go to the other copies
@@ -855,13 +871,18 @@ __global__ __launch_bounds__(512) void k_gdn_chunk_scan(
             uint16_t *S1h = S0hb[(ci + 1) & 1], *S1l = S0lb[(ci + 1) & 1];
 #pragma unroll
             for (int r = 0; r < 2; r++) {
-                const int i0 = wr * 32 + r * 16;
+                const int o = wr * 32 + r * 16 + kq;
+                u16x4 h4, l4;
 #pragma unroll
                 for (int i = 0; i < 4; i++) {
-                    const int n = kq + i, col = i0 + r16;
-                    S1T[n * KP + col] = sn[r][i];
-                    split_bf(sn[r][i], S1h[n * SB + col], S1l[n * SB + col]);
+                    uint16_t a0, a1;
+                    split_bf(sn[r][i], a0, a1);
+                    h4[i] = a0;
+                    l4[i] = a1;
                 }
+                *reinterpret_cast<f32x4 *>(S1T + r16 * KP + o) = sn[r];
+                *reinterpret_cast<u16x4 *>(S1h + r16 * SB + o) = h4;
+                *reinterpret_cast<u16x4 *>(S1l + r16 * SB + o) = l4;
             }
             if (more && tid < 3 * C) Fsb[(ci + 1) & 1][tid] = oth.f;
         };
