@@ -595,7 +595,10 @@ __global__ __launch_bounds__(256) void k_gdn_prep(
 // loads, the rows parked in LDS as codes (17 KiB a block, 8 blocks per CU
 // to hide the serial sums), one lane per row for the ordered sum of
 // squares, then elementwise from the registers with 16-byte z loads and
-// y stores. The remaining blocks
+// y stores. The rows, z and y are each touched once: streaming
+// (non-temporal) loads and stores keep them from displacing the next
+// kernels' operands in L2 (T=4096 layer step 0.217 -> 0.212 ms). The
+// remaining blocks
 // write each sequence's new conv state (the last three pre-conv inputs of
 // [old state | tokens]) after every reader of the old one has finished.
 __global__ __launch_bounds__(256) void k_gdn_post(
@@ -623,8 +626,8 @@ __global__ __launch_bounds__(256) void k_gdn_post(
         for (int k = 0; k < NPC; k++) {
             const int e = tid + 256 * k, row = e / (DV / 8), c8 = (e % (DV / 8)) * 8;
             if (row < nr) {
-                ov[k] = *reinterpret_cast<const u16x8 *>(ob + (r0 + row) * DV + c8);
-                zv8[k] = *reinterpret_cast<const u16x8 *>(z + (r0 + row) * DV + c8);
+                ov[k] = __builtin_nontemporal_load(reinterpret_cast<const u16x8 *>(ob + (r0 + row) * DV + c8));
+                zv8[k] = __builtin_nontemporal_load(reinterpret_cast<const u16x8 *>(z + (r0 + row) * DV + c8));
             }
         }
 #pragma unroll
@@ -651,7 +654,7 @@ __global__ __launch_bounds__(256) void k_gdn_post(
                     const float x2 = rndf(x1 * bf2f(wv[i]));
                     out[i] = f2bf(x2 * silu_f[zv[i]]);     // silu(z), fp32
                 }
-                *reinterpret_cast<u16x8 *>(y + off) = out;
+                __builtin_nontemporal_store(out, reinterpret_cast<u16x8 *>(y + off));
             }
         }
         return;
