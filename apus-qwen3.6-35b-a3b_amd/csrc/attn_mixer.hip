@@ -180,7 +180,7 @@ __device__ __forceinline__ void prep_block(
 #pragma unroll
             for (int i = 0; i < 8; i++) {
                 const float f = bf2f(v[i]);
-                ss = ss + f * f;
+                ss = fmaf(f, f, ss);   // f * f exact: bf16 squared
             }
         }
         rs[tid] = 1.0f / sqrtf(ss / (float)D + kEps);

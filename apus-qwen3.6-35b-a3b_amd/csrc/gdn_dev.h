@@ -71,6 +71,10 @@ __device__ __forceinline__ float decay_of(uint16_t a, float A_log,
 
 // Ascending sum of squares of a row of 128 bf16 codes (16-byte aligned),
 // one rounding per mul and add (the l2norm's ordered sum, c/gdn.h:402-416).
+// The squares of bf16 values are exact in fp32 (8-bit significands) when
+// in the normal range, so one fused multiply-add rounds where the
+// reference's multiply-then-add does (only a square below 2^-126 could
+// differ, and only while the running sum is that small too).
 __device__ __forceinline__ float row_sumsq(const uint16_t *row) {
     typedef unsigned short u16x8_t __attribute__((ext_vector_type(8)));
     const u16x8_t *x8 = reinterpret_cast<const u16x8_t *>(row);
@@ -81,7 +85,7 @@ __device__ __forceinline__ float row_sumsq(const uint16_t *row) {
 #pragma unroll
         for (int i = 0; i < 8; i++) {
             const float x = bf2f(v[i]);
-            ss = ss + x * x;
+            ss = fmaf(x, x, ss);
         }
     }
     return ss;

@@ -110,20 +110,21 @@ struct CuArgs {
 
 constexpr int KT = 4;                          // tokens per chunk
 
-// Ascending sum of squares of 128 LDS floats (one rounding per mul and
-// add). Unrolled by four 16-byte reads: enough reads in flight to cover
-// most of their latency, few enough registers to run beside a live state
-// tile.
+// Ascending sum of squares of 128 LDS floats, each a bf16 value (one
+// rounding per mul and add; fused as in apus::row_sumsq, exact for the
+// same reason). Unrolled by four 16-byte reads: enough reads in flight to
+// cover most of their latency, few enough registers to run beside a live
+// state tile.
 __device__ __forceinline__ float sumsq128(const float *x) {
     const float4 *x4 = reinterpret_cast<const float4 *>(x);
     float ss = 0.0f;
 #pragma unroll 4
     for (int i = 0; i < 32; i++) {
         const float4 v = x4[i];
-        ss = ss + v.x * v.x;
-        ss = ss + v.y * v.y;
-        ss = ss + v.z * v.z;
-        ss = ss + v.w * v.w;
+        ss = fmaf(v.x, v.x, ss);
+        ss = fmaf(v.y, v.y, ss);
+        ss = fmaf(v.z, v.z, ss);
+        ss = fmaf(v.w, v.w, ss);
     }
     return ss;
 }
@@ -403,17 +404,18 @@ constexpr int PC = 4 * DK;   // pre-conv channels of one K head: q, k, 2 x v
 
 // Ascending sum of squares of one 128-float LDS row, one rounding per mul
 // and add, with 16-byte reads kept in flight ahead of the add chain (over a
-// row of 128 bf16 codes: gdn_dev.h).
+// row of 128 bf16 codes: gdn_dev.h). The row holds bf16 values, so the
+// fused form is exact as there.
 __device__ __forceinline__ float row_sumsq(const float *row) {
     const float4 *x4 = reinterpret_cast<const float4 *>(row);
     float ss = 0.0f;
 #pragma unroll 8
     for (int j = 0; j < DK / 4; j++) {
         const float4 v = x4[j];
-        ss = ss + v.x * v.x;
-        ss = ss + v.y * v.y;
-        ss = ss + v.z * v.z;
-        ss = ss + v.w * v.w;
+        ss = fmaf(v.x, v.x, ss);
+        ss = fmaf(v.y, v.y, ss);
+        ss = fmaf(v.z, v.z, ss);
+        ss = fmaf(v.w, v.w, ss);
     }
     return ss;
 }

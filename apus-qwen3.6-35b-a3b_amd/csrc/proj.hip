@@ -9,7 +9,8 @@
 //                (ascending, one rounding per multiply and per add: the
 //                scalar anchor c/bf16.h:285-293, which the reference's
 //                threaded and Metal paths reproduce bitwise). Bitwise
-//                against the reference. The weight row is read 16 bytes
+//                against the reference (products below fp32's normal range
+//                aside: see k_gemm_seq). The weight row is read 16 bytes
 //                at a time, 16 to 32 pieces ahead of the add chain; the x row
 //                is staged in LDS once per wavefront.
 //   k_gemm_tile  the 32x32x16 bf16 MFMA with fp32 accumulation, for every
@@ -48,8 +49,13 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 // One output per lane: outputs blockIdx.x*64 + lane of row blockIdx.y.
 // VEC: K is a multiple of 8 and the rows are 16-byte aligned. XF: the x
 // row is staged in LDS as fp32 (widened once per wavefront instead of once
-// per output; K up to 16384), so a k costs the weight's widening, one
-// multiply and one add.
+// per output; K up to 16384), so a k costs the weight's widening and one
+// fused multiply-add. The product of two bf16 values (8-bit significands)
+// is exact in fp32 whenever it lies in fp32's normal range, so the fused
+// form rounds exactly where the reference's multiply-then-add does: once,
+// at the add. Only a product below 2^-126 in magnitude (a subnormal,
+// which the reference rounds before adding) can differ, and then only if
+// the running sum is itself that small. (25.4 -> 21.0 us for 12352 x 2048.)
 template <bool VEC, bool XF = false>
 __global__ __launch_bounds__(64) void k_gemm_seq(const uint16_t *__restrict__ w,
                                                  const uint16_t *__restrict__ x,
@@ -113,7 +119,7 @@ __global__ __launch_bounds__(64) void k_gemm_seq(const uint16_t *__restrict__ w,
                 float xv[8];
                 xk(p + i, xv);
 #pragma unroll
-                for (int j = 0; j < 8; j++) acc = acc + bf2f(qa[i][j]) * xv[j];
+                for (int j = 0; j < 8; j++) acc = fmaf(bf2f(qa[i][j]), xv[j], acc);
             }
 #pragma unroll
             for (int i = 0; i < R; i++) qa[i] = w8[min(p + 2 * R + i, n8 - 1)];
@@ -124,7 +130,7 @@ __global__ __launch_bounds__(64) void k_gemm_seq(const uint16_t *__restrict__ w,
                 float xv[8];
                 xk(p + R + i, xv);
 #pragma unroll
-                for (int j = 0; j < 8; j++) acc = acc + bf2f(qb[i][j]) * xv[j];
+                for (int j = 0; j < 8; j++) acc = fmaf(bf2f(qb[i][j]), xv[j], acc);
             }
         }
         for (int i = 0; p + i < n8; i++) {
@@ -132,7 +138,7 @@ __global__ __launch_bounds__(64) void k_gemm_seq(const uint16_t *__restrict__ w,
             float xv[8];
             xk(p + i, xv);
 #pragma unroll
-            for (int j = 0; j < 8; j++) acc = acc + bf2f(wv[j]) * xv[j];
+            for (int j = 0; j < 8; j++) acc = fmaf(bf2f(wv[j]), xv[j], acc);
         }
     } else {
         for (int k = 0; k < K; k++) acc = acc + bf2f(wr[k]) * bf2f(xr[k]);

@@ -63,6 +63,26 @@ def test_gemm_dev_bitwise(hip, orc, M, O, K):
     assert np.array_equal(y.cpu().numpy().view(np.uint16), orc.bf16_gemm(w, x))
 
 
+def test_gemm_dev_bitwise_wide_range(hip, orc):
+    """Operands whose magnitudes span 2^-60 .. 2^60 (every product still in
+    fp32's normal range): the sequential kernel's fused multiply-add rounds
+    where the reference's multiply-then-add does, so the result stays
+    bitwise; exact zeros and sign mixes included."""
+    import torch
+    rng = np.random.default_rng(77)
+    O, K, M = 4096, 2048, 2
+    def wide(shape):
+        v = rng.standard_normal(shape) * np.exp2(rng.integers(-60, 61, shape))
+        v[rng.random(shape) < 0.05] = 0.0
+        return synth.bf16_bits(v.astype(np.float32))
+    w, x = wide((O, K)), wide((M, K))
+    y = torch.empty((M, O), dtype=torch.int16, device="cuda")
+    hip.bf16_gemm_dev(_dev(torch, w), _dev(torch, x), y, exact=True)
+    torch.cuda.synchronize()
+    assert np.array_equal(y.cpu().numpy().view(np.uint16), orc.bf16_gemm(w, x))
+    assert np.array_equal(hip.bf16_gemv(w, np.ascontiguousarray(x[0])), orc.bf16_gemm(w, x)[0])
+
+
 # one shape per tile configuration of the MFMA GEMM (64 x 64, 128 x 128,
 # 128 x 256, 256 x 256), with ragged row / output edges and an output count
 # that is not a multiple of 4 (the element-store epilogue)
