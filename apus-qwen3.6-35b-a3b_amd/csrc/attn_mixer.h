@@ -67,11 +67,12 @@ int attn_meta(size_t B, const int32_t *cu, const int32_t *pos0, const int32_t *r
               size_t *max_tok);
 
 // q/k (1+w) RMSNorm, RoPE at each token's position, append k and v to the
-// cache; writes the roped q into qn [Ttot, nh, d]. max_pos: one past the
-// largest position written (RoPE table size); maxnb: attn_max_vblocks.
+// cache; writes the roped q into qn [Ttot, nh, d] (with qrows false, only
+// the k rows and the appends: the caller forms q itself). max_pos: one past
+// the largest position written (RoPE table size); maxnb: attn_max_vblocks.
 int attn_prep(const ApusHipAttnLayer *L, const AttnSeqs &sq, const int32_t *dmeta,
               size_t Ttot, size_t max_pos, int maxnb, const uint16_t *qg, const uint16_t *k,
-              const uint16_t *v, const KvRef &kv, uint16_t *qn);
+              const uint16_t *v, const KvRef &kv, uint16_t *qn, bool qrows = true);
 
 // the most 32-position cache blocks one sequence's new tokens touch
 int attn_max_vblocks(size_t B, const int32_t *cu, const int32_t *pos0);

@@ -118,9 +118,12 @@ __device__ __forceinline__ void prep_block(
     int bid, PrepLds &L, const Meta &mt, const AttnSeqs &sq, const uint16_t *__restrict__ qg,
     const uint16_t *__restrict__ kin, const uint16_t *__restrict__ qn_w,
     const uint16_t *__restrict__ kn_w, const uint16_t *__restrict__ rope, const KvRef &kv,
-    uint16_t *__restrict__ qn, int nh, int nkv, int nrows, int rpb, uint16_t *__restrict__ tr_kf) {
+    uint16_t *__restrict__ qn, int nh, int nkv, int nrows, int rpb, uint16_t *__restrict__ tr_kf,
+    int qrows) {
     const int32_t *cu = mt.cu, *pos0 = mt.pos0;
-    const int nslot = nh + nkv;
+    // rows are (token, q head or kv head), or with qrows == 0 (a prefill,
+    // whose flash kernel forms its q rows itself) (token, kv head) only
+    const int nslot = qrows ? nh + nkv : nkv, s0 = qrows ? 0 : nh;
     const int r0 = bid * rpb, nr = min(rpb, nrows - r0);
     const int tid = threadIdx.x;
     uint16_t *xs = L.xs, *rcs = L.rcs;
@@ -141,7 +144,7 @@ __device__ __forceinline__ void prep_block(
 #pragma unroll
     for (int k = 0; k < PRB * (D / 8) / 256; k++) {
         const int e = tid + 256 * k, r = min(e / (D / 8), nr - 1), pc = e % (D / 8);
-        const int row = r0 + r, tt = row / nslot, slot = row % nslot;
+        const int row = r0 + r, tt = row / nslot, slot = s0 + row % nslot;
         const uint16_t *x = slot < nh ? qg + ((size_t)tt * nh + slot) * 2 * D
                                       : kin + ((size_t)tt * nkv + (slot - nh)) * D;
         xv8[k] = *reinterpret_cast<const u16x8 *>(x + pc * 8);
@@ -153,7 +156,7 @@ __device__ __forceinline__ void prep_block(
         cv2[k] = *reinterpret_cast<const u16x8 *>(rope + (size_t)tpos[(r0 + r) / nslot - tt0] * ROT + pc * 8);
     }
     if (tid < nr) {                           // k rows' cache offsets, one lane per row
-        const int slot = (r0 + tid) % nslot, ti = (r0 + tid) / nslot - tt0;
+        const int slot = s0 + (r0 + tid) % nslot, ti = (r0 + tid) / nslot - tt0;
         if (slot >= nh) {
             const int pos = tpos[ti];
             rdst[tid] = ((kv_block_id(kv, thd[ti], pos / KVB) * nkv + (slot - nh)) * KVB +
@@ -198,7 +201,7 @@ __device__ __forceinline__ void prep_block(
     for (int it = 0; it < (nr + 7) / 8; it++) {
         const int r = it * 8 + (tid >> 5);
         if (r >= nr) break;
-        const int row = r0 + r, tt = row / nslot, slot = row % nslot;
+        const int row = r0 + r, tt = row / nslot, slot = s0 + row % nslot;
         const bool isq = slot < nh;
         const u16x8 wv = isq ? wq : wk;
         const float rr = rs[r];
@@ -288,12 +291,12 @@ __global__ __launch_bounds__(256) void k_attn_prep(
     const uint16_t *__restrict__ kin, const uint16_t *__restrict__ vin,
     const uint16_t *__restrict__ qn_w, const uint16_t *__restrict__ kn_w,
     const uint16_t *__restrict__ rope, KvRef kv, uint16_t *__restrict__ qn, int nh, int nkv,
-    int nrows, int rpb, int nprep, int maxnb, uint16_t *__restrict__ tr_kf) {
+    int nrows, int rpb, int nprep, int maxnb, uint16_t *__restrict__ tr_kf, int qrows) {
     __shared__ __attribute__((aligned(16))) char lds[kPrepKernLds];
     const Meta mt = meta_of(sq, dmeta);
     if ((int)blockIdx.x < nprep)
         prep_block((int)blockIdx.x, *reinterpret_cast<PrepLds *>(lds), mt, sq, qg, kin, qn_w,
-                   kn_w, rope, kv, qn, nh, nkv, nrows, rpb, tr_kf);
+                   kn_w, rope, kv, qn, nh, nkv, nrows, rpb, tr_kf, qrows);
     else
         vappend_block((int)blockIdx.x - nprep, reinterpret_cast<uint16_t *>(lds), mt, vin, kv,
                       nkv, maxnb);
@@ -1083,20 +1086,21 @@ int attn_meta(size_t B, const int32_t *cu, const int32_t *pos0, const int32_t *r
 
 int attn_prep(const ApusHipAttnLayer *L, const AttnSeqs &sq, const int32_t *dmeta,
               size_t Ttot, size_t max_pos, int maxnb, const uint16_t *qg, const uint16_t *k,
-              const uint16_t *v, const KvRef &kv, uint16_t *qn) {
+              const uint16_t *v, const KvRef &kv, uint16_t *qn, bool qrows) {
     const uint16_t *rope = rope_table(L->rot, L->theta, max_pos);
     if (!rope) return kErrHip;
-    const size_t nrows = Ttot * (L->nh + L->nkv);
+    const size_t nrows = Ttot * (qrows ? L->nh + L->nkv : L->nkv);
     // few rows (decode): small blocks, so they spread over the chip
     const int rpb = nrows < (size_t)8 * PRB * cu_count() ? 8 : PRB;
     const unsigned nprep = cdiv(nrows, rpb), nvapp = (unsigned)(sq.n * L->nkv * maxnb);
     APUS_TIMED("k_attn_prep",
                k_attn_prep<<<nprep + nvapp, 256, 0, stream()>>>(
         sq, dmeta, qg, k, v, L->qn_w, L->kn_w, rope, kv, qn, (int)L->nh, (int)L->nkv,
-        (int)nrows, rpb, (int)nprep, maxnb, attn_trace() ? attn_trace()->kf : nullptr));
+        (int)nrows, rpb, (int)nprep, maxnb, attn_trace() ? attn_trace()->kf : nullptr,
+        qrows ? 1 : 0));
     if (int r = launch_check("k_attn_prep")) return r;
     if (const ApusHipAttnTrace *tr = attn_trace()) {
-        if (tr->qf)
+        if (tr->qf && qrows)
             APUS_HIP_TRY(hipMemcpyAsync(tr->qf, qn, Ttot * L->nh * D * 2, hipMemcpyDeviceToDevice,
                                         stream()));
         if (tr->mgate) {

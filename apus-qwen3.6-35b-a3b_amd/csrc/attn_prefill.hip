@@ -474,7 +474,8 @@ __device__ __forceinline__ void fa_publish() {
 }
 
 __global__ __launch_bounds__(64 * NW) void k_attn_fa(
-    FaSeqs sq, const int32_t *__restrict__ dmeta, const uint16_t *__restrict__ qn,
+    FaSeqs sq, const int32_t *__restrict__ dmeta, const uint16_t *__restrict__ qn_w,
+    const uint16_t *__restrict__ rope,
     const uint16_t *__restrict__ qg, KvRef kv, int nh, int nkv, float scale,
     uint16_t *__restrict__ y, const uint16_t *__restrict__ sig_bf, uint16_t *__restrict__ tr_attno) {
     const int n = sq.n;
@@ -566,12 +567,77 @@ __global__ __launch_bounds__(64 * NW) void k_attn_fa(
 
     // query row of this lane: token 4w + l32/8, head l32%8 of the kv head
     const int tk = c.wave * 4 + c.l32 / GRP, head = kvh * GRP + c.l32 % GRP;
+    // The q row, formed here from the layer's input as k_attn_prep forms k
+    // (c/attn.h:175-236 via c/layer.h:300-312): (1+w) RMSNorm with the
+    // ascending sum of squares, then NeoX RoPE on dims 0..63 at the token's
+    // position, each product rounded as the reference rounds it. The lane
+    // holds dims 16 ks + 8 h .. +7; the sum runs over the 32 8-dim chunks in
+    // order, each continued by the half that holds it (the running value
+    // crosses to the other half after every chunk). A RoPE pair (d, d + 32)
+    // lies in chunks ks and ks + 2 of the same lane.
     bf16x8 q[D / 16];
     {
-        const uint16_t *qr = qn + ((size_t)(tb + min(tk, nt - 1)) * nh + head) * D + c.h * 8;
+        constexpr int R = 32;                  // rotary pairs (64 rotated dims)
+        const int tq = min(tk, nt - 1);
+        const uint16_t *xr = qg + ((size_t)(tb + tq) * nh + head) * 2 * D + c.h * 8;
+        float ss = 0.0f;
+        {
+            u16x8 xv[D / 16];
 #pragma unroll
-        for (int ks = 0; ks < D / 16; ks++)
-            q[ks] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u16x8 *>(qr + ks * 16));
+            for (int ks = 0; ks < D / 16; ks++) xv[ks] = *reinterpret_cast<const u16x8 *>(xr + ks * 16);
+#pragma unroll
+            for (int ks = 0; ks < D / 16; ks++) {
+#pragma unroll
+                for (int hh = 0; hh < 2; hh++) {
+                    float t = ss;
+#pragma unroll
+                    for (int e = 0; e < 8; e++) {
+                        const float f = bf2f(xv[ks][e]);
+                        t = fmaf(f, f, t);     // f * f exact: bf16 squared
+                    }
+                    const float o = __shfl_xor(t, 32);
+                    ss = c.h == hh ? t : o;
+                }
+            }
+        }
+        // the row is read again below, a chunk at a time (an L2 hit), so
+        // that the 64 registers of the first read are not live beside q
+        asm volatile("" ::: "memory");
+        const float rr = 1.0f / sqrtf(ss / (float)D + 1e-6f);
+        // normed value of dim e of the lane's chunk ks
+        auto nrm = [&](const u16x8 &xk, int e, const u16x8 &wv) {
+            return rndf((bf2f(xk[e]) * rr) * (1.0f + bf2f(wv[e])));
+        };
+        auto ldx = [&](int ks) { return *reinterpret_cast<const u16x8 *>(xr + ks * 16); };
+        const uint16_t *cs = rope + (size_t)(qpos0 + tq) * (2 * R);
+#pragma unroll
+        for (int ks = 0; ks < 2; ks++) {
+            const u16x8 w0 = *reinterpret_cast<const u16x8 *>(qn_w + ks * 16 + c.h * 8);
+            const u16x8 w1 = *reinterpret_cast<const u16x8 *>(qn_w + (ks + 2) * 16 + c.h * 8);
+            const int i0 = ks * 16 + c.h * 8;          // pair index of the chunk's first dim
+            const u16x8 cv = *reinterpret_cast<const u16x8 *>(cs + i0);
+            const u16x8 sv = *reinterpret_cast<const u16x8 *>(cs + R + i0);
+            const u16x8 x0 = ldx(ks), x1 = ldx(ks + 2);
+            u16x8 lo, hi;
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                const float a = nrm(x0, e, w0), b = nrm(x1, e, w1);
+                const float cc = bf2f(cv[e]), sn = bf2f(sv[e]);
+                lo[e] = f2bf(rndf(a * cc) + rndf(-b * sn));     // dim d < 32
+                hi[e] = f2bf(rndf(b * cc) + rndf(a * sn));      // dim d + 32
+            }
+            q[ks] = __builtin_bit_cast(bf16x8, lo);
+            q[ks + 2] = __builtin_bit_cast(bf16x8, hi);
+        }
+#pragma unroll
+        for (int ks = 4; ks < D / 16; ks++) {
+            const u16x8 wv = *reinterpret_cast<const u16x8 *>(qn_w + ks * 16 + c.h * 8);
+            const u16x8 xk = ldx(ks);
+            u16x8 out;
+#pragma unroll
+            for (int e = 0; e < 8; e++) out[e] = f2bf(nrm(xk, e, wv));
+            q[ks] = __builtin_bit_cast(bf16x8, out);
+        }
     }
     FaRow w{qpos0 + tk, -INFINITY, 0.0f, 0.0f};
 
@@ -736,17 +802,27 @@ int attn_prefill_kv(const ApusHipAttnLayer *L, size_t B, const int32_t *cu, cons
         fdm = (const int32_t *)upload_async(meta.data(), meta.size() * 4);
         if (!fdm) return kErrHip;
     }
-    uint16_t *qn = (uint16_t *)scratch(kScratchAttnQ, Ttot * L->nh * D * 2);
-    if (!qn) return kErrHip;
+    // the q rows are formed by the flash kernel itself; prep norms, ropes
+    // and appends the k rows (and, for a traced call, also writes the q rows
+    // the trace records; with one kv head a prep block's k rows would span
+    // more tokens than its metadata holds, so it keeps the q rows too)
+    const bool qrows = attn_trace() != nullptr || L->nkv < 2;
+    uint16_t *qn = nullptr;
+    if (qrows) {
+        qn = (uint16_t *)scratch(kScratchAttnQ, Ttot * L->nh * D * 2);
+        if (!qn) return kErrHip;
+    }
     if (int r = attn_prep(L, as, adm, Ttot, max_pos, attn_max_vblocks(B, cu, pos0), qg, k, v,
-                          kv, qn))
+                          kv, qn, qrows))
         return r;
+    const uint16_t *rope = rope_table(L->rot, L->theta, max_pos);
+    if (!rope) return kErrHip;
     const float scale = (float)(1.0 / sqrt((double)L->d));
     const ActTables *tabs = act_tables();
     if (!tabs) return kErrHip;
     APUS_TIMED("k_attn_fa",
                k_attn_fa<<<(unsigned)(ntiles * L->nkv), 64 * NW, 0, stream()>>>(
-                   fs, fdm, qn, qg, kv, (int)L->nh, (int)L->nkv, scale, y, tabs->sig_bf,
+                   fs, fdm, L->qn_w, rope, qg, kv, (int)L->nh, (int)L->nkv, scale, y, tabs->sig_bf,
                    attn_trace() ? attn_trace()->attno : nullptr));
     APUS_LAUNCHED("k_attn_fa");
     return kOk;
