@@ -571,9 +571,9 @@ __global__ __launch_bounds__(64 * NW) void k_attn_fa(
     // (c/attn.h:175-236 via c/layer.h:300-312): (1+w) RMSNorm with the
     // ascending sum of squares, then NeoX RoPE on dims 0..63 at the token's
     // position, each product rounded as the reference rounds it. The lane
-    // holds dims 16 ks + 8 h .. +7; the sum runs over the 32 8-dim chunks in
-    // order, each continued by the half that holds it (the running value
-    // crosses to the other half after every chunk). A RoPE pair (d, d + 32)
+    // holds dims 16 ks + 8 h .. +7, and lane l ^ 32 the other 8 of each 16;
+    // each lane takes its partner's chunks by exchange and runs the whole
+    // ascending sum over the 32 8-dim chunks itself. A RoPE pair (d, d + 32)
     // lies in chunks ks and ks + 2 of the same lane.
     bf16x8 q[D / 16];
     {
@@ -585,18 +585,25 @@ __global__ __launch_bounds__(64 * NW) void k_attn_fa(
             u16x8 xv[D / 16];
 #pragma unroll
             for (int ks = 0; ks < D / 16; ks++) xv[ks] = *reinterpret_cast<const u16x8 *>(xr + ks * 16);
+            // the other half's chunks (independent exchanges, all in flight
+            // together); then both halves run the whole chain, in order
+            u16x8 px[D / 16];
+#pragma unroll
+            for (int ks = 0; ks < D / 16; ks++) {
+                const uint4 u = __builtin_bit_cast(uint4, xv[ks]);
+                px[ks] = __builtin_bit_cast(u16x8, make_uint4(__shfl_xor(u.x, 32), __shfl_xor(u.y, 32),
+                                                              __shfl_xor(u.z, 32), __shfl_xor(u.w, 32)));
+            }
 #pragma unroll
             for (int ks = 0; ks < D / 16; ks++) {
 #pragma unroll
                 for (int hh = 0; hh < 2; hh++) {
-                    float t = ss;
+                    const u16x8 xc = hh == c.h ? xv[ks] : px[ks];   // chunk (ks, hh)
 #pragma unroll
                     for (int e = 0; e < 8; e++) {
-                        const float f = bf2f(xv[ks][e]);
-                        t = fmaf(f, f, t);     // f * f exact: bf16 squared
+                        const float f = bf2f(xc[e]);
+                        ss = fmaf(f, f, ss);   // f * f exact: bf16 squared
                     }
-                    const float o = __shfl_xor(t, 32);
-                    ss = c.h == hh ? t : o;
                 }
             }
         }
