@@ -104,9 +104,14 @@ __global__ void k_gdn_unpack(const float *__restrict__ src, float *__restrict__ 
 // input slots and cu[2B+1..3B] the output slots.
 constexpr int kInlineSeqs = 480;
 constexpr int kInlineWords = 2 * kInlineSeqs + 1;
-struct CuArgs {
-    int32_t cu[kInlineWords];
+template <int NW> struct CuArgsN {
+    int32_t cu[NW];
 };
+using CuArgs = CuArgsN<kInlineWords>;
+// A call of a few sequences passes a short argument block instead: the
+// launch copies the whole by-value block, and 3.8 KiB of it cost ~0.3 us of
+// a one-sequence step.
+constexpr int kSmallWords = 16;
 
 constexpr int KT = 4;                          // tokens per chunk
 
@@ -198,10 +203,10 @@ __device__ __forceinline__ void recur_chunk(float (&sr)[DK], const float (*raw)[
     }
 }
 
-template <int MODE>
+template <int MODE, int NW>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
 void k_gdn_decode(
-    CuArgs ca, const int32_t *__restrict__ dcu, int nseq, const uint16_t *qkv,
+    CuArgsN<NW> ca, const int32_t *__restrict__ dcu, int nseq, const uint16_t *qkv,
     const uint16_t *z, const uint16_t *a, const uint16_t *b, const uint16_t *conv_w,
     const float *A_log, const float *dt_bias, const uint16_t *onorm_w,
     const uint16_t *conv_state, const float *S, uint16_t *conv_out, float *S_out,
@@ -810,12 +815,25 @@ static int gdn_decode_run(const ApusHipGdnLayer *L, size_t B, const int32_t *cu,
     const float qscale = (float)pow((double)L->dk, -0.5);
     int max_tok = 0;                           // the most tokens of one sequence
     for (size_t s = 0; s < B; s++) max_tok = std::max(max_tok, cu[s + 1] - cu[s]);
-    auto kern = max_tok <= 1 ? k_gdn_decode<0> : max_tok <= KT ? k_gdn_decode<1> : k_gdn_decode<2>;
-    APUS_TIMED("k_gdn_decode",
-               kern<<<(unsigned)(B * L->hk), 256, 0, stream()>>>(
-        ca, dcu, (int)B, qkv, z, a, b, L->conv_w, L->A_log, L->dt_bias, L->onorm_w,
-        conv_in, S_in, conv_out, S_out, y, (int)L->hk, qscale, dsin, dsout, (int)slots_inline,
-        tr ? tr->rec_o : nullptr));
+    auto launch = [&](auto args) {
+        constexpr int NW = sizeof(args.cu) / sizeof(int32_t);
+        auto kern = max_tok <= 1 ? k_gdn_decode<0, NW>
+                                 : max_tok <= KT ? k_gdn_decode<1, NW> : k_gdn_decode<2, NW>;
+        APUS_TIMED("k_gdn_decode",
+                   kern<<<(unsigned)(B * L->hk), 256, 0, stream()>>>(
+            args, dcu, (int)B, qkv, z, a, b, L->conv_w, L->A_log, L->dt_bias, L->onorm_w,
+            conv_in, S_in, conv_out, S_out, y, (int)L->hk, qscale, dsin, dsout,
+            (int)slots_inline, tr ? tr->rec_o : nullptr));
+    };
+    // the words the kernel reads: cu[0..B], then the inline slot maps
+    const size_t used = dcu ? 0 : (slots_inline ? 3 * B + 1 : B + 1);
+    if (used <= (size_t)kSmallWords) {
+        CuArgsN<kSmallWords> sa;
+        memcpy(sa.cu, ca.cu, sizeof(sa.cu));
+        launch(sa);
+    } else {
+        launch(ca);
+    }
     APUS_LAUNCHED("k_gdn_decode");
     if (tr && tr->onorm)                       // the gated norm's output is y
         APUS_HIP_TRY(hipMemcpyAsync(tr->onorm, y, (size_t)cu[B] * L->hv * DV * 2,
