@@ -28,15 +28,14 @@ def _td(torch, a):
     return torch.from_numpy(np.ascontiguousarray(a).view(np.int16)).to("cuda")
 
 
-def _run(hip, orc, rng, cu, pos0, max_seq, tag="", edit=None):
+def _run(hip, orc, rng, cu, pos0, max_seq, tag="", edit=None, dims=synth.ATTN_DIMS):
     import torch
-    dims = synth.ATTN_DIMS
     nh, nkv, d, rot, theta = dims
     B = len(cu) - 1
     T = int(cu[-1])
     print(f"[attn_prefill {tag}] B={B} T={T} pos0={list(pos0)[:6]} max_seq={max_seq}", flush=True)
-    w = synth.attn_weights(rng)
-    tok = synth.attn_tokens(rng, T)
+    w = synth.attn_weights(rng, dims)
+    tok = synth.attn_tokens(rng, T, dims)
     kc = synth.normal_bf16(rng, (B, max_seq, nkv, d))
     vc = synth.normal_bf16(rng, (B, max_seq, nkv, d))
     if edit:
@@ -88,6 +87,15 @@ def test_prefill_score_growth(hip, orc):
         kc[:, :32] = synth.bf16_bits(np.float32(-250.0))
     _run(hip, orc, np.random.default_rng(14), [0, 40, 75], [64, 96], 192, tag="growth",
          edit=edit)
+
+
+def test_prefill_one_kv_head(hip, orc):
+    """One kv head (8 q heads): the prep kernel then keeps forming the q rows
+    too (its k-row blocks would span more tokens than their metadata
+    holds), while the flash kernel forms its own."""
+    nh, nkv, d, rot, theta = synth.ATTN_DIMS
+    _run(hip, orc, np.random.default_rng(15), [0, 45, 80], [0, 70], 160, tag="nkv1",
+         dims=(8, 1, d, rot, theta))
 
 
 def test_prefill_tile_edges(hip, orc):
