@@ -6,7 +6,9 @@
 // k_attn_fa: one workgroup of 8 wavefronts (two per SIMD) per (32-token
 // query tile, kv head), tiles dealt longest first. The 8 q heads of the
 // kv head x 32 tokens are 256 query rows; wavefront w owns tokens
-// 4w..4w+3 (32 rows: one MFMA N-tile), its Q rows held in registers.
+// 4w..4w+3 (32 rows: one MFMA N-tile), its Q rows held in registers. It
+// forms those rows itself from the layer input ((1+w) RMSNorm, RoPE);
+// k_attn_prep forms the k rows and appends k and v to the cache.
 //
 // The attention runs over the keys twice:
 //   pass 1: S^T = K Q^T on MFMA 32x32x16 bf16 (fp32 accumulation); with
