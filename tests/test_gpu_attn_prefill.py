@@ -89,6 +89,13 @@ def test_prefill_score_growth(hip, orc):
          edit=edit)
 
 
+def test_prefill_long_prefix(hip, orc):
+    """A continuation after a 30,000-position cached prefix: RoPE at large
+    positions in the flash kernel's own q rows, and ~470 key tiles per
+    query tile with the query rows at their end."""
+    _run(hip, orc, np.random.default_rng(16), [0, 20], [30000], 30048, tag="long-prefix")
+
+
 def test_prefill_one_kv_head(hip, orc):
     """One kv head (8 q heads): the prep kernel then keeps forming the q rows
     too (its k-row blocks would span more tokens than their metadata
