@@ -492,7 +492,10 @@ int apus_hip_attn_layer_free(ApusHipAttnLayer *layer);
  * apus_bf16_gemv_hot / apus_bf16_gemm_hot, c/bf16.h:199-231) with their
  * argument lists. HOST pointers. The k sum runs in the reference's order
  * (ascending k, one rounding per multiply and per add, c/bf16.h:285-293),
- * so y is bitwise the reference's. w must be a stable weight: its device
+ * so y is bitwise the reference's. (The multiply and add run fused: a
+ * product of two bf16 values is exact in fp32, so the fused form rounds
+ * where the reference does; only a product below 2^-126 in magnitude,
+ * while the running sum is that small too, could round differently.) w must be a stable weight: its device
  * copy is made at the first call and reused while (w, O*K) is unchanged
  * (the Metal backend's stable-pointer rule, c/backend_metal.h:42-48);
  * apus_hip_bf16_weights_release drops every copy. */
